@@ -1,0 +1,72 @@
+"""ctypes binding of libbzpf.so (the C ABI declared in include/bzpf.h).
+
+The library is built in-tree by ``boltz_mlx_amd/build.py`` (``__graft_entry__.build()``). There is no fallback:
+importing the compute path without the library, or calling it without a ROCm device, raises.
+"""
+
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "libbzpf.so")
+
+F32, F16 = 0, 1
+
+vp, i32, i64, f32 = C.c_void_p, C.c_int, C.c_int64, C.c_float
+
+# name -> argtypes (restype is int unless listed in _RESTYPES)
+SIGNATURES = {
+    "bzpf_version": [],
+    "bzpf_last_error": [],
+    "bzpf_trimul_ld": [i64],
+    "bzpf_layernorm": [vp, i32, vp, vp, f32, vp, i32, i64, i32, vp],
+    "bzpf_add_ln": [vp, vp, i32, f32, i32, vp, vp, f32, vp, i32, i32, i64, i32, vp],
+    "bzpf_trimul_proj": [vp, vp, vp, f32, i32, vp, i32, i64, i64, i32, vp],
+    "bzpf_trimul_contract": [vp, vp, i32, i64, i64, i32, vp],
+    "bzpf_trimul_tail": [vp, vp, vp, f32, vp, vp, vp, vp, i32, vp, vp, f32, vp, i32, i64, i64, i32, vp],
+    "bzpf_triattn_proj": [vp, vp, i32, vp, vp, i32, i64, i32, i32, i32, vp],
+    "bzpf_triattn_core": [vp, vp, vp, i64, i64, f32, vp, i32, i64, i32, i32, vp],
+    "bzpf_linear_resid_ln": [vp, vp, i32, vp, i32, vp, vp, f32, vp, i32, i64, i32, vp],
+    "bzpf_transition": [vp, vp, vp, vp, i32, vp, vp, f32, vp, i32, i64, i32, i32, vp],
+    "bzpf_linear": [vp, vp, vp, vp, i32, i32, i64, i32, i32, i32, vp],
+    "bzpf_swiglu": [vp, vp, i32, i64, i32, vp],
+    "bzpf_seq_attention": [vp, vp, vp, vp, i64, vp, vp, f32, vp, i64, i32, i64, i32, i32, vp],
+    "bzpf_pair_bias": [vp, vp, vp, f32, vp, vp, i32, i64, i32, i32, vp],
+}
+_RESTYPES = {"bzpf_version": C.c_char_p, "bzpf_last_error": C.c_char_p, "bzpf_trimul_ld": i64}
+
+_lib = None
+
+
+class BzpfError(RuntimeError):
+    pass
+
+
+def load(path: str = LIB_PATH):
+    """Load (once) and return the library with argtypes set. Raises if it has not been built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    # torch first: its HIP runtime (torch/lib/libamdhip64.so, soname libamdhip64.so.7) must be the one mapped
+    # when the library resolves libamdhip64.so.7, so that the process holds a single runtime instance.
+    import torch  # noqa: F401
+
+    if not os.path.exists(path):
+        raise BzpfError(f"{path} not found: build it with `python -c 'import __graft_entry__ as g; g.build()'` "
+                        "(or python boltz_mlx_amd/build.py)")
+    lib = C.CDLL(path)
+    for name, args in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.argtypes = args
+        fn.restype = _RESTYPES.get(name, i32)
+    _lib = lib
+    return lib
+
+
+def call(name: str, *args) -> None:
+    """Call an entry point; a non-zero status raises BzpfError with the library's message."""
+    rc = getattr(load(), name)(*args)
+    if rc != 0:
+        msg = load().bzpf_last_error().decode()
+        raise BzpfError(f"{name} failed ({rc}): {msg}")

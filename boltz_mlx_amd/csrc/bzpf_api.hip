@@ -1,0 +1,219 @@
+// C-ABI entry points (declared in include/bzpf.h): argument validation, dispatch to the launchers, error capture.
+#include <cstdarg>
+#include <cstdio>
+
+#include "../../include/bzpf.h"
+#include "bzpf_kernels.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int done(hipError_t e, const char* what) {
+  if (e == hipSuccess) {
+    g_err[0] = 0;
+    return BZPF_OK;
+  }
+  return fail(BZPF_ELAUNCH, "%s: %s", what, hipGetErrorString(e));
+}
+
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool dt_ok(int dt) { return dt == BZPF_F32 || dt == BZPF_F16; }
+hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
+
+}  // namespace
+
+#define REQUIRE(cond, ...) \
+  do {                     \
+    if (!(cond)) return fail(BZPF_EINVAL, __VA_ARGS__); \
+  } while (0)
+#define REQUIRE_PTR(p) REQUIRE((p) != nullptr && aligned16(p), "%s: %s must be a non-null 16-byte aligned pointer", __func__, #p)
+
+extern "C" {
+
+const char* bzpf_version(void) { return "bzpf 0.1.0 (gfx950)"; }
+
+const char* bzpf_last_error(void) { return g_err; }
+
+int64_t bzpf_trimul_ld(int64_t N) { return (N + 63) / 64 * 64; }
+
+int bzpf_layernorm(const void* x, int x_dt, const float* w, const float* b, float eps, void* y, int y_dt,
+                   int64_t rows, int D, void* stream) {
+  REQUIRE_PTR(x);
+  REQUIRE_PTR(y);
+  REQUIRE(dt_ok(x_dt) && dt_ok(y_dt), "bzpf_layernorm: bad dtype %d/%d", x_dt, y_dt);
+  REQUIRE(D % 64 == 0 && D >= 64 && D <= 1024 && (D / 64 <= 6 || D / 64 == 8 || D / 64 == 12 || D / 64 == 16),
+          "bzpf_layernorm: unsupported D=%d", D);
+  REQUIRE(rows >= 0, "bzpf_layernorm: rows < 0");
+  if (rows == 0) return BZPF_OK;
+  return done(bzpf::launch_layernorm(x, x_dt, w, b, eps, y, y_dt, rows, D, S(stream)), "bzpf_layernorm");
+}
+
+int bzpf_add_ln(float* z, const void* y, int y_dt, float y_scale, int trans_y, const float* w, const float* b,
+                float eps, void* ln, int ln_dt, int trans_out, int64_t N, int D, void* stream) {
+  REQUIRE_PTR(z);
+  REQUIRE_PTR(y);
+  REQUIRE(ln == nullptr || aligned16(ln), "bzpf_add_ln: ln misaligned");
+  REQUIRE(dt_ok(y_dt) && dt_ok(ln_dt), "bzpf_add_ln: bad dtype");
+  REQUIRE(D % 64 == 0 && D >= 64 && D <= 384 && D != 320, "bzpf_add_ln: unsupported D=%d", D);
+  REQUIRE(N >= 0, "bzpf_add_ln: N < 0");
+  if (N == 0) return BZPF_OK;
+  return done(bzpf::launch_add_ln(z, y, y_dt, y_scale, trans_y, w, b, eps, ln, ln_dt, trans_out, N, D, S(stream)),
+              "bzpf_add_ln");
+}
+
+int bzpf_trimul_proj(const void* xn, const void* w_pg, const float* pair_mask, float scale, int incoming, void* ab,
+                     int dt, int64_t N, int64_t ld, int D, void* stream) {
+  REQUIRE_PTR(xn);
+  REQUIRE_PTR(w_pg);
+  REQUIRE_PTR(ab);
+  REQUIRE(pair_mask != nullptr, "bzpf_trimul_proj: pair_mask is NULL");
+  REQUIRE(dt_ok(dt), "bzpf_trimul_proj: bad dtype %d", dt);
+  REQUIRE(D == 128, "bzpf_trimul_proj: D must be 128 (got %d)", D);
+  REQUIRE(N >= 1 && ld == bzpf_trimul_ld(N), "bzpf_trimul_proj: N=%lld ld=%lld (ld must be bzpf_trimul_ld(N))",
+          (long long)N, (long long)ld);
+  return done(bzpf::launch_trimul_proj(xn, w_pg, pair_mask, scale, incoming, ab, dt, N, ld, S(stream)),
+              "bzpf_trimul_proj");
+}
+
+int bzpf_trimul_contract(const void* ab, void* o, int dt, int64_t N, int64_t ld, int D, void* stream) {
+  REQUIRE_PTR(ab);
+  REQUIRE_PTR(o);
+  REQUIRE(dt_ok(dt), "bzpf_trimul_contract: bad dtype %d", dt);
+  REQUIRE(D >= 1 && D <= 65535, "bzpf_trimul_contract: bad D=%d", D);
+  REQUIRE(N >= 1 && ld == bzpf_trimul_ld(N), "bzpf_trimul_contract: N=%lld ld=%lld", (long long)N, (long long)ld);
+  return done(bzpf::launch_trimul_contract(ab, o, dt, N, ld, D, S(stream)), "bzpf_trimul_contract");
+}
+
+int bzpf_trimul_tail(const void* o, const float* norm_out_w, const float* norm_out_b, float eps_out,
+                     const void* w_po, const void* xn, const void* w_go, float* z, int accumulate,
+                     const float* next_w, const float* next_b, float next_eps, void* xn_next, int dt, int64_t N,
+                     int64_t ld, int D, void* stream) {
+  REQUIRE_PTR(o);
+  REQUIRE_PTR(w_po);
+  REQUIRE_PTR(xn);
+  REQUIRE_PTR(w_go);
+  REQUIRE_PTR(z);
+  REQUIRE(norm_out_w && norm_out_b, "bzpf_trimul_tail: norm_out weight/bias required");
+  REQUIRE(next_w == nullptr || (next_b != nullptr && xn_next != nullptr),
+          "bzpf_trimul_tail: next LN needs next_b and xn_next");
+  REQUIRE(dt_ok(dt), "bzpf_trimul_tail: bad dtype %d", dt);
+  REQUIRE(D == 128, "bzpf_trimul_tail: D must be 128 (got %d)", D);
+  REQUIRE(N >= 1 && ld == bzpf_trimul_ld(N), "bzpf_trimul_tail: N=%lld ld=%lld", (long long)N, (long long)ld);
+  return done(bzpf::launch_trimul_tail(o, norm_out_w, norm_out_b, eps_out, w_po, xn, w_go, z, accumulate, next_w,
+                                       next_b, next_eps, xn_next, dt, N, ld, S(stream)),
+              "bzpf_trimul_tail");
+}
+
+int bzpf_triattn_proj(const void* xn, const void* w, int trans, void* qkvg, void* tri_bias, int dt, int64_t N, int D,
+                      int H, int C, void* stream) {
+  REQUIRE_PTR(xn);
+  REQUIRE_PTR(w);
+  REQUIRE_PTR(qkvg);
+  REQUIRE(tri_bias != nullptr, "bzpf_triattn_proj: tri_bias is NULL");
+  REQUIRE(dt_ok(dt), "bzpf_triattn_proj: bad dtype %d", dt);
+  REQUIRE(D == 128 && H >= 1 && H * C == 128 && (C == 16 || C == 32 || C == 64),
+          "bzpf_triattn_proj: need D = H*C = 128, C in {16,32,64} (D=%d H=%d C=%d)", D, H, C);
+  REQUIRE(N >= 1, "bzpf_triattn_proj: N < 1");
+  return done(bzpf::launch_triattn_proj(xn, w, trans, qkvg, tri_bias, dt, N, H, C, S(stream)), "bzpf_triattn_proj");
+}
+
+int bzpf_triattn_core(const void* qkvg, const void* tri_bias, const float* mask, int64_t mask_si, int64_t mask_sk,
+                      float inf, void* out, int dt, int64_t N, int H, int C, void* stream) {
+  REQUIRE_PTR(qkvg);
+  REQUIRE(tri_bias != nullptr && mask != nullptr && out != nullptr, "bzpf_triattn_core: NULL pointer");
+  REQUIRE(dt_ok(dt), "bzpf_triattn_core: bad dtype %d", dt);
+  REQUIRE(H >= 1 && H <= 65535 && (C == 16 || C == 32 || C == 64), "bzpf_triattn_core: H=%d C=%d", H, C);
+  REQUIRE(N >= 1 && N <= 65535, "bzpf_triattn_core: N=%lld out of range", (long long)N);
+  return done(bzpf::launch_triattn_core(qkvg, tri_bias, mask, mask_si, mask_sk, inf, out, dt, N, H, C, S(stream)),
+              "bzpf_triattn_core");
+}
+
+int bzpf_linear_resid_ln(const void* x, const void* w, int trans, float* z, int accumulate, const float* next_w,
+                         const float* next_b, float next_eps, void* xn_next, int dt, int64_t N, int D, void* stream) {
+  REQUIRE_PTR(x);
+  REQUIRE_PTR(w);
+  REQUIRE_PTR(z);
+  REQUIRE(next_w == nullptr || (next_b != nullptr && xn_next != nullptr),
+          "bzpf_linear_resid_ln: next LN needs next_b and xn_next");
+  REQUIRE(dt_ok(dt), "bzpf_linear_resid_ln: bad dtype %d", dt);
+  REQUIRE(D == 128, "bzpf_linear_resid_ln: D must be 128 (got %d)", D);
+  REQUIRE(N >= 1, "bzpf_linear_resid_ln: N < 1");
+  return done(bzpf::launch_linear_resid_ln(x, w, trans, z, accumulate, next_w, next_b, next_eps, xn_next, dt, N,
+                                           S(stream)),
+              "bzpf_linear_resid_ln");
+}
+
+int bzpf_transition(const void* xn, const void* w12, const void* w3, float* z, int accumulate, const float* next_w,
+                    const float* next_b, float next_eps, void* xn_next, int dt, int64_t rows, int D, int hidden,
+                    void* stream) {
+  REQUIRE_PTR(xn);
+  REQUIRE_PTR(w12);
+  REQUIRE_PTR(w3);
+  REQUIRE_PTR(z);
+  REQUIRE(next_w == nullptr || (next_b != nullptr && xn_next != nullptr),
+          "bzpf_transition: next LN needs next_b and xn_next");
+  REQUIRE(dt_ok(dt), "bzpf_transition: bad dtype %d", dt);
+  REQUIRE(D == 128 && hidden >= 64 && hidden % 64 == 0, "bzpf_transition: need D=128, hidden %% 64 == 0 (D=%d H=%d)",
+          D, hidden);
+  REQUIRE(rows >= 0, "bzpf_transition: rows < 0");
+  if (rows == 0) return BZPF_OK;
+  return done(bzpf::launch_transition(xn, w12, w3, z, accumulate, next_w, next_b, next_eps, xn_next, dt, rows, hidden,
+                                      S(stream)),
+              "bzpf_transition");
+}
+
+int bzpf_linear(const void* x, const void* w, const float* bias, void* y, int dt, int y_dt, int64_t rows, int K,
+                int M, int accumulate, void* stream) {
+  REQUIRE_PTR(x);
+  REQUIRE_PTR(w);
+  REQUIRE(y != nullptr, "bzpf_linear: y is NULL");
+  REQUIRE(dt_ok(dt) && dt_ok(y_dt), "bzpf_linear: bad dtype");
+  REQUIRE(K >= 8 && K % 8 == 0 && M >= 1, "bzpf_linear: need K %% 8 == 0, M >= 1 (K=%d M=%d)", K, M);
+  REQUIRE(!accumulate || y_dt == BZPF_F32, "bzpf_linear: accumulate needs an fp32 y");
+  REQUIRE(rows >= 0, "bzpf_linear: rows < 0");
+  if (rows == 0) return BZPF_OK;
+  return done(bzpf::launch_linear(x, w, bias, y, dt, y_dt, rows, K, M, accumulate ? 1 : 0, S(stream)), "bzpf_linear");
+}
+
+int bzpf_swiglu(const void* h, void* a, int dt, int64_t rows, int hidden, void* stream) {
+  REQUIRE(h != nullptr && a != nullptr, "bzpf_swiglu: NULL pointer");
+  REQUIRE(dt_ok(dt), "bzpf_swiglu: bad dtype");
+  REQUIRE(rows >= 0 && hidden >= 1, "bzpf_swiglu: bad sizes");
+  if (rows == 0) return BZPF_OK;
+  return done(bzpf::launch_swiglu(h, a, dt, rows, hidden, S(stream)), "bzpf_swiglu");
+}
+
+int bzpf_seq_attention(const void* q, const void* k, const void* v, const void* g, int64_t ld_in, const void* bias,
+                       const float* mask, float inf, void* out, int64_t ld_out, int dt, int64_t N, int H, int hd,
+                       void* stream) {
+  REQUIRE(q && k && v && g && bias && mask && out, "bzpf_seq_attention: NULL pointer");
+  REQUIRE(dt_ok(dt), "bzpf_seq_attention: bad dtype");
+  REQUIRE(hd == 16 || hd == 24 || hd == 32 || hd == 48 || hd == 64, "bzpf_seq_attention: hd=%d unsupported", hd);
+  REQUIRE(H >= 1 && H <= 65535 && N >= 1 && ld_in >= (int64_t)H * hd && ld_out >= (int64_t)H * hd,
+          "bzpf_seq_attention: bad sizes");
+  return done(bzpf::launch_seq_attention(q, k, v, g, ld_in, bias, mask, inf, out, ld_out, dt, N, H, hd, S(stream)),
+              "bzpf_seq_attention");
+}
+
+int bzpf_pair_bias(const float* z, const float* ln_w, const float* ln_b, float eps, const void* w, void* out, int dt,
+                   int64_t rows, int D, int H, void* stream) {
+  REQUIRE_PTR(z);
+  REQUIRE_PTR(w);
+  REQUIRE(ln_w && ln_b && out, "bzpf_pair_bias: NULL pointer");
+  REQUIRE(dt_ok(dt), "bzpf_pair_bias: bad dtype");
+  REQUIRE(D == 128 && H >= 1 && H <= 16, "bzpf_pair_bias: need D=128, 1 <= H <= 16 (D=%d H=%d)", D, H);
+  REQUIRE(rows >= 0, "bzpf_pair_bias: rows < 0");
+  if (rows == 0) return BZPF_OK;
+  return done(bzpf::launch_pair_bias(z, ln_w, ln_b, eps, w, out, dt, rows, H, S(stream)), "bzpf_pair_bias");
+}
+
+}  // extern "C"

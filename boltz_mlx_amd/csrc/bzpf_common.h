@@ -1,0 +1,156 @@
+// Shared device helpers for the bzpf gfx950 kernels: storage types, MFMA fragment traits, LDS tile copies,
+// wave reductions and the residual + LayerNorm epilogue used by every pair-track kernel that updates z.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef _Float16 half_t;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef float f2 __attribute__((ext_vector_type(2)));
+
+#define LDS_ALIGN __attribute__((aligned(16)))
+
+namespace bzpf {
+
+constexpr int WG = 256;  // threads per workgroup (4 waves of 64)
+
+__device__ __forceinline__ float to_f(float x) { return x; }
+__device__ __forceinline__ float to_f(half_t x) { return (float)x; }
+template <typename T> __device__ __forceinline__ T from_f(float x);
+template <> __device__ __forceinline__ float from_f<float>(float x) { return x; }
+template <> __device__ __forceinline__ half_t from_f<half_t>(float x) { return (half_t)x; }
+
+__device__ __forceinline__ float sigmoidf_(float x) { return 1.0f / (1.0f + __expf(-x)); }
+__device__ __forceinline__ float siluf_(float x) { return x / (1.0f + __expf(-x)); }
+
+// One 16x16 output block of D = A * B^T per MFMA, A and B both K-contiguous ("NT").
+// Lane l holds A[l%16][k0 + (l/16)*KP .. +KP-1] and B[l%16][same k] (B row = output column);
+// the accumulator f4 holds D[(l/16)*4 + i][l%16], i = 0..3 (layouts checked on gfx950).
+template <typename T> struct Mfma;
+template <> struct Mfma<float> {
+  static constexpr int KP = 1;   // K elements per lane per instruction
+  static constexpr int KS = 4;   // K per instruction
+  typedef float frag;
+  __device__ static __forceinline__ frag load(const float* p) { return *p; }
+  __device__ static __forceinline__ f4 run(frag a, frag b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+  }
+};
+template <> struct Mfma<half_t> {
+  static constexpr int KP = 8;
+  static constexpr int KS = 32;
+  typedef half8 frag;
+  __device__ static __forceinline__ frag load(const half_t* p) { return *reinterpret_cast<const half8*>(p); }
+  __device__ static __forceinline__ f4 run(frag a, frag b, f4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+// LDS row padding (elements) that keeps 16-byte fragment reads of 16 consecutive rows conflict-free.
+template <typename T> struct Pad { static constexpr int v = 16 / sizeof(T); };
+
+// acc[mb][nb] += A[16 mb .. +15][0:K] * B[16 nb .. +15][0:K]^T, A/B in LDS with leading dims lda/ldb.
+template <typename T, int MB, int NB>
+__device__ __forceinline__ void wave_mma(f4 (&acc)[MB][NB], const T* As, int lda, const T* Bs, int ldb, int K) {
+  const int l = threadIdx.x & 63;
+  constexpr int KP = Mfma<T>::KP, KS = Mfma<T>::KS;
+  const T* ap = As + (l & 15) * lda + (l >> 4) * KP;
+  const T* bp = Bs + (l & 15) * ldb + (l >> 4) * KP;
+#pragma unroll 2
+  for (int k0 = 0; k0 < K; k0 += KS) {
+    typename Mfma<T>::frag a[MB], b[NB];
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) a[mb] = Mfma<T>::load(ap + 16 * mb * lda + k0);
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) b[nb] = Mfma<T>::load(bp + 16 * nb * ldb + k0);
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+      for (int nb = 0; nb < NB; nb++) acc[mb][nb] = Mfma<T>::run(a[mb], b[nb], acc[mb][nb]);
+  }
+}
+
+template <int MB, int NB>
+__device__ __forceinline__ void zero_acc(f4 (&acc)[MB][NB]) {
+#pragma unroll
+  for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+    for (int nb = 0; nb < NB; nb++) acc[mb][nb] = f4{0.f, 0.f, 0.f, 0.f};
+}
+
+// 16-byte vector of T.
+template <typename T> struct Vec16 { static constexpr int n = 16 / sizeof(T); };
+struct alignas(16) U128 { uint32_t w[4]; };
+
+// Copy `rows` rows of K elements (K % Vec16 == 0) from global into LDS [rows][ld]. src_row(r) gives the global
+// row pointer; rows >= valid are zero-filled when zero_invalid, else read from src_row as given.
+template <typename T, typename RowFn>
+__device__ __forceinline__ void load_rows(T* dst, int ld, int rows, int K, RowFn src_row) {
+  constexpr int VE = Vec16<T>::n;
+  const int per_row = K / VE;
+  for (int e = threadIdx.x; e < rows * per_row; e += blockDim.x) {
+    const int r = e / per_row, c = (e - r * per_row) * VE;
+    const T* s = src_row(r);
+    U128 v;
+    if (s) v = *reinterpret_cast<const U128*>(s + c);
+    else v = U128{{0u, 0u, 0u, 0u}};
+    *reinterpret_cast<U128*>(dst + r * ld + c) = v;
+  }
+}
+
+// Sum over groups of G consecutive lanes (G a power of two <= 64).
+template <int G>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+  return v;
+}
+template <int G>
+__device__ __forceinline__ float group_max(float v) {
+#pragma unroll
+  for (int o = G / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+  return v;
+}
+
+// Residual + LayerNorm epilogue over a tile of up to 64 rows of D=128 fp32 updates held in LDS (Ys[r][ldy]).
+// Row r updates z row zrow(r) (skipped when < 0): z = (accumulate ? z : 0) + y; when lnw != nullptr also writes
+// LN(z) (eps, affine lnw/lnb) to xn_next row zrow(r). 4 threads per row, 32 channels each (two-pass statistics).
+template <typename TO, typename RowFn>
+__device__ __forceinline__ void resid_ln_epilogue(const float* Ys, int ldy, int rows, RowFn zrow, float* z,
+                                                  int accumulate, const float* lnw, const float* lnb, float eps,
+                                                  TO* xn_next) {
+  constexpr int D = 128;
+  const int t = threadIdx.x;
+  const int r = t >> 2, q = t & 3;
+  if (r >= rows) return;  // rows <= 64 and blockDim == 256: whole 4-lane groups exit together
+  const int64_t zr = zrow(r);
+  if (zr < 0) return;
+  float v[32];
+  float* zp = z + zr * D + q * 32;
+  const float* yp = Ys + r * ldy + q * 32;
+#pragma unroll
+  for (int c = 0; c < 32; c += 4) {
+    f4 y = *reinterpret_cast<const f4*>(yp + c);
+    f4 zz = accumulate ? *reinterpret_cast<const f4*>(zp + c) : f4{0.f, 0.f, 0.f, 0.f};
+    zz += y;
+    *reinterpret_cast<f4*>(zp + c) = zz;
+    v[c] = zz[0]; v[c + 1] = zz[1]; v[c + 2] = zz[2]; v[c + 3] = zz[3];
+  }
+  if (lnw == nullptr) return;
+  float s = 0.f;
+#pragma unroll
+  for (int c = 0; c < 32; c++) s += v[c];
+  const float mean = group_sum<4>(s) * (1.0f / D);
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < 32; c++) { const float d = v[c] - mean; ss += d * d; }
+  const float rstd = 1.0f / sqrtf(group_sum<4>(ss) * (1.0f / D) + eps);
+  TO* op = xn_next + zr * D + q * 32;
+#pragma unroll
+  for (int c = 0; c < 32; c++) op[c] = from_f<TO>((v[c] - mean) * rstd * lnw[q * 32 + c] + lnb[q * 32 + c]);
+}
+
+}  // namespace bzpf

@@ -1,0 +1,48 @@
+// Internal launchers (host side) behind the C-ABI in bzpf_api.hip. All take device pointers and launch on `st`.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace bzpf {
+
+enum { DT_F32 = 0, DT_F16 = 1 };
+
+hipError_t launch_layernorm(const void* x, int x_dt, const float* w, const float* b, float eps, void* y, int y_dt,
+                            int64_t rows, int D, hipStream_t st);
+hipError_t launch_add_ln(float* z, const void* y, int y_dt, float scale, int trans_y, const float* w, const float* b,
+                         float eps, void* ln, int ln_dt, int trans_out, int64_t N, int D, hipStream_t st);
+
+hipError_t launch_trimul_proj(const void* xn, const void* w, const float* mask, float scale, int incoming, void* ab,
+                              int dt, int64_t N, int64_t ld, hipStream_t st);
+hipError_t launch_trimul_contract(const void* ab, void* o, int dt, int64_t N, int64_t ld, int D, hipStream_t st);
+hipError_t launch_trimul_tail(const void* o, const float* now, const float* nob, float eps_out, const void* w_po,
+                              const void* xn, const void* w_go, float* z, int accumulate, const float* lnw,
+                              const float* lnb, float eps_next, void* xn_next, int dt, int64_t N, int64_t ld,
+                              hipStream_t st);
+
+hipError_t launch_triattn_proj(const void* xn, const void* w, int trans, void* qkvg, void* tb, int dt, int64_t N,
+                               int H, int C, hipStream_t st);
+hipError_t launch_triattn_core(const void* qkvg, const void* tb, const float* mask, int64_t mask_si,
+                               int64_t mask_sk, float inf, void* out, int dt, int64_t N, int H, int C,
+                               hipStream_t st);
+hipError_t launch_triattn_core_simple(const void* qkvg, const void* tb, const float* mask, int64_t mask_si,
+                                      int64_t mask_sk, float inf, void* out, int dt, int64_t N, int H, int C,
+                                      hipStream_t st);
+hipError_t launch_linear_resid_ln(const void* x, const void* w, int trans, float* z, int accumulate,
+                                  const float* lnw, const float* lnb, float eps, void* xn_next, int dt, int64_t N,
+                                  hipStream_t st);
+hipError_t launch_transition(const void* xn, const void* w12, const void* w3, float* z, int accumulate,
+                             const float* lnw, const float* lnb, float eps, void* xn_next, int dt, int64_t rows,
+                             int hidden, hipStream_t st);
+
+hipError_t launch_linear(const void* x, const void* w, const float* bias, void* y, int dt, int y_dt, int64_t rows,
+                         int K, int M, int epi, hipStream_t st);
+hipError_t launch_swiglu(const void* h, void* a, int dt, int64_t R, int H, hipStream_t st);
+hipError_t launch_seq_attention(const void* q, const void* k, const void* v, const void* g, int64_t ld_in,
+                                const void* bias, const float* mask, float inf, void* out, int64_t ld_out, int dt,
+                                int64_t N, int H, int hd, hipStream_t st);
+hipError_t launch_pair_bias(const float* z, const float* lnw, const float* lnb, float eps, const void* w, void* out,
+                            int dt, int64_t rows, int H, hipStream_t st);
+
+}  // namespace bzpf

@@ -1,0 +1,308 @@
+// Triangle attention (starting and ending node) as three kernels:
+//   proj  : q|k|v|g planes [4H][N*N][C] and the triangle bias tb [H][N*N] from the LayerNorm output, reading the
+//           positions transposed for the ending node (so the core never sees the orientation);
+//   core  : per row i and head h, out[i, j, h*C:(h+1)*C] = sigmoid(g) * softmax_k(q.k/sqrt(C) + inf*(mask-1) + tb)
+//           v, flash-style with online softmax (a reference VALU kernel here; the fp16 MFMA kernel is in
+//           bzpf_triattn_mfma.hip);
+//   linear_resid_ln : z[src(p)] (+)= out[p] W_o^T, then the next LayerNorm of the updated row.
+// Reference behaviour: boltz_mlx/layers/triangular_attention/attention.py:27-93 (fp32), 95-190 (f16),
+// primitives.py:40-75 (q scaled before q.k; logits + mask_bias + tri_bias), kernels.py:538-600 (summation order
+// (qk + mask_bias) + tri_bias), kernels_nax3.py:176-198 (linear_o + residual + next LN, transposed read of z).
+#include "bzpf_common.h"
+#include "bzpf_kernels.h"
+
+namespace bzpf {
+
+// ---------------------------------------------------------------- projection
+// grid: (ceil(N^2 / 64) position tiles, ceil(M / 64) column chunks), M = 4*H*C + H; block 256.
+template <typename T>
+__global__ __launch_bounds__(256) void triattn_proj_kernel(const T* __restrict__ xn, const T* __restrict__ w,
+                                                           int trans, T* __restrict__ qkvg, T* __restrict__ tb,
+                                                           int64_t N, int H, int C) {
+  constexpr int D = 128, PAD = Pad<T>::v, LDX = D + PAD, LDO = 64 + PAD;
+  __shared__ LDS_ALIGN T Xs[64 * LDX];
+  __shared__ LDS_ALIGN T Ws[64 * LDX];
+  __shared__ LDS_ALIGN T Os[64 * LDO];
+  const int64_t NN = N * N;
+  const int64_t p0 = (int64_t)blockIdx.x * 64;
+  const int HC = H * C, M = 4 * HC + H;
+  const int c0 = blockIdx.y * 64;
+  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int rows = (int)((NN - p0) < 64 ? (NN - p0) : 64);
+
+  load_rows<T>(Xs, LDX, 64, D, [&](int r) -> const T* {
+    int64_t p = p0 + (r < rows ? r : rows - 1);
+    if (trans) { const int64_t i = p / N, j = p - i * N; p = j * N + i; }
+    return xn + p * D;
+  });
+  load_rows<T>(Ws, LDX, 64, D, [&](int r) -> const T* { return (c0 + r < M) ? w + (int64_t)(c0 + r) * D : nullptr; });
+  __syncthreads();
+  f4 acc[1][4];
+  zero_acc(acc);
+  wave_mma<T, 1, 4>(acc, Xs + 16 * wave * LDX, LDX, Ws, LDX, D);
+#pragma unroll
+  for (int nb = 0; nb < 4; nb++)
+#pragma unroll
+    for (int e = 0; e < 4; e++)
+      Os[(16 * wave + (l >> 4) * 4 + e) * LDO + 16 * nb + (l & 15)] = from_f<T>(acc[0][nb][e]);
+  __syncthreads();
+  if (c0 < 4 * HC) {
+    // 64 / C plane-heads of C contiguous channels per position
+    constexpr int VE = Vec16<T>::n;
+    const int vpr = C / VE;            // vectors per (plane-head, position)
+    const int nph = 64 / C;            // plane-heads in this chunk
+    for (int e = threadIdx.x; e < nph * 64 * vpr; e += 256) {
+      const int ph = e / (64 * vpr);
+      const int rem = e - ph * 64 * vpr;
+      const int r = rem / vpr, d = (rem - r * vpr) * VE;
+      if (r >= rows) continue;
+      const int64_t plane = (c0 + ph * C) / C;
+      T* dst = qkvg + (plane * NN + p0 + r) * C + d;
+      *reinterpret_cast<U128*>(dst) = *reinterpret_cast<const U128*>(Os + r * LDO + ph * C + d);
+    }
+  } else {
+    for (int e = threadIdx.x; e < H * 64; e += 256) {
+      const int h = e / 64, r = e - h * 64;
+      if (r < rows && c0 + h < M) tb[(int64_t)h * NN + p0 + r] = Os[r * LDO + (4 * HC + h - c0)];
+    }
+  }
+}
+
+// ---------------------------------------------------------------- attention core (reference VALU kernel)
+// One thread per query j; a 64-thread workgroup owns (row i, head h, 64 queries). Keys are staged TK at a time in
+// LDS (K, V and the [64 x TK] bias tile, all loaded coalesced). Rows share the bias: bias[h][j][k].
+// order 0 (triangle): s = (q*scale).k, s += inf*(m-1), s += bias.  order 1 (sequence): s = (q.k)*scale + bias,
+// s += (1-m)*(-inf). Element (row i, position j, head h, channel d) of q/k/v/g is at
+// base + i*s_row + j*s_pos + h*s_head + d; the output uses o_row/o_pos/o_head.
+struct AttnArgs {
+  const void *q, *k, *v, *g, *bias;
+  const float* mask;
+  void* out;
+  int64_t s_row, s_pos, s_head;
+  int64_t o_row, o_pos, o_head;
+  int64_t b_head;        // bias head stride (bias[h*b_head + j*J + k])
+  int64_t m_row, m_key;  // mask strides
+  float inf, scale;
+  int64_t J;
+  int order;
+};
+
+template <typename T, int HD>
+__global__ __launch_bounds__(64) void attn_simple_kernel(AttnArgs a) {
+  constexpr int TK = 32;
+  __shared__ float Ks[TK][HD + 1];
+  __shared__ float Vs[TK][HD + 1];
+  __shared__ float Bs[64][TK + 1];
+  __shared__ float Mk[TK];
+  const int64_t J = a.J;
+  const int t = threadIdx.x;
+  const int64_t j = (int64_t)blockIdx.x * 64 + t;
+  const int64_t h = blockIdx.y, i = blockIdx.z;
+  const bool valid = j < J;
+  const T* qb = static_cast<const T*>(a.q) + i * a.s_row + h * a.s_head;
+  const T* kb = static_cast<const T*>(a.k) + i * a.s_row + h * a.s_head;
+  const T* vb = static_cast<const T*>(a.v) + i * a.s_row + h * a.s_head;
+  const T* bb = static_cast<const T*>(a.bias) + h * a.b_head;
+  float q[HD], acc[HD];
+#pragma unroll
+  for (int d = 0; d < HD; d++) {
+    const float qv = valid ? to_f(qb[j * a.s_pos + d]) : 0.f;
+    q[d] = a.order == 0 ? qv * a.scale : qv;
+    acc[d] = 0.f;
+  }
+  float m = -INFINITY, lsum = 0.f;
+  const int64_t j0 = (int64_t)blockIdx.x * 64;
+  for (int64_t k0 = 0; k0 < J; k0 += TK) {
+    __syncthreads();
+    for (int e = t; e < TK * HD; e += 64) {
+      const int kk = e / HD, d = e - kk * HD;
+      const int64_t key = k0 + kk;
+      Ks[kk][d] = key < J ? to_f(kb[key * a.s_pos + d]) : 0.f;
+      Vs[kk][d] = key < J ? to_f(vb[key * a.s_pos + d]) : 0.f;
+    }
+    for (int e = t; e < 64 * TK; e += 64) {
+      const int qq = e / TK, kk = e - qq * TK;
+      const int64_t jq = j0 + qq, key = k0 + kk;
+      Bs[qq][kk] = (jq < J && key < J) ? to_f(bb[jq * J + key]) : 0.f;
+    }
+    if (t < TK) {
+      const int64_t key = k0 + t;
+      Mk[t] = key < J ? a.mask[i * a.m_row + key * a.m_key] : 0.f;
+    }
+    __syncthreads();
+    const int kend = (int)((J - k0) < TK ? (J - k0) : TK);
+    for (int kk = 0; kk < kend; kk++) {
+      float s = 0.f;
+#pragma unroll
+      for (int d = 0; d < HD; d++) s += q[d] * Ks[kk][d];
+      if (a.order == 0) {
+        s += a.inf * (Mk[kk] - 1.0f);
+        s += Bs[t][kk];
+      } else {
+        s = s * a.scale + Bs[t][kk];
+        s += (1.0f - Mk[kk]) * (-a.inf);
+      }
+      const float mn = fmaxf(m, s);
+      const float corr = __expf(m - mn);
+      const float p = __expf(s - mn);
+      lsum = lsum * corr + p;
+#pragma unroll
+      for (int d = 0; d < HD; d++) acc[d] = acc[d] * corr + p * Vs[kk][d];
+      m = mn;
+    }
+  }
+  if (!valid) return;
+  const float inv = 1.0f / lsum;
+  const T* gb = static_cast<const T*>(a.g) + i * a.s_row + h * a.s_head + j * a.s_pos;
+  T* ob = static_cast<T*>(a.out) + i * a.o_row + j * a.o_pos + h * a.o_head;
+#pragma unroll
+  for (int d = 0; d < HD; d++) ob[d] = from_f<T>(acc[d] * inv * sigmoidf_(to_f(gb[d])));
+}
+
+template <typename T>
+static hipError_t attn_simple_launch(const AttnArgs& a, int64_t rows, int H, int hd, hipStream_t st) {
+  const dim3 grid((unsigned)((a.J + 63) / 64), (unsigned)H, (unsigned)rows);
+  switch (hd) {
+    case 16: attn_simple_kernel<T, 16><<<grid, 64, 0, st>>>(a); break;
+    case 24: attn_simple_kernel<T, 24><<<grid, 64, 0, st>>>(a); break;
+    case 32: attn_simple_kernel<T, 32><<<grid, 64, 0, st>>>(a); break;
+    case 48: attn_simple_kernel<T, 48><<<grid, 64, 0, st>>>(a); break;
+    case 64: attn_simple_kernel<T, 64><<<grid, 64, 0, st>>>(a); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- linear_o + residual + next LN
+// grid: ceil(N^2 / 64) position tiles; block 256 (wave w: rows 16w..16w+15, all 128 columns).
+template <typename T>
+__global__ __launch_bounds__(256) void linear_resid_ln_kernel(const T* __restrict__ x, const T* __restrict__ w,
+                                                              int trans, float* __restrict__ z, int accumulate,
+                                                              const float* __restrict__ lnw,
+                                                              const float* __restrict__ lnb, float eps,
+                                                              T* __restrict__ xn_next, int64_t N) {
+  constexpr int D = 128, PAD = Pad<T>::v, LDX = D + PAD, LDY = D + 4;
+  constexpr int X_BYTES = 64 * LDX * (int)sizeof(T), Y_BYTES = 64 * LDY * 4;
+  __shared__ LDS_ALIGN char smem[X_BYTES > Y_BYTES ? X_BYTES : Y_BYTES];
+  __shared__ LDS_ALIGN T Ws[64 * LDX];
+  T* Xs = reinterpret_cast<T*>(smem);
+  float* Ys = reinterpret_cast<float*>(smem);
+  const int64_t NN = N * N;
+  const int64_t p0 = (int64_t)blockIdx.x * 64;
+  const int rows = (int)((NN - p0) < 64 ? (NN - p0) : 64);
+  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
+  load_rows<T>(Xs, LDX, 64, D, [&](int r) { return x + (p0 + (r < rows ? r : rows - 1)) * D; });
+  f4 acc[1][8];
+  zero_acc(acc);
+  for (int cc = 0; cc < 2; cc++) {
+    __syncthreads();
+    load_rows<T>(Ws, LDX, 64, D, [&](int r) { return w + (int64_t)(64 * cc + r) * D; });
+    __syncthreads();
+    f4 t4[1][4];
+    zero_acc(t4);
+    wave_mma<T, 1, 4>(t4, Xs + 16 * wave * LDX, LDX, Ws, LDX, D);
+#pragma unroll
+    for (int nb = 0; nb < 4; nb++) acc[0][4 * cc + nb] = t4[0][nb];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int nb = 0; nb < 8; nb++)
+#pragma unroll
+    for (int e = 0; e < 4; e++) Ys[(16 * wave + (l >> 4) * 4 + e) * LDY + 16 * nb + (l & 15)] = acc[0][nb][e];
+  __syncthreads();
+  resid_ln_epilogue<T>(Ys, LDY, rows, [&](int r) -> int64_t {
+    int64_t p = p0 + r;
+    if (trans) { const int64_t i = p / N, j = p - i * N; p = j * N + i; }
+    return p;
+  }, z, accumulate, lnw, lnb, eps, xn_next);
+}
+
+template <typename T>
+static hipError_t proj_t(const void* xn, const void* w, int trans, void* qkvg, void* tb, int64_t N, int H, int C,
+                         hipStream_t st) {
+  const int M = 4 * H * C + H;
+  const dim3 grid((unsigned)((N * N + 63) / 64), (unsigned)((M + 63) / 64));
+  triattn_proj_kernel<T><<<grid, 256, 0, st>>>(static_cast<const T*>(xn), static_cast<const T*>(w), trans,
+                                               static_cast<T*>(qkvg), static_cast<T*>(tb), N, H, C);
+  return hipGetLastError();
+}
+
+hipError_t launch_triattn_proj(const void* xn, const void* w, int trans, void* qkvg, void* tb, int dt, int64_t N,
+                               int H, int C, hipStream_t st) {
+  return dt == DT_F16 ? proj_t<half_t>(xn, w, trans, qkvg, tb, N, H, C, st)
+                      : proj_t<float>(xn, w, trans, qkvg, tb, N, H, C, st);
+}
+
+hipError_t launch_triattn_core_simple(const void* qkvg, const void* tb, const float* mask, int64_t mask_si,
+                                      int64_t mask_sk, float inf, void* out, int dt, int64_t N, int H, int C,
+                                      hipStream_t st) {
+  const int64_t NN = N * N;
+  const size_t es = dt == DT_F16 ? 2 : 4;
+  const char* base = static_cast<const char*>(qkvg);
+  const int64_t plane = (int64_t)H * NN * C;  // elements per q / k / v / g plane group
+  AttnArgs a;
+  a.q = base;
+  a.k = base + plane * es;
+  a.v = base + 2 * plane * es;
+  a.g = base + 3 * plane * es;
+  a.bias = tb;
+  a.mask = mask;
+  a.out = out;
+  a.s_row = N * C; a.s_pos = C; a.s_head = NN * C;
+  a.o_row = N * H * C; a.o_pos = (int64_t)H * C; a.o_head = C;
+  a.b_head = NN;
+  a.m_row = mask_si; a.m_key = mask_sk;
+  a.inf = inf;
+  a.scale = 1.0f / sqrtf((float)C);
+  a.J = N;
+  a.order = 0;
+  return dt == DT_F16 ? attn_simple_launch<half_t>(a, N, H, C, st) : attn_simple_launch<float>(a, N, H, C, st);
+}
+
+hipError_t launch_seq_attention(const void* q, const void* k, const void* v, const void* g, int64_t ld_in,
+                                const void* bias, const float* mask, float inf, void* out, int64_t ld_out, int dt,
+                                int64_t N, int H, int hd, hipStream_t st) {
+  AttnArgs a;
+  a.q = q; a.k = k; a.v = v; a.g = g;
+  a.bias = bias;
+  a.mask = mask;
+  a.out = out;
+  a.s_row = 0; a.s_pos = ld_in; a.s_head = hd;
+  a.o_row = 0; a.o_pos = ld_out; a.o_head = hd;
+  a.b_head = N * N;
+  a.m_row = 0; a.m_key = 1;
+  a.inf = inf;
+  a.scale = 1.0f / sqrtf((float)hd);
+  a.J = N;
+  a.order = 1;
+  return dt == DT_F16 ? attn_simple_launch<half_t>(a, 1, H, hd, st) : attn_simple_launch<float>(a, 1, H, hd, st);
+}
+
+template <typename T>
+static hipError_t lrl_t(const void* x, const void* w, int trans, float* z, int accumulate, const float* lnw,
+                        const float* lnb, float eps, void* xn_next, int64_t N, hipStream_t st) {
+  const dim3 grid((unsigned)((N * N + 63) / 64));
+  linear_resid_ln_kernel<T><<<grid, 256, 0, st>>>(static_cast<const T*>(x), static_cast<const T*>(w), trans, z,
+                                                  accumulate, lnw, lnb, eps, static_cast<T*>(xn_next), N);
+  return hipGetLastError();
+}
+
+hipError_t launch_linear_resid_ln(const void* x, const void* w, int trans, float* z, int accumulate,
+                                  const float* lnw, const float* lnb, float eps, void* xn_next, int dt, int64_t N,
+                                  hipStream_t st) {
+  return dt == DT_F16 ? lrl_t<half_t>(x, w, trans, z, accumulate, lnw, lnb, eps, xn_next, N, st)
+                      : lrl_t<float>(x, w, trans, z, accumulate, lnw, lnb, eps, xn_next, N, st);
+}
+
+}  // namespace bzpf
+
+namespace bzpf {
+
+// Core dispatch: every storage type runs the reference VALU kernel until the MFMA kernel is selected here.
+hipError_t launch_triattn_core(const void* qkvg, const void* tb, const float* mask, int64_t mask_si,
+                               int64_t mask_sk, float inf, void* out, int dt, int64_t N, int H, int C,
+                               hipStream_t st) {
+  return launch_triattn_core_simple(qkvg, tb, mask, mask_si, mask_sk, inf, out, dt, N, H, C, st);
+}
+
+}  // namespace bzpf

@@ -1,0 +1,270 @@
+"""torch-facing wrappers of the bzpf C ABI, plus the precision policy of the pair path.
+
+Every wrapper checks devices, dtypes, shapes and contiguity on the host, then calls the C entry point on torch's
+current HIP stream with raw device pointers. Outputs and intermediates are allocated here with torch (the C side
+never allocates). There is no CPU path: a CPU tensor or a missing library raises.
+
+Precision (mirrors the reference's BOLTZ_MLX_PRECISION, boltz_mlx/kernels.py:1212-1220): "fp32" keeps every
+operand in fp32 (the parity build); "f16" stores GEMM operands, LayerNorm outputs and intermediates in fp16 with
+fp32 accumulation, fp32 LayerNorm statistics and softmax, and fp32 residual streams. In f16 the triangle
+multiplication operands a, b are pre-scaled by 2^-TRIMULT_K and norm_out's eps by 2^-4K, which cancels exactly
+(boltz_mlx/kernels.py:1393-1396, layers/norm.py:12-17).
+"""
+
+from __future__ import annotations
+
+import os
+
+import torch
+
+from boltz_mlx_amd import _lib
+from boltz_mlx_amd._lib import F16, F32, call
+
+PRECISION = os.environ.get("BOLTZ_MLX_PRECISION", "fp32")
+TRIMULT_K = int(os.environ.get("BOLTZ_MLX_TRIMULT_K", "4"))
+
+
+def set_precision(mode: str) -> None:
+    """"fp32" or "f16" (process-wide, like the reference's environment switch)."""
+    global PRECISION
+    if mode not in ("fp32", "f16"):
+        raise ValueError(f"precision must be 'fp32' or 'f16', got {mode!r}")
+    PRECISION = mode
+
+
+def f16() -> bool:
+    return PRECISION == "f16"
+
+
+def storage_dtype() -> torch.dtype:
+    return torch.float16 if f16() else torch.float32
+
+
+def _dt(t: torch.Tensor) -> int:
+    if t.dtype == torch.float32:
+        return F32
+    if t.dtype == torch.float16:
+        return F16
+    raise TypeError(f"unsupported dtype {t.dtype}")
+
+
+def _stream():
+    return torch.cuda.current_stream().cuda_stream
+
+
+def _p(t):
+    return None if t is None else t.data_ptr()
+
+
+def _dev(*ts):
+    for t in ts:
+        if t is not None and (not t.is_cuda or not t.is_contiguous()):
+            raise ValueError("bzpf kernels need contiguous ROCm device tensors")
+
+
+def trimul_ld(N: int) -> int:
+    return int(_lib.load().bzpf_trimul_ld(N))
+
+
+# ------------------------------------------------------------------------------------------------ weight caches
+
+def wcache(owner: torch.nn.Module, name: str, *params: torch.Tensor, dtype=None) -> torch.Tensor:
+    """concatenate(params, 0) in `dtype` (default: the storage dtype), cached on `owner` and rebuilt when a source
+    parameter changes (data pointer or in-place version). Mirrors the reference's w16 cache
+    (boltz_mlx/kernels.py:1330-1357)."""
+    dtype = dtype or storage_dtype()
+    key = (dtype,) + tuple((p.data_ptr(), p._version, p.device) for p in params)
+    hit = owner.__dict__.get("_bzpf_cache", {}).get(name)
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    with torch.no_grad():
+        w = params[0] if len(params) == 1 else torch.cat(list(params), 0)
+        w = w.detach().to(dtype).contiguous()
+    owner.__dict__.setdefault("_bzpf_cache", {})[name] = (key, w)
+    return w
+
+
+def f32c(t: torch.Tensor) -> torch.Tensor:
+    return t.detach().float().contiguous()
+
+
+# ------------------------------------------------------------------------------------------------ wrappers
+
+def layer_norm(x: torch.Tensor, weight, bias, eps: float = 1e-5, out_dtype=torch.float32) -> torch.Tensor:
+    """LayerNorm over the last axis (boltz_mlx/kernels.py:482-507)."""
+    x = x.contiguous()
+    _dev(x)
+    D = x.shape[-1]
+    y = torch.empty(x.shape, dtype=out_dtype, device=x.device)
+    w = None if weight is None else f32c(weight)
+    b = None if bias is None else f32c(bias)
+    call("bzpf_layernorm", _p(x), _dt(x), _p(w), _p(b), float(eps), _p(y), _dt(y), x.numel() // D, D, _stream())
+    return y
+
+
+def add_ln(z: torch.Tensor, y: torch.Tensor, ln=None, scale: float = 1.0, trans_y: bool = False,
+           trans_out: bool = False, out_dtype=torch.float16):
+    """In place z += y * scale over [N, N, D] (y optionally read transposed); returns LN(z) (optionally transposed)
+    when `ln` (a LayerNorm module) is given (boltz_mlx/kernels.py:1448-1480)."""
+    _dev(z, y)
+    if z.dtype != torch.float32 or z.shape != y.shape:
+        raise ValueError("add_ln: z must be fp32 and y the same shape")
+    N, D = z.shape[-2], z.shape[-1]
+    if z.dim() != 3 or z.shape[0] != N:
+        raise ValueError("add_ln: z must be [N, N, D]")
+    out = None
+    w = b = None
+    eps = 1e-5
+    if ln is not None:
+        out = torch.empty(z.shape, dtype=out_dtype, device=z.device)
+        w, b, eps = f32c(ln.weight), f32c(ln.bias), ln.eps
+    call("bzpf_add_ln", _p(z), _p(y), _dt(y), float(scale), int(trans_y), _p(w), _p(b), float(eps), _p(out),
+         _dt(out) if out is not None else F32, int(trans_out), N, D, _stream())
+    return out
+
+
+def trimul_proj(xn, w_pg, mask, scale: float, incoming: bool, N: int) -> torch.Tensor:
+    _dev(xn, w_pg, mask)
+    if mask.dtype != torch.float32 or mask.numel() != N * N:
+        raise ValueError("trimul_proj: mask must be fp32 [N, N]")
+    D = xn.shape[-1]
+    if w_pg.shape != (4 * D, D) or w_pg.dtype != xn.dtype or xn.numel() != N * N * D:
+        raise ValueError("trimul_proj: shape/dtype mismatch")
+    ld = trimul_ld(N)
+    ab = torch.empty((2 * D, N, ld), dtype=xn.dtype, device=xn.device)
+    call("bzpf_trimul_proj", _p(xn), _p(w_pg), _p(mask), float(scale), int(incoming), _p(ab), _dt(xn), N, ld, D,
+         _stream())
+    return ab
+
+
+def trimul_contract(ab: torch.Tensor, N: int) -> torch.Tensor:
+    _dev(ab)
+    D = ab.shape[0] // 2
+    ld = trimul_ld(N)
+    if ab.shape != (2 * D, N, ld):
+        raise ValueError("trimul_contract: ab must be [2D, N, ld]")
+    o = torch.empty((D, N, ld), dtype=ab.dtype, device=ab.device)
+    call("bzpf_trimul_contract", _p(ab), _p(o), _dt(ab), N, ld, D, _stream())
+    return o
+
+
+def trimul_tail(o, norm_out, eps_out: float, w_po, xn, w_go, z, accumulate: bool, next_ln=None, N: int = 0):
+    """z (+)= p_out(LN_out(o)) * sigmoid(g_out(xn)); returns next_ln(z) in the storage dtype when next_ln is given."""
+    _dev(o, w_po, xn, w_go, z)
+    D = o.shape[0]
+    ld = trimul_ld(N)
+    if z.dtype != torch.float32 or z.numel() != N * N * D or o.shape != (D, N, ld):
+        raise ValueError("trimul_tail: shape/dtype mismatch")
+    nxt = nw = nb = None
+    neps = 1e-5
+    if next_ln is not None:
+        nxt = torch.empty((N * N, D), dtype=xn.dtype, device=xn.device)
+        nw, nb, neps = f32c(next_ln.weight), f32c(next_ln.bias), next_ln.eps
+    call("bzpf_trimul_tail", _p(o), _p(f32c(norm_out.weight)), _p(f32c(norm_out.bias)), float(eps_out), _p(w_po),
+         _p(xn), _p(w_go), _p(z), int(accumulate), _p(nw), _p(nb), float(neps), _p(nxt), _dt(xn), N, ld, D,
+         _stream())
+    return nxt
+
+
+def triattn_proj(xn, w, trans: bool, N: int, H: int, C: int):
+    _dev(xn, w)
+    D = xn.shape[-1]
+    if w.shape != (4 * H * C + H, D) or w.dtype != xn.dtype or xn.numel() != N * N * D:
+        raise ValueError("triattn_proj: shape/dtype mismatch")
+    qkvg = torch.empty((4 * H, N * N, C), dtype=xn.dtype, device=xn.device)
+    tb = torch.empty((H, N * N), dtype=xn.dtype, device=xn.device)
+    call("bzpf_triattn_proj", _p(xn), _p(w), int(trans), _p(qkvg), _p(tb), _dt(xn), N, D, H, C, _stream())
+    return qkvg, tb
+
+
+def triattn_core(qkvg, tb, mask, trans: bool, inf: float, N: int, H: int, C: int) -> torch.Tensor:
+    """mask: the pair mask [N, N] fp32 in the natural orientation; the ending node (trans) reads it transposed."""
+    _dev(qkvg, tb, mask)
+    if mask.dtype != torch.float32 or mask.numel() != N * N:
+        raise ValueError("triattn_core: mask must be fp32 [N, N]")
+    out = torch.empty((N * N, H * C), dtype=qkvg.dtype, device=qkvg.device)
+    si, sk = (1, N) if trans else (N, 1)
+    call("bzpf_triattn_core", _p(qkvg), _p(tb), _p(mask), si, sk, float(inf), _p(out), _dt(qkvg), N, H, C,
+         _stream())
+    return out
+
+
+def linear_resid_ln(x, w, trans: bool, z, accumulate: bool, next_ln=None, N: int = 0):
+    _dev(x, w, z)
+    D = z.shape[-1]
+    if z.dtype != torch.float32 or x.numel() != N * N * D or w.shape != (D, D):
+        raise ValueError("linear_resid_ln: shape/dtype mismatch")
+    nxt = nw = nb = None
+    neps = 1e-5
+    if next_ln is not None:
+        nxt = torch.empty((N * N, D), dtype=x.dtype, device=x.device)
+        nw, nb, neps = f32c(next_ln.weight), f32c(next_ln.bias), next_ln.eps
+    call("bzpf_linear_resid_ln", _p(x), _p(w), int(trans), _p(z), int(accumulate), _p(nw), _p(nb), float(neps),
+         _p(nxt), _dt(x), N, D, _stream())
+    return nxt
+
+
+def transition(xn, w12, w3, z, accumulate: bool, next_ln=None):
+    _dev(xn, w12, w3, z)
+    D = z.shape[-1]
+    rows = z.numel() // D
+    hidden = w3.shape[1]
+    if xn.numel() != rows * D or w12.shape != (2 * hidden, D) or w3.shape != (D, hidden):
+        raise ValueError("transition: shape mismatch")
+    nxt = nw = nb = None
+    neps = 1e-5
+    if next_ln is not None:
+        nxt = torch.empty((rows, D), dtype=xn.dtype, device=xn.device)
+        nw, nb, neps = f32c(next_ln.weight), f32c(next_ln.bias), next_ln.eps
+    call("bzpf_transition", _p(xn), _p(w12), _p(w3), _p(z), int(accumulate), _p(nw), _p(nb), float(neps), _p(nxt),
+         _dt(xn), rows, D, hidden, _stream())
+    return nxt
+
+
+def linear(x, w, bias=None, out=None, out_dtype=None, accumulate: bool = False) -> torch.Tensor:
+    """y = x w^T + bias over the rows of x (w [M, K] in x's dtype); accumulate adds into the fp32 `out`."""
+    _dev(x, w)
+    K = x.shape[-1]
+    M = w.shape[0]
+    rows = x.numel() // K
+    if w.shape[1] != K or w.dtype != x.dtype:
+        raise ValueError("linear: shape/dtype mismatch")
+    if out is None:
+        out = torch.empty(x.shape[:-1] + (M,), dtype=out_dtype or x.dtype, device=x.device)
+    _dev(out)
+    b = None if bias is None else f32c(bias)
+    call("bzpf_linear", _p(x), _p(w), _p(b), _p(out), _dt(x), _dt(out), rows, K, M, int(accumulate), _stream())
+    return out
+
+
+def swiglu(h: torch.Tensor) -> torch.Tensor:
+    _dev(h)
+    H = h.shape[-1] // 2
+    rows = h.numel() // (2 * H)
+    a = torch.empty(h.shape[:-1] + (H,), dtype=h.dtype, device=h.device)
+    call("bzpf_swiglu", _p(h), _p(a), _dt(h), rows, H, _stream())
+    return a
+
+
+def seq_attention(q, k, v, g, bias, mask, inf: float, H: int) -> torch.Tensor:
+    """q/k/v/g [N, H*hd], bias [H, N, N], mask [N] fp32 -> [N, H*hd]."""
+    _dev(q, k, v, g, bias, mask)
+    N, HD = q.shape
+    hd = HD // H
+    if bias.shape != (H, N, N) or mask.numel() != N or mask.dtype != torch.float32:
+        raise ValueError("seq_attention: bias must be [H, N, N] and mask fp32 [N]")
+    out = torch.empty_like(q)
+    call("bzpf_seq_attention", _p(q), _p(k), _p(v), _p(g), HD, _p(bias), _p(mask), float(inf), _p(out), HD,
+         _dt(q), N, H, hd, _stream())
+    return out
+
+
+def pair_bias(z: torch.Tensor, ln, w: torch.Tensor) -> torch.Tensor:
+    """Linear(LN(z)) for z fp32 [N, N, D] as [H, N, N] in w's dtype."""
+    _dev(z, w)
+    N, D = z.shape[0], z.shape[-1]
+    H = w.shape[0]
+    out = torch.empty((H, N, N), dtype=w.dtype, device=z.device)
+    call("bzpf_pair_bias", _p(z), _p(f32c(ln.weight)), _p(f32c(ln.bias)), float(ln.eps), _p(w), _p(out), _dt(w),
+         N * N, D, H, _stream())
+    return out

@@ -1,0 +1,177 @@
+"""PairformerLayer / PairformerModule (and the no-sequence variants) on the bzpf kernels.
+
+Same constructors, parameter names and call signatures as boltz_mlx/layers/pairformer.py:23-153 (v2 layers,
+inference only). The layer runs the reference order (pairformer.py:84-93, strict path 238-247 of the MLX port):
+z += tri_mul_out; z += tri_mul_in; z += tri_att_start; z += tri_att_end; z += transition_z; then
+s += attention(pre_norm_s(s), z, mask, k_in=pre_norm_s(s)); s += transition_s(s).
+
+Each pair update is one fused kernel chain that adds its result into z in place and writes the next module's
+LayerNorm output (the reference's add_ln / *_addln epilogues, kernels_nax3.py), so z is read and written once
+per update. PairformerModule clones its inputs once and carries the next layer's norm_in output from each
+layer's transition (the reference's PAIRLNX carry, pairformer.py:145-148, 243-246).
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from boltz_mlx_amd import kernels as K
+from boltz_mlx_amd.layers.attentionv2 import AttentionPairBias as AttentionPairBiasV2
+from boltz_mlx_amd.layers.norm import LayerNorm
+from boltz_mlx_amd.layers.transition import Transition
+from boltz_mlx_amd.layers.triangular_attention.attention import (
+    TriangleAttentionEndingNode,
+    TriangleAttentionStartingNode,
+)
+from boltz_mlx_amd.layers.triangular_mult import TriangleMultiplicationIncoming, TriangleMultiplicationOutgoing
+
+
+def _pair_chain(layer, z: torch.Tensor, pm: torch.Tensor, xn_in: Optional[torch.Tensor], next_ln):
+    """The five pair updates on one batch element z [N, N, D] (fp32, updated in place) with pair mask pm [N, N]
+    fp32. Returns next_ln(z_new) in the storage dtype (or None)."""
+    N, D = z.shape[0], z.shape[-1]
+    xn = layer.tri_mul_out.norm_in.to_storage(z).reshape(N * N, D) if xn_in is None else xn_in
+    xn = layer.tri_mul_out.fused(xn, pm, z, True, next_ln=layer.tri_mul_in.norm_in)
+    xn = layer.tri_mul_in.fused(xn, pm, z, True, next_ln=layer.tri_att_start.layer_norm)
+    xn = layer.tri_att_start.fused(xn, pm, z, True, next_ln=layer.tri_att_end.layer_norm)
+    xn = layer.tri_att_end.fused(xn, pm, z, True, next_ln=layer.transition_z.norm)
+    return layer.transition_z.fused(xn, z, True, next_ln=next_ln)
+
+
+class PairformerLayer(torch.nn.Module):
+    def __init__(self, token_s: int, token_z: int, num_heads: int = 16, dropout: float = 0.25,
+                 pairwise_head_width: int = 32, pairwise_num_heads: int = 4, post_layer_norm: bool = False,
+                 v2: bool = True) -> None:
+        super().__init__()
+        if not v2:
+            raise NotImplementedError("only the v2 pairformer layer is provided")
+        self.token_z = token_z
+        self.dropout = dropout  # unused at inference
+        self.num_heads = num_heads
+        self.post_layer_norm = post_layer_norm
+        self.pre_norm_s = LayerNorm(token_s)
+        self.attention = AttentionPairBiasV2(token_s, token_z, num_heads)
+        self.tri_mul_out = TriangleMultiplicationOutgoing(token_z)
+        self.tri_mul_in = TriangleMultiplicationIncoming(token_z)
+        self.tri_att_start = TriangleAttentionStartingNode(token_z, pairwise_head_width, pairwise_num_heads, inf=1e9)
+        self.tri_att_end = TriangleAttentionEndingNode(token_z, pairwise_head_width, pairwise_num_heads, inf=1e9)
+        self.transition_s = Transition(token_s, token_s * 4)
+        self.transition_z = Transition(token_z, token_z * 4)
+        self.s_post_norm = LayerNorm(token_s) if post_layer_norm else torch.nn.Identity()
+
+    def forward(self, s: torch.Tensor, z: torch.Tensor, mask: torch.Tensor, pair_mask: torch.Tensor,
+                chunk_size_tri_attn: Optional[int] = None, use_kernels: bool = False, use_cuequiv_mul: bool = False,
+                use_cuequiv_attn: bool = False, xn_in: Optional[torch.Tensor] = None,
+                next_ln=None) -> tuple[torch.Tensor, torch.Tensor]:
+        """s [B, N, token_s], z [B, N, N, token_z], mask [B, N], pair_mask [B, N, N] -> (s, z) (new tensors).
+        chunk_size_tri_attn / use_* are accepted and ignored. xn_in: tri_mul_out.norm_in(z) in the storage dtype
+        ([N*N, D], B = 1) as carried by PairformerModule."""
+        s = s.to(torch.float32).clone().contiguous()
+        z = z.to(torch.float32).clone().contiguous()
+        self.inplace(s, z, mask.to(torch.float32).contiguous(), pair_mask.to(torch.float32).contiguous(),
+                     xn_in=xn_in, next_ln=None)
+        return s, z
+
+    def inplace(self, s: torch.Tensor, z: torch.Tensor, mask: torch.Tensor, pair_mask: torch.Tensor,
+                xn_in: Optional[torch.Tensor] = None, next_ln=None) -> Optional[torch.Tensor]:
+        """Update fp32 s and z in place (masks fp32 contiguous). Returns next_ln(z_new) for B = 1, else None."""
+        B = z.shape[0]
+        xn_next = None
+        for b in range(B):
+            xn_next = _pair_chain(self, z[b], pair_mask[b], xn_in if B == 1 else None,
+                                  next_ln if B == 1 else None)
+            self._s_track(s[b], z[b], mask[b])
+        if not isinstance(self.s_post_norm, torch.nn.Identity):
+            s.copy_(self.s_post_norm(s))
+        return xn_next
+
+    def _s_track(self, s: torch.Tensor, z: torch.Tensor, mask: torch.Tensor) -> None:
+        dt = K.storage_dtype()
+        s_n = K.layer_norm(s, self.pre_norm_s.weight, self.pre_norm_s.bias, self.pre_norm_s.eps, out_dtype=dt)
+        self.attention.fused(s_n, s_n, self.attention.pair_bias(z), mask, s, accumulate=True)
+        self.transition_s.unfused(self.transition_s.norm.to_storage(s), out=s, accumulate=True)
+
+
+class PairformerModule(torch.nn.Module):
+    def __init__(self, token_s: int, token_z: int, num_blocks: int, num_heads: int = 16, dropout: float = 0.25,
+                 pairwise_head_width: int = 32, pairwise_num_heads: int = 4, post_layer_norm: bool = False,
+                 activation_checkpointing: bool = False, v2: bool = True, **kwargs) -> None:
+        super().__init__()
+        self.token_z = token_z
+        self.num_blocks = num_blocks
+        self.dropout = dropout
+        self.num_heads = num_heads
+        self.post_layer_norm = post_layer_norm
+        self.layers = torch.nn.ModuleList([
+            PairformerLayer(token_s, token_z, num_heads, dropout, pairwise_head_width, pairwise_num_heads,
+                            post_layer_norm, v2)
+            for _ in range(num_blocks)
+        ])
+
+    def forward(self, s: torch.Tensor, z: torch.Tensor, mask: torch.Tensor, pair_mask: torch.Tensor,
+                use_kernels: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+        s = s.to(torch.float32).clone().contiguous()
+        z = z.to(torch.float32).clone().contiguous()
+        self.inplace(s, z, mask.to(torch.float32).contiguous(), pair_mask.to(torch.float32).contiguous())
+        return s, z
+
+    def inplace(self, s: torch.Tensor, z: torch.Tensor, mask: torch.Tensor, pair_mask: torch.Tensor) -> None:
+        """Run every layer on fp32 s, z in place (masks fp32 contiguous)."""
+        n, xn = len(self.layers), None
+        for i, layer in enumerate(self.layers):
+            nxt = self.layers[i + 1].tri_mul_out.norm_in if i + 1 < n else None
+            xn = layer.inplace(s, z, mask, pair_mask, xn_in=xn, next_ln=nxt)
+
+
+class PairformerNoSeqLayer(torch.nn.Module):
+    def __init__(self, token_z: int, dropout: float = 0.25, pairwise_head_width: int = 32,
+                 pairwise_num_heads: int = 4, post_layer_norm: bool = False) -> None:
+        super().__init__()
+        self.token_z = token_z
+        self.dropout = dropout
+        self.post_layer_norm = post_layer_norm
+        self.tri_mul_out = TriangleMultiplicationOutgoing(token_z)
+        self.tri_mul_in = TriangleMultiplicationIncoming(token_z)
+        self.tri_att_start = TriangleAttentionStartingNode(token_z, pairwise_head_width, pairwise_num_heads, inf=1e9)
+        self.tri_att_end = TriangleAttentionEndingNode(token_z, pairwise_head_width, pairwise_num_heads, inf=1e9)
+        self.transition_z = Transition(token_z, token_z * 4)
+
+    def forward(self, z: torch.Tensor, pair_mask: torch.Tensor, chunk_size_tri_attn: Optional[int] = None,
+                use_kernels: bool = False, use_cuequiv_mul: bool = False, use_cuequiv_attn: bool = False,
+                xn_in: Optional[torch.Tensor] = None, next_ln=None) -> torch.Tensor:
+        z = z.to(torch.float32).clone().contiguous()
+        self.inplace(z, pair_mask.to(torch.float32).contiguous(), xn_in=xn_in)
+        return z
+
+    def inplace(self, z: torch.Tensor, pair_mask: torch.Tensor, xn_in=None, next_ln=None):
+        B = z.shape[0]
+        xn_next = None
+        for b in range(B):
+            xn_next = _pair_chain(self, z[b], pair_mask[b], xn_in if B == 1 else None, next_ln if B == 1 else None)
+        return xn_next
+
+
+class PairformerNoSeqModule(torch.nn.Module):
+    def __init__(self, token_z: int, num_blocks: int, dropout: float = 0.25, pairwise_head_width: int = 32,
+                 pairwise_num_heads: int = 4, post_layer_norm: bool = False, activation_checkpointing: bool = False,
+                 **kwargs) -> None:
+        super().__init__()
+        self.token_z = token_z
+        self.num_blocks = num_blocks
+        self.dropout = dropout
+        self.post_layer_norm = post_layer_norm
+        self.layers = torch.nn.ModuleList([
+            PairformerNoSeqLayer(token_z, dropout, pairwise_head_width, pairwise_num_heads, post_layer_norm)
+            for _ in range(num_blocks)
+        ])
+
+    def forward(self, z: torch.Tensor, pair_mask: torch.Tensor, use_kernels: bool = False) -> torch.Tensor:
+        z = z.to(torch.float32).clone().contiguous()
+        pm = pair_mask.to(torch.float32).contiguous()
+        n, xn = len(self.layers), None
+        for i, layer in enumerate(self.layers):
+            nxt = self.layers[i + 1].tri_mul_out.norm_in if i + 1 < n else None
+            xn = layer.inplace(z, pm, xn_in=xn, next_ln=nxt)
+        return z

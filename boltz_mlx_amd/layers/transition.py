@@ -1,0 +1,56 @@
+"""SwiGLU Transition on the bzpf kernels.
+
+Same constructor, parameters and call signature as boltz_mlx/layers/transition.py:12-54
+(``Transition(dim=128, hidden=512, out_dim=None)(x, chunk_size=None, xn=None)``; fc1 is the SiLU branch,
+148-154). For the pair width (dim 128, out_dim 128) one fused kernel does LN -> fc1|fc2 -> SwiGLU -> fc3 with the
+hidden activations kept on chip; other widths (the s track, dim 384) run LN, the up-projection, SwiGLU and the
+down-projection as separate bzpf kernels.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from boltz_mlx_amd import kernels as K
+from boltz_mlx_amd.layers.norm import LayerNorm
+
+
+class Transition(torch.nn.Module):
+    def __init__(self, dim: int = 128, hidden: int = 512, out_dim: Optional[int] = None) -> None:
+        super().__init__()
+        if out_dim is None:
+            out_dim = dim
+        self.norm = LayerNorm(dim, eps=1e-5)
+        self.fc1 = torch.nn.Linear(dim, hidden, bias=False)
+        self.fc2 = torch.nn.Linear(dim, hidden, bias=False)
+        self.fc3 = torch.nn.Linear(hidden, out_dim, bias=False)
+        self.hidden = hidden
+
+    def _pair_kernel(self) -> bool:
+        return self.fc1.in_features == 128 and self.fc3.out_features == 128 and self.hidden % 64 == 0
+
+    def forward(self, x: torch.Tensor, chunk_size: Optional[int] = None,
+                xn: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """x: [..., dim] fp32 -> [..., out_dim] fp32. chunk_size is accepted and ignored (the fused kernel keeps
+        no [rows, hidden] intermediate)."""
+        xn = self.norm.to_storage(x) if xn is None else xn.contiguous()
+        if self._pair_kernel():
+            out = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+            self.fused(xn, out, accumulate=False)
+            return out
+        return self.unfused(xn)
+
+    def fused(self, xn: torch.Tensor, z: torch.Tensor, accumulate: bool = True, next_ln=None):
+        """z (+)= transition from xn = norm(z) (storage dtype); returns next_ln(z_new) when next_ln is given."""
+        w12 = K.wcache(self, "w12", self.fc1.weight, self.fc2.weight)
+        w3 = K.wcache(self, "w3", self.fc3.weight)
+        return K.transition(xn, w12, w3, z, accumulate, next_ln)
+
+    def unfused(self, xn: torch.Tensor, out: Optional[torch.Tensor] = None, accumulate: bool = False):
+        """fc3(SwiGLU(xn fc12^T)) as separate kernels; accumulate adds into the fp32 `out`."""
+        w12 = K.wcache(self, "w12", self.fc1.weight, self.fc2.weight)
+        w3 = K.wcache(self, "w3", self.fc3.weight)
+        a = K.swiglu(K.linear(xn, w12))
+        return K.linear(a, w3, out=out, out_dtype=torch.float32, accumulate=accumulate)

@@ -1,0 +1,73 @@
+"""Triangle attention (starting / ending node) on the bzpf kernels.
+
+Same constructor, parameters and call signature as boltz_mlx/layers/triangular_attention/attention.py:12-35,
+193-200 (``TriangleAttention(c_in, c_hidden, no_heads, starting=True, inf=1e9)(x, mask=None, chunk_size=None,
+use_kernels=False, xn=None, keep_t=False)`` returns the update). Three kernels per batch element: the fused
+q|k|v|g|tri-bias projection (reading positions transposed for the ending node), the flash core, and linear_o +
+residual (+ next LN) writing back at the un-transposed position.
+
+Difference from the reference: ``xn`` is the LayerNorm output in the natural (un-transposed) layout for both
+nodes, since the projection kernel reads the ending node's positions transposed itself.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from boltz_mlx_amd import kernels as K
+from boltz_mlx_amd.layers.triangular_attention.primitives import Attention, LayerNorm
+
+
+class TriangleAttention(torch.nn.Module):
+    def __init__(self, c_in: int, c_hidden: int, no_heads: int, starting: bool = True, inf: float = 1e9) -> None:
+        super().__init__()
+        self.c_in = c_in
+        self.c_hidden = c_hidden
+        self.no_heads = no_heads
+        self.starting = starting
+        self.inf = inf
+        self.layer_norm = LayerNorm(c_in)
+        self.linear = torch.nn.Linear(c_in, no_heads, bias=False)
+        self.mha = Attention(c_in, c_in, c_in, c_hidden, no_heads)
+
+    def forward(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None, chunk_size: Optional[int] = None,
+                use_kernels: bool = False, xn: Optional[torch.Tensor] = None, keep_t: bool = False) -> torch.Tensor:
+        """x: [B, I, J, C_in] fp32; mask: [B, I, J]. chunk_size / use_kernels are accepted and ignored (the core is
+        flash-style and never materialises the logits)."""
+        B, N, M, D = x.shape
+        if N != M:
+            raise ValueError("triangle attention needs a square pair representation")
+        if mask is None:
+            mask = torch.ones(x.shape[:-1], dtype=torch.float32, device=x.device)
+        mask = mask.to(torch.float32).contiguous()
+        out = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+        for b in range(B):
+            xb = self.layer_norm.to_storage(x[b]) if xn is None else xn[b].contiguous()
+            self.fused(xb.reshape(N * N, D), mask[b], out[b], accumulate=False)
+        if keep_t and not self.starting:
+            out = out.transpose(1, 2).contiguous()
+        return out
+
+    def fused(self, xn: torch.Tensor, mask: torch.Tensor, z: torch.Tensor, accumulate: bool = True, next_ln=None):
+        """z (+)= self(z) from xn = layer_norm(z) ([N*N, D], storage dtype, natural layout) and the pair mask [N, N]
+        fp32 (natural layout); returns next_ln(z_new) when next_ln is given."""
+        N = z.shape[0]
+        H, C = self.no_heads, self.mha.c_hidden
+        mha = self.mha
+        w = K.wcache(self, "w_qkvgb", mha.linear_q.weight, mha.linear_k.weight, mha.linear_v.weight,
+                     mha.linear_g.weight, self.linear.weight)
+        trans = not self.starting
+        qkvg, tb = K.triattn_proj(xn, w, trans, N, H, C)
+        core = K.triattn_core(qkvg, tb, mask, trans, self.inf, N, H, C)
+        del qkvg, tb
+        return K.linear_resid_ln(core, K.wcache(self, "w_o", mha.linear_o.weight), trans, z, accumulate, next_ln, N)
+
+
+TriangleAttentionStartingNode = TriangleAttention
+
+
+class TriangleAttentionEndingNode(TriangleAttention):
+    def __init__(self, c_in: int, c_hidden: int, no_heads: int, inf: float = 1e9) -> None:
+        super().__init__(c_in, c_hidden, no_heads, starting=False, inf=inf)

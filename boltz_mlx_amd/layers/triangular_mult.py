@@ -1,0 +1,63 @@
+"""Triangle multiplication (outgoing / incoming) on the bzpf kernels.
+
+Same constructor, parameters and call signature as boltz_mlx/layers/triangular_mult.py:27-65, 190-195
+(``TriangleMultiplicationOutgoing(dim)(x, mask, use_kernels=False, xn=None)`` returns the update, not the
+residual sum). The computation is three kernels per batch element: projection + gate + mask into channel-major
+a|b, the per-channel N x N x N contraction, and the fused tail (norm_out, p_out, g_out gate, residual, next LN).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from boltz_mlx_amd import kernels as K
+from boltz_mlx_amd.layers.norm import LayerNorm
+
+
+class _TriangleMultiplication(torch.nn.Module):
+    outgoing: bool = True
+
+    def __init__(self, dim: int = 128) -> None:
+        super().__init__()
+        self.norm_in = LayerNorm(dim, eps=1e-5)
+        self.p_in = torch.nn.Linear(dim, 2 * dim, bias=False)
+        self.g_in = torch.nn.Linear(dim, 2 * dim, bias=False)
+        self.norm_out = LayerNorm(dim)
+        self.p_out = torch.nn.Linear(dim, dim, bias=False)
+        self.g_out = torch.nn.Linear(dim, dim, bias=False)
+
+    def forward(self, x: torch.Tensor, mask: torch.Tensor, use_kernels: bool = False,
+                xn: torch.Tensor | None = None) -> torch.Tensor:
+        """x: [B, N, N, D] fp32; mask: [B, N, N]. `use_kernels` is accepted and ignored. xn: norm_in(x) already
+        computed (storage dtype, [B, N, N, D])."""
+        B, N, M, D = x.shape
+        if N != M:
+            raise ValueError("triangle multiplication needs a square pair representation")
+        out = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+        mask = mask.to(torch.float32).contiguous()
+        for b in range(B):
+            xb = self.norm_in.to_storage(x[b]) if xn is None else xn[b].contiguous()
+            self.fused(xb.reshape(N * N, D), mask[b], out[b], accumulate=False)
+        return out
+
+    def fused(self, xn: torch.Tensor, mask: torch.Tensor, z: torch.Tensor, accumulate: bool = True,
+              next_ln=None):
+        """z (+)= self(z) from xn = norm_in(z) ([N*N, D], storage dtype) and mask [N, N] fp32; returns
+        next_ln(z_new) in the storage dtype when next_ln is given."""
+        N = z.shape[0]
+        kexp = K.TRIMULT_K if K.f16() else 0
+        w_pg = K.wcache(self, "w_pg", self.p_in.weight, self.g_in.weight)
+        ab = K.trimul_proj(xn, w_pg, mask, 2.0 ** -kexp, not self.outgoing, N)
+        o = K.trimul_contract(ab, N)
+        del ab
+        return K.trimul_tail(o, self.norm_out, self.norm_out.eps * 2.0 ** (-4 * kexp),
+                             K.wcache(self, "w_po", self.p_out.weight), xn,
+                             K.wcache(self, "w_go", self.g_out.weight), z, accumulate, next_ln, N)
+
+
+class TriangleMultiplicationOutgoing(_TriangleMultiplication):
+    outgoing = True
+
+
+class TriangleMultiplicationIncoming(_TriangleMultiplication):
+    outgoing = False

@@ -1,0 +1,138 @@
+/*
+ * bzpf — MI355X (gfx950) kernels for the Boltz-2 Pairformer pair path, C ABI.
+ *
+ * Every entry point takes device pointers, plain sizes and a hipStream_t passed as `void*`, launches on that
+ * stream and returns 0, or a negative status (BZPF_EINVAL for a rejected argument, BZPF_ELAUNCH for a launch
+ * failure) with a message in bzpf_last_error(). Nothing here allocates or frees device memory and nothing
+ * synchronises: the caller owns every buffer (inputs, outputs and intermediates) and the stream order.
+ *
+ * Storage types: BZPF_F32 (fp32) or BZPF_F16 (fp16 operands, fp32 accumulation / statistics / softmax). The pair
+ * representation z is always fp32 [N, N, 128] row-major. Pointers are 16-byte aligned; D = c_z = 128 for the
+ * pair kernels.
+ *
+ * Each entry point replaces a kernel wrapper of the reference (paths relative to the reference checkout,
+ * jackryan225/boltz-mlx), which launched MSL source through mx.fast.metal_kernel (boltz_mlx/kernels.py:315-324).
+ */
+#ifndef BZPF_H
+#define BZPF_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BZPF_F32 0
+#define BZPF_F16 1
+
+#define BZPF_OK 0
+#define BZPF_EINVAL (-1)
+#define BZPF_ELAUNCH (-2)
+
+/* Library version string. */
+const char* bzpf_version(void);
+
+/* Message of the last failing call on this host thread ("" when none). */
+const char* bzpf_last_error(void);
+
+/* Row pitch (elements) of the channel-major triangle-multiplication buffers: N rounded up to 64. */
+int64_t bzpf_trimul_ld(int64_t N);
+
+/* Row LayerNorm over D channels (D % 64 == 0, D <= 1024): two-pass fp32 statistics, (x-mean)*rsqrt(var+eps)*w+b;
+ * w / b may be NULL. Replaces kernels.layer_norm (boltz_mlx/kernels.py:482-507) and LayerNorm.__call__/.f16
+ * (boltz_mlx/layers/norm.py:9-17). */
+int bzpf_layernorm(const void* x, int x_dt, const float* w, const float* b, float eps, void* y, int y_dt,
+                   int64_t rows, int D, void* stream);
+
+/* z[r] += y[trans_y ? T(r) : r] * y_scale over the N*N rows of z [N, N, D] (T swaps the two token axes); then,
+ * when ln != NULL, ln[trans_out ? T(r) : r] = LN(z[r]). Replaces kernels.add_ln (boltz_mlx/kernels.py:1448-1480)
+ * and kernels.radd (1305-1310). */
+int bzpf_add_ln(float* z, const void* y, int y_dt, float y_scale, int trans_y, const float* w, const float* b,
+                float eps, void* ln, int ln_dt, int trans_out, int64_t N, int D, void* stream);
+
+/* Triangle-multiplication projection: for c < 2D and the position (i, k) (incoming: (k, i)),
+ *   ab[c][i][k] = (xn.W[c]) * sigmoid(xn.W[2D + c]) * pair_mask * scale,  k < N;   ab[c][i][k] = 0 for N <= k < ld.
+ * xn [N*N, D] (dt), W = [p_in.weight; g_in.weight] [4D, D] (dt), pair_mask [N, N] fp32, ab [2D][N][ld] (dt),
+ * ld = bzpf_trimul_ld(N). scale = 1 in fp32 mode, 2^-K in fp16 mode. Replaces the projection of
+ * TriangleMultiplication._fast_b1 / _f16_contract (boltz_mlx/layers/triangular_mult.py:67-88, 143-170) and
+ * kernels_nax2.trimul_proj_nax (boltz_mlx/kernels_nax2.py:202-304). */
+int bzpf_trimul_proj(const void* xn, const void* w_pg, const float* pair_mask, float scale, int incoming, void* ab,
+                     int dt, int64_t N, int64_t ld, int D, void* stream);
+
+/* Per-channel contraction o[c][i][j] = sum_k ab[c][i][k] * ab[D + c][j][k] for c < D, o [D][N][ld] (dt; columns
+ * j >= N are not written). Replaces the mx.matmul contraction (boltz_mlx/layers/triangular_mult.py:90-93, 172-175)
+ * and kernels_nax2.trimul_contract_nax (boltz_mlx/kernels_nax2.py:315-407). */
+int bzpf_trimul_contract(const void* ab, void* o, int dt, int64_t N, int64_t ld, int D, void* stream);
+
+/* Triangle-multiplication tail: at each position p = (i, j),
+ *   y = (LN_out(o[:, i, j]; eps_out) . W_po^T) * sigmoid(xn[p] . W_go^T);  z[p] = (accumulate ? z[p] : 0) + y;
+ *   and, when next_w != NULL, xn_next[p] = LN_next(z[p]).
+ * Replaces the output half of TriangleMultiplication (boltz_mlx/layers/triangular_mult.py:98-118) and
+ * kernels_nax3.trimul_tail_addln / trimul_tail3_addln (boltz_mlx/kernels_nax3.py:200-268, 357-393, 1061-1206). */
+int bzpf_trimul_tail(const void* o, const float* norm_out_w, const float* norm_out_b, float eps_out,
+                     const void* w_po, const void* xn, const void* w_go, float* z, int accumulate,
+                     const float* next_w, const float* next_b, float next_eps, void* xn_next, int dt, int64_t N,
+                     int64_t ld, int D, void* stream);
+
+/* Triangle-attention projection of the LayerNorm output xn [N*N, D] with W = [linear_q; linear_k; linear_v;
+ * linear_g; linear] ([4*H*C + H, D]) at the position (i, j) (trans: (j, i), the ending node):
+ *   qkvg[(s*H + h)][p][c] for s in {q, k, v, g} ([4H][N*N][C]) and tri_bias[h][p] ([H][N*N]).
+ * Replaces the fused projection of TriangleAttention (boltz_mlx/layers/triangular_attention/attention.py:49-69,
+ * 100-104) and kernels_nax3.pair_proj16 (boltz_mlx/kernels_nax3.py:538-700). */
+int bzpf_triattn_proj(const void* xn, const void* w, int trans, void* qkvg, void* tri_bias, int dt, int64_t N, int D,
+                      int H, int C, void* stream);
+
+/* Flash triangle-attention core: for row i, head h, query j,
+ *   out[i][j][h*C + c] = sigmoid(g) * sum_k softmax_k((q/sqrt(C)).k + inf*(mask[i*mask_si + k*mask_sk] - 1)
+ *                                                     + tri_bias[h][j*N + k]) v[k][c]
+ * (fp32 softmax). out [N*N, H*C] (dt). Replaces kernels.tri_attention_fused (boltz_mlx/kernels.py:531-945) and
+ * kernels_nax.tri_attention_nax (boltz_mlx/kernels_nax.py:323-558). */
+int bzpf_triattn_core(const void* qkvg, const void* tri_bias, const float* mask, int64_t mask_si, int64_t mask_sk,
+                      float inf, void* out, int dt, int64_t N, int H, int C, void* stream);
+
+/* Output projection + residual + next LayerNorm: y = x[p] . W^T (x [N*N, D], W [D, D]) added to z at the position
+ * p (trans: the transposed position, the ending node), then xn_next = LN_next(z) at that position when
+ * next_w != NULL. Replaces kernels_nax3.linear_addln (boltz_mlx/kernels_nax3.py:176-198, 320-354) and the
+ * linear_o + radd of the strict path (boltz_mlx/layers/triangular_attention/attention.py:72-77). */
+int bzpf_linear_resid_ln(const void* x, const void* w, int trans, float* z, int accumulate, const float* next_w,
+                         const float* next_b, float next_eps, void* xn_next, int dt, int64_t N, int D, void* stream);
+
+/* Transition: z[r] = (accumulate ? z[r] : 0) + fc3(silu(xn[r].fc1^T) * (xn[r].fc2^T)) over `rows` rows of D = 128,
+ * w12 = [fc1.weight; fc2.weight] [2*hidden, D], w3 = fc3.weight [D, hidden]; then xn_next = LN_next(z) when
+ * next_w != NULL. Replaces kernels.transition_fused (boltz_mlx/kernels.py:1122-1155),
+ * kernels_nax2.transition_nax (boltz_mlx/kernels_nax2.py:54-190) and kernels_nax3.transition_lnx / transition3
+ * (boltz_mlx/kernels_nax3.py:713-827, 1381-1482). */
+int bzpf_transition(const void* xn, const void* w12, const void* w3, float* z, int accumulate, const float* next_w,
+                    const float* next_b, float next_eps, void* xn_next, int dt, int64_t rows, int D, int hidden,
+                    void* stream);
+
+/* Linear layer y[r] = x[r] . W^T + bias (K % 8 == 0; bias may be NULL); accumulate != 0 adds into an fp32 y.
+ * Replaces the nn.Linear / kernels.lin16 calls of the s track (boltz_mlx/layers/attentionv2.py:50-52, 70, 84;
+ * boltz_mlx/kernels.py:1360-1370). */
+int bzpf_linear(const void* x, const void* w, const float* bias, void* y, int dt, int y_dt, int64_t rows, int K,
+                int M, int accumulate, void* stream);
+
+/* a[r][c] = silu(h[r][c]) * h[r][hidden + c]. Replaces the SwiGLU of Transition
+ * (boltz_mlx/layers/transition.py:148-154; kernels.swiglu16, boltz_mlx/kernels.py:1378-1386). */
+int bzpf_swiglu(const void* h, void* a, int dt, int64_t rows, int hidden, void* stream);
+
+/* Sequence attention with pair bias: for head h and query j,
+ *   out[j][h*hd + c] = sigmoid(g[j][h*hd + c]) * sum_k softmax_k(q.k/sqrt(hd) + bias[h][j][k]
+ *                                                                 + (1 - mask[k]) * (-inf)) v[k][h*hd + c]
+ * q/k/v/g rows of pitch ld_in, out rows of pitch ld_out. Replaces the attention core of AttentionPairBias
+ * (boltz_mlx/layers/attentionv2.py:70-83). */
+int bzpf_seq_attention(const void* q, const void* k, const void* v, const void* g, int64_t ld_in, const void* bias,
+                       const float* mask, float inf, void* out, int64_t ld_out, int dt, int64_t N, int H, int hd,
+                       void* stream);
+
+/* Pair bias out[h][r] = LN(z[r]; ln_w, ln_b, eps) . W[h] for r < rows (z fp32 [rows, D = 128], W [H, D], H <= 16).
+ * Replaces proj_z of AttentionPairBias (boltz_mlx/layers/attentionv2.py:37-39, 57-66) and the pair-bias epilogue of
+ * kernels_nax3.transition_lnx (boltz_mlx/kernels_nax3.py:713-768). */
+int bzpf_pair_bias(const float* z, const float* ln_w, const float* ln_b, float eps, const void* w, void* out, int dt,
+                   int64_t rows, int D, int H, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BZPF_H */

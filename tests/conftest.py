@@ -1,0 +1,114 @@
+"""Shared test helpers: the `gpu` marker, the reference's parameter layout and seeded inputs.
+
+The parameter names and shapes below are the reference checkpoint layout of one PairformerLayer
+(nn.Linear.weight is [out, in]; boltz_mlx/layers/pairformer.py:23-57, triangular_mult.py:10-17,
+triangular_attention/attention.py:15-25 with primitives.py:20-38, transition.py:15-25, attentionv2.py:15-41).
+"""
+
+from __future__ import annotations
+
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs an MI355X (runs the HIP kernels through the C-ABI library)")
+
+
+# ----------------------------------------------------------------------------------------------------------------
+# reference parameter layout
+# ----------------------------------------------------------------------------------------------------------------
+
+def shapes_tri_mul(D: int) -> dict:
+    return {
+        "norm_in.weight": (D,), "norm_in.bias": (D,),
+        "p_in.weight": (2 * D, D), "g_in.weight": (2 * D, D),
+        "norm_out.weight": (D,), "norm_out.bias": (D,),
+        "p_out.weight": (D, D), "g_out.weight": (D, D),
+    }
+
+
+def shapes_tri_att(c_in: int, c_hidden: int, heads: int) -> dict:
+    hc = c_hidden * heads
+    return {
+        "layer_norm.weight": (c_in,), "layer_norm.bias": (c_in,),
+        "linear.weight": (heads, c_in),
+        "mha.linear_q.weight": (hc, c_in), "mha.linear_k.weight": (hc, c_in),
+        "mha.linear_v.weight": (hc, c_in), "mha.linear_o.weight": (c_in, hc),
+        "mha.linear_g.weight": (hc, c_in),
+    }
+
+
+def shapes_transition(dim: int, hidden: int) -> dict:
+    return {
+        "norm.weight": (dim,), "norm.bias": (dim,),
+        "fc1.weight": (hidden, dim), "fc2.weight": (hidden, dim), "fc3.weight": (dim, hidden),
+    }
+
+
+def shapes_attention(c_s: int, c_z: int, heads: int) -> dict:
+    return {
+        "proj_q.weight": (c_s, c_s), "proj_q.bias": (c_s,),
+        "proj_k.weight": (c_s, c_s), "proj_v.weight": (c_s, c_s), "proj_g.weight": (c_s, c_s),
+        "proj_z.0.weight": (c_z,), "proj_z.0.bias": (c_z,), "proj_z.1.weight": (heads, c_z),
+        "proj_o.weight": (c_s, c_s),
+    }
+
+
+def _prefixed(prefix: str, d: dict) -> dict:
+    return {f"{prefix}.{k}": v for k, v in d.items()}
+
+
+def shapes_layer(token_s: int, token_z: int, heads: int = 16, pw: int = 32, pheads: int = 4) -> dict:
+    out = {"pre_norm_s.weight": (token_s,), "pre_norm_s.bias": (token_s,)}
+    out.update(_prefixed("attention", shapes_attention(token_s, token_z, heads)))
+    out.update(_prefixed("tri_mul_out", shapes_tri_mul(token_z)))
+    out.update(_prefixed("tri_mul_in", shapes_tri_mul(token_z)))
+    out.update(_prefixed("tri_att_start", shapes_tri_att(token_z, pw, pheads)))
+    out.update(_prefixed("tri_att_end", shapes_tri_att(token_z, pw, pheads)))
+    out.update(_prefixed("transition_s", shapes_transition(token_s, 4 * token_s)))
+    out.update(_prefixed("transition_z", shapes_transition(token_z, 4 * token_z)))
+    return out
+
+
+def rand_params(shapes: dict, seed: int, std: float = 0.02, ln_random: bool = True,
+                dtype=np.float64) -> dict:
+    """Seeded parameters in sorted-name order: matrices and biases ~ N(0, std); LayerNorm weights
+    1 + N(0, 0.1) and biases N(0, 0.1) when `ln_random` (so a swapped or dropped affine term shows), else 1 / 0."""
+    rng = np.random.default_rng(seed)
+    out = {}
+    for name in sorted(shapes):
+        shp = shapes[name]
+        is_ln = len(shp) == 1 and not name.endswith("proj_q.bias")
+        if is_ln and name.endswith("weight"):
+            v = 1.0 + 0.1 * rng.standard_normal(shp) if ln_random else np.ones(shp)
+        elif is_ln:
+            v = 0.1 * rng.standard_normal(shp) if ln_random else np.zeros(shp)
+        else:
+            v = std * rng.standard_normal(shp)
+        out[name] = v.astype(dtype)
+    return out
+
+
+def pair_inputs(N: int, D: int, seed: int, n_pad: int = 0, B: int = 1, dtype=np.float64):
+    """z ~ N(0,1) [B, N, N, D]; token mask with the last n_pad tokens padded; pair_mask = tok_i * tok_j
+    (the trunk's mask construction, model.py:171-172)."""
+    rng = np.random.default_rng(seed)
+    z = rng.standard_normal((B, N, N, D)).astype(dtype)
+    tok = np.ones((B, N), dtype=dtype)
+    if n_pad:
+        tok[:, N - n_pad:] = 0
+    pm = tok[:, :, None] * tok[:, None, :]
+    return z, tok, pm
+
+
+@pytest.fixture
+def rng():
+    return np.random.default_rng(1234)

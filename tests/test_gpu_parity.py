@@ -1,0 +1,250 @@
+"""GPU parity: every bzpf module and kernel against the CPU oracle on the same seeded inputs.
+
+fp32 mode is the parity build: max|d| / max|ref| <= 1e-5 against the oracle evaluated in float32 (the
+reference's own CPU path is MLX fp32; float32 also reproduces its rounding of fully masked attention rows, where
+every logit rounds to -1e9 and the softmax is uniform).
+
+f16 mode (fp16 operands and intermediates, fp32 accumulation, statistics and softmax, fp32 residuals) is checked
+against the float64 oracle with the tolerances F16_TOL below, in the spirit of the reference's fp16 gates
+(tests/test_nax2_kernels.py: rel_fro <= 2e-3 / max_rel <= 1e-2 against same-rounding references; here the
+reference is full precision, so the fp16 storage rounding of every intermediate counts too).
+"""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from conftest import pair_inputs, rand_params, shapes_attention, shapes_layer, shapes_transition, shapes_tri_att, shapes_tri_mul
+
+pytestmark = pytest.mark.gpu
+
+FP32_TOL = 1e-5
+# (max_rel, rel_fro) for f16 mode vs the float64 oracle
+F16_TOL = {"module": (2e-2, 5e-3), "layer": (3e-2, 1e-2)}
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _device():
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    from boltz_mlx_amd import _lib
+
+    _lib.load()
+    torch.backends.cuda.matmul.allow_tf32 = False
+    yield
+
+
+@pytest.fixture
+def precision(request):
+    from boltz_mlx_amd import kernels as K
+
+    old = K.PRECISION
+    K.set_precision(request.param)
+    yield request.param
+    K.set_precision(old)
+
+
+def dev(x, dtype=torch.float32):
+    return torch.tensor(np.asarray(x), dtype=dtype, device="cuda")
+
+
+def load(mod, params):
+    from boltz_mlx_amd.weights import load_module
+
+    load_module(mod, params)
+    return mod.cuda()
+
+
+def check(name, got, ref, prec, level="module"):
+    m = O.metrics(got, ref)
+    print(f"{name} [{prec}]: max_rel={m['max_rel']:.3e} rel_fro={m['rel_fro']:.3e} max_abs={m['max_abs']:.3e}",
+          flush=True)
+    assert m["finite"], name
+    if prec == "fp32":
+        assert m["max_rel"] <= FP32_TOL, (name, m)
+    else:
+        mr, rf = F16_TOL[level]
+        assert m["max_rel"] <= mr and m["rel_fro"] <= rf, (name, m)
+
+
+def oracle_dtype(prec):
+    return np.float32 if prec == "fp32" else np.float64
+
+
+def cast(d, dt):
+    return {k: np.asarray(v, dtype=dt) for k, v in d.items()}
+
+
+# ------------------------------------------------------------------------------------------------ LayerNorm
+
+@pytest.mark.parametrize("D", [128, 384])
+@pytest.mark.parametrize("io", [("f32", "f32"), ("f32", "f16"), ("f16", "f32")])
+def test_layernorm(D, io):
+    from boltz_mlx_amd import kernels as K
+
+    rng = np.random.default_rng(D)
+    rows = 1037
+    x = rng.standard_normal((rows, D)) * 2 + 0.5
+    w, b = 1 + 0.1 * rng.standard_normal(D), 0.1 * rng.standard_normal(D)
+    tin = torch.float16 if io[0] == "f16" else torch.float32
+    tout = torch.float16 if io[1] == "f16" else torch.float32
+    xg = dev(x, tin)
+    y = K.layer_norm(xg, dev(w), dev(b), 1e-5, out_dtype=tout).float().cpu().numpy()
+    ref = O.layer_norm(xg.float().cpu().numpy().astype(np.float64), w, b, 1e-5)
+    tol = 1e-5 if io == ("f32", "f32") else 2e-3
+    assert O.metrics(y, ref)["max_rel"] <= tol
+
+
+@pytest.mark.parametrize("trans_y,trans_out", [(0, 0), (1, 0), (0, 1), (1, 1)])
+def test_add_ln(trans_y, trans_out):
+    from boltz_mlx_amd import kernels as K
+    from boltz_mlx_amd.layers.norm import LayerNorm
+
+    N, D = 19, 128
+    rng = np.random.default_rng(5)
+    z = rng.standard_normal((N, N, D))
+    y = rng.standard_normal((N, N, D))
+    ln = LayerNorm(D).cuda()
+    with torch.no_grad():
+        ln.weight.copy_(dev(1 + 0.1 * rng.standard_normal(D)))
+        ln.bias.copy_(dev(0.1 * rng.standard_normal(D)))
+    zg = dev(z)
+    out = K.add_ln(zg, dev(y), ln, scale=0.5, trans_y=bool(trans_y), trans_out=bool(trans_out),
+                   out_dtype=torch.float32)
+    yy = y.swapaxes(0, 1) if trans_y else y
+    zr = z + 0.5 * yy
+    lr = O.layer_norm(zr, ln.weight.detach().cpu().numpy(), ln.bias.detach().cpu().numpy())
+    if trans_out:
+        lr = lr.swapaxes(0, 1)
+    assert O.metrics(zg.cpu().numpy(), zr)["max_rel"] <= 1e-6
+    assert O.metrics(out.cpu().numpy(), lr)["max_rel"] <= 1e-5
+
+
+# ------------------------------------------------------------------------------------------------ raw contraction
+
+@pytest.mark.parametrize("N", [1, 63, 64, 65, 130])
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16])
+def test_trimul_contract_raw(N, dt):
+    from boltz_mlx_amd import kernels as K
+
+    D = 8
+    ld = K.trimul_ld(N)
+    rng = np.random.default_rng(N)
+    ab = np.zeros((2 * D, N, ld))
+    ab[:, :, :N] = rng.integers(-3, 4, size=(2 * D, N, N))  # small integers: exact in fp16 with fp32 accumulation
+    o = K.trimul_contract(dev(ab, dt), N).float().cpu().numpy()[:, :, :N]
+    ref = np.einsum("dik,djk->dij", ab[:D, :, :N], ab[D:, :, :N])
+    if dt == torch.float16:
+        ref = ref.astype(np.float16).astype(np.float64)  # the store rounds to fp16
+    assert np.array_equal(o, ref)
+
+
+# ------------------------------------------------------------------------------------------------ modules
+
+TRI_N = [1, 2, 17, 33, 70, 130]
+
+
+@pytest.mark.parametrize("precision", ["fp32", "f16"], indirect=True)
+@pytest.mark.parametrize("outgoing", [True, False])
+@pytest.mark.parametrize("N", TRI_N)
+def test_tri_mul(precision, outgoing, N):
+    from boltz_mlx_amd.layers.triangular_mult import TriangleMultiplicationIncoming, TriangleMultiplicationOutgoing
+
+    D = 128
+    p = rand_params(shapes_tri_mul(D), seed=100 + N, std=0.1)
+    x, _, pm = pair_inputs(N, D, seed=N, n_pad=N // 5)
+    if N > 3:
+        pm[0, 1, 2] = 0
+    odt = oracle_dtype(precision)
+    ref = O.tri_mul(x.astype(odt), pm.astype(odt), cast(p, odt), outgoing)
+    mod = load((TriangleMultiplicationOutgoing if outgoing else TriangleMultiplicationIncoming)(D), p)
+    got = mod(dev(x), dev(pm)).cpu().numpy()
+    check(f"tri_mul_{'out' if outgoing else 'in'} N={N}", got, ref, precision)
+
+
+@pytest.mark.parametrize("precision", ["fp32", "f16"], indirect=True)
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("N", [1, 2, 9, 33, 65, 100])
+def test_tri_att(precision, starting, N):
+    from boltz_mlx_amd.layers.triangular_attention.attention import (TriangleAttentionEndingNode,
+                                                                     TriangleAttentionStartingNode)
+
+    D, C, H = 128, 32, 4
+    p = rand_params(shapes_tri_att(D, C, H), seed=200 + N, std=0.1)
+    x, _, pm = pair_inputs(N, D, seed=N + 7, n_pad=N // 5)
+    if N > 3:
+        pm[0, 2, 1] = 0
+    odt = np.float32  # fully masked rows follow the fp32 rounding (see the module docstring)
+    ref = O.tri_att(x.astype(odt), pm.astype(odt), cast(p, odt), starting, row_chunk=16)
+    mod = load(TriangleAttentionStartingNode(D, C, H) if starting else TriangleAttentionEndingNode(D, C, H), p)
+    got = mod(dev(x), dev(pm)).cpu().numpy()
+    check(f"tri_att_{'start' if starting else 'end'} N={N}", got, ref, precision)
+
+
+@pytest.mark.parametrize("precision", ["fp32", "f16"], indirect=True)
+@pytest.mark.parametrize("dim,rows", [(128, 1), (128, 37), (128, 4111), (384, 5), (384, 300)])
+def test_transition(precision, dim, rows):
+    from boltz_mlx_amd.layers.transition import Transition
+
+    p = rand_params(shapes_transition(dim, 4 * dim), seed=300 + rows, std=0.1)
+    x = np.random.default_rng(rows).standard_normal((rows, dim))
+    odt = oracle_dtype(precision)
+    ref = O.transition(x.astype(odt), cast(p, odt))
+    got = load(Transition(dim, 4 * dim), p)(dev(x)).cpu().numpy()
+    check(f"transition dim={dim} rows={rows}", got, ref, precision)
+
+
+@pytest.mark.parametrize("precision", ["fp32", "f16"], indirect=True)
+@pytest.mark.parametrize("N", [5, 40, 129])
+def test_attention_pair_bias(precision, N):
+    from boltz_mlx_amd.layers.attentionv2 import AttentionPairBias
+
+    cs, cz, H = 384, 128, 16
+    p = rand_params(shapes_attention(cs, cz, H), seed=400 + N, std=0.1)
+    rng = np.random.default_rng(N)
+    s = rng.standard_normal((1, N, cs))
+    z = rng.standard_normal((1, N, N, cz))
+    mask = np.ones((1, N))
+    mask[:, -(N // 5):] = 0 if N >= 5 else 1
+    odt = np.float32
+    ref = O.attention_pair_bias(s.astype(odt), z.astype(odt), mask.astype(odt), s.astype(odt), cast(p, odt), H)
+    got = load(AttentionPairBias(cs, cz, H), p)(dev(s), dev(z), dev(mask), dev(s)).cpu().numpy()
+    check(f"attention_pair_bias N={N}", got, ref, precision)
+
+
+@pytest.mark.parametrize("precision", ["fp32", "f16"], indirect=True)
+@pytest.mark.parametrize("N,n_pad", [(24, 3), (50, 0)])
+def test_pairformer_layer(precision, N, n_pad):
+    from boltz_mlx_amd.layers.pairformer import PairformerLayer
+
+    cs, cz, H = 384, 128, 16
+    p = rand_params(shapes_layer(cs, cz, H), seed=500 + N, std=0.05)
+    z, tok, pm = pair_inputs(N, cz, seed=N, n_pad=n_pad)
+    s = np.random.default_rng(N + 1).standard_normal((1, N, cs))
+    odt = np.float32
+    s_r, z_r = O.pairformer_layer(s.astype(odt), z.astype(odt), tok.astype(odt), pm.astype(odt), cast(p, odt), H)
+    layer = load(PairformerLayer(cs, cz, H), p)
+    s_g, z_g = layer(dev(s), dev(z), dev(tok), dev(pm))
+    check(f"pairformer_layer z N={N}", z_g.cpu().numpy(), z_r, precision, "layer")
+    check(f"pairformer_layer s N={N}", s_g.cpu().numpy(), s_r, precision, "layer")
+
+
+@pytest.mark.parametrize("precision", ["fp32", "f16"], indirect=True)
+def test_pairformer_module_two_blocks(precision):
+    from boltz_mlx_amd.layers.pairformer import PairformerModule
+
+    N, cs, cz, H, nb = 20, 384, 128, 16, 2
+    m = PairformerModule(cs, cz, nb, H)
+    p = {}
+    for i in range(nb):
+        p.update({f"layers.{i}.{k}": v for k, v in rand_params(shapes_layer(cs, cz, H), seed=600 + i, std=0.05).items()})
+    z, tok, pm = pair_inputs(N, cz, seed=61, n_pad=2)
+    s = np.random.default_rng(62).standard_normal((1, N, cs))
+    odt = np.float32
+    s_r, z_r = O.pairformer_module(s.astype(odt), z.astype(odt), tok.astype(odt), pm.astype(odt), cast(p, odt), nb, H)
+    m = load(m, p)
+    s_g, z_g = m(dev(s), dev(z), dev(tok), dev(pm))
+    check("pairformer_module z", z_g.cpu().numpy(), z_r, precision, "layer")
+    check("pairformer_module s", s_g.cpu().numpy(), s_r, precision, "layer")

@@ -1,0 +1,221 @@
+"""Pairformer trunk benchmark on one MI355X: Pairformer blocks/s at N=1000 (and N=400), fp16 mixed precision.
+
+Workload (the 64-block trunk configuration): PairformerModule(token_s=384, token_z=128, 64 blocks, 16 s-heads,
+triangle attention 4 x 32), synthetic seeded inputs z ~ N(0,1) [1, N, N, 128], s ~ N(0,1) [1, N, 384], 5% of the
+tokens padded (pair_mask = tok_i tok_j), random-init weights ~ N(0, 0.02) with LayerNorm gamma=1 beta=0. A step is
+one Pairformer block (layer i % 64 of the trunk, applied in place to the resident z and s), so --steps 64 is one
+full trunk pass. Inputs and weights are resident in HBM before the timed region.
+
+Prints one JSON line. `roofline` is for the kernel with the largest share of the timed region, from HIP events
+recorded around every launch on the launch stream; `cpu_baseline` times the numpy oracle (reference-equivalent
+fp32 CPU path) on one block at N=400 and scales it to N=1000 by the FLOP ratio.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+MFMA_F16_PEAK_TFLOPS = 2500.0
+
+
+def block_flops(N: int) -> float:
+    """Algorithmic FLOP of one Pairformer block (triangle ops, transitions, s track)."""
+    return 1536.0 * N ** 3 + 1121792.0 * N ** 2 + 5013504.0 * N
+
+
+def kernel_work(name: str, N: int, H: int = 4, C: int = 32, D: int = 128) -> tuple[float, float]:
+    """(algorithmic FLOP, algorithmic HBM bytes) of one launch of a pair-track entry point at N tokens, fp16
+    storage, fp32 z: the per-unit figures times the units one launch processes."""
+    R = N * N
+    if name == "bzpf_trimul_contract":   # 128 channels of N x N x N; read a, b, write o (fp16)
+        return 2.0 * D * N ** 3, 6.0 * D * N ** 2
+    if name == "bzpf_triattn_core":      # QK^T and PV per (row, head); q|k|v|g + bias + mask read, out written
+        return 4.0 * H * C * N ** 3, (2 * 4 * H * C + 2 * H + 4 + 2 * H * C) * float(R)
+    if name == "bzpf_transition":        # 128 -> 2x512 -> 128 per row; xn in, z r/w, next LN out
+        return 393216.0 * R, R * D * (2 + 4 + 4 + 2.0)
+    if name == "bzpf_trimul_proj":       # 128 -> 512 per row; xn in, a|b (256 ch) out
+        return 131072.0 * R, R * (D * 2 + 256 * 2.0)
+    if name == "bzpf_trimul_tail":       # two 128 x 128 GEMMs per row; o, xn in, z r/w, next LN out
+        return 65536.0 * R, R * (256 + 256 + 1024 + 256.0)
+    if name == "bzpf_triattn_proj":      # 128 -> 516 per row; xn in, q|k|v|g + bias out
+        return 2.0 * 128 * (4 * H * C + H) * R, R * (D * 2 + (4 * H * C + H) * 2.0)
+    if name == "bzpf_linear_resid_ln":   # 128 x 128 per row; x in, z r/w, next LN out
+        return 2.0 * 128 * 128 * R, R * (256 + 1024 + 256.0)
+    if name == "bzpf_pair_bias":         # LN + 128 -> 16 per row; z in, bias out
+        return 2.0 * 128 * 16 * R, R * (512 + 32.0)
+    return 0.0, 0.0
+
+
+def roofline_for(name: str, ms: float, N: int) -> dict:
+    fl, by = kernel_work(name, N)
+    t_fl = fl / (MFMA_F16_PEAK_TFLOPS * 1e12)
+    t_by = by / (HBM_PEAK_GBS * 1e9)
+    if t_fl >= t_by:
+        ach = fl / (ms * 1e-3) / 1e12
+        return {"kernel": name, "bound": "mfma", "achieved": round(ach, 2), "peak": MFMA_F16_PEAK_TFLOPS,
+                "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
+                "avg_ms": round(ms, 4), "algorithmic_flop": fl, "algorithmic_bytes": by}
+    ach = by / (ms * 1e-3) / 1e9
+    return {"kernel": name, "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "avg_ms": round(ms, 4),
+            "algorithmic_flop": fl, "algorithmic_bytes": by}
+
+
+def make_trunk(N: int, blocks: int, seed: int, device):
+    import numpy as np
+    import torch
+
+    from boltz_mlx_amd.layers.pairformer import PairformerModule
+    from boltz_mlx_amd.weights import load_module, synthetic_state
+
+    m = PairformerModule(384, 128, blocks, 16)
+    load_module(m, synthetic_state(m, seed))
+    m = m.to(device)
+    rng = np.random.default_rng(seed + 1)
+    z = torch.tensor(rng.standard_normal((1, N, N, 128), dtype=np.float32), device=device)
+    s = torch.tensor(rng.standard_normal((1, N, 384), dtype=np.float32), device=device)
+    tok = torch.ones((1, N), dtype=torch.float32, device=device)
+    tok[:, N - int(round(0.05 * N)):] = 0
+    pm = (tok[:, :, None] * tok[:, None, :]).contiguous()
+    return m, s, z, tok, pm
+
+
+def run_blocks(m, s, z, tok, pm, start: int, count: int, xn=None):
+    """Apply `count` consecutive blocks of the trunk (cycling) in place; carries the next norm_in output."""
+    n = len(m.layers)
+    for k in range(count):
+        i = (start + k) % n
+        nxt = m.layers[(i + 1) % n].tri_mul_out.norm_in
+        xn = m.layers[i].inplace(s, z, tok, pm, xn_in=xn, next_ln=nxt)
+    return xn
+
+
+def cpu_baseline(N_sample: int = 400, N_target: int = 1000) -> dict:
+    import numpy as np
+
+    import oracle as O
+    from boltz_mlx_amd.layers.pairformer import PairformerLayer
+    from boltz_mlx_amd.weights import synthetic_state
+
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    except Exception:  # threadpoolctl absent: report the visible cores
+        threads = os.cpu_count()
+    p = synthetic_state(PairformerLayer(384, 128, 16), seed=0)
+    rng = np.random.default_rng(1)
+    z = rng.standard_normal((1, N_sample, N_sample, 128), dtype=np.float32)
+    s = rng.standard_normal((1, N_sample, 384), dtype=np.float32)
+    tok = np.ones((1, N_sample), np.float32)
+    tok[:, N_sample - int(round(0.05 * N_sample)):] = 0
+    pm = tok[:, :, None] * tok[:, None, :]
+    t0 = time.perf_counter()
+    O.pairformer_layer(s, z, tok, pm, p, 16)
+    dt = time.perf_counter() - t0
+    scale = block_flops(N_target) / block_flops(N_sample)
+    return {"value": round(1.0 / (dt * scale), 6), "unit": "blocks/s", "cores": int(threads), "kind": "port",
+            "sample": f"one PairformerLayer at N={N_sample} (numpy float32 oracle, 5% padded) in {dt:.2f} s, "
+                      f"scaled by the block FLOP ratio {scale:.2f} to N={N_target} (estimate)"}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=64, help="timed Pairformer blocks at N")
+    ap.add_argument("--warmup", type=int, default=4)
+    ap.add_argument("--n", type=int, default=1000)
+    ap.add_argument("--n-small", type=int, default=400)
+    ap.add_argument("--blocks", type=int, default=64)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from boltz_mlx_amd import kernels as K
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm device", file=sys.stderr)
+        return 1
+    K.set_precision("f16")
+    dev = torch.device("cuda:0")
+    torch.backends.cuda.matmul.allow_tf32 = False
+    result_small = None
+    with torch.no_grad():
+        # N = 400 blocks/s (secondary figure)
+        if args.n_small:
+            m, s, z, tok, pm = make_trunk(args.n_small, args.blocks, 0, dev)
+            xn = run_blocks(m, s, z, tok, pm, 0, 2)
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            run_blocks(m, s, z, tok, pm, 2, 16, xn)
+            torch.cuda.synchronize()
+            result_small = 16 / (time.perf_counter() - t0)
+            del m, s, z, tok, pm
+            torch.cuda.empty_cache()
+        m, s, z, tok, pm = make_trunk(args.n, args.blocks, 0, dev)
+        xn = run_blocks(m, s, z, tok, pm, 0, args.warmup)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        run_blocks(m, s, z, tok, pm, args.warmup, args.steps, xn)
+        torch.cuda.synchronize()
+        dt = time.perf_counter() - t0
+        finite = bool(torch.isfinite(z).all().item() and torch.isfinite(s).all().item())
+        # per-kernel breakdown: HIP events around every launch on the launch stream, over the same number of blocks
+        K.start_timing()
+        t1 = time.perf_counter()
+        run_blocks(m, s, z, tok, pm, args.warmup + args.steps, args.steps, xn)
+        torch.cuda.synchronize()
+        dt_ev = time.perf_counter() - t1
+        times = K.stop_timing()
+    total = {k: sum(v) for k, v in times.items()}
+    dom = max(total, key=total.get)
+    roof = roofline_for(dom, total[dom] / len(times[dom]), args.n)
+    breakdown = {k: {"ms_total": round(v, 3), "launches": len(times[k]), "share": round(v / sum(total.values()), 4)}
+                 for k, v in sorted(total.items(), key=lambda kv: -kv[1])}
+    per_kernel_roof = {k: roofline_for(k, total[k] / len(times[k]), args.n) for k in total
+                       if kernel_work(k, args.n)[0] > 0}
+    value = args.steps / dt
+    out = {
+        "metric": "Pairformer blocks/sec at N=1000 fp16",
+        "value": round(value, 4),
+        "unit": "blocks/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(1e3 * dt / args.steps, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16",
+        "data": "synthetic (seeded N(0,1) z and s, random-init weights N(0,0.02), 5% padded tokens)",
+        "config": {"workload": f"pairformer_trunk_{args.blocks}blocks_N{args.n}_fp16", "N": args.n,
+                   "blocks": args.blocks, "token_s": 384, "token_z": 128, "s_heads": 16,
+                   "tri_heads": 4, "tri_head_dim": 32, "pad_frac": 0.05, "parallelism": "none (1 GPU)"},
+        "blocks_per_s_n400": None if result_small is None else round(result_small, 4),
+        "tflops_effective": round(value * block_flops(args.n) / 1e12, 2),
+        "finite": finite,
+        "roofline": roof,
+        "kernel_breakdown": breakdown,
+        "kernel_roofline": per_kernel_roof,
+        "timed_with_events_s": round(dt_ev, 4),
+    }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -127,13 +127,17 @@ int bzpf_triattn_proj(const void* xn, const void* w, int trans, void* qkvg, void
 }
 
 int bzpf_triattn_core(const void* qkvg, const void* tri_bias, const float* mask, int64_t mask_si, int64_t mask_sk,
-                      float inf, void* out, int dt, int64_t N, int H, int C, void* stream) {
+                      float inf, void* out, int dt, int64_t N, int H, int C, int impl, void* stream) {
   REQUIRE_PTR(qkvg);
-  REQUIRE(tri_bias != nullptr && mask != nullptr && out != nullptr, "bzpf_triattn_core: NULL pointer");
+  REQUIRE_PTR(out);
+  REQUIRE(tri_bias != nullptr && mask != nullptr, "bzpf_triattn_core: NULL pointer");
   REQUIRE(dt_ok(dt), "bzpf_triattn_core: bad dtype %d", dt);
   REQUIRE(H >= 1 && H <= 65535 && (C == 16 || C == 32 || C == 64), "bzpf_triattn_core: H=%d C=%d", H, C);
   REQUIRE(N >= 1 && N <= 65535, "bzpf_triattn_core: N=%lld out of range", (long long)N);
-  return done(bzpf::launch_triattn_core(qkvg, tri_bias, mask, mask_si, mask_sk, inf, out, dt, N, H, C, S(stream)),
+  REQUIRE(impl >= 0 && impl <= 2, "bzpf_triattn_core: impl must be 0 (auto), 1 (VALU) or 2 (MFMA)");
+  REQUIRE(impl != 2 || (dt == BZPF_F16 && C == 32), "bzpf_triattn_core: the MFMA core needs fp16 and C = 32");
+  return done(bzpf::launch_triattn_core(qkvg, tri_bias, mask, mask_si, mask_sk, inf, out, dt, N, H, C, impl,
+                                        S(stream)),
               "bzpf_triattn_core");
 }
 

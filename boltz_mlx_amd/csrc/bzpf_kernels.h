@@ -24,8 +24,11 @@ hipError_t launch_trimul_tail(const void* o, const float* now, const float* nob,
 hipError_t launch_triattn_proj(const void* xn, const void* w, int trans, void* qkvg, void* tb, int dt, int64_t N,
                                int H, int C, hipStream_t st);
 hipError_t launch_triattn_core(const void* qkvg, const void* tb, const float* mask, int64_t mask_si,
-                               int64_t mask_sk, float inf, void* out, int dt, int64_t N, int H, int C,
+                               int64_t mask_sk, float inf, void* out, int dt, int64_t N, int H, int C, int impl,
                                hipStream_t st);
+hipError_t launch_triattn_core_f16_mfma(const void* qkvg, const void* tb, const float* mask, int64_t mask_si,
+                                        int64_t mask_sk, float inf, void* out, int64_t N, int H, int C,
+                                        hipStream_t st);
 hipError_t launch_triattn_core_simple(const void* qkvg, const void* tb, const float* mask, int64_t mask_si,
                                       int64_t mask_sk, float inf, void* out, int dt, int64_t N, int H, int C,
                                       hipStream_t st);

@@ -298,10 +298,15 @@ hipError_t launch_linear_resid_ln(const void* x, const void* w, int trans, float
 
 namespace bzpf {
 
-// Core dispatch: every storage type runs the reference VALU kernel until the MFMA kernel is selected here.
+// Core dispatch (impl mirrors the reference's scalar / mma choice, boltz_mlx/kernels.py:902-945): 0 = MFMA for
+// fp16 with C = 32, else the VALU kernel; 1 = the VALU kernel; 2 = MFMA (fp16, C = 32 only).
 hipError_t launch_triattn_core(const void* qkvg, const void* tb, const float* mask, int64_t mask_si,
-                               int64_t mask_sk, float inf, void* out, int dt, int64_t N, int H, int C,
+                               int64_t mask_sk, float inf, void* out, int dt, int64_t N, int H, int C, int impl,
                                hipStream_t st) {
+  const bool mfma_ok = dt == DT_F16 && C == 32;
+  if (impl == 2 && !mfma_ok) return hipErrorInvalidValue;
+  if ((impl == 0 && mfma_ok) || impl == 2)
+    return launch_triattn_core_f16_mfma(qkvg, tb, mask, mask_si, mask_sk, inf, out, N, H, C, st);
   return launch_triattn_core_simple(qkvg, tb, mask, mask_si, mask_sk, inf, out, dt, N, H, C, st);
 }
 

@@ -18,10 +18,42 @@ import os
 import torch
 
 from boltz_mlx_amd import _lib
-from boltz_mlx_amd._lib import F16, F32, call
+from boltz_mlx_amd._lib import F16, F32
+from boltz_mlx_amd._lib import call as _call
 
 PRECISION = os.environ.get("BOLTZ_MLX_PRECISION", "fp32")
 TRIMULT_K = int(os.environ.get("BOLTZ_MLX_TRIMULT_K", "4"))
+
+
+# Per-entry-point HIP event timing (off unless a dict is installed with start_timing()).
+_TIMING: dict | None = None
+
+
+def start_timing() -> None:
+    """Record a start/end torch.cuda.Event pair on the current stream around every bzpf launch from now on."""
+    global _TIMING
+    _TIMING = {}
+
+
+def stop_timing() -> dict:
+    """Synchronise and return {entry point: [milliseconds per launch, ...]}; stops recording."""
+    global _TIMING
+    t, _TIMING = _TIMING, None
+    if not t:
+        return {}
+    torch.cuda.synchronize()
+    return {name: [a.elapsed_time(b) for a, b in pairs] for name, pairs in t.items()}
+
+
+def call(name: str, *args) -> None:
+    if _TIMING is None:
+        _call(name, *args)
+        return
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    _call(name, *args)
+    b.record()
+    _TIMING.setdefault(name, []).append((a, b))
 
 
 def set_precision(mode: str) -> None:
@@ -177,15 +209,19 @@ def triattn_proj(xn, w, trans: bool, N: int, H: int, C: int):
     return qkvg, tb
 
 
-def triattn_core(qkvg, tb, mask, trans: bool, inf: float, N: int, H: int, C: int) -> torch.Tensor:
-    """mask: the pair mask [N, N] fp32 in the natural orientation; the ending node (trans) reads it transposed."""
+TRIATT_IMPL = {"auto": 0, "scalar": 1, "mma": 2}[os.environ.get("BOLTZ_MLX_TRIATT_IMPL", "auto")]
+
+
+def triattn_core(qkvg, tb, mask, trans: bool, inf: float, N: int, H: int, C: int, impl: int | None = None):
+    """mask: the pair mask [N, N] fp32 in the natural orientation; the ending node (trans) reads it transposed.
+    impl: 0 auto, 1 VALU kernel, 2 MFMA kernel (default from BOLTZ_MLX_TRIATT_IMPL = auto | scalar | mma)."""
     _dev(qkvg, tb, mask)
     if mask.dtype != torch.float32 or mask.numel() != N * N:
         raise ValueError("triattn_core: mask must be fp32 [N, N]")
     out = torch.empty((N * N, H * C), dtype=qkvg.dtype, device=qkvg.device)
     si, sk = (1, N) if trans else (N, 1)
     call("bzpf_triattn_core", _p(qkvg), _p(tb), _p(mask), si, sk, float(inf), _p(out), _dt(qkvg), N, H, C,
-         _stream())
+         TRIATT_IMPL if impl is None else int(impl), _stream())
     return out
 
 

@@ -85,10 +85,12 @@ int bzpf_triattn_proj(const void* xn, const void* w, int trans, void* qkvg, void
 /* Flash triangle-attention core: for row i, head h, query j,
  *   out[i][j][h*C + c] = sigmoid(g) * sum_k softmax_k((q/sqrt(C)).k + inf*(mask[i*mask_si + k*mask_sk] - 1)
  *                                                     + tri_bias[h][j*N + k]) v[k][c]
- * (fp32 softmax). out [N*N, H*C] (dt). Replaces kernels.tri_attention_fused (boltz_mlx/kernels.py:531-945) and
+ * (fp32 softmax). out [N*N, H*C] (dt). impl selects the kernel like the reference's impl argument: 0 = auto (MFMA
+ * for fp16 with C = 32, else VALU), 1 = the VALU kernel, 2 = the MFMA kernel (fp16, C = 32).
+ * Replaces kernels.tri_attention_fused (boltz_mlx/kernels.py:531-945, impl "scalar" / "mma") and
  * kernels_nax.tri_attention_nax (boltz_mlx/kernels_nax.py:323-558). */
 int bzpf_triattn_core(const void* qkvg, const void* tri_bias, const float* mask, int64_t mask_si, int64_t mask_sk,
-                      float inf, void* out, int dt, int64_t N, int H, int C, void* stream);
+                      float inf, void* out, int dt, int64_t N, int H, int C, int impl, void* stream);
 
 /* Output projection + residual + next LayerNorm: y = x[p] . W^T (x [N*N, D], W [D, D]) added to z at the position
  * p (trans: the transposed position, the ending node), then xn_next = LN_next(z) at that position when

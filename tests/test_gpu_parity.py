@@ -248,3 +248,30 @@ def test_pairformer_module_two_blocks(precision):
     s_g, z_g = m(dev(s), dev(z), dev(tok), dev(pm))
     check("pairformer_module z", z_g.cpu().numpy(), z_r, precision, "layer")
     check("pairformer_module s", s_g.cpu().numpy(), s_r, precision, "layer")
+
+
+# ------------------------------------------------------------------------------------------------ fast vs slow core
+
+@pytest.mark.parametrize("N", [1, 2, 17, 64, 65, 130])
+@pytest.mark.parametrize("trans", [False, True])
+def test_triattn_core_mfma_vs_valu(N, trans):
+    """The fp16 MFMA flash core against the VALU reference kernel on identical fp16 inputs (the reference's own gate
+    for its fp16 core against the fp32-softmax kernel: <= 5e-3, tests/test_triatt_nax.py). Rows with padded keys, a
+    fully masked row and an asymmetric hole are included; trans reads the mask transposed (ending node)."""
+    from boltz_mlx_amd import kernels as K
+
+    H, C = 4, 32
+    rng = np.random.default_rng(N)
+    qkvg = dev(rng.standard_normal((4 * H, N * N, C)), torch.float16)
+    tb = dev(rng.standard_normal((H, N * N)), torch.float16)
+    mask = np.ones((N, N), np.float32)
+    if N > 4:
+        mask[:, -2:] = 0
+        mask[3, :] = 0
+        mask[1, 2] = 0
+    mg = dev(mask)
+    fast = K.triattn_core(qkvg, tb, mg, trans, 1e9, N, H, C, impl=2).float().cpu().numpy()
+    slow = K.triattn_core(qkvg, tb, mg, trans, 1e9, N, H, C, impl=1).float().cpu().numpy()
+    m = O.metrics(fast, slow)
+    print(f"core mfma vs valu N={N} trans={trans}: {m}", flush=True)
+    assert m["finite"] and m["max_rel"] <= 5e-3 and m["rel_fro"] <= 2e-3, m

@@ -19,14 +19,14 @@ vp, i32, i64, f32 = C.c_void_p, C.c_int, C.c_int64, C.c_float
 SIGNATURES = {
     "bzpf_version": [],
     "bzpf_last_error": [],
-    "bzpf_trimul_ld": [i64],
+    "bzpf_row_pitch": [i64],
     "bzpf_layernorm": [vp, i32, vp, vp, f32, vp, i32, i64, i32, vp],
     "bzpf_add_ln": [vp, vp, i32, f32, i32, vp, vp, f32, vp, i32, i32, i64, i32, vp],
     "bzpf_trimul_proj": [vp, vp, vp, f32, i32, vp, i32, i64, i64, i32, vp],
     "bzpf_trimul_contract": [vp, vp, i32, i64, i64, i32, vp],
     "bzpf_trimul_tail": [vp, vp, vp, f32, vp, vp, vp, vp, i32, vp, vp, f32, vp, i32, i64, i64, i32, vp],
-    "bzpf_triattn_proj": [vp, vp, i32, vp, vp, i32, i64, i32, i32, i32, vp],
-    "bzpf_triattn_core": [vp, vp, vp, i64, i64, f32, vp, i32, i64, i32, i32, i32, vp],
+    "bzpf_triattn_proj": [vp, vp, i32, f32, f32, vp, vp, vp, i32, i64, i64, i32, i32, i32, vp],
+    "bzpf_triattn_core": [vp, vp, vp, vp, i64, i64, f32, vp, i32, i64, i64, i32, i32, i32, vp],
     "bzpf_linear_resid_ln": [vp, vp, i32, vp, i32, vp, vp, f32, vp, i32, i64, i32, vp],
     "bzpf_transition": [vp, vp, vp, vp, i32, vp, vp, f32, vp, i32, i64, i32, i32, vp],
     "bzpf_linear": [vp, vp, vp, vp, i32, i32, i64, i32, i32, i32, vp],
@@ -34,7 +34,7 @@ SIGNATURES = {
     "bzpf_seq_attention": [vp, vp, vp, vp, i64, vp, vp, f32, vp, i64, i32, i64, i32, i32, vp],
     "bzpf_pair_bias": [vp, vp, vp, f32, vp, vp, i32, i64, i32, i32, vp],
 }
-_RESTYPES = {"bzpf_version": C.c_char_p, "bzpf_last_error": C.c_char_p, "bzpf_trimul_ld": i64}
+_RESTYPES = {"bzpf_version": C.c_char_p, "bzpf_last_error": C.c_char_p, "bzpf_row_pitch": i64}
 
 _lib = None
 

@@ -23,6 +23,9 @@ HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 CFLAGS = [
     f"--offload-arch={ARCH}", "-O3", "-fPIC", "-std=c++17", "-Wall", "-Wno-unused-function",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # MFMA accumulators in VGPRs: the kernels read every accumulator back with VALU ops (softmax, epilogues),
+    # which the AGPR form would route through v_accvgpr moves
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-munsafe-fp-atomics", f"-I{INCLUDE}", f"-I{CSRC}",
 ]
 

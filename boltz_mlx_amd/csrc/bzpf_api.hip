@@ -43,7 +43,7 @@ const char* bzpf_version(void) { return "bzpf 0.1.0 (gfx950)"; }
 
 const char* bzpf_last_error(void) { return g_err; }
 
-int64_t bzpf_trimul_ld(int64_t N) { return (N + 63) / 64 * 64; }
+int64_t bzpf_row_pitch(int64_t N) { return (N + 63) / 64 * 64; }
 
 int bzpf_layernorm(const void* x, int x_dt, const float* w, const float* b, float eps, void* y, int y_dt,
                    int64_t rows, int D, void* stream) {
@@ -78,7 +78,7 @@ int bzpf_trimul_proj(const void* xn, const void* w_pg, const float* pair_mask, f
   REQUIRE(pair_mask != nullptr, "bzpf_trimul_proj: pair_mask is NULL");
   REQUIRE(dt_ok(dt), "bzpf_trimul_proj: bad dtype %d", dt);
   REQUIRE(D == 128, "bzpf_trimul_proj: D must be 128 (got %d)", D);
-  REQUIRE(N >= 1 && ld == bzpf_trimul_ld(N), "bzpf_trimul_proj: N=%lld ld=%lld (ld must be bzpf_trimul_ld(N))",
+  REQUIRE(N >= 1 && ld == bzpf_row_pitch(N), "bzpf_trimul_proj: N=%lld ld=%lld (ld must be bzpf_row_pitch(N))",
           (long long)N, (long long)ld);
   return done(bzpf::launch_trimul_proj(xn, w_pg, pair_mask, scale, incoming, ab, dt, N, ld, S(stream)),
               "bzpf_trimul_proj");
@@ -89,7 +89,7 @@ int bzpf_trimul_contract(const void* ab, void* o, int dt, int64_t N, int64_t ld,
   REQUIRE_PTR(o);
   REQUIRE(dt_ok(dt), "bzpf_trimul_contract: bad dtype %d", dt);
   REQUIRE(D >= 1 && D <= 65535, "bzpf_trimul_contract: bad D=%d", D);
-  REQUIRE(N >= 1 && ld == bzpf_trimul_ld(N), "bzpf_trimul_contract: N=%lld ld=%lld", (long long)N, (long long)ld);
+  REQUIRE(N >= 1 && ld == bzpf_row_pitch(N), "bzpf_trimul_contract: N=%lld ld=%lld", (long long)N, (long long)ld);
   return done(bzpf::launch_trimul_contract(ab, o, dt, N, ld, D, S(stream)), "bzpf_trimul_contract");
 }
 
@@ -107,36 +107,43 @@ int bzpf_trimul_tail(const void* o, const float* norm_out_w, const float* norm_o
           "bzpf_trimul_tail: next LN needs next_b and xn_next");
   REQUIRE(dt_ok(dt), "bzpf_trimul_tail: bad dtype %d", dt);
   REQUIRE(D == 128, "bzpf_trimul_tail: D must be 128 (got %d)", D);
-  REQUIRE(N >= 1 && ld == bzpf_trimul_ld(N), "bzpf_trimul_tail: N=%lld ld=%lld", (long long)N, (long long)ld);
+  REQUIRE(N >= 1 && ld == bzpf_row_pitch(N), "bzpf_trimul_tail: N=%lld ld=%lld", (long long)N, (long long)ld);
   return done(bzpf::launch_trimul_tail(o, norm_out_w, norm_out_b, eps_out, w_po, xn, w_go, z, accumulate, next_w,
                                        next_b, next_eps, xn_next, dt, N, ld, S(stream)),
               "bzpf_trimul_tail");
 }
 
-int bzpf_triattn_proj(const void* xn, const void* w, int trans, void* qkvg, void* tri_bias, int dt, int64_t N, int D,
-                      int H, int C, void* stream) {
+int bzpf_triattn_proj(const void* xn, const void* w, int trans, float q_scale, float bias_scale, void* qkg, void* vt,
+                      void* tri_bias, int dt, int64_t N, int64_t ldk, int D, int H, int C, void* stream) {
   REQUIRE_PTR(xn);
   REQUIRE_PTR(w);
-  REQUIRE_PTR(qkvg);
-  REQUIRE(tri_bias != nullptr, "bzpf_triattn_proj: tri_bias is NULL");
+  REQUIRE_PTR(qkg);
+  REQUIRE(vt != nullptr && tri_bias != nullptr, "bzpf_triattn_proj: NULL pointer");
   REQUIRE(dt_ok(dt), "bzpf_triattn_proj: bad dtype %d", dt);
   REQUIRE(D == 128 && H >= 1 && H * C == 128 && (C == 16 || C == 32 || C == 64),
           "bzpf_triattn_proj: need D = H*C = 128, C in {16,32,64} (D=%d H=%d C=%d)", D, H, C);
-  REQUIRE(N >= 1, "bzpf_triattn_proj: N < 1");
-  return done(bzpf::launch_triattn_proj(xn, w, trans, qkvg, tri_bias, dt, N, H, C, S(stream)), "bzpf_triattn_proj");
+  REQUIRE(N >= 1 && ldk == bzpf_row_pitch(N), "bzpf_triattn_proj: N=%lld ldk=%lld (ldk must be bzpf_row_pitch(N))",
+          (long long)N, (long long)ldk);
+  return done(bzpf::launch_triattn_proj(xn, w, trans, q_scale, bias_scale, qkg, vt, tri_bias, dt, N, ldk, H, C,
+                                        S(stream)),
+              "bzpf_triattn_proj");
 }
 
-int bzpf_triattn_core(const void* qkvg, const void* tri_bias, const float* mask, int64_t mask_si, int64_t mask_sk,
-                      float inf, void* out, int dt, int64_t N, int H, int C, int impl, void* stream) {
-  REQUIRE_PTR(qkvg);
+int bzpf_triattn_core(const void* qkg, const void* vt, const void* tri_bias, const float* mask, int64_t mask_si,
+                      int64_t mask_sk, float inf, void* out, int dt, int64_t N, int64_t ldk, int H, int C, int impl,
+                      void* stream) {
+  REQUIRE_PTR(qkg);
+  REQUIRE_PTR(vt);
+  REQUIRE_PTR(tri_bias);
   REQUIRE_PTR(out);
-  REQUIRE(tri_bias != nullptr && mask != nullptr, "bzpf_triattn_core: NULL pointer");
+  REQUIRE(mask != nullptr, "bzpf_triattn_core: mask is NULL");
   REQUIRE(dt_ok(dt), "bzpf_triattn_core: bad dtype %d", dt);
   REQUIRE(H >= 1 && H <= 65535 && (C == 16 || C == 32 || C == 64), "bzpf_triattn_core: H=%d C=%d", H, C);
-  REQUIRE(N >= 1 && N <= 65535, "bzpf_triattn_core: N=%lld out of range", (long long)N);
+  REQUIRE(N >= 1 && N <= 65535 && ldk == bzpf_row_pitch(N), "bzpf_triattn_core: N=%lld ldk=%lld", (long long)N,
+          (long long)ldk);
   REQUIRE(impl >= 0 && impl <= 2, "bzpf_triattn_core: impl must be 0 (auto), 1 (VALU) or 2 (MFMA)");
   REQUIRE(impl != 2 || (dt == BZPF_F16 && C == 32), "bzpf_triattn_core: the MFMA core needs fp16 and C = 32");
-  return done(bzpf::launch_triattn_core(qkvg, tri_bias, mask, mask_si, mask_sk, inf, out, dt, N, H, C, impl,
+  return done(bzpf::launch_triattn_core(qkg, vt, tri_bias, mask, mask_si, mask_sk, inf, out, dt, N, ldk, H, C, impl,
                                         S(stream)),
               "bzpf_triattn_core");
 }

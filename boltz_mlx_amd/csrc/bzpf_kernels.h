@@ -21,17 +21,17 @@ hipError_t launch_trimul_tail(const void* o, const float* now, const float* nob,
                               const float* lnb, float eps_next, void* xn_next, int dt, int64_t N, int64_t ld,
                               hipStream_t st);
 
-hipError_t launch_triattn_proj(const void* xn, const void* w, int trans, void* qkvg, void* tb, int dt, int64_t N,
-                               int H, int C, hipStream_t st);
-hipError_t launch_triattn_core(const void* qkvg, const void* tb, const float* mask, int64_t mask_si,
-                               int64_t mask_sk, float inf, void* out, int dt, int64_t N, int H, int C, int impl,
-                               hipStream_t st);
-hipError_t launch_triattn_core_f16_mfma(const void* qkvg, const void* tb, const float* mask, int64_t mask_si,
-                                        int64_t mask_sk, float inf, void* out, int64_t N, int H, int C,
-                                        hipStream_t st);
-hipError_t launch_triattn_core_simple(const void* qkvg, const void* tb, const float* mask, int64_t mask_si,
-                                      int64_t mask_sk, float inf, void* out, int dt, int64_t N, int H, int C,
-                                      hipStream_t st);
+hipError_t launch_triattn_proj(const void* xn, const void* w, int trans, float q_scale, float b_scale, void* qkg,
+                               void* vt, void* tb, int dt, int64_t N, int64_t ldk, int H, int C, hipStream_t st);
+hipError_t launch_triattn_core(const void* qkg, const void* vt, const void* tb, const float* mask, int64_t mask_si,
+                               int64_t mask_sk, float inf, void* out, int dt, int64_t N, int64_t ldk, int H, int C,
+                               int impl, hipStream_t st);
+hipError_t launch_triattn_core_f16_mfma(const void* qkg, const void* vt, const void* tb, const float* mask,
+                                        int64_t mask_si, int64_t mask_sk, float inf, void* out, int64_t N,
+                                        int64_t ldk, int H, int C, hipStream_t st);
+hipError_t launch_triattn_core_simple(const void* qkg, const void* vt, const void* tb, const float* mask,
+                                      int64_t mask_si, int64_t mask_sk, float inf, void* out, int dt, int64_t N,
+                                      int64_t ldk, int H, int C, hipStream_t st);
 hipError_t launch_linear_resid_ln(const void* x, const void* w, int trans, float* z, int accumulate,
                                   const float* lnw, const float* lnb, float eps, void* xn_next, int dt, int64_t N,
                                   hipStream_t st);

@@ -15,10 +15,15 @@ namespace bzpf {
 
 // ---------------------------------------------------------------- projection
 // grid: (ceil(N^2 / 64) position tiles, ceil(M / 64) column chunks), M = 4*H*C + H; block 256.
+// Outputs (position p = i*N + j of the attention frame; trans reads xn at (j, i)):
+//   qkg [3H][N*N][C]   q (times q_scale), k, g planes, C contiguous channels per position;
+//   vt  [H][N][C][ldk] v transposed per row i (keys contiguous), columns j >= N left unwritten;
+//   tb  [H][N][ldk]    tri bias (times b_scale) for query j, key k of row-independent head h.
 template <typename T>
 __global__ __launch_bounds__(256) void triattn_proj_kernel(const T* __restrict__ xn, const T* __restrict__ w,
-                                                           int trans, T* __restrict__ qkvg, T* __restrict__ tb,
-                                                           int64_t N, int H, int C) {
+                                                           int trans, float q_scale, float b_scale,
+                                                           T* __restrict__ qkg, T* __restrict__ vt,
+                                                           T* __restrict__ tb, int64_t N, int64_t ldk, int H, int C) {
   constexpr int D = 128, PAD = Pad<T>::v, LDX = D + PAD, LDO = 64 + PAD;
   __shared__ LDS_ALIGN T Xs[64 * LDX];
   __shared__ LDS_ALIGN T Ws[64 * LDX];
@@ -40,39 +45,128 @@ __global__ __launch_bounds__(256) void triattn_proj_kernel(const T* __restrict__
   f4 acc[1][4];
   zero_acc(acc);
   wave_mma<T, 1, 4>(acc, Xs + 16 * wave * LDX, LDX, Ws, LDX, D);
+  const int plane4 = c0 / HC;  // 0 q, 1 k, 2 v, 3 g, 4 tri bias (chunks never straddle planes: HC % 64 == 0)
+  const float sc = plane4 == 0 ? q_scale : (plane4 == 4 ? b_scale : 1.0f);
 #pragma unroll
   for (int nb = 0; nb < 4; nb++)
 #pragma unroll
     for (int e = 0; e < 4; e++)
-      Os[(16 * wave + (l >> 4) * 4 + e) * LDO + 16 * nb + (l & 15)] = from_f<T>(acc[0][nb][e]);
+      Os[(16 * wave + (l >> 4) * 4 + e) * LDO + 16 * nb + (l & 15)] = from_f<T>(acc[0][nb][e] * sc);
   __syncthreads();
-  if (c0 < 4 * HC) {
+  if (plane4 == 0 || plane4 == 1 || plane4 == 3) {
     // 64 / C plane-heads of C contiguous channels per position
     constexpr int VE = Vec16<T>::n;
-    const int vpr = C / VE;            // vectors per (plane-head, position)
-    const int nph = 64 / C;            // plane-heads in this chunk
+    const int vpr = C / VE;
+    const int nph = 64 / C;
+    const int pl0 = (plane4 == 3 ? 2 : plane4) * H + (c0 - plane4 * HC) / C;
     for (int e = threadIdx.x; e < nph * 64 * vpr; e += 256) {
       const int ph = e / (64 * vpr);
       const int rem = e - ph * 64 * vpr;
       const int r = rem / vpr, d = (rem - r * vpr) * VE;
       if (r >= rows) continue;
-      const int64_t plane = (c0 + ph * C) / C;
-      T* dst = qkvg + (plane * NN + p0 + r) * C + d;
+      T* dst = qkg + ((int64_t)(pl0 + ph) * NN + p0 + r) * C + d;
       *reinterpret_cast<U128*>(dst) = *reinterpret_cast<const U128*>(Os + r * LDO + ph * C + d);
+    }
+  } else if (plane4 == 2) {
+    // v transposed: consecutive lanes take consecutive positions (coalesced along keys)
+    const int r = threadIdx.x & 63, cg = threadIdx.x >> 6;
+    if (r < rows) {
+      const int64_t p = p0 + r, i = p / N, j = p - i * N;
+#pragma unroll 4
+      for (int u = 0; u < 16; u++) {
+        const int col = c0 - 2 * HC + cg * 16 + u;  // channel within the v plane group
+        const int hh = col / C, d = col - hh * C;
+        vt[(((int64_t)hh * N + i) * C + d) * ldk + j] = Os[r * LDO + cg * 16 + u];
+      }
     }
   } else {
     for (int e = threadIdx.x; e < H * 64; e += 256) {
-      const int h = e / 64, r = e - h * 64;
-      if (r < rows && c0 + h < M) tb[(int64_t)h * NN + p0 + r] = Os[r * LDO + (4 * HC + h - c0)];
+      const int hh = e / 64, r = e - hh * 64;
+      if (r < rows && c0 + hh < M) {
+        const int64_t p = p0 + r, i = p / N, j = p - i * N;
+        T* row = tb + ((int64_t)hh * N + i) * ldk;
+        row[j] = Os[r * LDO + (4 * HC + hh - c0)];
+        if (j == N - 1)  // finite padding: the MFMA core adds it before masking the keys past N with -inf
+          for (int64_t k = N; k < ldk; k++) row[k] = from_f<T>(0.0f);
+      }
     }
   }
 }
 
-// ---------------------------------------------------------------- attention core (reference VALU kernel)
-// One thread per query j; a 64-thread workgroup owns (row i, head h, 64 queries). Keys are staged TK at a time in
-// LDS (K, V and the [64 x TK] bias tile, all loaded coalesced). Rows share the bias: bias[h][j][k].
-// order 0 (triangle): s = (q*scale).k, s += inf*(m-1), s += bias.  order 1 (sequence): s = (q.k)*scale + bias,
-// s += (1-m)*(-inf). Element (row i, position j, head h, channel d) of q/k/v/g is at
+// ---------------------------------------------------------------- triangle attention core (reference VALU kernel)
+// One thread per query j; a 64-thread workgroup owns (row i, head h, 64 queries). K, V^T and the [64 x TK] bias
+// tile are staged TK keys at a time in LDS with coalesced loads. Logits are in base 2: q carries log2(e)/sqrt(C)
+// and the bias log2(e) (both applied by the projection), the key-mask bias is inf*(m-1)*log2(e); the order is the
+// reference's ((q.k) + mask_bias) + tri_bias and p = 2^(x - max).
+template <typename T, int C>
+__global__ __launch_bounds__(64) void triattn_core_valu(const T* __restrict__ qkg, const T* __restrict__ vt,
+                                                       const T* __restrict__ tb, const float* __restrict__ mask,
+                                                       int64_t mask_si, int64_t mask_sk, float inf,
+                                                       T* __restrict__ out, int64_t N, int64_t ldk, int H) {
+  constexpr int TK = 32;
+  constexpr float LOG2E = 1.4426950408889634f;
+  __shared__ float Ks[TK][C + 1];
+  __shared__ float Vs[TK][C + 1];
+  __shared__ float Bs[64][TK + 1];
+  __shared__ float Mk[TK];
+  const int t = threadIdx.x;
+  const int64_t NN = N * N;
+  const int64_t j = (int64_t)blockIdx.x * 64 + t, j0 = (int64_t)blockIdx.x * 64;
+  const int64_t h = blockIdx.y, i = blockIdx.z;
+  const bool valid = j < N;
+  const T* qb = qkg + (h * NN + i * N) * C;
+  const T* kb = qkg + ((H + h) * NN + i * N) * C;
+  const T* gb = qkg + ((2 * H + h) * NN + i * N) * C;
+  const T* vb = vt + (h * N + i) * C * ldk;
+  const T* bb = tb + h * N * ldk;
+  float q[C], acc[C];
+#pragma unroll
+  for (int d = 0; d < C; d++) {
+    q[d] = valid ? to_f(qb[j * C + d]) : 0.f;
+    acc[d] = 0.f;
+  }
+  float m = -INFINITY, lsum = 0.f;
+  for (int64_t k0 = 0; k0 < N; k0 += TK) {
+    __syncthreads();
+    for (int e = t; e < TK * C; e += 64) {
+      const int kk = e / C, d = e - kk * C;
+      Ks[kk][d] = k0 + kk < N ? to_f(kb[(k0 + kk) * C + d]) : 0.f;
+      const int d2 = e / TK, k2 = e - d2 * TK;
+      Vs[k2][d2] = k0 + k2 < N ? to_f(vb[d2 * ldk + k0 + k2]) : 0.f;
+    }
+    for (int e = t; e < 64 * TK; e += 64) {
+      const int qq = e / TK, kk = e - qq * TK;
+      Bs[qq][kk] = (j0 + qq < N && k0 + kk < N) ? to_f(bb[(j0 + qq) * ldk + k0 + kk]) : 0.f;
+    }
+    if (t < TK) Mk[t] = k0 + t < N ? inf * (mask[i * mask_si + (k0 + t) * mask_sk] - 1.0f) * LOG2E : 0.f;
+    __syncthreads();
+    const int kend = (int)((N - k0) < TK ? (N - k0) : TK);
+    for (int kk = 0; kk < kend; kk++) {
+      float s = 0.f;
+#pragma unroll
+      for (int d = 0; d < C; d++) s += q[d] * Ks[kk][d];
+      s += Mk[kk];
+      s += Bs[t][kk];
+      const float mn = fmaxf(m, s);
+      const float corr = exp2f(m - mn);
+      const float p = exp2f(s - mn);
+      lsum = lsum * corr + p;
+#pragma unroll
+      for (int d = 0; d < C; d++) acc[d] = acc[d] * corr + p * Vs[kk][d];
+      m = mn;
+    }
+  }
+  if (!valid) return;
+  const float inv = 1.0f / lsum;
+  T* ob = out + (i * N + j) * (int64_t)(H * C) + h * C;
+#pragma unroll
+  for (int d = 0; d < C; d++) ob[d] = from_f<T>(acc[d] * inv * sigmoidf_(to_f(gb[j * C + d])));
+}
+
+// ---------------------------------------------------------------- sequence attention (s track, VALU kernel)
+// One thread per query j; a 64-thread workgroup owns (head h, 64 queries). Keys are staged TK at a time in LDS
+// (K, V and the [64 x TK] bias tile, all loaded coalesced). order 0: s = (q*scale).k, s += inf*(m-1), s += bias;
+// order 1 (AttentionPairBias, attentionv2.py:76-81): s = (q.k)*scale + bias, s += (1-m)*(-inf). Element (row i, position j, head h, channel d) of q/k/v/g is at
 // base + i*s_row + j*s_pos + h*s_head + d; the output uses o_row/o_pos/o_head.
 struct AttnArgs {
   const void *q, *k, *v, *g, *bias;
@@ -218,45 +312,45 @@ __global__ __launch_bounds__(256) void linear_resid_ln_kernel(const T* __restric
 }
 
 template <typename T>
-static hipError_t proj_t(const void* xn, const void* w, int trans, void* qkvg, void* tb, int64_t N, int H, int C,
-                         hipStream_t st) {
+static hipError_t proj_t(const void* xn, const void* w, int trans, float q_scale, float b_scale, void* qkg, void* vt,
+                         void* tb, int64_t N, int64_t ldk, int H, int C, hipStream_t st) {
   const int M = 4 * H * C + H;
   const dim3 grid((unsigned)((N * N + 63) / 64), (unsigned)((M + 63) / 64));
-  triattn_proj_kernel<T><<<grid, 256, 0, st>>>(static_cast<const T*>(xn), static_cast<const T*>(w), trans,
-                                               static_cast<T*>(qkvg), static_cast<T*>(tb), N, H, C);
+  triattn_proj_kernel<T><<<grid, 256, 0, st>>>(static_cast<const T*>(xn), static_cast<const T*>(w), trans, q_scale,
+                                               b_scale, static_cast<T*>(qkg), static_cast<T*>(vt), static_cast<T*>(tb),
+                                               N, ldk, H, C);
   return hipGetLastError();
 }
 
-hipError_t launch_triattn_proj(const void* xn, const void* w, int trans, void* qkvg, void* tb, int dt, int64_t N,
-                               int H, int C, hipStream_t st) {
-  return dt == DT_F16 ? proj_t<half_t>(xn, w, trans, qkvg, tb, N, H, C, st)
-                      : proj_t<float>(xn, w, trans, qkvg, tb, N, H, C, st);
+hipError_t launch_triattn_proj(const void* xn, const void* w, int trans, float q_scale, float b_scale, void* qkg,
+                               void* vt, void* tb, int dt, int64_t N, int64_t ldk, int H, int C, hipStream_t st) {
+  return dt == DT_F16 ? proj_t<half_t>(xn, w, trans, q_scale, b_scale, qkg, vt, tb, N, ldk, H, C, st)
+                      : proj_t<float>(xn, w, trans, q_scale, b_scale, qkg, vt, tb, N, ldk, H, C, st);
 }
 
-hipError_t launch_triattn_core_simple(const void* qkvg, const void* tb, const float* mask, int64_t mask_si,
-                                      int64_t mask_sk, float inf, void* out, int dt, int64_t N, int H, int C,
-                                      hipStream_t st) {
-  const int64_t NN = N * N;
-  const size_t es = dt == DT_F16 ? 2 : 4;
-  const char* base = static_cast<const char*>(qkvg);
-  const int64_t plane = (int64_t)H * NN * C;  // elements per q / k / v / g plane group
-  AttnArgs a;
-  a.q = base;
-  a.k = base + plane * es;
-  a.v = base + 2 * plane * es;
-  a.g = base + 3 * plane * es;
-  a.bias = tb;
-  a.mask = mask;
-  a.out = out;
-  a.s_row = N * C; a.s_pos = C; a.s_head = NN * C;
-  a.o_row = N * H * C; a.o_pos = (int64_t)H * C; a.o_head = C;
-  a.b_head = NN;
-  a.m_row = mask_si; a.m_key = mask_sk;
-  a.inf = inf;
-  a.scale = 1.0f / sqrtf((float)C);
-  a.J = N;
-  a.order = 0;
-  return dt == DT_F16 ? attn_simple_launch<half_t>(a, N, H, C, st) : attn_simple_launch<float>(a, N, H, C, st);
+template <typename T>
+static hipError_t core_valu_t(const void* qkg, const void* vt, const void* tb, const float* mask, int64_t mask_si,
+                              int64_t mask_sk, float inf, void* out, int64_t N, int64_t ldk, int H, int C,
+                              hipStream_t st) {
+  const dim3 grid((unsigned)((N + 63) / 64), (unsigned)H, (unsigned)N);
+  const T* q = static_cast<const T*>(qkg);
+  const T* v = static_cast<const T*>(vt);
+  const T* b = static_cast<const T*>(tb);
+  T* o = static_cast<T*>(out);
+  switch (C) {
+    case 16: triattn_core_valu<T, 16><<<grid, 64, 0, st>>>(q, v, b, mask, mask_si, mask_sk, inf, o, N, ldk, H); break;
+    case 32: triattn_core_valu<T, 32><<<grid, 64, 0, st>>>(q, v, b, mask, mask_si, mask_sk, inf, o, N, ldk, H); break;
+    case 64: triattn_core_valu<T, 64><<<grid, 64, 0, st>>>(q, v, b, mask, mask_si, mask_sk, inf, o, N, ldk, H); break;
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+hipError_t launch_triattn_core_simple(const void* qkg, const void* vt, const void* tb, const float* mask,
+                                      int64_t mask_si, int64_t mask_sk, float inf, void* out, int dt, int64_t N,
+                                      int64_t ldk, int H, int C, hipStream_t st) {
+  return dt == DT_F16 ? core_valu_t<half_t>(qkg, vt, tb, mask, mask_si, mask_sk, inf, out, N, ldk, H, C, st)
+                      : core_valu_t<float>(qkg, vt, tb, mask, mask_si, mask_sk, inf, out, N, ldk, H, C, st);
 }
 
 hipError_t launch_seq_attention(const void* q, const void* k, const void* v, const void* g, int64_t ld_in,
@@ -300,14 +394,14 @@ namespace bzpf {
 
 // Core dispatch (impl mirrors the reference's scalar / mma choice, boltz_mlx/kernels.py:902-945): 0 = MFMA for
 // fp16 with C = 32, else the VALU kernel; 1 = the VALU kernel; 2 = MFMA (fp16, C = 32 only).
-hipError_t launch_triattn_core(const void* qkvg, const void* tb, const float* mask, int64_t mask_si,
-                               int64_t mask_sk, float inf, void* out, int dt, int64_t N, int H, int C, int impl,
-                               hipStream_t st) {
+hipError_t launch_triattn_core(const void* qkg, const void* vt, const void* tb, const float* mask, int64_t mask_si,
+                               int64_t mask_sk, float inf, void* out, int dt, int64_t N, int64_t ldk, int H, int C,
+                               int impl, hipStream_t st) {
   const bool mfma_ok = dt == DT_F16 && C == 32;
   if (impl == 2 && !mfma_ok) return hipErrorInvalidValue;
   if ((impl == 0 && mfma_ok) || impl == 2)
-    return launch_triattn_core_f16_mfma(qkvg, tb, mask, mask_si, mask_sk, inf, out, N, H, C, st);
-  return launch_triattn_core_simple(qkvg, tb, mask, mask_si, mask_sk, inf, out, dt, N, H, C, st);
+    return launch_triattn_core_f16_mfma(qkg, vt, tb, mask, mask_si, mask_sk, inf, out, N, ldk, H, C, st);
+  return launch_triattn_core_simple(qkg, vt, tb, mask, mask_si, mask_sk, inf, out, dt, N, ldk, H, C, st);
 }
 
 }  // namespace bzpf

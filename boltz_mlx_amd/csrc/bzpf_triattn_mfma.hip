@@ -1,12 +1,22 @@
 // fp16 flash triangle-attention core on MFMA (v_mfma_f32_16x16x32_f16), head width C = 32.
 //
-// Work unit: one (row i, head h, 64 queries); 4 waves of 16 queries. The logits are formed transposed,
-// S^T = K Q^T (A = a 16-key tile of K from LDS, B = the wave's Q fragment held in registers for the whole row), so
-// that every lane owns one query (l % 16) and 4 keys of each 16-key tile: the softmax statistics of a query live in
-// the 4 lanes l, l^16, l^32, l^48 and need two cross-lane steps per key block. The probabilities P^T are already
-// laid out as the B operand of O^T = V^T P^T (V staged transposed in LDS), so P never leaves registers.
-// Softmax and accumulation are fp32; the logit order follows the reference: (q.k * scale + mask_bias) + tri_bias
-// (boltz_mlx/kernels.py:579-581), so a fully masked row (every logit rounds to -1e9) gives uniform weights.
+// Work unit: one (head h, row i, 128 queries); 4 waves of 32 queries (two 16-query tiles each). The logits are
+// formed transposed, S^T = K Q^T + Cinit (A = a 16-key tile of K from LDS, shared by both query tiles; B = the
+// tile's Q fragment, held in registers for the whole row), so every lane owns one query (l % 16) and 4 keys of each
+// 16-key tile: a query's softmax statistics live in lanes l, l^16, l^32, l^48 and need two cross-lane steps per key
+// block. The MFMA accumulator is initialised with tri_bias - m (plus the key-mask bias in blocks that hold a masked
+// key), so the matrix core adds the bias and subtracts the running maximum. The maximum is raised lazily: only when
+// a block's logits exceed it by more than 2^8 (a wave-uniform branch) are the accumulators rescaled. The
+// probabilities P^T are already laid out as the B operand of O^T = V^T P^T (V^T tiles arrive transposed from the
+// projection), so P never leaves registers, and a third MFMA tile whose A operand is a constant row of ones
+// accumulates the softmax denominator on the matrix cores. The next key block's K, V^T, bias and mask are loaded
+// into registers while the current block computes.
+// Logits are base 2: the projection stores q * log2(e)/sqrt(C) and tri_bias * log2(e); the key-mask bias is
+// inf*(m-1)*log2(e). A row whose keys are all masked gets uniform weights over its N keys, which is what the
+// reference's rounding gives (every logit rounds to -inf*log2(e); boltz_mlx/kernels.py:579-581). Softmax and
+// accumulation are fp32, P is rounded to fp16 for the PV product.
+// Work units are ordered (h, i, query block) and dealt to the 8 XCDs in contiguous ranges, so the blocks of one
+// row share K / V^T in their XCD's L2 and each XCD keeps one head's bias resident.
 // Reference behaviour: boltz_mlx/kernels_nax.py:323-558 (f16 flash core), kernels.py:531-600.
 #include "bzpf_common.h"
 #include "bzpf_kernels.h"
@@ -15,151 +25,221 @@ namespace bzpf {
 
 namespace {
 
-typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+constexpr int NXCD = 8;
 
 template <int C>
-__global__ __launch_bounds__(256) void triattn_core_mfma(const half_t* __restrict__ qkvg,
+__global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __restrict__ qkg, const half_t* __restrict__ vt,
                                                          const half_t* __restrict__ tb,
                                                          const float* __restrict__ mask, int64_t mask_si,
                                                          int64_t mask_sk, float inf, half_t* __restrict__ out,
-                                                         int64_t N, int H) {
+                                                         int N, int ldk, int H, int64_t units, int64_t per_xcd) {
   static_assert(C == 32, "MFMA core is written for head width 32");
-  constexpr int BK = 64;             // keys per LDS stage
-  constexpr int LDK = C + 8;         // Ks row pitch (halves)
-  constexpr int LDV = BK + 8;        // Vt row pitch (halves)
-  __shared__ LDS_ALIGN half_t Ks[BK * LDK];
-  __shared__ LDS_ALIGN half_t Vt[C * LDV];
-  __shared__ float Mb[BK];
-
-  const int64_t NN = N * N;
-  const int64_t i = blockIdx.z;
-  const int h = blockIdx.y;
-  const int64_t j0 = (int64_t)blockIdx.x * 64;
-  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
-  const int g = l >> 4, qi = l & 15;
-  const int64_t jq = j0 + 16 * wave + qi;
-  const bool valid = jq < N;
-  const int64_t jc = valid ? jq : N - 1;
-  const int64_t plane = (int64_t)H * NN * C;  // elements between the q, k, v and g plane groups
-  const int64_t rowbase = ((int64_t)h * NN + i * N) * C;
-  const half_t* qp = qkvg + rowbase;
-  const half_t* kp = qkvg + plane + rowbase;
-  const half_t* vp = qkvg + 2 * plane + rowbase;
-  const half_t* gp = qkvg + 3 * plane + rowbase;
-  const half_t* bp = tb + (int64_t)h * NN + jc * N;  // bias row of this lane's query
-  const float scale = 1.0f / sqrtf((float)C);
+  constexpr int BK = 64;        // keys per LDS stage
+  constexpr int WQ = 128;       // queries per workgroup
+  constexpr int LDK = C + 8;    // Ks row pitch (halves)
+  constexpr int LDV = BK + 8;   // Vs row pitch (halves)
   constexpr float LOG2E = 1.4426950408889634f;
+  constexpr float THRESH = 8.0f;  // lazy rescale threshold (base-2 units)
+  __shared__ LDS_ALIGN half_t Ks[BK * LDK];
+  __shared__ LDS_ALIGN half_t Vs[C * LDV];
+  __shared__ LDS_ALIGN float Mb[BK];
+  constexpr int LDB = BK + 4;   // Bs row pitch (halves)
+  __shared__ LDS_ALIGN half_t Bs[WQ * LDB];
 
-  const half8 qf = *reinterpret_cast<const half8*>(qp + jc * C + g * 8);
-  f4 oacc[2] = {f4{0.f, 0.f, 0.f, 0.f}, f4{0.f, 0.f, 0.f, 0.f}};
-  float m = -INFINITY, lsum = 0.f;
+  const int64_t u = (int64_t)(blockIdx.x % NXCD) * per_xcd + blockIdx.x / NXCD;
+  if (u >= units) return;  // whole workgroup
+  const int nqb = (N + WQ - 1) / WQ;
+  const int qb = (int)(u % nqb);
+  const int64_t hi = u / nqb;
+  const int i = (int)(hi % N);
+  const int h = (int)(hi / N);
 
-  for (int64_t k0 = 0; k0 < N; k0 += BK) {
-    __syncthreads();
-    {
-      const int t = threadIdx.x, key = t >> 2, d8 = (t & 3) * 8;
-      const int64_t kk = k0 + key;
-      U128 kv = U128{{0u, 0u, 0u, 0u}}, vv = U128{{0u, 0u, 0u, 0u}};
-      if (kk < N) {
-        kv = *reinterpret_cast<const U128*>(kp + kk * C + d8);
-        vv = *reinterpret_cast<const U128*>(vp + kk * C + d8);
-      }
-      *reinterpret_cast<U128*>(Ks + key * LDK + d8) = kv;
-      const half_t* vh = reinterpret_cast<const half_t*>(&vv);
+  const int64_t NN = (int64_t)N * N;
+  const int t = threadIdx.x;
+  const int wave = t >> 6, l = t & 63;
+  const int g = l >> 4, qi = l & 15;
+  const half_t* qp = qkg + ((int64_t)h * NN + (int64_t)i * N) * C;
+  const half_t* kp = qkg + ((int64_t)(H + h) * NN + (int64_t)i * N) * C;
+  const half_t* gp = qkg + ((int64_t)(2 * H + h) * NN + (int64_t)i * N) * C;
+  const half_t* vp = vt + ((int64_t)h * N + i) * C * ldk;
+  const float* mrow = mask + (int64_t)i * mask_si;
+
+  // a row with every key masked: uniform weights (all logits equal in the reference's rounding)
+  int any_key = 0;
+  for (int k = t; k < N; k += 256) any_key |= (mrow[(int64_t)k * mask_sk] != 0.0f);
+  const bool row_masked = !__syncthreads_or(any_key);
+
+  int jq[2];
+  half8 qf[2];
+  f4 oacc[2][3];
+  float m[2];
 #pragma unroll
-      for (int u = 0; u < 8; u++) Vt[(d8 + u) * LDV + key] = vh[u];
-      if (t < BK) {
-        const int64_t kt = k0 + t;
-        Mb[t] = kt < N ? inf * (mask[i * mask_si + kt * mask_sk] - 1.0f) : -INFINITY;
-      }
+  for (int tq = 0; tq < 2; tq++) {
+    jq[tq] = qb * WQ + 32 * wave + 16 * tq + qi;
+    const int jc = jq[tq] < N ? jq[tq] : N - 1;
+    qf[tq] = *reinterpret_cast<const half8*>(qp + (int64_t)jc * C + g * 8);
+#pragma unroll
+    for (int dt = 0; dt < 3; dt++) oacc[tq][dt] = f4{0.f, 0.f, 0.f, 0.f};
+    m[tq] = row_masked ? 0.0f : -INFINITY;
+  }
+  const float munset = -0.5f * inf * LOG2E;
+  half8 ones;
+#pragma unroll
+  for (int e = 0; e < 8; e++) ones[e] = (half_t)(qi == 0 ? 1.0f : 0.0f);
+
+  // staging roles: K rows (64 keys x 32 channels) and V^T rows (32 channels x 64 keys), one 16-byte vector each;
+  // the bias tile (128 queries x 64 keys), four 16-byte vectors each
+  const int skey = t >> 2, sd8 = (t & 3) * 8;
+  const int vd = t >> 3, vk8 = (t & 7) * 8;
+  const int brow = t >> 1, bk32 = (t & 1) * 32;
+  const int bq = qb * WQ + brow;
+  const half_t* bsrc = tb + ((int64_t)h * N + (bq < N ? bq : N - 1)) * ldk + bk32;
+  half8 kreg, vreg, breg0, breg1, breg2, breg3;
+  float mbnext = 0.f;
+  auto prefetch = [&](int k0) {
+    int kk = k0 + skey;
+    if (kk >= N) kk = N - 1;
+    kreg = *reinterpret_cast<const half8*>(kp + (int64_t)kk * C + sd8);
+    vreg = *reinterpret_cast<const half8*>(vp + (int64_t)vd * ldk + k0 + vk8);
+    breg0 = *reinterpret_cast<const half8*>(bsrc + k0);
+    breg1 = *reinterpret_cast<const half8*>(bsrc + k0 + 8);
+    breg2 = *reinterpret_cast<const half8*>(bsrc + k0 + 16);
+    breg3 = *reinterpret_cast<const half8*>(bsrc + k0 + 24);
+    if (t < BK) mbnext = k0 + t < N ? inf * (mrow[(int64_t)(k0 + t) * mask_sk] - 1.0f) * LOG2E : -INFINITY;
+  };
+  prefetch(0);
+
+  for (int k0 = 0; k0 < N; k0 += BK) {
+    const bool tail = k0 + BK > N;
+    __syncthreads();  // the previous block's LDS reads are done
+    *reinterpret_cast<half8*>(Ks + skey * LDK + sd8) = kreg;
+    if (tail) {
+#pragma unroll
+      for (int e = 0; e < 8; e++)
+        if (k0 + vk8 + e >= N) vreg[e] = (half_t)0.0f;
     }
-    __syncthreads();
-    // S^T tiles: s[t4][e] = logit(query qi, key 16*t4 + 4g + e)
-    f4 s[4];
+    *reinterpret_cast<half8*>(Vs + vd * LDV + vk8) = vreg;
+    if (t < BK) Mb[t] = mbnext;
+    *reinterpret_cast<half8*>(Bs + brow * LDB + bk32) = breg0;
+    *reinterpret_cast<half8*>(Bs + brow * LDB + bk32 + 8) = breg1;
+    *reinterpret_cast<half8*>(Bs + brow * LDB + bk32 + 16) = breg2;
+    *reinterpret_cast<half8*>(Bs + brow * LDB + bk32 + 24) = breg3;
+    const bool masked = __syncthreads_or(t < BK && mbnext != 0.0f);
+    if (k0 + BK < N) prefetch(k0 + BK);
+
+    half8 kf[4];
 #pragma unroll
-    for (int t4 = 0; t4 < 4; t4++) {
-      const half8 kf = *reinterpret_cast<const half8*>(Ks + (16 * t4 + qi) * LDK + g * 8);
-      s[t4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf, qf, f4{0.f, 0.f, 0.f, 0.f}, 0, 0, 0);
-    }
-    float mloc = -INFINITY;
+    for (int t4 = 0; t4 < 4; t4++) kf[t4] = *reinterpret_cast<const half8*>(Ks + (16 * t4 + qi) * LDK + g * 8);
+    half8 vf[2][2];
 #pragma unroll
-    for (int t4 = 0; t4 < 4; t4++) {
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const int kl = 16 * t4 + 4 * g + e;
-        int64_t kk = k0 + kl;
-        if (kk >= N) kk = N - 1;  // in-bounds read; the key is excluded by Mb = -inf
-        float x = s[t4][e] * scale + Mb[kl];
-        x += (float)bp[kk];
-        s[t4][e] = x;
-        mloc = fmaxf(mloc, x);
-      }
-    }
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-    mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-    const float mn = fmaxf(m, mloc);
-    const float corr = exp2f((m - mn) * LOG2E);
-    lsum *= corr;
-    oacc[0] *= corr;
-    oacc[1] *= corr;
-    half_t p[4][4];
-#pragma unroll
-    for (int t4 = 0; t4 < 4; t4++)
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const float pe = exp2f((s[t4][e] - mn) * LOG2E);
-        lsum += pe;
-        p[t4][e] = (half_t)pe;
-      }
-    m = mn;
-    // O^T += V^T P^T over two 32-key slices
-#pragma unroll
-    for (int s2 = 0; s2 < 2; s2++) {
-      half8 pf;
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        pf[e] = p[2 * s2][e];
-        pf[4 + e] = p[2 * s2 + 1][e];
-      }
+    for (int s2 = 0; s2 < 2; s2++)
 #pragma unroll
       for (int dt = 0; dt < 2; dt++) {
-        const half_t* vr = Vt + (16 * dt + qi) * LDV + 32 * s2 + 4 * g;
+        const half_t* vr = Vs + (16 * dt + qi) * LDV + 32 * s2 + 4 * g;
         const half4 lo = *reinterpret_cast<const half4*>(vr);
-        const half4 hi = *reinterpret_cast<const half4*>(vr + 16);
-        half8 af;
-        af[0] = lo[0]; af[1] = lo[1]; af[2] = lo[2]; af[3] = lo[3];
-        af[4] = hi[0]; af[5] = hi[1]; af[6] = hi[2]; af[7] = hi[3];
-        oacc[dt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, pf, oacc[dt], 0, 0, 0);
+        const half4 hi4 = *reinterpret_cast<const half4*>(vr + 16);
+        vf[s2][dt] = half8{lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+      }
+#pragma unroll
+    for (int tq = 0; tq < 2; tq++) {
+      f4 s[4];
+      const half_t* brd = Bs + (32 * wave + 16 * tq + qi) * LDB + 4 * g;
+      if (row_masked) {
+        // uniform weights over keys < N: logit 0 with m = 0
+#pragma unroll
+        for (int t4 = 0; t4 < 4; t4++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) s[t4][e] = (k0 + 16 * t4 + 4 * g + e < N) ? 0.0f : -INFINITY;
+      } else {
+        // the maximum is "unset" until a key that is not masked has been seen (a masked logit is about
+        // -inf*log2(e)); subtracting such a maximum would cancel catastrophically
+        const bool unset = m[tq] <= munset;
+        const float mref = unset ? 0.0f : m[tq];
+        if (masked) {
+#pragma unroll
+          for (int t4 = 0; t4 < 4; t4++) {
+            const f4 mbv = *reinterpret_cast<const f4*>(Mb + 16 * t4 + 4 * g);
+            f4 c;
+            const half4 bv = *reinterpret_cast<const half4*>(brd + 16 * t4);
+#pragma unroll
+            for (int e = 0; e < 4; e++) c[e] = ((float)bv[e] + mbv[e]) - mref;
+            s[t4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[t4], qf[tq], c, 0, 0, 0);
+          }
+        } else {
+#pragma unroll
+          for (int t4 = 0; t4 < 4; t4++) {
+            f4 c;
+            const half4 bv = *reinterpret_cast<const half4*>(brd + 16 * t4);
+#pragma unroll
+            for (int e = 0; e < 4; e++) c[e] = (float)bv[e] - mref;
+            s[t4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[t4], qf[tq], c, 0, 0, 0);
+          }
+        }
+        float mloc = -INFINITY;
+#pragma unroll
+        for (int t4 = 0; t4 < 4; t4++)
+          mloc = fmaxf(mloc, fmaxf(fmaxf(s[t4][0], s[t4][1]), fmaxf(s[t4][2], s[t4][3])));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
+        // s holds logit - mref; raise the maximum only when the block exceeds it by more than 2^THRESH
+        const bool need = unset || mloc > THRESH;
+        if (__any(need)) {
+          const float mn = fmaxf(m[tq], mloc + mref);
+          const float corr = __builtin_amdgcn_exp2f(m[tq] - mn);
+#pragma unroll
+          for (int dt = 0; dt < 3; dt++) oacc[tq][dt] *= corr;
+          const float delta = mref - mn;
+#pragma unroll
+          for (int t4 = 0; t4 < 4; t4++) s[t4] += delta;
+          m[tq] = mn;
+        }
+      }
+#pragma unroll
+      for (int s2 = 0; s2 < 2; s2++) {
+        half8 pf;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          pf[e] = (half_t)__builtin_amdgcn_exp2f(s[2 * s2][e]);
+          pf[4 + e] = (half_t)__builtin_amdgcn_exp2f(s[2 * s2 + 1][e]);
+        }
+        oacc[tq][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[s2][0], pf, oacc[tq][0], 0, 0, 0);
+        oacc[tq][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[s2][1], pf, oacc[tq][1], 0, 0, 0);
+        oacc[tq][2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf, oacc[tq][2], 0, 0, 0);
       }
     }
   }
-  lsum += __shfl_xor(lsum, 16, 64);
-  lsum += __shfl_xor(lsum, 32, 64);
-  if (!valid) return;
-  const float inv = 1.0f / lsum;
-  // oacc[dt][e] = O^T[dim 16*dt + 4g + e][query qi]
-  const half_t* gq = gp + jq * C;
-  half_t* oq = out + (i * N + jq) * (int64_t)(H * C) + h * C;
+  // oacc[tq][dt][e] = O^T[channel 16*dt + 4g + e][query qi]; the row sum is row 0 of tile 2 (lane qi, e = 0)
 #pragma unroll
-  for (int dt = 0; dt < 2; dt++) {
-    const int d0 = 16 * dt + 4 * g;
-    const half4 gv = *reinterpret_cast<const half4*>(gq + d0);
-    half4 ov;
+  for (int tq = 0; tq < 2; tq++) {
+    const float lsum = __shfl(oacc[tq][2][0], qi, 64);
+    if (jq[tq] >= N) continue;
+    const float inv = 1.0f / lsum;
+    const half_t* gq = gp + (int64_t)jq[tq] * C;
+    half_t* oq = out + ((int64_t)i * N + jq[tq]) * (int64_t)(H * C) + h * C;
 #pragma unroll
-    for (int e = 0; e < 4; e++) ov[e] = (half_t)(oacc[dt][e] * inv * sigmoidf_((float)gv[e]));
-    *reinterpret_cast<half4*>(oq + d0) = ov;
+    for (int dt = 0; dt < 2; dt++) {
+      const int d0 = 16 * dt + 4 * g;
+      const half4 gv = *reinterpret_cast<const half4*>(gq + d0);
+      half4 ov;
+#pragma unroll
+      for (int e = 0; e < 4; e++) ov[e] = (half_t)(oacc[tq][dt][e] * inv * sigmoidf_((float)gv[e]));
+      *reinterpret_cast<half4*>(oq + d0) = ov;
+    }
   }
 }
 
 }  // namespace
 
-hipError_t launch_triattn_core_f16_mfma(const void* qkvg, const void* tb, const float* mask, int64_t mask_si,
-                                        int64_t mask_sk, float inf, void* out, int64_t N, int H, int C,
-                                        hipStream_t st) {
-  if (C != 32) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)((N + 63) / 64), (unsigned)H, (unsigned)N);
-  triattn_core_mfma<32><<<grid, 256, 0, st>>>(static_cast<const half_t*>(qkvg), static_cast<const half_t*>(tb), mask,
-                                              mask_si, mask_sk, inf, static_cast<half_t*>(out), N, H);
+hipError_t launch_triattn_core_f16_mfma(const void* qkg, const void* vt, const void* tb, const float* mask,
+                                        int64_t mask_si, int64_t mask_sk, float inf, void* out, int64_t N,
+                                        int64_t ldk, int H, int C, hipStream_t st) {
+  if (C != 32 || ldk % 64 != 0 || ldk < N || N > 65535) return hipErrorInvalidValue;
+  const int64_t units = (int64_t)H * N * ((N + 127) / 128);
+  const int64_t per_xcd = (units + NXCD - 1) / NXCD;
+  const dim3 grid((unsigned)(per_xcd * NXCD));
+  triattn_core_mfma<32><<<grid, 256, 0, st>>>(static_cast<const half_t*>(qkg), static_cast<const half_t*>(vt),
+                                              static_cast<const half_t*>(tb), mask, mask_si, mask_sk, inf,
+                                              static_cast<half_t*>(out), (int)N, (int)ldk, H, units, per_xcd);
   return hipGetLastError();
 }
 

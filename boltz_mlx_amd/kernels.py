@@ -94,8 +94,8 @@ def _dev(*ts):
             raise ValueError("bzpf kernels need contiguous ROCm device tensors")
 
 
-def trimul_ld(N: int) -> int:
-    return int(_lib.load().bzpf_trimul_ld(N))
+def row_pitch(N: int) -> int:
+    return int(_lib.load().bzpf_row_pitch(N))
 
 
 # ------------------------------------------------------------------------------------------------ weight caches
@@ -162,7 +162,7 @@ def trimul_proj(xn, w_pg, mask, scale: float, incoming: bool, N: int) -> torch.T
     D = xn.shape[-1]
     if w_pg.shape != (4 * D, D) or w_pg.dtype != xn.dtype or xn.numel() != N * N * D:
         raise ValueError("trimul_proj: shape/dtype mismatch")
-    ld = trimul_ld(N)
+    ld = row_pitch(N)
     ab = torch.empty((2 * D, N, ld), dtype=xn.dtype, device=xn.device)
     call("bzpf_trimul_proj", _p(xn), _p(w_pg), _p(mask), float(scale), int(incoming), _p(ab), _dt(xn), N, ld, D,
          _stream())
@@ -172,7 +172,7 @@ def trimul_proj(xn, w_pg, mask, scale: float, incoming: bool, N: int) -> torch.T
 def trimul_contract(ab: torch.Tensor, N: int) -> torch.Tensor:
     _dev(ab)
     D = ab.shape[0] // 2
-    ld = trimul_ld(N)
+    ld = row_pitch(N)
     if ab.shape != (2 * D, N, ld):
         raise ValueError("trimul_contract: ab must be [2D, N, ld]")
     o = torch.empty((D, N, ld), dtype=ab.dtype, device=ab.device)
@@ -184,7 +184,7 @@ def trimul_tail(o, norm_out, eps_out: float, w_po, xn, w_go, z, accumulate: bool
     """z (+)= p_out(LN_out(o)) * sigmoid(g_out(xn)); returns next_ln(z) in the storage dtype when next_ln is given."""
     _dev(o, w_po, xn, w_go, z)
     D = o.shape[0]
-    ld = trimul_ld(N)
+    ld = row_pitch(N)
     if z.dtype != torch.float32 or z.numel() != N * N * D or o.shape != (D, N, ld):
         raise ValueError("trimul_tail: shape/dtype mismatch")
     nxt = nw = nb = None
@@ -198,29 +198,40 @@ def trimul_tail(o, norm_out, eps_out: float, w_po, xn, w_go, z, accumulate: bool
     return nxt
 
 
+LOG2E = 1.4426950408889634
+
+
 def triattn_proj(xn, w, trans: bool, N: int, H: int, C: int):
+    """-> (qkg [3H, N*N, C], vt [H, N, C, ldk], tb [H, N, ldk]) in xn's dtype, q scaled by log2(e)/sqrt(C) and the
+    bias by log2(e) (the base-2 logits the core expects)."""
     _dev(xn, w)
     D = xn.shape[-1]
     if w.shape != (4 * H * C + H, D) or w.dtype != xn.dtype or xn.numel() != N * N * D:
         raise ValueError("triattn_proj: shape/dtype mismatch")
-    qkvg = torch.empty((4 * H, N * N, C), dtype=xn.dtype, device=xn.device)
-    tb = torch.empty((H, N * N), dtype=xn.dtype, device=xn.device)
-    call("bzpf_triattn_proj", _p(xn), _p(w), int(trans), _p(qkvg), _p(tb), _dt(xn), N, D, H, C, _stream())
-    return qkvg, tb
+    ldk = row_pitch(N)
+    qkg = torch.empty((3 * H, N * N, C), dtype=xn.dtype, device=xn.device)
+    vt = torch.empty((H, N, C, ldk), dtype=xn.dtype, device=xn.device)
+    tb = torch.empty((H, N, ldk), dtype=xn.dtype, device=xn.device)
+    call("bzpf_triattn_proj", _p(xn), _p(w), int(trans), LOG2E / C ** 0.5, LOG2E, _p(qkg), _p(vt), _p(tb), _dt(xn),
+         N, ldk, D, H, C, _stream())
+    return qkg, vt, tb
 
 
 TRIATT_IMPL = {"auto": 0, "scalar": 1, "mma": 2}[os.environ.get("BOLTZ_MLX_TRIATT_IMPL", "auto")]
 
 
-def triattn_core(qkvg, tb, mask, trans: bool, inf: float, N: int, H: int, C: int, impl: int | None = None):
+def triattn_core(qkg, vt, tb, mask, trans: bool, inf: float, N: int, H: int, C: int, impl: int | None = None):
     """mask: the pair mask [N, N] fp32 in the natural orientation; the ending node (trans) reads it transposed.
     impl: 0 auto, 1 VALU kernel, 2 MFMA kernel (default from BOLTZ_MLX_TRIATT_IMPL = auto | scalar | mma)."""
-    _dev(qkvg, tb, mask)
+    _dev(qkg, vt, tb, mask)
     if mask.dtype != torch.float32 or mask.numel() != N * N:
         raise ValueError("triattn_core: mask must be fp32 [N, N]")
-    out = torch.empty((N * N, H * C), dtype=qkvg.dtype, device=qkvg.device)
+    ldk = row_pitch(N)
+    if qkg.shape != (3 * H, N * N, C) or vt.shape != (H, N, C, ldk) or tb.shape != (H, N, ldk):
+        raise ValueError("triattn_core: buffers must come from triattn_proj")
+    out = torch.empty((N * N, H * C), dtype=qkg.dtype, device=qkg.device)
     si, sk = (1, N) if trans else (N, 1)
-    call("bzpf_triattn_core", _p(qkvg), _p(tb), _p(mask), si, sk, float(inf), _p(out), _dt(qkvg), N, H, C,
+    call("bzpf_triattn_core", _p(qkg), _p(vt), _p(tb), _p(mask), si, sk, float(inf), _p(out), _dt(qkg), N, ldk, H, C,
          TRIATT_IMPL if impl is None else int(impl), _stream())
     return out
 

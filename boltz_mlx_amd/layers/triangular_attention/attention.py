@@ -59,9 +59,9 @@ class TriangleAttention(torch.nn.Module):
         w = K.wcache(self, "w_qkvgb", mha.linear_q.weight, mha.linear_k.weight, mha.linear_v.weight,
                      mha.linear_g.weight, self.linear.weight)
         trans = not self.starting
-        qkvg, tb = K.triattn_proj(xn, w, trans, N, H, C)
-        core = K.triattn_core(qkvg, tb, mask, trans, self.inf, N, H, C)
-        del qkvg, tb
+        qkg, vt, tb = K.triattn_proj(xn, w, trans, N, H, C)
+        core = K.triattn_core(qkg, vt, tb, mask, trans, self.inf, N, H, C)
+        del qkg, vt, tb
         return K.linear_resid_ln(core, K.wcache(self, "w_o", mha.linear_o.weight), trans, z, accumulate, next_ln, N)
 
 

@@ -35,8 +35,9 @@ const char* bzpf_version(void);
 /* Message of the last failing call on this host thread ("" when none). */
 const char* bzpf_last_error(void);
 
-/* Row pitch (elements) of the channel-major triangle-multiplication buffers: N rounded up to 64. */
-int64_t bzpf_trimul_ld(int64_t N);
+/* Row pitch (elements) of the padded pair buffers (triangle-multiplication a|b and o, triangle-attention V^T and
+ * bias): N rounded up to 64. */
+int64_t bzpf_row_pitch(int64_t N);
 
 /* Row LayerNorm over D channels (D % 64 == 0, D <= 1024): two-pass fp32 statistics, (x-mean)*rsqrt(var+eps)*w+b;
  * w / b may be NULL. Replaces kernels.layer_norm (boltz_mlx/kernels.py:482-507) and LayerNorm.__call__/.f16
@@ -53,7 +54,7 @@ int bzpf_add_ln(float* z, const void* y, int y_dt, float y_scale, int trans_y, c
 /* Triangle-multiplication projection: for c < 2D and the position (i, k) (incoming: (k, i)),
  *   ab[c][i][k] = (xn.W[c]) * sigmoid(xn.W[2D + c]) * pair_mask * scale,  k < N;   ab[c][i][k] = 0 for N <= k < ld.
  * xn [N*N, D] (dt), W = [p_in.weight; g_in.weight] [4D, D] (dt), pair_mask [N, N] fp32, ab [2D][N][ld] (dt),
- * ld = bzpf_trimul_ld(N). scale = 1 in fp32 mode, 2^-K in fp16 mode. Replaces the projection of
+ * ld = bzpf_row_pitch(N). scale = 1 in fp32 mode, 2^-K in fp16 mode. Replaces the projection of
  * TriangleMultiplication._fast_b1 / _f16_contract (boltz_mlx/layers/triangular_mult.py:67-88, 143-170) and
  * kernels_nax2.trimul_proj_nax (boltz_mlx/kernels_nax2.py:202-304). */
 int bzpf_trimul_proj(const void* xn, const void* w_pg, const float* pair_mask, float scale, int incoming, void* ab,
@@ -75,22 +76,29 @@ int bzpf_trimul_tail(const void* o, const float* norm_out_w, const float* norm_o
                      int64_t ld, int D, void* stream);
 
 /* Triangle-attention projection of the LayerNorm output xn [N*N, D] with W = [linear_q; linear_k; linear_v;
- * linear_g; linear] ([4*H*C + H, D]) at the position (i, j) (trans: (j, i), the ending node):
- *   qkvg[(s*H + h)][p][c] for s in {q, k, v, g} ([4H][N*N][C]) and tri_bias[h][p] ([H][N*N]).
- * Replaces the fused projection of TriangleAttention (boltz_mlx/layers/triangular_attention/attention.py:49-69,
- * 100-104) and kernels_nax3.pair_proj16 (boltz_mlx/kernels_nax3.py:538-700). */
-int bzpf_triattn_proj(const void* xn, const void* w, int trans, void* qkvg, void* tri_bias, int dt, int64_t N, int D,
-                      int H, int C, void* stream);
+ * linear_g; linear] ([4*H*C + H, D]) at the position p = i*N + j (trans: xn is read at (j, i), the ending node):
+ *   qkg [3H][N*N][C]: q * q_scale (planes 0..H-1), k (H..2H-1), g (2H..3H-1);
+ *   vt [H][N][C][ldk]: v transposed per row i (vt[h][i][c][j] = v at (i, j)); columns j >= N are not written;
+ *   tri_bias [H][N][ldk]: tri_bias[h][j][k] = bias_scale * (linear at (j, k)); columns k >= N are set to 0.
+ * ldk = bzpf_row_pitch(N). bzpf_triattn_core expects q_scale = log2(e)/sqrt(C) and bias_scale = log2(e) (logits
+ * in base 2). Replaces the fused projection of TriangleAttention
+ * (boltz_mlx/layers/triangular_attention/attention.py:49-69, 100-104) and kernels_nax3.pair_proj16
+ * (boltz_mlx/kernels_nax3.py:538-700). */
+int bzpf_triattn_proj(const void* xn, const void* w, int trans, float q_scale, float bias_scale, void* qkg, void* vt,
+                      void* tri_bias, int dt, int64_t N, int64_t ldk, int D, int H, int C, void* stream);
 
-/* Flash triangle-attention core: for row i, head h, query j,
- *   out[i][j][h*C + c] = sigmoid(g) * sum_k softmax_k((q/sqrt(C)).k + inf*(mask[i*mask_si + k*mask_sk] - 1)
- *                                                     + tri_bias[h][j*N + k]) v[k][c]
- * (fp32 softmax). out [N*N, H*C] (dt). impl selects the kernel like the reference's impl argument: 0 = auto (MFMA
- * for fp16 with C = 32, else VALU), 1 = the VALU kernel, 2 = the MFMA kernel (fp16, C = 32).
- * Replaces kernels.tri_attention_fused (boltz_mlx/kernels.py:531-945, impl "scalar" / "mma") and
- * kernels_nax.tri_attention_nax (boltz_mlx/kernels_nax.py:323-558). */
-int bzpf_triattn_core(const void* qkvg, const void* tri_bias, const float* mask, int64_t mask_si, int64_t mask_sk,
-                      float inf, void* out, int dt, int64_t N, int H, int C, int impl, void* stream);
+/* Flash triangle-attention core over the projection's buffers: for row i, head h, query j,
+ *   out[i][j][h*C + c] = sigmoid(g) * sum_k softmax2_k(q.k + inf*(mask[i*mask_si + k*mask_sk] - 1)*log2(e)
+ *                                                      + tri_bias[h][j][k]) v[k][c]
+ * with softmax2 the base-2 softmax (2^x normalised; equal to the reference's softmax of the natural-log logits
+ * (q/sqrt(C)).k + inf*(mask-1) + linear, summed in that order). fp32 softmax and accumulation; out [N*N, H*C] (dt).
+ * impl selects the kernel like the reference's impl argument: 0 = auto (MFMA for fp16 with C = 32, else VALU),
+ * 1 = the VALU kernel, 2 = the MFMA kernel (fp16, C = 32). Replaces kernels.tri_attention_fused
+ * (boltz_mlx/kernels.py:531-945, impl "scalar" / "mma") and kernels_nax.tri_attention_nax
+ * (boltz_mlx/kernels_nax.py:323-558). */
+int bzpf_triattn_core(const void* qkg, const void* vt, const void* tri_bias, const float* mask, int64_t mask_si,
+                      int64_t mask_sk, float inf, void* out, int dt, int64_t N, int64_t ldk, int H, int C, int impl,
+                      void* stream);
 
 /* Output projection + residual + next LayerNorm: y = x[p] . W^T (x [N*N, D], W [D, D]) added to z at the position
  * p (trans: the transposed position, the ending node), then xn_next = LN_next(z) at that position when

@@ -41,11 +41,11 @@ def test_library_host_only_calls():
 
     lib = _lib.load()
     assert lib.bzpf_version().decode().startswith("bzpf")
-    assert lib.bzpf_trimul_ld(1) == 64 and lib.bzpf_trimul_ld(64) == 64 and lib.bzpf_trimul_ld(65) == 128
+    assert lib.bzpf_row_pitch(1) == 64 and lib.bzpf_row_pitch(64) == 64 and lib.bzpf_row_pitch(65) == 128
     # argument validation happens on the host, before any launch
     rc = lib.bzpf_trimul_proj(None, None, None, 1.0, 0, None, 0, 10, 64, 128, None)
     assert rc == -1 and b"xn" in lib.bzpf_last_error()
-    rc = lib.bzpf_triattn_proj(None, None, 0, None, None, 0, 10, 128, 4, 32, None)
+    rc = lib.bzpf_triattn_proj(None, None, 0, 1.0, 1.0, None, None, None, 0, 10, 64, 128, 4, 32, None)
     assert rc == -1
 
 

@@ -130,7 +130,7 @@ def test_trimul_contract_raw(N, dt):
     from boltz_mlx_amd import kernels as K
 
     D = 8
-    ld = K.trimul_ld(N)
+    ld = K.row_pitch(N)
     rng = np.random.default_rng(N)
     ab = np.zeros((2 * D, N, ld))
     ab[:, :, :N] = rng.integers(-3, 4, size=(2 * D, N, N))  # small integers: exact in fp16 with fp32 accumulation
@@ -262,16 +262,24 @@ def test_triattn_core_mfma_vs_valu(N, trans):
 
     H, C = 4, 32
     rng = np.random.default_rng(N)
-    qkvg = dev(rng.standard_normal((4 * H, N * N, C)), torch.float16)
-    tb = dev(rng.standard_normal((H, N * N)), torch.float16)
+    ldk = K.row_pitch(N)
+    qkg = dev(rng.standard_normal((3 * H, N * N, C)), torch.float16)
+    vt = dev(rng.standard_normal((H, N, C, ldk)), torch.float16)
+    tb = dev(2 * rng.standard_normal((H, N, ldk)), torch.float16)
+    # V^T padding is never written by the projection: NaN there proves it is never used; the bias padding is 0, as
+    # the projection writes it
+    vt[..., N:] = float("nan")
+    tb[..., N:] = 0.0
     mask = np.ones((N, N), np.float32)
     if N > 4:
         mask[:, -2:] = 0
         mask[3, :] = 0
         mask[1, 2] = 0
+    if N > 100:
+        mask[5, :70] = 0  # a whole leading key block masked: the running maximum starts from masked logits
     mg = dev(mask)
-    fast = K.triattn_core(qkvg, tb, mg, trans, 1e9, N, H, C, impl=2).float().cpu().numpy()
-    slow = K.triattn_core(qkvg, tb, mg, trans, 1e9, N, H, C, impl=1).float().cpu().numpy()
+    fast = K.triattn_core(qkg, vt, tb, mg, trans, 1e9, N, H, C, impl=2).float().cpu().numpy()
+    slow = K.triattn_core(qkg, vt, tb, mg, trans, 1e9, N, H, C, impl=1).float().cpu().numpy()
     m = O.metrics(fast, slow)
     print(f"core mfma vs valu N={N} trans={trans}: {m}", flush=True)
     assert m["finite"] and m["max_rel"] <= 5e-3 and m["rel_fro"] <= 2e-3, m

@@ -1,5 +1,5 @@
-// Shared device helpers for the bzpf gfx950 kernels: storage types, MFMA fragment traits, LDS tile copies,
-// wave reductions and the residual + LayerNorm epilogue used by every pair-track kernel that updates z.
+// Shared device helpers for the bzpf gfx950 kernels: storage types, MFMA fragment traits, LDS tile copies and wave
+// reductions.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -84,6 +84,7 @@ __device__ __forceinline__ void zero_acc(f4 (&acc)[MB][NB]) {
 // 16-byte vector of T.
 template <typename T> struct Vec16 { static constexpr int n = 16 / sizeof(T); };
 struct alignas(16) U128 { uint32_t w[4]; };
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 
 // Copy `rows` rows of K elements (K % Vec16 == 0) from global into LDS [rows][ld]. src_row(r) gives the global
 // row pointer; rows >= valid are zero-filled when zero_invalid, else read from src_row as given.
@@ -94,10 +95,9 @@ __device__ __forceinline__ void load_rows(T* dst, int ld, int rows, int K, RowFn
   for (int e = threadIdx.x; e < rows * per_row; e += blockDim.x) {
     const int r = e / per_row, c = (e - r * per_row) * VE;
     const T* s = src_row(r);
-    U128 v;
-    if (s) v = *reinterpret_cast<const U128*>(s + c);
-    else v = U128{{0u, 0u, 0u, 0u}};
-    *reinterpret_cast<U128*>(dst + r * ld + c) = v;
+    u32x4_t v = u32x4_t{0u, 0u, 0u, 0u};
+    if (s) v = *reinterpret_cast<const u32x4_t*>(s + c);
+    *reinterpret_cast<u32x4_t*>(dst + r * ld + c) = v;
   }
 }
 
@@ -113,44 +113,6 @@ __device__ __forceinline__ float group_max(float v) {
 #pragma unroll
   for (int o = G / 2; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
   return v;
-}
-
-// Residual + LayerNorm epilogue over a tile of up to 64 rows of D=128 fp32 updates held in LDS (Ys[r][ldy]).
-// Row r updates z row zrow(r) (skipped when < 0): z = (accumulate ? z : 0) + y; when lnw != nullptr also writes
-// LN(z) (eps, affine lnw/lnb) to xn_next row zrow(r). 4 threads per row, 32 channels each (two-pass statistics).
-template <typename TO, typename RowFn>
-__device__ __forceinline__ void resid_ln_epilogue(const float* Ys, int ldy, int rows, RowFn zrow, float* z,
-                                                  int accumulate, const float* lnw, const float* lnb, float eps,
-                                                  TO* xn_next) {
-  constexpr int D = 128;
-  const int t = threadIdx.x;
-  const int r = t >> 2, q = t & 3;
-  if (r >= rows) return;  // rows <= 64 and blockDim == 256: whole 4-lane groups exit together
-  const int64_t zr = zrow(r);
-  if (zr < 0) return;
-  float v[32];
-  float* zp = z + zr * D + q * 32;
-  const float* yp = Ys + r * ldy + q * 32;
-#pragma unroll
-  for (int c = 0; c < 32; c += 4) {
-    f4 y = *reinterpret_cast<const f4*>(yp + c);
-    f4 zz = accumulate ? *reinterpret_cast<const f4*>(zp + c) : f4{0.f, 0.f, 0.f, 0.f};
-    zz += y;
-    *reinterpret_cast<f4*>(zp + c) = zz;
-    v[c] = zz[0]; v[c + 1] = zz[1]; v[c + 2] = zz[2]; v[c + 3] = zz[3];
-  }
-  if (lnw == nullptr) return;
-  float s = 0.f;
-#pragma unroll
-  for (int c = 0; c < 32; c++) s += v[c];
-  const float mean = group_sum<4>(s) * (1.0f / D);
-  float ss = 0.f;
-#pragma unroll
-  for (int c = 0; c < 32; c++) { const float d = v[c] - mean; ss += d * d; }
-  const float rstd = 1.0f / sqrtf(group_sum<4>(ss) * (1.0f / D) + eps);
-  TO* op = xn_next + zr * D + q * 32;
-#pragma unroll
-  for (int c = 0; c < 32; c++) op[c] = from_f<TO>((v[c] - mean) * rstd * lnw[q * 32 + c] + lnb[q * 32 + c]);
 }
 
 }  // namespace bzpf

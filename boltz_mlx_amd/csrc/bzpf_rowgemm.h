@@ -1,0 +1,154 @@
+// Transposed row-tile GEMM building blocks for the pair kernels (K = 128 input channels per row).
+//
+// The kernels compute Y^T = W X^T on MFMA: A = a 16-row block of the weight W (output channels, K-contiguous, staged
+// in LDS), B = X^T for 16 rows of X (positions, K-contiguous, loaded once per tile straight from global memory into
+// registers). The accumulator then holds, per lane l, row l % 16 of X and the 4 consecutive output channels
+// 16*cb + 4*(l/16) + e, e = 0..3: every row lives in 4 lanes (l, l^16, l^32, l^48), so row-wise epilogues (residual
+// add, LayerNorm) need two cross-lane steps, and each lane writes 4 contiguous outputs.
+// K is split in lane-group blocks: MFMA step s of lane group g = l/16 takes k = 32*g + s*KP + t (t < KP), which is a
+// permutation of the sum over k shared by A and B, so a lane reads 32 contiguous channels of its row.
+#pragma once
+
+#include "bzpf_common.h"
+
+namespace bzpf {
+
+template <typename T> struct RG;
+template <> struct RG<half_t> {
+  static constexpr int STEPS = 4;  // MFMA steps over K = 128
+  typedef half8 frag;
+  __device__ static __forceinline__ void load_row(frag (&f)[STEPS], const half_t* p, int g) {
+#pragma unroll
+    for (int s = 0; s < STEPS; s++) f[s] = *reinterpret_cast<const half8*>(p + 32 * g + 8 * s);
+  }
+  __device__ static __forceinline__ void zero(frag (&f)[STEPS]) {
+#pragma unroll
+    for (int s = 0; s < STEPS; s++)
+#pragma unroll
+      for (int t = 0; t < 8; t++) f[s][t] = (half_t)0.0f;
+  }
+};
+template <> struct RG<float> {
+  static constexpr int STEPS = 32;
+  typedef float frag;
+  __device__ static __forceinline__ void load_row(frag (&f)[STEPS], const float* p, int g) {
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+      const f4 v = *reinterpret_cast<const f4*>(p + 32 * g + 4 * j);
+      f[4 * j] = v[0]; f[4 * j + 1] = v[1]; f[4 * j + 2] = v[2]; f[4 * j + 3] = v[3];
+    }
+  }
+  __device__ static __forceinline__ void zero(frag (&f)[STEPS]) {
+#pragma unroll
+    for (int s = 0; s < STEPS; s++) f[s] = 0.0f;
+  }
+};
+
+// Row blocks per wave: fp16 tiles are 128 rows per workgroup (2 blocks per wave), fp32 tiles 64 rows.
+template <typename T> struct RowBlocks { static constexpr int v = sizeof(T) == 2 ? 2 : 1; };
+
+// acc[rb][cb] += W[16 cb .. +15][0:128] . X[rb]^T for CB column blocks of the LDS weight chunk Ws (pitch ldw).
+template <typename T, int RB, int CB>
+__device__ __forceinline__ void mma_rows(f4 (&acc)[RB][CB], const typename RG<T>::frag (&x)[RB][RG<T>::STEPS],
+                                         const T* Ws, int ldw) {
+  const int l = threadIdx.x & 63, g = l >> 4;
+#pragma unroll
+  for (int cb = 0; cb < CB; cb++) {
+    const T* wp = Ws + (16 * cb + (l & 15)) * ldw + 32 * g;
+    if constexpr (sizeof(T) == 2) {
+#pragma unroll
+      for (int s = 0; s < 4; s++) {
+        const half8 a = *reinterpret_cast<const half8*>(wp + 8 * s);
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++)
+          acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, x[rb][s], acc[rb][cb], 0, 0, 0);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 8; j++) {
+        const f4 a = *reinterpret_cast<const f4*>(wp + 4 * j);
+#pragma unroll
+        for (int t = 0; t < 4; t++)
+#pragma unroll
+          for (int rb = 0; rb < RB; rb++)
+            acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t], x[rb][4 * j + t], acc[rb][cb], 0, 0, 0);
+      }
+    }
+  }
+}
+
+// Copy `rows` rows of `k` elements (k % (16 / sizeof(T)) == 0) into LDS [rows][ld]; row r comes from src(r)
+// (nullptr: zeros).
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+template <typename T, typename RowFn>
+__device__ __forceinline__ void lds_rows(T* dst, int ld, int rows, int k, RowFn src) {
+  constexpr int VE = 16 / sizeof(T);
+  const int per = k / VE;
+  for (int e = threadIdx.x; e < rows * per; e += blockDim.x) {
+    const int r = e / per, c = (e - r * per) * VE;
+    const T* s = src(r);
+    u32x4 v = u32x4{0u, 0u, 0u, 0u};
+    if (s) v = *reinterpret_cast<const u32x4*>(s + c);
+    *reinterpret_cast<u32x4*>(dst + r * ld + c) = v;
+  }
+}
+
+// 4 consecutive elements of T from / to memory as fp32.
+__device__ __forceinline__ f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
+__device__ __forceinline__ f4 ld4(const half_t* p) {
+  const half4 h = *reinterpret_cast<const half4*>(p);
+  return f4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+}
+__device__ __forceinline__ void st4(float* p, f4 v) { *reinterpret_cast<f4*>(p) = v; }
+__device__ __forceinline__ void st4(half_t* p, f4 v) {
+  *reinterpret_cast<half4*>(p) = half4{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
+}
+
+// Residual + LayerNorm epilogue on the transposed accumulator of 8 column blocks (D = 128 channels): for each of the
+// lane's rows, z[zr] = (accumulate ? z[zr] : 0) + y, then xn_next[zr] = LN(z[zr]) when lnw != nullptr. zrow(rb)
+// returns the z row of the lane's row in block rb (< 0: no row; the lane still joins the cross-lane reductions).
+template <typename TO, int RB, typename ZRow>
+__device__ __forceinline__ void resid_ln_rows(const f4 (&y)[RB][8], ZRow zrow, float* __restrict__ z, int accumulate,
+                                              const float* __restrict__ lnw, const float* __restrict__ lnb, float eps,
+                                              TO* __restrict__ xn_next) {
+  constexpr int D = 128;
+  const int l = threadIdx.x & 63, g = l >> 4;
+#pragma unroll
+  for (int rb = 0; rb < RB; rb++) {
+    const int64_t zr = zrow(rb);
+    f4 v[8];
+    float s = 0.f;
+#pragma unroll
+    for (int cb = 0; cb < 8; cb++) {
+      const int c = 16 * cb + 4 * g;
+      v[cb] = y[rb][cb];
+      if (zr >= 0) {
+        if (accumulate) v[cb] += ld4(z + zr * D + c);
+        st4(z + zr * D + c, v[cb]);
+      }
+      s += v[cb][0] + v[cb][1] + v[cb][2] + v[cb][3];
+    }
+    if (lnw == nullptr) continue;
+    s += __shfl_xor(s, 16, 64);
+    s += __shfl_xor(s, 32, 64);
+    const float mean = s * (1.0f / D);
+    float ss = 0.f;
+#pragma unroll
+    for (int cb = 0; cb < 8; cb++) {
+      const f4 d = v[cb] - mean;
+      ss += d[0] * d[0] + d[1] * d[1] + d[2] * d[2] + d[3] * d[3];
+    }
+    ss += __shfl_xor(ss, 16, 64);
+    ss += __shfl_xor(ss, 32, 64);
+    const float rstd = 1.0f / sqrtf(ss * (1.0f / D) + eps);
+    if (zr < 0) continue;
+#pragma unroll
+    for (int cb = 0; cb < 8; cb++) {
+      const int c = 16 * cb + 4 * g;
+      st4(xn_next + zr * D + c, (v[cb] - mean) * rstd * ld4(lnw + c) + ld4(lnb + c));
+    }
+  }
+}
+
+}  // namespace bzpf

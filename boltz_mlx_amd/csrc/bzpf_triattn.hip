@@ -80,106 +80,109 @@ __global__ __launch_bounds__(64) void triattn_core_valu(const T* __restrict__ qk
 }
 
 // ---------------------------------------------------------------- sequence attention (s track, VALU kernel)
-// One thread per query j; a 64-thread workgroup owns (head h, 64 queries). Keys are staged TK at a time in LDS
-// (K, V and the [64 x TK] bias tile, all loaded coalesced). order 0: s = (q*scale).k, s += inf*(m-1), s += bias;
-// order 1 (AttentionPairBias, attentionv2.py:76-81): s = (q.k)*scale + bias, s += (1-m)*(-inf). Element (row i, position j, head h, channel d) of q/k/v/g is at
-// base + i*s_row + j*s_pos + h*s_head + d; the output uses o_row/o_pos/o_head.
-struct AttnArgs {
-  const void *q, *k, *v, *g, *bias;
-  const float* mask;
-  void* out;
-  int64_t s_row, s_pos, s_head;
-  int64_t o_row, o_pos, o_head;
-  int64_t b_head;        // bias head stride (bias[h*b_head + j*J + k])
-  int64_t m_row, m_key;  // mask strides
-  float inf, scale;
-  int64_t J;
-  int order;
-};
-
+// AttentionPairBias core (attentionv2.py:76-83): for head h and query j,
+//   out[j][h*hd + d] = sigmoid(g[j][h*hd + d]) * sum_k softmax_k(q.k * scale + bias[h][j][k] + (1 - mask[k]) * -inf) v
+// A 256-thread workgroup owns (head h, 16 queries); the 16 threads of a query split the keys (key = 16 * t + lane)
+// with an online softmax each, and merge their (max, sum, accumulator) states with shuffles at the end. K, V and
+// the [16 x 64] bias tile are staged 64 keys at a time in LDS.
 template <typename T, int HD>
-__global__ __launch_bounds__(64) void attn_simple_kernel(AttnArgs a) {
-  constexpr int TK = 32;
+__global__ __launch_bounds__(256) void seq_attn_kernel(const T* __restrict__ q, const T* __restrict__ k,
+                                                       const T* __restrict__ v, const T* __restrict__ g,
+                                                       int64_t ld_in, const T* __restrict__ bias,
+                                                       const float* __restrict__ mask, float inf,
+                                                       T* __restrict__ out, int64_t ld_out, int64_t N, float scale) {
+  constexpr int TK = 64;
   __shared__ float Ks[TK][HD + 1];
   __shared__ float Vs[TK][HD + 1];
-  __shared__ float Bs[64][TK + 1];
+  __shared__ float Bs[16][TK + 1];
   __shared__ float Mk[TK];
-  const int64_t J = a.J;
-  const int t = threadIdx.x;
-  const int64_t j = (int64_t)blockIdx.x * 64 + t;
-  const int64_t h = blockIdx.y, i = blockIdx.z;
-  const bool valid = j < J;
-  const T* qb = static_cast<const T*>(a.q) + i * a.s_row + h * a.s_head;
-  const T* kb = static_cast<const T*>(a.k) + i * a.s_row + h * a.s_head;
-  const T* vb = static_cast<const T*>(a.v) + i * a.s_row + h * a.s_head;
-  const T* bb = static_cast<const T*>(a.bias) + h * a.b_head;
-  float q[HD], acc[HD];
+  const int t = threadIdx.x, qi = t >> 4, kl = t & 15;
+  const int h = blockIdx.y;
+  const int64_t j0 = (int64_t)blockIdx.x * 16, j = j0 + qi;
+  const bool valid = j < N;
+  const int64_t jc = valid ? j : N - 1;
+  float qv[HD], acc[HD];
 #pragma unroll
   for (int d = 0; d < HD; d++) {
-    const float qv = valid ? to_f(qb[j * a.s_pos + d]) : 0.f;
-    q[d] = a.order == 0 ? qv * a.scale : qv;
+    qv[d] = to_f(q[jc * ld_in + h * HD + d]);
     acc[d] = 0.f;
   }
   float m = -INFINITY, lsum = 0.f;
-  const int64_t j0 = (int64_t)blockIdx.x * 64;
-  for (int64_t k0 = 0; k0 < J; k0 += TK) {
+  const T* bh = bias + (int64_t)h * N * N;
+  for (int64_t k0 = 0; k0 < N; k0 += TK) {
     __syncthreads();
-    for (int e = t; e < TK * HD; e += 64) {
+    for (int e = t; e < TK * HD; e += 256) {
       const int kk = e / HD, d = e - kk * HD;
-      const int64_t key = k0 + kk;
-      Ks[kk][d] = key < J ? to_f(kb[key * a.s_pos + d]) : 0.f;
-      Vs[kk][d] = key < J ? to_f(vb[key * a.s_pos + d]) : 0.f;
+      const bool in = k0 + kk < N;
+      Ks[kk][d] = in ? to_f(k[(k0 + kk) * ld_in + h * HD + d]) : 0.f;
+      Vs[kk][d] = in ? to_f(v[(k0 + kk) * ld_in + h * HD + d]) : 0.f;
     }
-    for (int e = t; e < 64 * TK; e += 64) {
+    for (int e = t; e < 16 * TK; e += 256) {
       const int qq = e / TK, kk = e - qq * TK;
-      const int64_t jq = j0 + qq, key = k0 + kk;
-      Bs[qq][kk] = (jq < J && key < J) ? to_f(bb[jq * J + key]) : 0.f;
+      Bs[qq][kk] = (j0 + qq < N && k0 + kk < N) ? to_f(bh[(j0 + qq) * N + k0 + kk]) : 0.f;
     }
-    if (t < TK) {
-      const int64_t key = k0 + t;
-      Mk[t] = key < J ? a.mask[i * a.m_row + key * a.m_key] : 0.f;
-    }
+    if (t < TK) Mk[t] = k0 + t < N ? mask[k0 + t] : 0.f;
     __syncthreads();
-    const int kend = (int)((J - k0) < TK ? (J - k0) : TK);
-    for (int kk = 0; kk < kend; kk++) {
-      float s = 0.f;
 #pragma unroll
-      for (int d = 0; d < HD; d++) s += q[d] * Ks[kk][d];
-      if (a.order == 0) {
-        s += a.inf * (Mk[kk] - 1.0f);
-        s += Bs[t][kk];
-      } else {
-        s = s * a.scale + Bs[t][kk];
-        s += (1.0f - Mk[kk]) * (-a.inf);
-      }
-      const float mn = fmaxf(m, s);
+    for (int u = 0; u < TK / 16; u++) {
+      const int kk = 16 * u + kl;
+      if (k0 + kk >= N) break;
+      float sc = 0.f;
+#pragma unroll
+      for (int d = 0; d < HD; d++) sc += qv[d] * Ks[kk][d];
+      sc = sc * scale + Bs[qi][kk];
+      sc += (1.0f - Mk[kk]) * (-inf);
+      const float mn = fmaxf(m, sc);
       const float corr = __expf(m - mn);
-      const float p = __expf(s - mn);
+      const float p = __expf(sc - mn);
       lsum = lsum * corr + p;
 #pragma unroll
       for (int d = 0; d < HD; d++) acc[d] = acc[d] * corr + p * Vs[kk][d];
       m = mn;
     }
   }
-  if (!valid) return;
-  const float inv = 1.0f / lsum;
-  const T* gb = static_cast<const T*>(a.g) + i * a.s_row + h * a.s_head + j * a.s_pos;
-  T* ob = static_cast<T*>(a.out) + i * a.o_row + j * a.o_pos + h * a.o_head;
+  // merge the 16 key lanes of each query (lanes 16*qi' .. 16*qi'+15 of the wave)
+  float mt = m;
 #pragma unroll
-  for (int d = 0; d < HD; d++) ob[d] = from_f<T>(acc[d] * inv * sigmoidf_(to_f(gb[d])));
+  for (int o = 8; o > 0; o >>= 1) mt = fmaxf(mt, __shfl_xor(mt, o, 64));
+  const float f = (m == -INFINITY) ? 0.f : __expf(m - mt);
+  lsum *= f;
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) lsum += __shfl_xor(lsum, o, 64);
+#pragma unroll
+  for (int d = 0; d < HD; d++) {
+    float a = acc[d] * f;
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) a += __shfl_xor(a, o, 64);
+    acc[d] = a;
+  }
+  if (!valid || kl != 0) return;
+  const float inv = 1.0f / lsum;
+#pragma unroll
+  for (int d = 0; d < HD; d++)
+    out[j * ld_out + h * HD + d] = from_f<T>(acc[d] * inv * sigmoidf_(to_f(g[j * ld_in + h * HD + d])));
 }
 
 template <typename T>
-static hipError_t attn_simple_launch(const AttnArgs& a, int64_t rows, int H, int hd, hipStream_t st) {
-  const dim3 grid((unsigned)((a.J + 63) / 64), (unsigned)H, (unsigned)rows);
+static hipError_t seq_attn_t(const void* q, const void* k, const void* v, const void* g, int64_t ld_in,
+                             const void* bias, const float* mask, float inf, void* out, int64_t ld_out, int64_t N,
+                             int H, int hd, hipStream_t st) {
+  const dim3 grid((unsigned)((N + 15) / 16), (unsigned)H);
+  const float scale = 1.0f / sqrtf((float)hd);
+#define BZ_SEQ(HDV)                                                                                              \
+  seq_attn_kernel<T, HDV><<<grid, 256, 0, st>>>(static_cast<const T*>(q), static_cast<const T*>(k),            \
+                                                static_cast<const T*>(v), static_cast<const T*>(g), ld_in,      \
+                                                static_cast<const T*>(bias), mask, inf, static_cast<T*>(out),   \
+                                                ld_out, N, scale)
   switch (hd) {
-    case 16: attn_simple_kernel<T, 16><<<grid, 64, 0, st>>>(a); break;
-    case 24: attn_simple_kernel<T, 24><<<grid, 64, 0, st>>>(a); break;
-    case 32: attn_simple_kernel<T, 32><<<grid, 64, 0, st>>>(a); break;
-    case 48: attn_simple_kernel<T, 48><<<grid, 64, 0, st>>>(a); break;
-    case 64: attn_simple_kernel<T, 64><<<grid, 64, 0, st>>>(a); break;
+    case 16: BZ_SEQ(16); break;
+    case 24: BZ_SEQ(24); break;
+    case 32: BZ_SEQ(32); break;
+    case 48: BZ_SEQ(48); break;
+    case 64: BZ_SEQ(64); break;
     default: return hipErrorInvalidValue;
   }
+#undef BZ_SEQ
   return hipGetLastError();
 }
 
@@ -211,20 +214,8 @@ hipError_t launch_triattn_core_simple(const void* qkg, const void* vt, const voi
 hipError_t launch_seq_attention(const void* q, const void* k, const void* v, const void* g, int64_t ld_in,
                                 const void* bias, const float* mask, float inf, void* out, int64_t ld_out, int dt,
                                 int64_t N, int H, int hd, hipStream_t st) {
-  AttnArgs a;
-  a.q = q; a.k = k; a.v = v; a.g = g;
-  a.bias = bias;
-  a.mask = mask;
-  a.out = out;
-  a.s_row = 0; a.s_pos = ld_in; a.s_head = hd;
-  a.o_row = 0; a.o_pos = ld_out; a.o_head = hd;
-  a.b_head = N * N;
-  a.m_row = 0; a.m_key = 1;
-  a.inf = inf;
-  a.scale = 1.0f / sqrtf((float)hd);
-  a.J = N;
-  a.order = 1;
-  return dt == DT_F16 ? attn_simple_launch<half_t>(a, 1, H, hd, st) : attn_simple_launch<float>(a, 1, H, hd, st);
+  return dt == DT_F16 ? seq_attn_t<half_t>(q, k, v, g, ld_in, bias, mask, inf, out, ld_out, N, H, hd, st)
+                      : seq_attn_t<float>(q, k, v, g, ld_in, bias, mask, inf, out, ld_out, N, H, hd, st);
 }
 
 // Core dispatch (impl mirrors the reference's scalar / mma choice, boltz_mlx/kernels.py:902-945): 0 = MFMA for

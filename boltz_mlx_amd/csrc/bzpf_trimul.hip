@@ -11,52 +11,119 @@
 namespace bzpf {
 
 // ---------------------------------------------------------------- per-channel contraction
-// o[c][i][j] = sum_{k < ld} a[c][i][k] * b[c][j][k]; grid (ceil(N/BT)^2, D); block 256 = 4 waves in 2 x 2, each
-// wave a (BT/2) x (BT/2) block of 16x16 MFMA tiles. BK = 32 keys per LDS stage.
-template <typename T, int BT>
-__global__ __launch_bounds__(256) void trimul_contract_kernel(const T* __restrict__ ab, T* __restrict__ o, int64_t N,
-                                                              int64_t ld, int D) {
-  constexpr int BK = 32, PAD = Pad<T>::v, LDK = BK + PAD;
-  constexpr int WB = BT / 32;  // 16x16 blocks per wave per dimension
-  __shared__ LDS_ALIGN T As[BT * LDK];
-  __shared__ LDS_ALIGN T Bs[BT * LDK];
-  const int64_t tiles = (N + BT - 1) / BT;
-  const int64_t ti = blockIdx.x / tiles, tj = blockIdx.x - ti * tiles;
-  const int64_t i0 = ti * BT, j0 = tj * BT;
-  const int64_t c = blockIdx.y;
+// o[c][i][j] = sum_{k < ld} a[c][i][k] * b[c][j][k], a = ab[c], b = ab[D + c] (k >= N is zero padding).
+// Workgroup: a 128 x 128 tile (i, j) of one channel, 4 waves in 2 x 2, each 64 x 64 = 4 x 4 MFMA blocks. The tile is
+// computed transposed, o^T = b a^T (A operand = rows of b, B operand = rows of a), so each lane holds 4 consecutive
+// j of one i and stores them as one vector. K advances BK elements per stage through a double-buffered LDS tile;
+// the next stage is loaded into registers while the current one computes. Lane group g of a wave reads the
+// contiguous k range [g*BK/4, (g+1)*BK/4) of each stage (a permutation of the k sum shared by A and B).
+// Tiles are ordered (channel, tile) and dealt to the XCDs in contiguous ranges, so one channel's a and b stay in
+// one XCD's L2.
+template <typename T>
+__global__ __launch_bounds__(256, 2) void trimul_contract_kernel(const T* __restrict__ ab, T* __restrict__ o,
+                                                                 int64_t N, int64_t ld, int D, int64_t tiles1,
+                                                                 int64_t units, int64_t per_xcd) {
+  constexpr int BT = 128;
+  constexpr int BK = sizeof(T) == 2 ? 64 : 32;      // k per stage: 128 bytes of a row
+  constexpr int KG = BK / 4;                        // contiguous k per lane group
+  constexpr int KP = Mfma<T>::KP;
+  constexpr int STEPS = KG / KP;
+  constexpr int LDT = BK + 16 / (int)sizeof(T);     // LDS row pitch (elements)
+  constexpr int VE = 16 / (int)sizeof(T);           // elements per 16-byte vector
+  constexpr int VPR = BK / VE;                      // vectors per row per stage (8)
+  constexpr int LOADS = 2 * BT * VPR / 256;         // 16-byte vectors per thread per stage (8)
+  __shared__ LDS_ALIGN T As[2][BT * LDT];           // rows of a (i)
+  __shared__ LDS_ALIGN T Bs[2][BT * LDT];           // rows of b (j)
+
+  const int64_t u = (int64_t)(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
+  if (u >= units) return;
+  const int64_t c = u / (tiles1 * tiles1);
+  const int64_t tt = u - c * tiles1 * tiles1;
+  const int64_t i0 = (tt / tiles1) * BT, j0 = (tt % tiles1) * BT;
   const T* a = ab + c * N * ld;
   const T* b = ab + ((int64_t)D + c) * N * ld;
-  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63;
-  const int wr = wave >> 1, wc = wave & 1;
+  const int t = threadIdx.x, wave = t >> 6, l = t & 63, g = l >> 4;
+  const int wi = wave >> 1, wj = wave & 1;
 
-  f4 acc[WB][WB];
+  // stage loads: vector v of thread t covers row (v*256 + t) / VPR of [a rows | b rows], column ((..) % VPR) * VE
+  u32x4_t reg[LOADS];
+  auto gload = [&](int64_t k0) {
+#pragma unroll
+    for (int v = 0; v < LOADS; v++) {
+      const int e = v * 256 + t, r = e / VPR, col = (e % VPR) * VE;
+      const bool isb = r >= BT;
+      int64_t row = (isb ? j0 : i0) + (isb ? r - BT : r);
+      if (row >= N) row = N - 1;
+      reg[v] = *reinterpret_cast<const u32x4_t*>((isb ? b : a) + row * ld + k0 + col);
+    }
+  };
+  auto lstore = [&](int buf) {
+#pragma unroll
+    for (int v = 0; v < LOADS; v++) {
+      const int e = v * 256 + t, r = e / VPR, col = (e % VPR) * VE;
+      T* dst = r >= BT ? Bs[buf] + (r - BT) * LDT : As[buf] + r * LDT;
+      *reinterpret_cast<u32x4_t*>(dst + col) = reg[v];
+    }
+  };
+
+  f4 acc[4][4];  // acc[jb][ib]: o^T block (j = 64*wj + 16*jb .., i = 64*wi + 16*ib ..)
   zero_acc(acc);
-  for (int64_t k0 = 0; k0 < ld; k0 += BK) {
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  const int nst = (int)(ld / BK);
+  for (int st = 0; st < nst; st++) {
+    const int buf = st & 1;
+    if (st + 1 < nst) gload((int64_t)(st + 1) * BK);
+    const T* Ab = As[buf];
+    const T* Bb = Bs[buf];
+#pragma unroll
+    for (int s = 0; s < STEPS; s++) {
+      typename Mfma<T>::frag fa[4], fb[4];
+#pragma unroll
+      for (int ib = 0; ib < 4; ib++)
+        fa[ib] = Mfma<T>::load(Ab + (64 * wi + 16 * ib + (l & 15)) * LDT + KG * g + KP * s);
+#pragma unroll
+      for (int jb = 0; jb < 4; jb++)
+        fb[jb] = Mfma<T>::load(Bb + (64 * wj + 16 * jb + (l & 15)) * LDT + KG * g + KP * s);
+#pragma unroll
+      for (int jb = 0; jb < 4; jb++)
+#pragma unroll
+        for (int ib = 0; ib < 4; ib++) acc[jb][ib] = Mfma<T>::run(fb[jb], fa[ib], acc[jb][ib]);
+    }
+    if (st + 1 < nst) lstore(buf ^ 1);
     __syncthreads();
-    load_rows<T>(As, LDK, BT, BK, [&](int r) { int64_t ii = i0 + r; if (ii >= N) ii = N - 1; return a + ii * ld + k0; });
-    load_rows<T>(Bs, LDK, BT, BK, [&](int r) { int64_t jj = j0 + r; if (jj >= N) jj = N - 1; return b + jj * ld + k0; });
-    __syncthreads();
-    wave_mma<T, WB, WB>(acc, As + (wr * BT / 2) * LDK, LDK, Bs + (wc * BT / 2) * LDK, LDK, BK);
   }
+  // acc[jb][ib][e] = o[i = i0 + 64 wi + 16 ib + (l & 15)][j = j0 + 64 wj + 16 jb + 4 g + e]
   T* oc = o + c * N * ld;
 #pragma unroll
-  for (int mb = 0; mb < WB; mb++)
+  for (int ib = 0; ib < 4; ib++) {
+    const int64_t i = i0 + 64 * wi + 16 * ib + (l & 15);
+    if (i >= N) continue;
 #pragma unroll
-    for (int nb = 0; nb < WB; nb++)
-#pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const int64_t ii = i0 + wr * BT / 2 + 16 * mb + (l >> 4) * 4 + e;
-        const int64_t jj = j0 + wc * BT / 2 + 16 * nb + (l & 15);
-        if (ii < N && jj < N) oc[ii * ld + jj] = from_f<T>(acc[mb][nb][e]);
+    for (int jb = 0; jb < 4; jb++) {
+      const int64_t j = j0 + 64 * wj + 16 * jb + 4 * g;
+      if (j >= ld) continue;
+      T* dst = oc + i * ld + j;
+      if constexpr (sizeof(T) == 2) {
+        *reinterpret_cast<half4*>(dst) =
+            half4{(half_t)acc[jb][ib][0], (half_t)acc[jb][ib][1], (half_t)acc[jb][ib][2], (half_t)acc[jb][ib][3]};
+      } else {
+        *reinterpret_cast<f4*>(dst) = acc[jb][ib];
       }
+    }
+  }
 }
 
 template <typename T>
 static hipError_t contract_t(const void* ab, void* o, int64_t N, int64_t ld, int D, hipStream_t st) {
-  constexpr int BT = 64;
-  const int64_t tiles = (N + BT - 1) / BT;
-  const dim3 grid((unsigned)(tiles * tiles), (unsigned)D);
-  trimul_contract_kernel<T, BT><<<grid, 256, 0, st>>>(static_cast<const T*>(ab), static_cast<T*>(o), N, ld, D);
+  constexpr int BT = 128;
+  const int64_t tiles1 = (N + BT - 1) / BT;
+  const int64_t units = (int64_t)D * tiles1 * tiles1;
+  const int64_t per_xcd = (units + 7) / 8;
+  const dim3 grid((unsigned)(per_xcd * 8));
+  trimul_contract_kernel<T><<<grid, 256, 0, st>>>(static_cast<const T*>(ab), static_cast<T*>(o), N, ld, D, tiles1,
+                                                  units, per_xcd);
   return hipGetLastError();
 }
 

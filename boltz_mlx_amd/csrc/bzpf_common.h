@@ -108,6 +108,26 @@ __device__ __forceinline__ float group_sum(float v) {
   for (int o = G / 2; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
   return v;
 }
+// Reductions over the lanes l, l^16, l^32, l^48 (the 4 lane groups of a wave) with the gfx950 row / half-wave
+// swaps: permlane16_swap(x, x) returns the values of rows {2r, 2r+1} of each row pair as (first, second), and
+// permlane32_swap(x, x) the values of the two halves of the wave.
+__device__ __forceinline__ float xgroups_max(float v) {
+  const unsigned u = __float_as_uint(v);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float m = fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+  const unsigned w = __float_as_uint(m);
+  const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+  return fmaxf(__uint_as_float(b[0]), __uint_as_float(b[1]));
+}
+__device__ __forceinline__ float xgroups_sum(float v) {
+  const unsigned u = __float_as_uint(v);
+  const auto a = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  const float s = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const unsigned w = __float_as_uint(s);
+  const auto b = __builtin_amdgcn_permlane32_swap(w, w, false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 template <int G>
 __device__ __forceinline__ float group_max(float v) {
 #pragma unroll

@@ -130,18 +130,14 @@ __device__ __forceinline__ void resid_ln_rows(const f4 (&y)[RB][8], ZRow zrow, f
       s += v[cb][0] + v[cb][1] + v[cb][2] + v[cb][3];
     }
     if (lnw == nullptr) continue;
-    s += __shfl_xor(s, 16, 64);
-    s += __shfl_xor(s, 32, 64);
-    const float mean = s * (1.0f / D);
+    const float mean = xgroups_sum(s) * (1.0f / D);
     float ss = 0.f;
 #pragma unroll
     for (int cb = 0; cb < 8; cb++) {
       const f4 d = v[cb] - mean;
       ss += d[0] * d[0] + d[1] * d[1] + d[2] * d[2] + d[3] * d[3];
     }
-    ss += __shfl_xor(ss, 16, 64);
-    ss += __shfl_xor(ss, 32, 64);
-    const float rstd = 1.0f / sqrtf(ss * (1.0f / D) + eps);
+    const float rstd = 1.0f / sqrtf(xgroups_sum(ss) * (1.0f / D) + eps);
     if (zr < 0) continue;
 #pragma unroll
     for (int cb = 0; cb < 8; cb++) {

@@ -45,6 +45,7 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
   __shared__ LDS_ALIGN float Mb[BK];
   constexpr int LDB = BK + 4;   // Bs row pitch (halves)
   __shared__ LDS_ALIGN half_t Bs[WQ * LDB];
+  __shared__ int MaskedFlag;
 
   const int64_t u = (int64_t)(blockIdx.x % NXCD) * per_xcd + blockIdx.x / NXCD;
   if (u >= units) return;  // whole workgroup
@@ -124,7 +125,12 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
     *reinterpret_cast<half8*>(Bs + brow * LDB + bk32 + 8) = breg1;
     *reinterpret_cast<half8*>(Bs + brow * LDB + bk32 + 16) = breg2;
     *reinterpret_cast<half8*>(Bs + brow * LDB + bk32 + 24) = breg3;
-    const bool masked = __syncthreads_or(t < BK && mbnext != 0.0f);
+    if (wave == 0) {
+      const bool any_masked = __any(mbnext != 0.0f);
+      if (l == 0) MaskedFlag = any_masked;
+    }
+    __syncthreads();
+    const bool masked = MaskedFlag != 0;
     if (k0 + BK < N) prefetch(k0 + BK);
 
     half8 kf[4];
@@ -140,73 +146,79 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
         const half4 hi4 = *reinterpret_cast<const half4*>(vr + 16);
         vf[s2][dt] = half8{lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
       }
+    f4 s[2][4];
+    if (row_masked) {
+      // uniform weights over keys < N: logit 0 with m = 0
 #pragma unroll
-    for (int tq = 0; tq < 2; tq++) {
-      f4 s[4];
-      const half_t* brd = Bs + (32 * wave + 16 * tq + qi) * LDB + 4 * g;
-      if (row_masked) {
-        // uniform weights over keys < N: logit 0 with m = 0
+      for (int tq = 0; tq < 2; tq++)
 #pragma unroll
         for (int t4 = 0; t4 < 4; t4++)
 #pragma unroll
-          for (int e = 0; e < 4; e++) s[t4][e] = (k0 + 16 * t4 + 4 * g + e < N) ? 0.0f : -INFINITY;
-      } else {
-        // the maximum is "unset" until a key that is not masked has been seen (a masked logit is about
-        // -inf*log2(e)); subtracting such a maximum would cancel catastrophically
-        const bool unset = m[tq] <= munset;
-        const float mref = unset ? 0.0f : m[tq];
-        if (masked) {
+          for (int e = 0; e < 4; e++) s[tq][t4][e] = (k0 + 16 * t4 + 4 * g + e < N) ? 0.0f : -INFINITY;
+    } else {
+      // the maximum is "unset" until a key that is not masked has been seen (a masked logit is about
+      // -inf*log2(e)); subtracting such a maximum would cancel catastrophically
+      float mref[2];
+      bool unset[2];
 #pragma unroll
-          for (int t4 = 0; t4 < 4; t4++) {
+      for (int tq = 0; tq < 2; tq++) {
+        unset[tq] = m[tq] <= munset;
+        mref[tq] = unset[tq] ? 0.0f : m[tq];
+        const half_t* brd = Bs + (32 * wave + 16 * tq + qi) * LDB + 4 * g;
+#pragma unroll
+        for (int t4 = 0; t4 < 4; t4++) {
+          const half4 bv = *reinterpret_cast<const half4*>(brd + 16 * t4);
+          f4 c;
+          if (masked) {
             const f4 mbv = *reinterpret_cast<const f4*>(Mb + 16 * t4 + 4 * g);
-            f4 c;
-            const half4 bv = *reinterpret_cast<const half4*>(brd + 16 * t4);
 #pragma unroll
-            for (int e = 0; e < 4; e++) c[e] = ((float)bv[e] + mbv[e]) - mref;
-            s[t4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[t4], qf[tq], c, 0, 0, 0);
+            for (int e = 0; e < 4; e++) c[e] = ((float)bv[e] + mbv[e]) - mref[tq];
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; e++) c[e] = (float)bv[e] - mref[tq];
           }
-        } else {
-#pragma unroll
-          for (int t4 = 0; t4 < 4; t4++) {
-            f4 c;
-            const half4 bv = *reinterpret_cast<const half4*>(brd + 16 * t4);
-#pragma unroll
-            for (int e = 0; e < 4; e++) c[e] = (float)bv[e] - mref;
-            s[t4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[t4], qf[tq], c, 0, 0, 0);
-          }
+          s[tq][t4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[t4], qf[tq], c, 0, 0, 0);
         }
-        float mloc = -INFINITY;
+      }
+      float mloc[2];
+#pragma unroll
+      for (int tq = 0; tq < 2; tq++) {
+        float mx = -INFINITY;
 #pragma unroll
         for (int t4 = 0; t4 < 4; t4++)
-          mloc = fmaxf(mloc, fmaxf(fmaxf(s[t4][0], s[t4][1]), fmaxf(s[t4][2], s[t4][3])));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 16, 64));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32, 64));
-        // s holds logit - mref; raise the maximum only when the block exceeds it by more than 2^THRESH
-        const bool need = unset || mloc > THRESH;
-        if (__any(need)) {
-          const float mn = fmaxf(m[tq], mloc + mref);
+          mx = fmaxf(mx, fmaxf(fmaxf(s[tq][t4][0], s[tq][t4][1]), fmaxf(s[tq][t4][2], s[tq][t4][3])));
+        mloc[tq] = xgroups_max(mx);
+      }
+      // s holds logit - mref; raise the maximum only when the block exceeds it by more than 2^THRESH
+      const bool need = unset[0] || unset[1] || mloc[0] > THRESH || mloc[1] > THRESH;
+      if (__any(need)) {
+#pragma unroll
+        for (int tq = 0; tq < 2; tq++) {
+          const float mn = fmaxf(m[tq], mloc[tq] + mref[tq]);
           const float corr = __builtin_amdgcn_exp2f(m[tq] - mn);
 #pragma unroll
           for (int dt = 0; dt < 3; dt++) oacc[tq][dt] *= corr;
-          const float delta = mref - mn;
+          const float delta = mref[tq] - mn;
 #pragma unroll
-          for (int t4 = 0; t4 < 4; t4++) s[t4] += delta;
+          for (int t4 = 0; t4 < 4; t4++) s[tq][t4] += delta;
           m[tq] = mn;
         }
       }
+    }
+#pragma unroll
+    for (int tq = 0; tq < 2; tq++)
 #pragma unroll
       for (int s2 = 0; s2 < 2; s2++) {
         half8 pf;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-          pf[e] = (half_t)__builtin_amdgcn_exp2f(s[2 * s2][e]);
-          pf[4 + e] = (half_t)__builtin_amdgcn_exp2f(s[2 * s2 + 1][e]);
+          pf[e] = (half_t)__builtin_amdgcn_exp2f(s[tq][2 * s2][e]);
+          pf[4 + e] = (half_t)__builtin_amdgcn_exp2f(s[tq][2 * s2 + 1][e]);
         }
         oacc[tq][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[s2][0], pf, oacc[tq][0], 0, 0, 0);
         oacc[tq][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[s2][1], pf, oacc[tq][1], 0, 0, 0);
         oacc[tq][2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf, oacc[tq][2], 0, 0, 0);
       }
-    }
   }
   // oacc[tq][dt][e] = O^T[channel 16*dt + 4g + e][query qi]; the row sum is row 0 of tile 2 (lane qi, e = 0)
 #pragma unroll

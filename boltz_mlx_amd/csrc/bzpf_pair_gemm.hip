@@ -215,10 +215,9 @@ __global__ __launch_bounds__(256) void triattn_proj_k(const T* __restrict__ xn, 
           for (int e = 0; e < 4; e++) {
             const int hh = col - 4 * HC + e;
             if (hh >= H) continue;
-            T* row = tb + ((int64_t)hh * N + pi) * ldk;
-            row[pj] = from_f<T>(v[e]);
+            tb[tb_offset(hh, pi, pj, N, ldk)] = from_f<T>(v[e]);
             if (pj == N - 1)  // finite padding: the MFMA core adds it before masking keys past N
-              for (int64_t k = N; k < ldk; k++) row[k] = from_f<T>(0.0f);
+              for (int64_t k = N; k < ldk; k++) tb[tb_offset(hh, pi, k, N, ldk)] = from_f<T>(0.0f);
           }
         }
       }

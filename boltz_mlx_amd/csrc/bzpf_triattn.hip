@@ -34,7 +34,6 @@ __global__ __launch_bounds__(64) void triattn_core_valu(const T* __restrict__ qk
   const T* kb = qkg + ((H + h) * NN + i * N) * C;
   const T* gb = qkg + ((2 * H + h) * NN + i * N) * C;
   const T* vb = vt + (h * N + i) * C * ldk;
-  const T* bb = tb + h * N * ldk;
   float q[C], acc[C];
 #pragma unroll
   for (int d = 0; d < C; d++) {
@@ -52,7 +51,7 @@ __global__ __launch_bounds__(64) void triattn_core_valu(const T* __restrict__ qk
     }
     for (int e = t; e < 64 * TK; e += 64) {
       const int qq = e / TK, kk = e - qq * TK;
-      Bs[qq][kk] = (j0 + qq < N && k0 + kk < N) ? to_f(bb[(j0 + qq) * ldk + k0 + kk]) : 0.f;
+      Bs[qq][kk] = (j0 + qq < N && k0 + kk < N) ? to_f(tb[tb_offset(h, j0 + qq, k0 + kk, N, ldk)]) : 0.f;
     }
     if (t < TK) Mk[t] = k0 + t < N ? inf * (mask[i * mask_si + (k0 + t) * mask_sk] - 1.0f) * LOG2E : 0.f;
     __syncthreads();

@@ -10,7 +10,8 @@
 // probabilities P^T are already laid out as the B operand of O^T = V^T P^T (V^T tiles arrive transposed from the
 // projection), so P never leaves registers, and a third MFMA tile whose A operand is a constant row of ones
 // accumulates the softmax denominator on the matrix cores. The next key block's K, V^T, bias and mask are loaded
-// into registers while the current block computes.
+// into registers while the current block computes; the bias arrives in the fragment-ordered layout (tb_offset), two
+// 16-byte loads per lane and tile, without passing through LDS.
 // Logits are base 2: the projection stores q * log2(e)/sqrt(C) and tri_bias * log2(e); the key-mask bias is
 // inf*(m-1)*log2(e). A row whose keys are all masked gets uniform weights over its N keys, which is what the
 // reference's rounding gives (every logit rounds to -inf*log2(e); boltz_mlx/kernels.py:579-581). Softmax and
@@ -43,8 +44,6 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
   __shared__ LDS_ALIGN half_t Ks[BK * LDK];
   __shared__ LDS_ALIGN half_t Vs[C * LDV];
   __shared__ LDS_ALIGN float Mb[BK];
-  constexpr int LDB = BK + 4;   // Bs row pitch (halves)
-  __shared__ LDS_ALIGN half_t Bs[WQ * LDB];
   __shared__ int MaskedFlag;
 
   const int64_t u = (int64_t)(blockIdx.x % NXCD) * per_xcd + blockIdx.x / NXCD;
@@ -88,27 +87,38 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
 #pragma unroll
   for (int e = 0; e < 8; e++) ones[e] = (half_t)(qi == 0 ? 1.0f : 0.0f);
 
-  // staging roles: K rows (64 keys x 32 channels) and V^T rows (32 channels x 64 keys), one 16-byte vector each;
-  // the bias tile (128 queries x 64 keys), four 16-byte vectors each
+  // staging roles: K rows (64 keys x 32 channels) and V^T rows (32 channels x 64 keys), one 16-byte vector each
   const int skey = t >> 2, sd8 = (t & 3) * 8;
   const int vd = t >> 3, vk8 = (t & 7) * 8;
-  const int brow = t >> 1, bk32 = (t & 1) * 32;
-  const int bq = qb * WQ + brow;
-  const half_t* bsrc = tb + ((int64_t)h * N + (bq < N ? bq : N - 1)) * ldk + bk32;
-  half8 kreg, vreg, breg0, breg1, breg2, breg3;
+  half8 kreg, vreg;
   float mbnext = 0.f;
+  // bias fragments (fragment-ordered layout): 16 contiguous values per lane per 16-query tile and 64-key block
+  const int njt = (N + 15) / 16, nkb = ldk / 64;
+  const half_t* bfp[2];
+#pragma unroll
+  for (int tq = 0; tq < 2; tq++) {
+    int jt = qb * (WQ / 16) + 2 * wave + tq;
+    if (jt >= njt) jt = njt - 1;
+    bfp[tq] = tb + ((((int64_t)h * njt + jt) * nkb) * 64 + l) * 16;
+  }
+  half8 bnext[2][2];
   auto prefetch = [&](int k0) {
     int kk = k0 + skey;
     if (kk >= N) kk = N - 1;
     kreg = *reinterpret_cast<const half8*>(kp + (int64_t)kk * C + sd8);
     vreg = *reinterpret_cast<const half8*>(vp + (int64_t)vd * ldk + k0 + vk8);
-    breg0 = *reinterpret_cast<const half8*>(bsrc + k0);
-    breg1 = *reinterpret_cast<const half8*>(bsrc + k0 + 8);
-    breg2 = *reinterpret_cast<const half8*>(bsrc + k0 + 16);
-    breg3 = *reinterpret_cast<const half8*>(bsrc + k0 + 24);
     if (t < BK) mbnext = k0 + t < N ? inf * (mrow[(int64_t)(k0 + t) * mask_sk] - 1.0f) * LOG2E : -INFINITY;
   };
+  auto prefetch_bias = [&](int k0) {
+#pragma unroll
+    for (int tq = 0; tq < 2; tq++) {
+      const half_t* bq = bfp[tq] + (int64_t)(k0 / 64) * 1024;
+      bnext[tq][0] = *reinterpret_cast<const half8*>(bq);
+      bnext[tq][1] = *reinterpret_cast<const half8*>(bq + 8);
+    }
+  };
   prefetch(0);
+  prefetch_bias(0);
 
   for (int k0 = 0; k0 < N; k0 += BK) {
     const bool tail = k0 + BK > N;
@@ -121,10 +131,6 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
     }
     *reinterpret_cast<half8*>(Vs + vd * LDV + vk8) = vreg;
     if (t < BK) Mb[t] = mbnext;
-    *reinterpret_cast<half8*>(Bs + brow * LDB + bk32) = breg0;
-    *reinterpret_cast<half8*>(Bs + brow * LDB + bk32 + 8) = breg1;
-    *reinterpret_cast<half8*>(Bs + brow * LDB + bk32 + 16) = breg2;
-    *reinterpret_cast<half8*>(Bs + brow * LDB + bk32 + 24) = breg3;
     if (wave == 0) {
       const bool any_masked = __any(mbnext != 0.0f);
       if (l == 0) MaskedFlag = any_masked;
@@ -136,16 +142,6 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
     half8 kf[4];
 #pragma unroll
     for (int t4 = 0; t4 < 4; t4++) kf[t4] = *reinterpret_cast<const half8*>(Ks + (16 * t4 + qi) * LDK + g * 8);
-    half8 vf[2][2];
-#pragma unroll
-    for (int s2 = 0; s2 < 2; s2++)
-#pragma unroll
-      for (int dt = 0; dt < 2; dt++) {
-        const half_t* vr = Vs + (16 * dt + qi) * LDV + 32 * s2 + 4 * g;
-        const half4 lo = *reinterpret_cast<const half4*>(vr);
-        const half4 hi4 = *reinterpret_cast<const half4*>(vr + 16);
-        vf[s2][dt] = half8{lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-      }
     f4 s[2][4];
     if (row_masked) {
       // uniform weights over keys < N: logit 0 with m = 0
@@ -164,10 +160,11 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
       for (int tq = 0; tq < 2; tq++) {
         unset[tq] = m[tq] <= munset;
         mref[tq] = unset[tq] ? 0.0f : m[tq];
-        const half_t* brd = Bs + (32 * wave + 16 * tq + qi) * LDB + 4 * g;
 #pragma unroll
         for (int t4 = 0; t4 < 4; t4++) {
-          const half4 bv = *reinterpret_cast<const half4*>(brd + 16 * t4);
+          const half8 bh = bnext[tq][t4 >> 1];
+          const int o4 = (t4 & 1) * 4;
+          const half4 bv = half4{bh[o4], bh[o4 + 1], bh[o4 + 2], bh[o4 + 3]};
           f4 c;
           if (masked) {
             const f4 mbv = *reinterpret_cast<const f4*>(Mb + 16 * t4 + 4 * g);
@@ -180,6 +177,7 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
           s[tq][t4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[t4], qf[tq], c, 0, 0, 0);
         }
       }
+      if (k0 + BK < N) prefetch_bias(k0 + BK);  // the bias registers are free once the logits are formed
       float mloc[2];
 #pragma unroll
       for (int tq = 0; tq < 2; tq++) {
@@ -205,6 +203,17 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
         }
       }
     }
+    // V^T fragments, read after the logits so that their registers reuse those of the K fragments
+    half8 vf[2][2];
+#pragma unroll
+    for (int s2 = 0; s2 < 2; s2++)
+#pragma unroll
+      for (int dt = 0; dt < 2; dt++) {
+        const half_t* vr = Vs + (16 * dt + qi) * LDV + 32 * s2 + 4 * g;
+        const half4 lo = *reinterpret_cast<const half4*>(vr);
+        const half4 hi4 = *reinterpret_cast<const half4*>(vr + 16);
+        vf[s2][dt] = half8{lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+      }
 #pragma unroll
     for (int tq = 0; tq < 2; tq++)
 #pragma unroll

@@ -202,8 +202,8 @@ LOG2E = 1.4426950408889634
 
 
 def triattn_proj(xn, w, trans: bool, N: int, H: int, C: int):
-    """-> (qkg [3H, N*N, C], vt [H, N, C, ldk], tb [H, N, ldk]) in xn's dtype, q scaled by log2(e)/sqrt(C) and the
-    bias by log2(e) (the base-2 logits the core expects)."""
+    """-> (qkg [3H, N*N, C], vt [H, N, C, ldk], tb flat in the fragment-ordered layout of tri_bias_offsets) in
+    xn's dtype, q scaled by log2(e)/sqrt(C) and the bias by log2(e) (the base-2 logits the core expects)."""
     _dev(xn, w)
     D = xn.shape[-1]
     if w.shape != (4 * H * C + H, D) or w.dtype != xn.dtype or xn.numel() != N * N * D:
@@ -211,10 +211,30 @@ def triattn_proj(xn, w, trans: bool, N: int, H: int, C: int):
     ldk = row_pitch(N)
     qkg = torch.empty((3 * H, N * N, C), dtype=xn.dtype, device=xn.device)
     vt = torch.empty((H, N, C, ldk), dtype=xn.dtype, device=xn.device)
-    tb = torch.empty((H, N, ldk), dtype=xn.dtype, device=xn.device)
+    tb = torch.empty((tri_bias_numel(N, H),), dtype=xn.dtype, device=xn.device)
     call("bzpf_triattn_proj", _p(xn), _p(w), int(trans), LOG2E / C ** 0.5, LOG2E, _p(qkg), _p(vt), _p(tb), _dt(xn),
          N, ldk, D, H, C, _stream())
     return qkg, vt, tb
+
+
+def tri_bias_numel(N: int, H: int) -> int:
+    """Elements of the fragment-ordered triangle-bias buffer: H * (N rounded up to 16) * row_pitch(N)."""
+    return H * ((N + 15) // 16) * 16 * row_pitch(N)
+
+
+def tri_bias_offsets(N: int, H: int):
+    """Index of element (h, j, k) of a dense [H, N, N] bias in the fragment-ordered layout the attention core reads
+    (16-query tile, 64-key block, lane 16*g + qi owning keys 16*t4 + 4*g + e contiguously), as an int64 array."""
+    import numpy as np
+
+    ldk = row_pitch(N)
+    njt, nkb = (N + 15) // 16, ldk // 64
+    h = np.arange(H)[:, None, None]
+    j = np.arange(N)[None, :, None]
+    k = np.arange(N)[None, None, :]
+    jt, qi, kb, kk = j >> 4, j & 15, k >> 6, k & 63
+    t4, g, e = kk >> 4, (kk >> 2) & 3, kk & 3
+    return (((h * njt + jt) * nkb + kb) * 64 + (g * 16 + qi)) * 16 + t4 * 4 + e
 
 
 TRIATT_IMPL = {"auto": 0, "scalar": 1, "mma": 2}[os.environ.get("BOLTZ_MLX_TRIATT_IMPL", "auto")]
@@ -227,7 +247,7 @@ def triattn_core(qkg, vt, tb, mask, trans: bool, inf: float, N: int, H: int, C: 
     if mask.dtype != torch.float32 or mask.numel() != N * N:
         raise ValueError("triattn_core: mask must be fp32 [N, N]")
     ldk = row_pitch(N)
-    if qkg.shape != (3 * H, N * N, C) or vt.shape != (H, N, C, ldk) or tb.shape != (H, N, ldk):
+    if qkg.shape != (3 * H, N * N, C) or vt.shape != (H, N, C, ldk) or tb.numel() != tri_bias_numel(N, H):
         raise ValueError("triattn_core: buffers must come from triattn_proj")
     out = torch.empty((N * N, H * C), dtype=qkg.dtype, device=qkg.device)
     si, sk = (1, N) if trans else (N, 1)

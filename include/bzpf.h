@@ -79,7 +79,9 @@ int bzpf_trimul_tail(const void* o, const float* norm_out_w, const float* norm_o
  * linear_g; linear] ([4*H*C + H, D]) at the position p = i*N + j (trans: xn is read at (j, i), the ending node):
  *   qkg [3H][N*N][C]: q * q_scale (planes 0..H-1), k (H..2H-1), g (2H..3H-1);
  *   vt [H][N][C][ldk]: v transposed per row i (vt[h][i][c][j] = v at (i, j)); columns j >= N are not written;
- *   tri_bias [H][N][ldk]: tri_bias[h][j][k] = bias_scale * (linear at (j, k)); columns k >= N are set to 0.
+ *   tri_bias: bias_scale * (linear at (j, k)) for head h, query j, key k, in the fragment-ordered layout the
+ *     attention core reads: element (h, j, k) at (((h*NJ + j/16)*(ldk/64) + k/64)*64 + 16*((k%16)/4) + j%16)*16
+ *     + 4*((k%64)/16) + k%4 with NJ = ceil(N/16) (H*16*NJ*ldk elements); keys N <= k < ldk are set to 0.
  * ldk = bzpf_row_pitch(N). bzpf_triattn_core expects q_scale = log2(e)/sqrt(C) and bias_scale = log2(e) (logits
  * in base 2). Replaces the fused projection of TriangleAttention
  * (boltz_mlx/layers/triangular_attention/attention.py:49-69, 100-104) and kernels_nax3.pair_proj16
@@ -89,7 +91,7 @@ int bzpf_triattn_proj(const void* xn, const void* w, int trans, float q_scale, f
 
 /* Flash triangle-attention core over the projection's buffers: for row i, head h, query j,
  *   out[i][j][h*C + c] = sigmoid(g) * sum_k softmax2_k(q.k + inf*(mask[i*mask_si + k*mask_sk] - 1)*log2(e)
- *                                                      + tri_bias[h][j][k]) v[k][c]
+ *                                                      + tri_bias(h, j, k)) v[k][c]
  * with softmax2 the base-2 softmax (2^x normalised; equal to the reference's softmax of the natural-log logits
  * (q/sqrt(C)).k + inf*(mask-1) + linear, summed in that order). fp32 softmax and accumulation; out [N*N, H*C] (dt).
  * impl selects the kernel like the reference's impl argument: 0 = auto (MFMA for fp16 with C = 32, else VALU),

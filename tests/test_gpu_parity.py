@@ -252,6 +252,39 @@ def test_pairformer_module_two_blocks(precision):
 
 # ------------------------------------------------------------------------------------------------ fast vs slow core
 
+def _tb_index(N, H):
+    """Offsets of (h, j, k) for k < row_pitch(N) (the padded key range) in the fragment-ordered bias layout."""
+    from boltz_mlx_amd import kernels as K
+
+    ldk = K.row_pitch(N)
+    njt, nkb = (N + 15) // 16, ldk // 64
+    h = np.arange(H)[:, None, None]
+    j = np.arange(N)[None, :, None]
+    k = np.arange(ldk)[None, None, :]
+    jt, qi, kb, kk = j >> 4, j & 15, k >> 6, k & 63
+    t4, g, e = kk >> 4, (kk >> 2) & 3, kk & 3
+    return (((h * njt + jt) * nkb + kb) * 64 + (g * 16 + qi)) * 16 + t4 * 4 + e
+
+
+@pytest.mark.parametrize("trans", [False, True])
+def test_tri_bias_layout_matches_projection(trans):
+    """The projection writes the bias at tri_bias_offsets and zero-fills keys past N (read back from the buffer)."""
+    from boltz_mlx_amd import kernels as K
+
+    N, H, C = 70, 4, 32
+    rng = np.random.default_rng(3)
+    xn = dev(rng.standard_normal((N * N, 128)), torch.float16)
+    w = dev(0.1 * rng.standard_normal((4 * H * C + H, 128)), torch.float16)
+    _, _, tb = K.triattn_proj(xn, w, trans, N, H, C)
+    got = tb.float().cpu().numpy()
+    ref = (xn.float() @ w[4 * H * C:].float().T).cpu().numpy() * K.LOG2E  # bias of position (a, b) = [a*N + b]
+    ref = ref.reshape(N, N, H).transpose(2, 0, 1)
+    if trans:  # the ending node's bias for (query j, key k) is the projection at (k, j)
+        ref = ref.transpose(0, 2, 1)
+    assert np.allclose(got[K.tri_bias_offsets(N, H)], ref, rtol=4e-3, atol=4e-3)
+    assert np.all(got[_tb_index(N, H)[:, :, N:].ravel()] == 0)
+
+
 @pytest.mark.parametrize("N", [1, 2, 17, 64, 65, 130])
 @pytest.mark.parametrize("trans", [False, True])
 def test_triattn_core_mfma_vs_valu(N, trans):
@@ -265,11 +298,15 @@ def test_triattn_core_mfma_vs_valu(N, trans):
     ldk = K.row_pitch(N)
     qkg = dev(rng.standard_normal((3 * H, N * N, C)), torch.float16)
     vt = dev(rng.standard_normal((H, N, C, ldk)), torch.float16)
-    tb = dev(2 * rng.standard_normal((H, N, ldk)), torch.float16)
-    # V^T padding is never written by the projection: NaN there proves it is never used; the bias padding is 0, as
-    # the projection writes it
+    # bias in the fragment-ordered layout: keys past N are 0 (as the projection writes them); slots of queries past N
+    # are never read for a valid query and hold NaN here to prove it
+    tb_np = np.full(K.tri_bias_numel(N, H), np.nan, dtype=np.float32)
+    dense = np.zeros((H, N, ldk), dtype=np.float32)
+    dense[:, :, :N] = 2 * rng.standard_normal((H, N, N))
+    tb_np[_tb_index(N, H).ravel()] = dense.ravel()
+    tb = dev(tb_np, torch.float16)
+    # V^T padding is never written by the projection: NaN there proves it is never used
     vt[..., N:] = float("nan")
-    tb[..., N:] = 0.0
     mask = np.ones((N, N), np.float32)
     if N > 4:
         mask[:, -2:] = 0

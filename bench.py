@@ -55,18 +55,30 @@ def kernel_work(name: str, N: int, H: int = 4, C: int = 32, D: int = 128) -> tup
     return 0.0, 0.0
 
 
+def profiled_traffic(name: str, N: int):
+    """HBM bytes per launch of `name` at N from the committed rocprofv3 FETCH_SIZE / WRITE_SIZE summary
+    (profiles/traffic_N{N}_fp16.json, counters scaled by the copy-kernel calibration), or None."""
+    path = os.path.join(ROOT, "profiles", f"traffic_N{N}_fp16.json")
+    try:
+        with open(path) as f:
+            return json.load(f)["kernels"][name]["traffic_bytes"]
+    except (OSError, KeyError, ValueError):
+        return None
+
+
 def roofline_for(name: str, ms: float, N: int) -> dict:
     fl, by = kernel_work(name, N)
+    traffic = profiled_traffic(name, N)
     t_fl = fl / (MFMA_F16_PEAK_TFLOPS * 1e12)
     t_by = by / (HBM_PEAK_GBS * 1e9)
     if t_fl >= t_by:
         ach = fl / (ms * 1e-3) / 1e12
         return {"kernel": name, "bound": "mfma", "achieved": round(ach, 2), "peak": MFMA_F16_PEAK_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK_TFLOPS, 4), "traffic": None,
+                "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK_TFLOPS, 4), "traffic": traffic,
                 "avg_ms": round(ms, 4), "algorithmic_flop": fl, "algorithmic_bytes": by}
     ach = by / (ms * 1e-3) / 1e9
     return {"kernel": name, "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None, "avg_ms": round(ms, 4),
+            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic, "avg_ms": round(ms, 4),
             "algorithmic_flop": fl, "algorithmic_bytes": by}
 
 
@@ -136,6 +148,9 @@ def main() -> int:
     ap.add_argument("--n-small", type=int, default=400)
     ap.add_argument("--blocks", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--calibrate-copy", action="store_true",
+                    help="end with one 512 MiB device-to-device copy (the known-size kernel that scales the "
+                         "FETCH_SIZE / WRITE_SIZE counters of rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -179,6 +194,13 @@ def main() -> int:
         torch.cuda.synchronize()
         dt_ev = time.perf_counter() - t1
         times = K.stop_timing()
+        if args.calibrate_copy:
+            a = torch.empty(128 << 20, dtype=torch.float32, device=dev).fill_(1.0)
+            b = torch.empty_like(a)
+            torch.cuda.synchronize()
+            b.copy_(a)
+            torch.cuda.synchronize()
+            del a, b
     total = {k: sum(v) for k, v in times.items()}
     dom = max(total, key=total.get)
     roof = roofline_for(dom, total[dom] / len(times[dom]), args.n)

@@ -3,7 +3,9 @@ inputs and weights).
 
 The reference commits no golden vectors for this path (its module dumps are generated from upstream torch and
 git-ignored), so these fixtures pin the oracle against regressions and give the GPU tests fixed vectors. Every row
-of every mask keeps at least one unmasked key, so fp32 evaluation agrees with these float64 outputs to ~1e-6.
+and every column of every pair mask keeps at least one unmasked entry, so neither the starting node (rows) nor the
+ending node (columns) sees a fully masked row, and fp32 evaluation agrees with these float64 outputs to ~1e-6. (On
+a fully masked row the fp32 reference rounds every logit to -inf * 1 and averages uniformly; float64 does not.)
 
 Run: python tests/golden/make_golden.py
 """
@@ -33,7 +35,8 @@ def pair(N, D, seed):
     tok = np.ones((1, N), np.float32)
     tok[:, -2:] = 0
     pm = tok[:, :, None] * tok[:, None, :]
-    pm[:, -2:, 0] = 1  # padded rows keep one key: no fully masked row
+    pm[:, -2:, 0] = 1  # padded rows keep one key: no fully masked row in the starting frame
+    pm[:, 0, -2:] = 1  # padded columns keep one entry: none in the ending frame either
     pm[0, 3, 5] = 0
     return z, pm
 

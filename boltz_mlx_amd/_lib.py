@@ -43,11 +43,13 @@ class BzpfError(RuntimeError):
     pass
 
 
-def load(path: str = LIB_PATH):
-    """Load (once) and return the library with argtypes set. Raises if it has not been built."""
+def load(path: str | None = None):
+    """Load (once) and return the library with argtypes set (default path: LIB_PATH as it is at the first call).
+    Raises if it has not been built."""
     global _lib
     if _lib is not None:
         return _lib
+    path = path or LIB_PATH
     # torch first: its HIP runtime (torch/lib/libamdhip64.so, soname libamdhip64.so.7) must be the one mapped
     # when the library resolves libamdhip64.so.7, so that the process holds a single runtime instance.
     import torch  # noqa: F401

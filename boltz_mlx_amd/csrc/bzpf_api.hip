@@ -2,7 +2,7 @@
 #include <cstdarg>
 #include <cstdio>
 
-#include "../../include/bzpf.h"
+#include "bzpf.h"
 #include "bzpf_kernels.h"
 
 namespace {

@@ -22,47 +22,70 @@ constexpr int D = 128;
 template <typename T> constexpr int ldw_of() { return D + Pad<T>::v; }
 
 // ---------------------------------------------------------------- triangle multiplication projection
-// grid: N * tiles_per_row, tiles of TM positions (i, k0 .. k0+TM) of the padded row of length ld.
+// Persistent, one 1024-thread workgroup per CU. The launch covers output channels [c_lo, c_lo + PCH): the projection
+// rows c_lo.. and gate rows 2D + c_lo.. of w (PCH = 256 in fp16: all of them; 128 in fp32, two launches) are staged in
+// LDS once; each wave then streams tiles of TW positions (i, k0 .. k0 + TW) over the padded rows of length ld,
+// computing (ROWS orientation) runs of 16 bytes per channel for ab[c][i][k] (incoming: xn read at (k, i)).
+template <typename T> constexpr int proj_ch() { return sizeof(T) == 2 ? 256 : 128; }
+
 template <typename T>
-__global__ __launch_bounds__(256) void trimul_proj_k(const T* __restrict__ xn, const T* __restrict__ w,
-                                                     const float* __restrict__ mask, float scale, int incoming,
-                                                     T* __restrict__ ab, int64_t N, int64_t ld) {
-  constexpr int RB = RowBlocks<T>::v, TM = 64 * RB, STEPS = RG<T>::STEPS, LDW = ldw_of<T>();
-  __shared__ LDS_ALIGN T Ws[64 * LDW];
-  const int64_t tpr = (ld + TM - 1) / TM;
-  const int64_t i = blockIdx.x / tpr;
-  const int64_t k0 = (blockIdx.x - i * tpr) * TM;
-  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 4;
+__global__ __launch_bounds__(1024) void trimul_proj_k(const T* __restrict__ xn, const T* __restrict__ w,
+                                                      const float* __restrict__ mask, float scale, int incoming,
+                                                      T* __restrict__ ab, int64_t N, int64_t ld, int c_lo) {
+  using RT = RunTile<T>;
+  constexpr int RB = RT::RB, TW = RT::TW, STEPS = RG<T>::STEPS, LDW = ldw_of<T>(), PCH = proj_ch<T>();
+  __shared__ LDS_ALIGN T Ws[2 * PCH * LDW];  // rows [0, PCH): projections, [PCH, 2 PCH): gates
+  lds_rows<T>(Ws, LDW, 2 * PCH, D,
+              [&](int r) { return w + (int64_t)(r < PCH ? c_lo + r : 2 * D + c_lo + r - PCH) * D; });
+  __syncthreads();
+  const int l = threadIdx.x & 63, g = l >> 4, r = l & 15;
+  const int tpr = (int)(ld / TW), ntiles = (int)N * tpr, stride = gridDim.x * 16;
+  int t = grid_wave(16);
+  if (t >= ntiles) return;
 
   typename RG<T>::frag x[RB][STEPS];
-  int64_t kpos[RB];
-  float mk[RB];
-#pragma unroll
-  for (int rb = 0; rb < RB; rb++) {
-    kpos[rb] = k0 + wave * 16 * RB + 16 * rb + (l & 15);
-    const int64_t kc = kpos[rb] < N ? kpos[rb] : N - 1;
-    const int64_t src = incoming ? (kc * N + i) : (i * N + kc);
-    RG<T>::load_row(x[rb], xn + src * D, g);
-    mk[rb] = kpos[rb] < N ? mask[src] * scale : 0.0f;  // padding columns k >= N are written as 0
-  }
-  for (int c0 = 0; c0 < 2 * D; c0 += 32) {
-    __syncthreads();
-    lds_rows<T>(Ws, LDW, 64, D, [&](int r) { return w + (int64_t)(r < 32 ? c0 + r : 2 * D + c0 + r - 32) * D; });
-    __syncthreads();
-    f4 acc[RB][4];
-    zero_acc(acc);
-    mma_rows<T, RB, 4>(acc, x, Ws, LDW);
+  float mk[RB];  // mask * scale of the row this lane loads (0 past N: padding columns are written as 0)
+  const auto load = [&](int tt, typename RG<T>::frag (&xx)[RB][STEPS], float (&mm)[RB]) {
+    const int i = tt / tpr, k0 = (tt - i * tpr) * TW;
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) {
-      if (kpos[rb] >= ld) continue;
+      const int64_t k = k0 + RT::pos(rb, r), kc = k < N ? k : N - 1;
+      const int64_t src = incoming ? kc * N + i : (int64_t)i * N + kc;
+      RG<T>::load_row(xx[rb], xn + src * D, g);
+      mm[rb] = k < N ? mask[src] * scale : 0.0f;
+    }
+  };
+  load(t, x, mk);
+  for (; t < ntiles; t += stride) {
+    const int i = t / tpr, k0 = (t - i * tpr) * TW;
+    float mo[RB][4];  // mask of this lane's output positions RUN g + 4 rb + e, loaded by lane 4 g + e
 #pragma unroll
-      for (int cb = 0; cb < 2; cb++)
+    for (int rb = 0; rb < RB; rb++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          const int ch = c0 + 16 * cb + 4 * g + e;
-          const float v = acc[rb][cb][e] * sigmoidf_(acc[rb][cb + 2][e]) * mk[rb];
-          ab[((int64_t)ch * N + i) * ld + kpos[rb]] = from_f<T>(v);
-        }
+      for (int e = 0; e < 4; e++) mo[rb][e] = __shfl(mk[rb], 4 * g + e);
+    typename RG<T>::frag xnext[RB][STEPS];
+    float mnext[RB];
+    load(min(t + stride, ntiles - 1), xnext, mnext);
+    T* dst = ab + ((int64_t)(c_lo + r) * N + i) * ld + k0 + RT::RUN * g;
+    for (int cb = 0; cb < PCH / 16; cb++) {
+      f4 pa[RB][1], ga[RB][1];
+      zero_acc(pa);
+      zero_acc(ga);
+      mma_rows<T, RB, 1, true>(pa, x, Ws + 16 * cb * LDW, LDW);
+      mma_rows<T, RB, 1, true>(ga, x, Ws + (PCH + 16 * cb) * LDW, LDW);
+      float v[RT::RUN];
+#pragma unroll
+      for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+        for (int e = 0; e < 4; e++) v[4 * rb + e] = pa[rb][0][e] * sigmoidf_(ga[rb][0][e]) * mo[rb][e];
+      st_run(dst + (int64_t)16 * cb * N * ld, v);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) {
+      mk[rb] = mnext[rb];
+#pragma unroll
+      for (int s = 0; s < STEPS; s++) x[rb][s] = xnext[rb][s];
     }
   }
 }
@@ -160,109 +183,153 @@ __global__ __launch_bounds__(256) void trimul_tail_k(const T* __restrict__ o, co
 }
 
 // ---------------------------------------------------------------- triangle attention projection
-// grid: ceil(N^2 / TM) position tiles; M = 4*H*C + H output channels in 64-channel chunks.
+// Persistent like trimul_proj. Rows of w: q [0, D), k [D, 2D), v [2D, 3D), g [3D, 4D), triangle bias [4D, 4D + H)
+// (H * C = D). A launch stages the rows [r_lo, r_hi) of that list with the bias block padded to 16 zero rows
+// (fp16: all 4D + 16 rows; fp32: [0, 2D) and [2D, 4D + 16) in two launches). Each wave streams tiles of TW positions
+// (i, j0 .. j0 + TW) of the padded rows (length ldk), position (i, j) reading xn at (i, j) (trans: (j, i)):
+//   q, k, g : transposed orientation; the staging permutes each 32-row group (LDS row 32 m + 16 c + rr holds channel
+//             32 m + 8 (rr / 4) + 4 c + rr % 4), so the lane of group g holds channels 8 g .. 8 g + 7 of its position:
+//             one 16-byte run of qkg[plane][i N + j][:] (q scaled by q_scale);
+//   v       : ROWS orientation, 16-byte runs of keys of vt[h][i][d][:] (zeros past N);
+//   bias    : ROWS orientation, runs of 4 keys of the fragment-ordered bias (scaled by b_scale, zeros past N).
+template <typename T> constexpr int attn_rows() { return sizeof(T) == 2 ? 4 * D + 16 : 2 * D + 16; }
+
+__device__ __forceinline__ void st8(half_t* p, const float (&v)[8]) { st_run(p, v); }
+__device__ __forceinline__ void st8(float* p, const float (&v)[8]) {
+  *reinterpret_cast<f4*>(p) = f4{v[0], v[1], v[2], v[3]};
+  *reinterpret_cast<f4*>(p + 4) = f4{v[4], v[5], v[6], v[7]};
+}
+
+// 12 waves (3 per SIMD, up to 168 VGPRs): the two row sets (current and prefetched) plus the per-lane store addresses
+// of the three output layouts do not fit the 128 VGPRs of 4 waves per SIMD.
+constexpr int ATTN_PROJ_WAVES = 12;
+
 template <typename T>
-__global__ __launch_bounds__(256) void triattn_proj_k(const T* __restrict__ xn, const T* __restrict__ w, int trans,
-                                                      float q_scale, float b_scale, T* __restrict__ qkg,
-                                                      T* __restrict__ vt, T* __restrict__ tb, int64_t N, int64_t ldk,
-                                                      int H, int C) {
-  constexpr int RB = RowBlocks<T>::v, TM = 64 * RB, STEPS = RG<T>::STEPS, LDW = ldw_of<T>();
-  __shared__ LDS_ALIGN T Ws[64 * LDW];
+__global__ __launch_bounds__(64 * ATTN_PROJ_WAVES) void triattn_proj_k(const T* __restrict__ xn,
+                                                                        const T* __restrict__ w, int trans,
+                                                                        float q_scale, float b_scale,
+                                                                        T* __restrict__ qkg, T* __restrict__ vt,
+                                                                        T* __restrict__ tb, int64_t N, int64_t ldk,
+                                                                        int H, int C, int r_lo, int r_hi) {
+  using RT = RunTile<T>;
+  constexpr int RB = RT::RB, TW = RT::TW, STEPS = RG<T>::STEPS, LDW = ldw_of<T>();
+  __shared__ LDS_ALIGN T Ws[attn_rows<T>() * LDW];
+  lds_rows<T>(Ws, LDW, r_hi - r_lo, D, [&](int lr) -> const T* {
+    const int R = r_lo + lr;
+    if (R >= 4 * D) return R - 4 * D < H ? w + (int64_t)R * D : nullptr;
+    if (R >= 2 * D && R < 3 * D) return w + (int64_t)R * D;
+    const int q = R & 31, rr = q & 15;
+    return w + (int64_t)((R & ~31) + 8 * (rr >> 2) + 4 * (q >> 4) + (rr & 3)) * D;
+  });
+  __syncthreads();
+  const int l = threadIdx.x & 63, g = l >> 4, r = l & 15;
   const int64_t NN = N * N;
-  const int64_t p0 = (int64_t)blockIdx.x * TM;
-  const int HC = H * C, M = 4 * HC + H;
-  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 4;
+  const int tpr = (int)(ldk / TW), ntiles = (int)N * tpr, stride = gridDim.x * ATTN_PROJ_WAVES;
+  int t = grid_wave(ATTN_PROJ_WAVES);
+  if (t >= ntiles) return;
 
   typename RG<T>::frag x[RB][STEPS];
-  int64_t pos[RB];
-#pragma unroll
-  for (int rb = 0; rb < RB; rb++) {
-    pos[rb] = p0 + wave * 16 * RB + 16 * rb + (l & 15);
-    int64_t p = pos[rb] < NN ? pos[rb] : NN - 1;
-    if (trans) { const int64_t a = p / N, b = p - a * N; p = b * N + a; }
-    RG<T>::load_row(x[rb], xn + p * D, g);
-  }
-  for (int c0 = 0; c0 < M; c0 += 64) {
-    __syncthreads();
-    lds_rows<T>(Ws, LDW, 64, D, [&](int r) -> const T* { return c0 + r < M ? w + (int64_t)(c0 + r) * D : nullptr; });
-    __syncthreads();
-    f4 acc[RB][4];
-    zero_acc(acc);
-    mma_rows<T, RB, 4>(acc, x, Ws, LDW);
-    const int plane4 = c0 / HC;  // 0 q, 1 k, 2 v, 3 g, 4 tri bias (HC % 64 == 0: chunks never straddle)
-    const float sc = plane4 == 0 ? q_scale : (plane4 == 4 ? b_scale : 1.0f);
+  const auto load = [&](int tt, typename RG<T>::frag (&xx)[RB][STEPS]) {
+    const int i = tt / tpr, j0 = (tt - i * tpr) * TW;
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) {
-      const int64_t p = pos[rb];
-      if (p >= NN) continue;
-      const int64_t pi = p / N, pj = p - pi * N;
+      const int64_t j = j0 + RT::pos(rb, r), jc = j < N ? j : N - 1;
+      RG<T>::load_row(xx[rb], xn + (trans ? jc * N + i : (int64_t)i * N + jc) * D, g);
+    }
+  };
+  load(t, x);
+  for (; t < ntiles; t += stride) {
+    const int i = t / tpr, j0 = (t - i * tpr) * TW;
+    typename RG<T>::frag xnext[RB][STEPS];
+    load(min(t + stride, ntiles - 1), xnext);
+    // ROWS orientation: key j0 + RUN g + 4 rb + e is inside the row
+    const auto valid = [&](int rb, int e) { return j0 + RT::RUN * g + 4 * rb + e < N ? 1.0f : 0.0f; };
+    for (int m = 0; m < r_hi - r_lo; m += 32) {
+      const int R = r_lo + m;
+      const T* wb = Ws + m * LDW;
+      if (R >= 4 * D) {  // triangle bias (16-row block, H valid rows)
+        f4 acc[RB][1];
+        zero_acc(acc);
+        mma_rows<T, RB, 1, true>(acc, x, wb, LDW);
+        if (r < H) {
 #pragma unroll
-      for (int cb = 0; cb < 4; cb++) {
-        const int col = c0 + 16 * cb + 4 * g;  // 4 consecutive channels col .. col+3
-        const f4 v = acc[rb][cb] * sc;
-        if (plane4 == 0 || plane4 == 1 || plane4 == 3) {
-          const int within = col - plane4 * HC;
-          const int64_t plane = (int64_t)(plane4 == 3 ? 2 : plane4) * H + within / C;
-          st4(qkg + (plane * NN + p) * C + (within % C), v);
-        } else if (plane4 == 2) {
-          const int within = col - 2 * HC;
-          const int hh = within / C, d = within % C;
-          T* dst = vt + (((int64_t)hh * N + pi) * C + d) * ldk + pj;
-#pragma unroll
-          for (int e = 0; e < 4; e++) dst[(int64_t)e * ldk] = from_f<T>(v[e]);
-        } else {
-#pragma unroll
-          for (int e = 0; e < 4; e++) {
-            const int hh = col - 4 * HC + e;
-            if (hh >= H) continue;
-            tb[tb_offset(hh, pi, pj, N, ldk)] = from_f<T>(v[e]);
-            if (pj == N - 1)  // finite padding: the MFMA core adds it before masking keys past N
-              for (int64_t k = N; k < ldk; k++) tb[tb_offset(hh, pi, k, N, ldk)] = from_f<T>(0.0f);
+          for (int rb = 0; rb < RB; rb++) {
+            const f4 v = acc[rb][0] * b_scale;
+            st4(tb + tb_offset(r, i, j0 + RT::RUN * g + 4 * rb, N, ldk),
+                f4{v[0] * valid(rb, 0), v[1] * valid(rb, 1), v[2] * valid(rb, 2), v[3] * valid(rb, 3)});
           }
         }
+      } else if (R >= 2 * D && R < 3 * D) {  // v
+        f4 acc[RB][2];
+        zero_acc(acc);
+        mma_rows_grouped<T, RB, 2, 1, true>(acc, x, wb, LDW);
+#pragma unroll
+        for (int c = 0; c < 2; c++) {
+          const int ch = R - 2 * D + 16 * c + r, h = ch / C, d = ch - h * C;
+          float v[RT::RUN];
+#pragma unroll
+          for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+            for (int e = 0; e < 4; e++) v[4 * rb + e] = acc[rb][c][e] * valid(rb, e);
+          st_run(vt + (((int64_t)h * N + i) * C + d) * ldk + j0 + RT::RUN * g, v);
+        }
+      } else {  // q, k, g
+        f4 acc[RB][2];
+        zero_acc(acc);
+        mma_rows_grouped<T, RB, 2, 1, false>(acc, x, wb, LDW);
+        const int P = R / D, within = R - P * D + 8 * g, h = within / C, d = within - h * C;
+        const int64_t plane = (int64_t)(P == 3 ? 2 : P) * H + h;
+        const float sc = P == 0 ? q_scale : 1.0f;
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++) {
+          const int64_t j = j0 + RT::pos(rb, r);
+          if (j >= N) continue;
+          const float v[8] = {acc[rb][0][0] * sc, acc[rb][0][1] * sc, acc[rb][0][2] * sc, acc[rb][0][3] * sc,
+                              acc[rb][1][0] * sc, acc[rb][1][1] * sc, acc[rb][1][2] * sc, acc[rb][1][3] * sc};
+          st8(qkg + (plane * NN + (int64_t)i * N + j) * C + d, v);
+        }
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+      for (int s = 0; s < STEPS; s++) x[rb][s] = xnext[rb][s];
   }
 }
 
 // ---------------------------------------------------------------- linear_o + residual + next LayerNorm
+// Persistent: W (128 x 128) is staged in LDS once per workgroup; each wave then streams 16-row tiles with no
+// barriers, loading the next tile's rows and the current tile's residual rows ahead of its MFMAs.
 template <typename T>
-__global__ __launch_bounds__(256) void linear_resid_ln_k(const T* __restrict__ x_in, const T* __restrict__ w,
-                                                         int trans, float* __restrict__ z, int accumulate,
-                                                         const float* __restrict__ lnw, const float* __restrict__ lnb,
-                                                         float eps, T* __restrict__ xn_next, int64_t N) {
-  constexpr int RB = RowBlocks<T>::v, TM = 64 * RB, STEPS = RG<T>::STEPS, LDW = ldw_of<T>();
-  __shared__ LDS_ALIGN T Ws[64 * LDW];
+__global__ __launch_bounds__(256, sizeof(T) == 2 ? 4 : 2) void linear_resid_ln_k(const T* __restrict__ x_in, const T* __restrict__ w,
+                                                            int trans, float* __restrict__ z, int accumulate,
+                                                            const float* __restrict__ lnw,
+                                                            const float* __restrict__ lnb, float eps,
+                                                            T* __restrict__ xn_next, int64_t N) {
+  constexpr int STEPS = RG<T>::STEPS, LDW = ldw_of<T>();
+  __shared__ LDS_ALIGN T Ws[D * LDW];
+  lds_rows<T>(Ws, LDW, D, D, [&](int r) { return w + (int64_t)r * D; });
+  __syncthreads();
   const int64_t NN = N * N;
-  const int64_t p0 = (int64_t)blockIdx.x * TM;
-  const int wave = threadIdx.x >> 6, l = threadIdx.x & 63, g = l >> 4;
-  typename RG<T>::frag x[RB][STEPS];
-  int64_t pos[RB];
-#pragma unroll
-  for (int rb = 0; rb < RB; rb++) {
-    pos[rb] = p0 + wave * 16 * RB + 16 * rb + (l & 15);
-    RG<T>::load_row(x[rb], x_in + (pos[rb] < NN ? pos[rb] : NN - 1) * D, g);
+  const int ntiles = (int)((NN + 15) / 16), stride = gridDim.x * 4;
+  const int l = threadIdx.x & 63, g = l >> 4;
+  int t = grid_wave(4);
+  typename RG<T>::frag x[1][STEPS];
+  if (t < ntiles) RG<T>::load_row(x[0], x_in + min((int64_t)t * 16 + (l & 15), NN - 1) * D, g);
+  for (; t < ntiles; t += stride) {
+    int64_t zr = (int64_t)t * 16 + (l & 15);
+    if (zr >= NN) zr = -1;
+    else if (trans) { const int64_t a = zr / N; zr = (zr - a * N) * N + a; }
+    const auto zrow = [&](int) { return zr; };
+    f4 zv[1][8];
+    load_z_rows<1>(zv, zrow, z, accumulate);
+    f4 y[1][8];
+    zero_acc(y);
+    mma_rows_grouped<T, 1, 8, 2>(y, x, Ws, LDW);
+    if (t + stride < ntiles) RG<T>::load_row(x[0], x_in + min((int64_t)(t + stride) * 16 + (l & 15), NN - 1) * D, g);
+    resid_ln_apply<T, 1>(y, zv, zrow, z, lnw, lnb, eps, xn_next);
   }
-  f4 y[RB][8];
-#pragma unroll
-  for (int cc = 0; cc < 2; cc++) {
-    __syncthreads();
-    lds_rows<T>(Ws, LDW, 64, D, [&](int r) { return w + (int64_t)(64 * cc + r) * D; });
-    __syncthreads();
-    f4 acc[RB][4];
-    zero_acc(acc);
-    mma_rows<T, RB, 4>(acc, x, Ws, LDW);
-#pragma unroll
-    for (int rb = 0; rb < RB; rb++)
-#pragma unroll
-      for (int cb = 0; cb < 4; cb++) y[rb][4 * cc + cb] = acc[rb][cb];
-  }
-  resid_ln_rows<T, RB>(y, [&](int rb) -> int64_t {
-    int64_t p = pos[rb];
-    if (p >= NN) return -1;
-    if (trans) { const int64_t a = p / N, b = p - a * N; p = b * N + a; }
-    return p;
-  }, z, accumulate, lnw, lnb, eps, xn_next);
 }
 
 // ---------------------------------------------------------------- transition
@@ -358,11 +425,19 @@ __global__ __launch_bounds__(256) void transition_k(const T* __restrict__ xn, co
 template <typename T>
 static hipError_t tm_proj(const void* xn, const void* w, const float* mask, float scale, int incoming, void* ab,
                           int64_t N, int64_t ld, hipStream_t st) {
-  constexpr int TM = 64 * RowBlocks<T>::v;
-  const dim3 grid((unsigned)(N * ((ld + TM - 1) / TM)));
-  trimul_proj_k<T><<<grid, 256, 0, st>>>(static_cast<const T*>(xn), static_cast<const T*>(w), mask, scale, incoming,
-                                         static_cast<T*>(ab), N, ld);
-  return hipGetLastError();
+  static int cache[kMaxDevices];
+  const int resident = resident_grid(trimul_proj_k<T>, 1024, cache);
+  if (resident <= 0) return hipErrorInvalidDevice;
+  const int64_t ntiles = N * (ld / RunTile<T>::TW);  // ld is a multiple of 64
+  if (ntiles >= (1LL << 30)) return hipErrorInvalidValue;  // tile indices are 32-bit in the kernel
+  const dim3 grid((unsigned)std::min<int64_t>(resident, (ntiles + 15) / 16));
+  for (int c_lo = 0; c_lo < 2 * D; c_lo += proj_ch<T>()) {
+    trimul_proj_k<T><<<grid, 1024, 0, st>>>(static_cast<const T*>(xn), static_cast<const T*>(w), mask, scale,
+                                            incoming, static_cast<T*>(ab), N, ld, c_lo);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 hipError_t launch_trimul_proj(const void* xn, const void* w, const float* mask, float scale, int incoming, void* ab,
@@ -396,12 +471,22 @@ hipError_t launch_trimul_tail(const void* o, const float* now, const float* nob,
 template <typename T>
 static hipError_t ta_proj(const void* xn, const void* w, int trans, float q_scale, float b_scale, void* qkg, void* vt,
                           void* tb, int64_t N, int64_t ldk, int H, int C, hipStream_t st) {
-  constexpr int TM = 64 * RowBlocks<T>::v;
-  const dim3 grid((unsigned)((N * N + TM - 1) / TM));
-  triattn_proj_k<T><<<grid, 256, 0, st>>>(static_cast<const T*>(xn), static_cast<const T*>(w), trans, q_scale,
-                                          b_scale, static_cast<T*>(qkg), static_cast<T*>(vt), static_cast<T*>(tb), N,
-                                          ldk, H, C);
-  return hipGetLastError();
+  if (H * C != D || H > 16 || C % 8) return hipErrorInvalidValue;
+  static int cache[kMaxDevices];
+  const int resident = resident_grid(triattn_proj_k<T>, 64 * ATTN_PROJ_WAVES, cache);
+  if (resident <= 0) return hipErrorInvalidDevice;
+  const int64_t ntiles = N * (ldk / RunTile<T>::TW);  // ldk is a multiple of 64
+  if (ntiles >= (1LL << 30)) return hipErrorInvalidValue;  // tile indices are 32-bit in the kernel
+  const dim3 grid((unsigned)std::min<int64_t>(resident, (ntiles + ATTN_PROJ_WAVES - 1) / ATTN_PROJ_WAVES));
+  const int bounds[3] = {0, sizeof(T) == 2 ? 4 * D + 16 : 2 * D, 4 * D + 16};
+  for (int p = 0; p < (sizeof(T) == 2 ? 1 : 2); p++) {
+    triattn_proj_k<T><<<grid, 64 * ATTN_PROJ_WAVES, 0, st>>>(
+        static_cast<const T*>(xn), static_cast<const T*>(w), trans, q_scale, b_scale, static_cast<T*>(qkg),
+        static_cast<T*>(vt), static_cast<T*>(tb), N, ldk, H, C, bounds[p], bounds[p + 1]);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 hipError_t launch_triattn_proj(const void* xn, const void* w, int trans, float q_scale, float b_scale, void* qkg,
@@ -413,8 +498,12 @@ hipError_t launch_triattn_proj(const void* xn, const void* w, int trans, float q
 template <typename T>
 static hipError_t lrl(const void* x, const void* w, int trans, float* z, int accumulate, const float* lnw,
                       const float* lnb, float eps, void* xn_next, int64_t N, hipStream_t st) {
-  constexpr int TM = 64 * RowBlocks<T>::v;
-  const dim3 grid((unsigned)((N * N + TM - 1) / TM));
+  static int cache[kMaxDevices];
+  const int resident = resident_grid(linear_resid_ln_k<T>, 256, cache);
+  if (resident <= 0) return hipErrorInvalidDevice;
+  const int64_t waves = (N * N + 15) / 16;
+  if (waves >= (1LL << 30)) return hipErrorInvalidValue;  // tile indices are 32-bit in the kernel
+  const dim3 grid((unsigned)std::min<int64_t>(resident, (waves + 3) / 4));
   linear_resid_ln_k<T><<<grid, 256, 0, st>>>(static_cast<const T*>(x), static_cast<const T*>(w), trans, z, accumulate,
                                              lnw, lnb, eps, static_cast<T*>(xn_next), N);
   return hipGetLastError();

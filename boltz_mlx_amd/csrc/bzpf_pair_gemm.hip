@@ -300,13 +300,17 @@ __global__ __launch_bounds__(64 * ATTN_PROJ_WAVES) void triattn_proj_k(const T* 
 
 // ---------------------------------------------------------------- linear_o + residual + next LayerNorm
 // Persistent: W (128 x 128) is staged in LDS once per workgroup; each wave then streams 16-row tiles with no
-// barriers, loading the next tile's rows and the current tile's residual rows ahead of its MFMAs.
+// barriers. The rows and residual rows of the wave's next tile are loaded a whole tile ahead (one HBM round trip is
+// longer than the compute of the waves sharing a SIMD). On a wave's last tile the clamped "next" tile may be another
+// wave's; those loads are never used.
 template <typename T>
-__global__ __launch_bounds__(256, sizeof(T) == 2 ? 4 : 2) void linear_resid_ln_k(const T* __restrict__ x_in, const T* __restrict__ w,
-                                                            int trans, float* __restrict__ z, int accumulate,
-                                                            const float* __restrict__ lnw,
-                                                            const float* __restrict__ lnb, float eps,
-                                                            T* __restrict__ xn_next, int64_t N) {
+__global__ __launch_bounds__(256, sizeof(T) == 2 ? 3 : 2) void linear_resid_ln_k(const T* __restrict__ x_in,
+                                                                                const T* __restrict__ w, int trans,
+                                                                                float* __restrict__ z, int accumulate,
+                                                                                const float* __restrict__ lnw,
+                                                                                const float* __restrict__ lnb,
+                                                                                float eps, T* __restrict__ xn_next,
+                                                                                int64_t N) {
   constexpr int STEPS = RG<T>::STEPS, LDW = ldw_of<T>();
   __shared__ LDS_ALIGN T Ws[D * LDW];
   lds_rows<T>(Ws, LDW, D, D, [&](int r) { return w + (int64_t)r * D; });
@@ -315,20 +319,34 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 4 : 2) void linear_resid_ln_k
   const int ntiles = (int)((NN + 15) / 16), stride = gridDim.x * 4;
   const int l = threadIdx.x & 63, g = l >> 4;
   int t = grid_wave(4);
+  if (t >= ntiles) return;
+  const auto zrow_of = [&](int tt) -> int64_t {
+    int64_t p = (int64_t)tt * 16 + (l & 15);
+    if (p >= NN) return -1;
+    if (trans) { const int64_t a = p / N; p = (p - a * N) * N + a; }
+    return p;
+  };
+  const auto load = [&](int tt, typename RG<T>::frag (&xx)[1][STEPS], f4 (&zz)[1][8]) {
+    RG<T>::load_row(xx[0], x_in + min((int64_t)tt * 16 + (l & 15), NN - 1) * D, g);
+    const int64_t zr = zrow_of(tt);
+    load_z_rows<1>(zz, [&](int) { return zr; }, z, accumulate);
+  };
   typename RG<T>::frag x[1][STEPS];
-  if (t < ntiles) RG<T>::load_row(x[0], x_in + min((int64_t)t * 16 + (l & 15), NN - 1) * D, g);
+  f4 zv[1][8];
+  load(t, x, zv);
   for (; t < ntiles; t += stride) {
-    int64_t zr = (int64_t)t * 16 + (l & 15);
-    if (zr >= NN) zr = -1;
-    else if (trans) { const int64_t a = zr / N; zr = (zr - a * N) * N + a; }
-    const auto zrow = [&](int) { return zr; };
-    f4 zv[1][8];
-    load_z_rows<1>(zv, zrow, z, accumulate);
+    typename RG<T>::frag xnext[1][STEPS];
+    f4 znext[1][8];
+    load(min(t + stride, ntiles - 1), xnext, znext);
     f4 y[1][8];
     zero_acc(y);
     mma_rows_grouped<T, 1, 8, 2>(y, x, Ws, LDW);
-    if (t + stride < ntiles) RG<T>::load_row(x[0], x_in + min((int64_t)(t + stride) * 16 + (l & 15), NN - 1) * D, g);
-    resid_ln_apply<T, 1>(y, zv, zrow, z, lnw, lnb, eps, xn_next);
+    const int64_t zr = zrow_of(t);
+    resid_ln_apply<T, 1>(y, zv, [&](int) { return zr; }, z, lnw, lnb, eps, xn_next);
+#pragma unroll
+    for (int s = 0; s < STEPS; s++) x[0][s] = xnext[0][s];
+#pragma unroll
+    for (int cb = 0; cb < 8; cb++) zv[0][cb] = znext[0][cb];
   }
 }
 
@@ -416,6 +434,131 @@ __global__ __launch_bounds__(256) void transition_k(const T* __restrict__ xn, co
   }
   resid_ln_rows<T, RB>(out, [&](int rb) -> int64_t { return row[rb] < rows_total ? row[rb] : -1; }, z, accumulate, lnw,
                        lnb, eps, xn_next);
+}
+
+// fp16 transition, persistent: one 512-thread workgroup per CU walks 256-row tiles (8 waves x 32 rows). The hidden
+// dimension streams through LDS in chunks of 64 units (fc1 and fc2 rows, fc3 columns: 48 KB). Chunk q + 1 is loaded
+// into registers while chunk q computes from LDS and is written to the other buffer afterwards, so a chunk costs one
+// barrier and no exposed L2 latency; the buffer written in step q was last read in step q - 1, which every wave
+// finished before the barrier of step q - 1. The chunk sequence runs on across tiles (the weights repeat), and the
+// next tile's rows are loaded during the current tile's last chunk.
+constexpr int TR_WAVES = 8, TR_HCH = 64;
+
+__global__ __launch_bounds__(64 * TR_WAVES) void transition_f16_k(const half_t* __restrict__ xn,
+                                                                  const half_t* __restrict__ w12,
+                                                                  const half_t* __restrict__ w3,
+                                                                  float* __restrict__ z, int accumulate,
+                                                                  const float* __restrict__ lnw,
+                                                                  const float* __restrict__ lnb, float eps,
+                                                                  half_t* __restrict__ xn_next, int64_t rows_total,
+                                                                  int hidden) {
+  using T = half_t;
+  constexpr int RB = 2, STEPS = RG<T>::STEPS, LDW = ldw_of<T>(), LDH = TR_HCH + Pad<T>::v, HB = TR_HCH / 16;
+  constexpr int TROWS = 16 * RB * TR_WAVES;
+  constexpr int VPT = 3 * 1024 / (64 * TR_WAVES);  // 16-byte vectors of a chunk per thread
+  __shared__ LDS_ALIGN T W1s[2][TR_HCH * LDW];
+  __shared__ LDS_ALIGN T W2s[2][TR_HCH * LDW];
+  __shared__ LDS_ALIGN T W3s[2][D * LDH];
+  const int t = threadIdx.x, l = t & 63, g = l >> 4;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int nch = hidden / TR_HCH;
+  const int64_t ntiles = (rows_total + TROWS - 1) / TROWS;
+  int64_t tile = blockIdx.x;
+  if (tile >= ntiles) return;  // whole workgroup
+
+  // chunk staging: vector v of thread t is element e = (v & 1) * 512 + t of matrix v / 2 (fc1, fc2: 64 rows x 16
+  // vectors; fc3: 128 rows x 8 vectors of the chunk's 64 columns)
+  u32x4 pre[VPT];
+  // element offsets of the thread's vectors in chunk 0 (chunk c adds c * TR_HCH * D in fc1/fc2, c * TR_HCH in fc3)
+  uint32_t goff[VPT];
+#pragma unroll
+  for (int v = 0; v < VPT; v++) {
+    const int m = v >> 1, e = (v & 1) * 512 + t;
+    goff[v] = m < 2 ? (uint32_t)(m * hidden + (e >> 4)) * D + (e & 15) * 8 : (uint32_t)(e >> 3) * hidden + (e & 7) * 8;
+  }
+  const auto gload = [&](int c) {
+    const uint32_t h12 = (uint32_t)c * TR_HCH * D, h3 = (uint32_t)c * TR_HCH;
+#pragma unroll
+    for (int v = 0; v < VPT; v++)
+      pre[v] = *reinterpret_cast<const u32x4*>(v < 4 ? w12 + (goff[v] + h12) : w3 + (goff[v] + h3));
+  };
+  const auto lstore = [&](int buf) {
+#pragma unroll
+    for (int v = 0; v < VPT; v++) {
+      const int m = v >> 1, e = (v & 1) * 512 + t;
+      T* dst = m == 0 ? W1s[buf] + (e >> 4) * LDW + (e & 15) * 8
+                      : (m == 1 ? W2s[buf] + (e >> 4) * LDW + (e & 15) * 8 : W3s[buf] + (e >> 3) * LDH + (e & 7) * 8);
+      *reinterpret_cast<u32x4*>(dst) = pre[v];
+    }
+  };
+  const auto xload = [&](int64_t tl, typename RG<T>::frag (&xx)[RB][STEPS]) {
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) {
+      const int64_t row = tl * TROWS + wave * 16 * RB + 16 * rb + (l & 15);
+      RG<T>::load_row(xx[rb], xn + (row < rows_total ? row : rows_total - 1) * D, g);
+    }
+  };
+
+  typename RG<T>::frag x[RB][STEPS];
+  xload(tile, x);
+  gload(0);
+  lstore(0);
+  __syncthreads();
+  gload(nch > 1 ? 1 : 0);
+  int q = 0;  // chunks computed so far (LDS buffer parity)
+  for (; tile < ntiles; tile += gridDim.x) {
+    f4 out[RB][8];
+    zero_acc(out);
+    typename RG<T>::frag xnext[RB][STEPS];
+    for (int c = 0; c < nch; c++, q++) {
+      const int buf = q & 1;
+      if (c == nch - 1) xload(min(tile + (int64_t)gridDim.x, ntiles - 1), xnext);
+      f4 a[RB][HB];
+#pragma unroll
+      for (int hb = 0; hb < HB; hb++) {
+        f4 h1[RB][1], h2[RB][1];
+        zero_acc(h1);
+        zero_acc(h2);
+        mma_rows<T, RB, 1>(h1, x, W1s[buf] + 16 * hb * LDW, LDW);
+        mma_rows<T, RB, 1>(h2, x, W2s[buf] + 16 * hb * LDW, LDW);
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) a[rb][hb][e] = siluf_(h1[rb][0][e]) * h2[rb][0][e];
+      }
+#pragma unroll
+      for (int m = 0; m < HB / 2; m++) {
+        half8 bf[RB];
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) {
+            bf[rb][e] = (half_t)a[rb][2 * m][e];
+            bf[rb][4 + e] = (half_t)a[rb][2 * m + 1][e];
+          }
+#pragma unroll
+        for (int ob = 0; ob < 8; ob++) {
+          const T* wr = W3s[buf] + (16 * ob + (l & 15)) * LDH + 32 * m + 4 * g;
+          const half4 lo = *reinterpret_cast<const half4*>(wr);
+          const half4 hi = *reinterpret_cast<const half4*>(wr + 16);
+          const half8 af = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+          for (int rb = 0; rb < RB; rb++)
+            out[rb][ob] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[rb], out[rb][ob], 0, 0, 0);
+        }
+      }
+      lstore(buf ^ 1);
+      __syncthreads();
+      gload(c + 2 < nch ? c + 2 : c + 2 - nch >= nch ? 0 : c + 2 - nch);
+    }
+    const int64_t row0 = tile * TROWS + wave * 16 * RB + (l & 15);
+    resid_ln_rows<T, RB>(out, [&](int rb) -> int64_t { return row0 + 16 * rb < rows_total ? row0 + 16 * rb : -1; }, z,
+                         accumulate, lnw, lnb, eps, xn_next);
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+      for (int s2 = 0; s2 < STEPS; s2++) x[rb][s2] = xnext[rb][s2];
+  }
 }
 
 }  // namespace
@@ -528,9 +671,25 @@ static hipError_t trans_t(const void* xn, const void* w12, const void* w3, float
   return hipGetLastError();
 }
 
+static hipError_t trans_f16(const void* xn, const void* w12, const void* w3, float* z, int accumulate,
+                            const float* lnw, const float* lnb, float eps, void* xn_next, int64_t rows, int hidden,
+                            hipStream_t st) {
+  static int cache[kMaxDevices];
+  const int resident = resident_grid(transition_f16_k, 64 * TR_WAVES, cache);
+  if (resident <= 0) return hipErrorInvalidDevice;
+  const int64_t ntiles = (rows + 16 * 2 * TR_WAVES - 1) / (16 * 2 * TR_WAVES);
+  const dim3 grid((unsigned)std::min<int64_t>(resident, ntiles));
+  transition_f16_k<<<grid, 64 * TR_WAVES, 0, st>>>(static_cast<const half_t*>(xn), static_cast<const half_t*>(w12),
+                                                   static_cast<const half_t*>(w3), z, accumulate, lnw, lnb, eps,
+                                                   static_cast<half_t*>(xn_next), rows, hidden);
+  return hipGetLastError();
+}
+
 hipError_t launch_transition(const void* xn, const void* w12, const void* w3, float* z, int accumulate,
                              const float* lnw, const float* lnb, float eps, void* xn_next, int dt, int64_t rows,
                              int hidden, hipStream_t st) {
+  if (dt == DT_F16 && hidden % TR_HCH == 0 && (int64_t)2 * hidden * D < (1LL << 31))
+    return trans_f16(xn, w12, w3, z, accumulate, lnw, lnb, eps, xn_next, rows, hidden, st);
   return dt == DT_F16 ? trans_t<half_t, 64>(xn, w12, w3, z, accumulate, lnw, lnb, eps, xn_next, rows, hidden, st)
                       : trans_t<float, 32>(xn, w12, w3, z, accumulate, lnw, lnb, eps, xn_next, rows, hidden, st);
 }

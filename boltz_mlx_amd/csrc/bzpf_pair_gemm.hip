@@ -182,6 +182,132 @@ __global__ __launch_bounds__(256) void trimul_tail_k(const T* __restrict__ o, co
                        lnb, eps_next, xn_next);
 }
 
+// fp16 tail, persistent: one 768-thread workgroup per CU (12 waves, 3 per SIMD) with g_out and p_out resident in LDS.
+// LN_out's affine part is folded into p_out when it is staged (columns scaled by gamma, bias W_po . beta), so the
+// kernel only normalises. Each wave streams tiles of 16 positions (i, j0 .. j0 + 15): its lanes load 4-channel x
+// 8-position blocks of the channel-major o (lane l: channels 4 (l / 2) .. + 3, positions 8 (l % 2) .. + 7), write
+// them as [position][channel] rows of a wave-private LDS tile (two byte permutes per position) and read the usual
+// row fragments back, with no barrier (a wave's LDS accesses complete in order). The next tile's o block and gate
+// inputs are loaded while the current tile computes; its residual rows are issued at the start of the tile. The
+// gates are computed first and held as fp16 (sigmoid values in (0, 1)), which keeps the tile within 168 VGPRs.
+constexpr int TAIL_WAVES = 12;
+
+__global__ __launch_bounds__(64 * TAIL_WAVES) void trimul_tail_f16_k(
+    const half_t* __restrict__ o, const float* __restrict__ now, const float* __restrict__ nob, float eps_out,
+    const half_t* __restrict__ w_po, const half_t* __restrict__ xn, const half_t* __restrict__ w_go,
+    float* __restrict__ z, int accumulate, const float* __restrict__ lnw, const float* __restrict__ lnb,
+    float eps_next, half_t* __restrict__ xn_next, int64_t N, int64_t ld) {
+  using T = half_t;
+  constexpr int STEPS = RG<T>::STEPS, LDW = ldw_of<T>(), LDT = D + Pad<T>::v;
+  __shared__ LDS_ALIGN T Wg[D * LDW];
+  __shared__ LDS_ALIGN T Wp[D * LDW];  // p_out with gamma_out folded into its columns
+  __shared__ LDS_ALIGN float Bp[D];    // p_out . beta_out
+  __shared__ LDS_ALIGN T Ts[TAIL_WAVES][16 * LDT];
+  lds_rows<T>(Wg, LDW, D, D, [&](int r) { return w_go + (int64_t)r * D; });
+  for (int e = threadIdx.x; e < D * D / 8; e += blockDim.x) {
+    const int r = e >> 4, c = (e & 15) * 8;
+    const half8 wv = *reinterpret_cast<const half8*>(w_po + (int64_t)r * D + c);
+    half8 sv;
+#pragma unroll
+    for (int u = 0; u < 8; u++) sv[u] = (half_t)((float)wv[u] * now[c + u]);
+    *reinterpret_cast<half8*>(Wp + r * LDW + c) = sv;
+  }
+  if (threadIdx.x < 4 * D) {  // 4 lanes per output channel, 32 inputs each
+    const int c = threadIdx.x >> 2, q = threadIdx.x & 3;
+    float acc = 0.f;
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const half8 wv = *reinterpret_cast<const half8*>(w_po + (int64_t)c * D + 32 * q + 8 * v);
+#pragma unroll
+      for (int u = 0; u < 8; u++) acc += (float)wv[u] * nob[32 * q + 8 * v + u];
+    }
+    acc += __shfl_xor(acc, 1, 64);
+    acc += __shfl_xor(acc, 2, 64);
+    if (q == 0) Bp[c] = acc;
+  }
+  __syncthreads();
+
+  const int l = threadIdx.x & 63, g = l >> 4, r = l & 15;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  T* ts = Ts[wave];
+  const int tpr = (int)((N + 15) / 16), ntiles = (int)N * tpr, stride = gridDim.x * TAIL_WAVES;
+  int t = grid_wave(TAIL_WAVES);
+  if (t >= ntiles) return;
+  const int ocg = l >> 1, opc = l & 1;
+  const auto load = [&](int tt, half8 (&ob)[4], typename RG<T>::frag (&xf)[1][STEPS]) {
+    const int i = tt / tpr, j0 = (tt - i * tpr) * 16;
+#pragma unroll
+    for (int u = 0; u < 4; u++)
+      ob[u] = *reinterpret_cast<const half8*>(o + ((int64_t)(4 * ocg + u) * N + i) * ld + j0 + 8 * opc);
+    const int64_t jc = j0 + r < N ? j0 + r : N - 1;
+    RG<T>::load_row(xf[0], xn + ((int64_t)i * N + jc) * D, g);
+  };
+  half8 ob[4];
+  typename RG<T>::frag xf[1][STEPS];
+  load(t, ob, xf);
+  for (; t < ntiles; t += stride) {
+    const int i = t / tpr, j0 = (t - i * tpr) * 16;
+    const int64_t zr = j0 + r < N ? (int64_t)i * N + j0 + r : -1;
+    const auto zrow = [&](int) { return zr; };
+    f4 zv[1][8];
+    load_z_rows<1>(zv, zrow, z, accumulate);
+    // o block -> [position][channel] rows of the wave's tile
+#pragma unroll
+    for (int v = 0; v < 8; v++)
+      *reinterpret_cast<half4*>(ts + (8 * opc + v) * LDT + 4 * ocg) = half4{ob[0][v], ob[1][v], ob[2][v], ob[3][v]};
+    half8 obn[4];
+    typename RG<T>::frag xfn[1][STEPS];
+    load(min(t + stride, ntiles - 1), obn, xfn);
+    // gates first (their inputs are free afterwards), kept as fp16
+    half4 gate[8];
+    {
+      f4 ga[1][8];
+      zero_acc(ga);
+      mma_rows_grouped<T, 1, 8, 1>(ga, xf, Wg, LDW);
+#pragma unroll
+      for (int cb = 0; cb < 8; cb++)
+        gate[cb] = half4{(half_t)sigmoidf_(ga[0][cb][0]), (half_t)sigmoidf_(ga[0][cb][1]),
+                         (half_t)sigmoidf_(ga[0][cb][2]), (half_t)sigmoidf_(ga[0][cb][3])};
+    }
+    // LN_out of this lane's position (channels 32 g .. 32 g + 31 here, the rest in lanes l ^ 16, l ^ 32, l ^ 48)
+    typename RG<T>::frag of[1][STEPS];
+    RG<T>::load_row(of[0], ts + r * LDT, g);
+    float sum = 0.f;
+#pragma unroll
+    for (int s2 = 0; s2 < STEPS; s2++)
+#pragma unroll
+      for (int u = 0; u < 8; u++) sum += (float)of[0][s2][u];
+    const float mean = xgroups_sum(sum) * (1.0f / D);
+    float ss = 0.f;
+#pragma unroll
+    for (int s2 = 0; s2 < STEPS; s2++)
+#pragma unroll
+      for (int u = 0; u < 8; u++) {
+        const float d = (float)of[0][s2][u] - mean;
+        ss += d * d;
+      }
+    const float rstd = 1.0f / sqrtf(xgroups_sum(ss) * (1.0f / D) + eps_out);
+#pragma unroll
+    for (int s2 = 0; s2 < STEPS; s2++)
+#pragma unroll
+      for (int u = 0; u < 8; u++) of[0][s2][u] = (half_t)(((float)of[0][s2][u] - mean) * rstd);
+    f4 y[1][8];
+    zero_acc(y);
+    mma_rows_grouped<T, 1, 8, 1>(y, of, Wp, LDW);
+#pragma unroll
+    for (int cb = 0; cb < 8; cb++) {
+      const f4 bp = *reinterpret_cast<const f4*>(Bp + 16 * cb + 4 * g);
+#pragma unroll
+      for (int e = 0; e < 4; e++) y[0][cb][e] = (y[0][cb][e] + bp[e]) * (float)gate[cb][e];
+    }
+    resid_ln_apply<T, 1>(y, zv, zrow, z, lnw, lnb, eps_next, xn_next);
+#pragma unroll
+    for (int u = 0; u < 4; u++) ob[u] = obn[u];
+#pragma unroll
+    for (int s2 = 0; s2 < STEPS; s2++) xf[0][s2] = xfn[0][s2];
+  }
+}
+
 // ---------------------------------------------------------------- triangle attention projection
 // Persistent like trimul_proj. Rows of w: q [0, D), k [D, 2D), v [2D, 3D), g [3D, 4D), triangle bias [4D, 4D + H)
 // (H * C = D). A launch stages the rows [r_lo, r_hi) of that list with the bias block padded to 16 zero rows
@@ -601,10 +727,28 @@ static hipError_t tm_tail(const void* o, const float* now, const float* nob, flo
   return hipGetLastError();
 }
 
+static hipError_t tm_tail_f16(const void* o, const float* now, const float* nob, float eps_out, const void* w_po,
+                              const void* xn, const void* w_go, float* z, int accumulate, const float* lnw,
+                              const float* lnb, float eps_next, void* xn_next, int64_t N, int64_t ld, hipStream_t st) {
+  static int cache[kMaxDevices];
+  const int resident = resident_grid(trimul_tail_f16_k, 64 * TAIL_WAVES, cache);
+  if (resident <= 0) return hipErrorInvalidDevice;
+  const int64_t ntiles = N * ((N + 15) / 16);
+  if (ntiles >= (1LL << 30)) return hipErrorInvalidValue;  // tile indices are 32-bit in the kernel
+  const dim3 grid((unsigned)std::min<int64_t>(resident, (ntiles + TAIL_WAVES - 1) / TAIL_WAVES));
+  trimul_tail_f16_k<<<grid, 64 * TAIL_WAVES, 0, st>>>(static_cast<const half_t*>(o), now, nob, eps_out,
+                                                      static_cast<const half_t*>(w_po), static_cast<const half_t*>(xn),
+                                                      static_cast<const half_t*>(w_go), z, accumulate, lnw, lnb,
+                                                      eps_next, static_cast<half_t*>(xn_next), N, ld);
+  return hipGetLastError();
+}
+
 hipError_t launch_trimul_tail(const void* o, const float* now, const float* nob, float eps_out, const void* w_po,
                               const void* xn, const void* w_go, float* z, int accumulate, const float* lnw,
                               const float* lnb, float eps_next, void* xn_next, int dt, int64_t N, int64_t ld,
                               hipStream_t st) {
+  if (dt == DT_F16)
+    return tm_tail_f16(o, now, nob, eps_out, w_po, xn, w_go, z, accumulate, lnw, lnb, eps_next, xn_next, N, ld, st);
   return dt == DT_F16 ? tm_tail<half_t>(o, now, nob, eps_out, w_po, xn, w_go, z, accumulate, lnw, lnb, eps_next,
                                         xn_next, N, ld, st)
                       : tm_tail<float>(o, now, nob, eps_out, w_po, xn, w_go, z, accumulate, lnw, lnb, eps_next,

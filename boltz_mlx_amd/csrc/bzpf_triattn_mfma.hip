@@ -71,7 +71,7 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
 
   const int64_t NN = (int64_t)N * N;
   const int t = threadIdx.x;
-  const int wave = t >> 6, l = t & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63;
   const int g = l >> 4, qi = l & 15;
   const half_t* qp = qkg + ((int64_t)h * NN + (int64_t)i * N) * C;
   const half_t* kp = qkg + ((int64_t)(H + h) * NN + (int64_t)i * N) * C;
@@ -133,6 +133,7 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
     m[tq] = -INFINITY;
   }
   const float munset = -0.5f * inf * LOG2E;
+  const float infl = inf * LOG2E;  // key-mask bias inf * (m - 1) * log2(e) = m * infl - infl
   half8 ones;
 #pragma unroll
   for (int e = 0; e < 8; e++) ones[e] = (half_t)(qi == 0 ? 1.0f : 0.0f);
@@ -144,32 +145,40 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
   const int nblk = (N + BK - 1) / BK;
   half8 kreg, vreg;
   float mraw;
+  // Row-local sources as buffer resources: each lane's offset is fixed and the block offset rides in the scalar
+  // offset, so the loads need no address arithmetic; keys past N read as zeros (range-checked).
+  constexpr int RSRC_CFG = 0x00020000;  // raw buffer, 32-bit data format
+  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)kp, 0, N * C * 2, RSRC_CFG);
+  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)vp, 0, C * ldk * 2, RSRC_CFG);
+  const int koff = (skey * C + sd8) * 2, voff = (vd * ldk + vk8) * 2;
   // bias fragments (fragment-ordered layout): 16 contiguous values per lane per 16-query tile and 64-key block
   const int njt = (N + 15) / 16, nkb = ldk / 64;
-  const half_t* bfp[2];
+  __amdgpu_buffer_rsrc_t brs[2];
 #pragma unroll
   for (int tq = 0; tq < 2; tq++) {
     int jt = qb * (WQ / 16) + 2 * wave + tq;
     if (jt >= njt) jt = njt - 1;
-    bfp[tq] = tb + ((((int64_t)h * njt + jt) * nkb) * 64 + l) * 16;
+    brs[tq] = __builtin_amdgcn_make_buffer_rsrc((void*)(tb + (((int64_t)h * njt + jt) * nkb) * 1024), 0, nkb * 2048,
+                                                RSRC_CFG);
   }
   half8 bcur[2][2];
-  // loads of block kb (clamped to the last block, so the loop issues them unconditionally)
+  // mask: lane l reads key kb * 64 + l; only the partial last block clamps (to key N - 1)
+  const float* mbase = mrow + (int64_t)l * mask_sk;
+  const float* mlast = mrow + (int64_t)(N - 1) * mask_sk;
+  // loads of block kb (kb < nblk; the loop clamps, so it issues them unconditionally)
   auto prefetch = [&](int kb) {
-    const int k0 = (kb < nblk ? kb : nblk - 1) * BK;
-    const int kk = k0 + skey < N ? k0 + skey : N - 1;
-    kreg = *reinterpret_cast<const half8*>(kp + (int64_t)kk * C + sd8);
-    vreg = *reinterpret_cast<const half8*>(vp + (int64_t)vd * ldk + k0 + vk8);
-    const int km = k0 + l < N ? k0 + l : N - 1;
-    mraw = mrow[(int64_t)km * mask_sk];
+    kreg = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(krs, koff, kb * BK * C * 2, 0));
+    vreg = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff, kb * BK * 2, 0));
+    const float* mp = mbase + (int64_t)kb * BK * mask_sk;
+    if (kb * BK + BK > N) mp = kb * BK + l < N ? mp : mlast;
+    mraw = *mp;
   };
   auto prefetch_bias = [&](int kb) {
-    const int kc = kb < nblk ? kb : nblk - 1;
 #pragma unroll
     for (int tq = 0; tq < 2; tq++) {
-      const half_t* bq = bfp[tq] + (int64_t)kc * 1024;
-      bcur[tq][0] = *reinterpret_cast<const half8*>(bq);
-      bcur[tq][1] = *reinterpret_cast<const half8*>(bq + 8);
+      bcur[tq][0] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(brs[tq], l * 32, kb * 2048, 0));
+      bcur[tq][1] =
+          __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(brs[tq], l * 32 + 16, kb * 2048, 0));
     }
   };
   // Issue order pinned to the loop's (K, V^T, mask, then bias): the wait counter merges the prologue and the loop
@@ -192,11 +201,11 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
     }
     *reinterpret_cast<half8*>(Vb + vd * LDV + vk8) = vreg;
     // key-mask bias of key k0 + l (keys past N: -inf); uniform across waves, so each wave decides by itself
-    const float mbias = k0 + l < N ? inf * (mraw - 1.0f) * LOG2E : -INFINITY;
+    const float mbias = k0 + l < N ? fmaf(mraw, infl, -infl) : -INFINITY;
     const bool masked = __any(mbias != 0.0f);
     if (masked) Mb[wave][l] = mbias;
     __syncthreads();
-    prefetch(kb + 1);
+    prefetch(kb + 1 < nblk ? kb + 1 : nblk - 1);
 
     half8 kf[4];
 #pragma unroll
@@ -240,7 +249,7 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
         }
       }
     }
-    prefetch_bias(kb + 1);  // the bias registers are free once the logits are formed
+    prefetch_bias(kb + 1 < nblk ? kb + 1 : nblk - 1);  // the bias registers are free once the logits are formed
     float mloc[2];
 #pragma unroll
     for (int tq = 0; tq < 2; tq++) {

@@ -22,16 +22,21 @@ constexpr int D = 128;
 template <typename T> constexpr int ldw_of() { return D + Pad<T>::v; }
 
 // ---------------------------------------------------------------- triangle multiplication projection
-// Persistent, one 1024-thread workgroup per CU. The launch covers output channels [c_lo, c_lo + PCH): the projection
-// rows c_lo.. and gate rows 2D + c_lo.. of w (PCH = 256 in fp16: all of them; 128 in fp32, two launches) are staged in
-// LDS once; each wave then streams tiles of TW positions (i, k0 .. k0 + TW) over the padded rows of length ld,
-// computing (ROWS orientation) runs of 16 bytes per channel for ab[c][i][k] (incoming: xn read at (k, i)).
+// Persistent, one 768-thread workgroup per CU (12 waves, up to 168 VGPRs each). The launch covers output channels
+// [c_lo, c_lo + PCH): the projection rows c_lo.. and gate rows 2D + c_lo.. of w (PCH = 256 in fp16: all of them;
+// 128 in fp32, two launches) are staged in LDS once; each wave then streams tiles of 2 TW positions
+// (i, k0 .. k0 + 2 TW) over the padded rows of length ld as two halves of TW, computing (ROWS orientation) two
+// 16-byte runs per channel: a whole 128-byte line of ab[c][i][k] (fp16) per channel row and tile, written by one
+// wave with two adjacent stores (incoming: xn read at (k, i)). Two halves of row fragments leave no registers for
+// loading the next tile ahead; 12 waves per CU cover the load latency instead.
 template <typename T> constexpr int proj_ch() { return sizeof(T) == 2 ? 256 : 128; }
+constexpr int PROJ_WAVES = 12;
 
 template <typename T>
-__global__ __launch_bounds__(1024) void trimul_proj_k(const T* __restrict__ xn, const T* __restrict__ w,
-                                                      const float* __restrict__ mask, float scale, int incoming,
-                                                      T* __restrict__ ab, int64_t N, int64_t ld, int c_lo) {
+__global__ __launch_bounds__(64 * PROJ_WAVES) void trimul_proj_k(const T* __restrict__ xn, const T* __restrict__ w,
+                                                                 const float* __restrict__ mask, float scale,
+                                                                 int incoming, T* __restrict__ ab, int64_t N,
+                                                                 int64_t ld, int c_lo) {
   using RT = RunTile<T>;
   constexpr int RB = RT::RB, TW = RT::TW, STEPS = RG<T>::STEPS, LDW = ldw_of<T>(), PCH = proj_ch<T>();
   __shared__ LDS_ALIGN T Ws[2 * PCH * LDW];  // rows [0, PCH): projections, [PCH, 2 PCH): gates
@@ -39,53 +44,52 @@ __global__ __launch_bounds__(1024) void trimul_proj_k(const T* __restrict__ xn, 
               [&](int r) { return w + (int64_t)(r < PCH ? c_lo + r : 2 * D + c_lo + r - PCH) * D; });
   __syncthreads();
   const int l = threadIdx.x & 63, g = l >> 4, r = l & 15;
-  const int tpr = (int)(ld / TW), ntiles = (int)N * tpr, stride = gridDim.x * 16;
-  int t = grid_wave(16);
+  const int tpr = (int)(ld / (2 * TW)), ntiles = (int)N * tpr, stride = gridDim.x * PROJ_WAVES;
+  int t = grid_wave(PROJ_WAVES);
   if (t >= ntiles) return;
 
-  typename RG<T>::frag x[RB][STEPS];
-  float mk[RB];  // mask * scale of the row this lane loads (0 past N: padding columns are written as 0)
-  const auto load = [&](int tt, typename RG<T>::frag (&xx)[RB][STEPS], float (&mm)[RB]) {
-    const int i = tt / tpr, k0 = (tt - i * tpr) * TW;
+  typedef typename RG<T>::frag Frag;
+  Frag x[2][RB][STEPS];
+  float mk[2][RB];  // mask * scale of the rows this lane loads (0 past N: padding columns are written as 0)
+  const auto load = [&](int tt, Frag (&xx)[2][RB][STEPS], float (&mm)[2][RB]) {
+    const int i = tt / tpr, k0 = (tt - i * tpr) * 2 * TW;
 #pragma unroll
-    for (int rb = 0; rb < RB; rb++) {
-      const int64_t k = k0 + RT::pos(rb, r), kc = k < N ? k : N - 1;
-      const int64_t src = incoming ? kc * N + i : (int64_t)i * N + kc;
-      RG<T>::load_row(xx[rb], xn + src * D, g);
-      mm[rb] = k < N ? mask[src] * scale : 0.0f;
-    }
+    for (int hh = 0; hh < 2; hh++)
+#pragma unroll
+      for (int rb = 0; rb < RB; rb++) {
+        const int64_t k = k0 + hh * TW + RT::pos(rb, r), kc = k < N ? k : N - 1;
+        const int64_t src = incoming ? kc * N + i : (int64_t)i * N + kc;
+        RG<T>::load_row(xx[hh][rb], xn + src * D, g);
+        mm[hh][rb] = k < N ? mask[src] * scale : 0.0f;
+      }
   };
-  load(t, x, mk);
   for (; t < ntiles; t += stride) {
-    const int i = t / tpr, k0 = (t - i * tpr) * TW;
-    float mo[RB][4];  // mask of this lane's output positions RUN g + 4 rb + e, loaded by lane 4 g + e
+    load(t, x, mk);
+    const int i = t / tpr, k0 = (t - i * tpr) * 2 * TW;
+    float mo[2][RB][4];  // mask of this lane's output positions RUN g + 4 rb + e of each half, from lane 4 g + e
 #pragma unroll
-    for (int rb = 0; rb < RB; rb++)
-#pragma unroll
-      for (int e = 0; e < 4; e++) mo[rb][e] = __shfl(mk[rb], 4 * g + e);
-    typename RG<T>::frag xnext[RB][STEPS];
-    float mnext[RB];
-    load(min(t + stride, ntiles - 1), xnext, mnext);
-    T* dst = ab + ((int64_t)(c_lo + r) * N + i) * ld + k0 + RT::RUN * g;
-    for (int cb = 0; cb < PCH / 16; cb++) {
-      f4 pa[RB][1], ga[RB][1];
-      zero_acc(pa);
-      zero_acc(ga);
-      mma_rows<T, RB, 1, true>(pa, x, Ws + 16 * cb * LDW, LDW);
-      mma_rows<T, RB, 1, true>(ga, x, Ws + (PCH + 16 * cb) * LDW, LDW);
-      float v[RT::RUN];
+    for (int hh = 0; hh < 2; hh++)
 #pragma unroll
       for (int rb = 0; rb < RB; rb++)
 #pragma unroll
-        for (int e = 0; e < 4; e++) v[4 * rb + e] = pa[rb][0][e] * sigmoidf_(ga[rb][0][e]) * mo[rb][e];
-      st_run(dst + (int64_t)16 * cb * N * ld, v);
+        for (int e = 0; e < 4; e++) mo[hh][rb][e] = __shfl(mk[hh][rb], 4 * g + e);
+    T* dst = ab + ((int64_t)(c_lo + r) * N + i) * ld + k0 + RT::RUN * g;
+    for (int cb = 0; cb < PCH / 16; cb++) {
+#pragma unroll
+      for (int hh = 0; hh < 2; hh++) {
+        f4 pa[RB][1], ga[RB][1];
+        zero_acc(pa);
+        zero_acc(ga);
+        mma_rows<T, RB, 1, true>(pa, x[hh], Ws + 16 * cb * LDW, LDW);
+        mma_rows<T, RB, 1, true>(ga, x[hh], Ws + (PCH + 16 * cb) * LDW, LDW);
+        float v[RT::RUN];
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+          for (int e = 0; e < 4; e++) v[4 * rb + e] = pa[rb][0][e] * sigmoidf_(ga[rb][0][e]) * mo[hh][rb][e];
+        st_run(dst + (int64_t)16 * cb * N * ld + hh * TW, v);
+      }
       __builtin_amdgcn_sched_barrier(0);
-    }
-#pragma unroll
-    for (int rb = 0; rb < RB; rb++) {
-      mk[rb] = mnext[rb];
-#pragma unroll
-      for (int s = 0; s < STEPS; s++) x[rb][s] = xnext[rb][s];
     }
   }
 }
@@ -695,13 +699,13 @@ template <typename T>
 static hipError_t tm_proj(const void* xn, const void* w, const float* mask, float scale, int incoming, void* ab,
                           int64_t N, int64_t ld, hipStream_t st) {
   static int cache[kMaxDevices];
-  const int resident = resident_grid(trimul_proj_k<T>, 1024, cache);
+  const int resident = resident_grid(trimul_proj_k<T>, 64 * PROJ_WAVES, cache);
   if (resident <= 0) return hipErrorInvalidDevice;
-  const int64_t ntiles = N * (ld / RunTile<T>::TW);  // ld is a multiple of 64
+  const int64_t ntiles = N * (ld / (2 * RunTile<T>::TW));  // ld is a multiple of 64
   if (ntiles >= (1LL << 30)) return hipErrorInvalidValue;  // tile indices are 32-bit in the kernel
-  const dim3 grid((unsigned)std::min<int64_t>(resident, (ntiles + 15) / 16));
+  const dim3 grid((unsigned)std::min<int64_t>(resident, (ntiles + PROJ_WAVES - 1) / PROJ_WAVES));
   for (int c_lo = 0; c_lo < 2 * D; c_lo += proj_ch<T>()) {
-    trimul_proj_k<T><<<grid, 1024, 0, st>>>(static_cast<const T*>(xn), static_cast<const T*>(w), mask, scale,
+    trimul_proj_k<T><<<grid, 64 * PROJ_WAVES, 0, st>>>(static_cast<const T*>(xn), static_cast<const T*>(w), mask, scale,
                                             incoming, static_cast<T*>(ab), N, ld, c_lo);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;

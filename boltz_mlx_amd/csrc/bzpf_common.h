@@ -10,6 +10,7 @@ typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 typedef float f4 __attribute__((ext_vector_type(4)));
 typedef float f2 __attribute__((ext_vector_type(2)));
+typedef float f16x __attribute__((ext_vector_type(16)));  // accumulator of one 32 x 32 MFMA block
 
 #define LDS_ALIGN __attribute__((aligned(16)))
 
@@ -28,6 +29,14 @@ template <> __device__ __forceinline__ half_t from_f<half_t>(float x) { return (
 // exp(-x) = inf gives rcp(inf) = 0, so both saturate like the exact forms.
 __device__ __forceinline__ float sigmoidf_(float x) { return __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
 __device__ __forceinline__ float siluf_(float x) { return x * __builtin_amdgcn_rcpf(1.0f + __expf(-x)); }
+
+// A wave-uniform pointer the compiler must treat as redefined where this is called. Inside a tile loop it keeps the
+// per-lane addresses derived from the pointer (64-bit pairs per lane) from being hoisted out of the loop, where they
+// outlive the register budget and spill; recomputing them costs one 64-bit add each per tile.
+template <typename P> __device__ __forceinline__ P* opaque_ptr(P* p) {
+  asm volatile("" : "+s"(p));
+  return p;
+}
 
 // One 16x16 output block of D = A * B^T per MFMA, A and B both K-contiguous ("NT").
 // Lane l holds A[l%16][k0 + (l/16)*KP .. +KP-1] and B[l%16][same k] (B row = output column);

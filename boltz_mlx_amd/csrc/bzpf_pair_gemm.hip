@@ -206,6 +206,7 @@ __global__ __launch_bounds__(64 * TAIL_WAVES) void trimul_tail_f16_k(
   __shared__ LDS_ALIGN T Wg[D * LDW];
   __shared__ LDS_ALIGN T Wp[D * LDW];  // p_out with gamma_out folded into its columns
   __shared__ LDS_ALIGN float Bp[D];    // p_out . beta_out
+  __shared__ LDS_ALIGN float Lw[D], Lb[D];  // the next LayerNorm (read per lane from LDS, not by hoisted pointers)
   __shared__ LDS_ALIGN T Ts[TAIL_WAVES][16 * LDT];
   lds_rows<T>(Wg, LDW, D, D, [&](int r) { return w_go + (int64_t)r * D; });
   for (int e = threadIdx.x; e < D * D / 8; e += blockDim.x) {
@@ -215,6 +216,10 @@ __global__ __launch_bounds__(64 * TAIL_WAVES) void trimul_tail_f16_k(
 #pragma unroll
     for (int u = 0; u < 8; u++) sv[u] = (half_t)((float)wv[u] * now[c + u]);
     *reinterpret_cast<half8*>(Wp + r * LDW + c) = sv;
+  }
+  if (lnw != nullptr && threadIdx.x < D) {
+    Lw[threadIdx.x] = lnw[threadIdx.x];
+    Lb[threadIdx.x] = lnb[threadIdx.x];
   }
   if (threadIdx.x < 4 * D) {  // 4 lanes per output channel, 32 inputs each
     const int c = threadIdx.x >> 2, q = threadIdx.x & 3;
@@ -238,11 +243,13 @@ __global__ __launch_bounds__(64 * TAIL_WAVES) void trimul_tail_f16_k(
   int t = grid_wave(TAIL_WAVES);
   if (t >= ntiles) return;
   const int ocg = l >> 1, opc = l & 1;
+  // o element offsets are 32-bit (the launcher checks D * N * ld < 2^31): channel rows of this lane, one apart
+  const uint32_t ochan = (uint32_t)(4 * ocg) * (uint32_t)N * (uint32_t)ld, orow = (uint32_t)N * (uint32_t)ld;
   const auto load = [&](int tt, half8 (&ob)[4], typename RG<T>::frag (&xf)[1][STEPS]) {
     const int i = tt / tpr, j0 = (tt - i * tpr) * 16;
+    const uint32_t oo = ochan + (uint32_t)i * (uint32_t)ld + (uint32_t)(j0 + 8 * opc);
 #pragma unroll
-    for (int u = 0; u < 4; u++)
-      ob[u] = *reinterpret_cast<const half8*>(o + ((int64_t)(4 * ocg + u) * N + i) * ld + j0 + 8 * opc);
+    for (int u = 0; u < 4; u++) ob[u] = *reinterpret_cast<const half8*>(o + (oo + u * orow));
     const int64_t jc = j0 + r < N ? j0 + r : N - 1;
     RG<T>::load_row(xf[0], xn + ((int64_t)i * N + jc) * D, g);
   };
@@ -253,8 +260,10 @@ __global__ __launch_bounds__(64 * TAIL_WAVES) void trimul_tail_f16_k(
     const int i = t / tpr, j0 = (t - i * tpr) * 16;
     const int64_t zr = j0 + r < N ? (int64_t)i * N + j0 + r : -1;
     const auto zrow = [&](int) { return zr; };
+    float* zt = opaque_ptr(z);
+    half_t* xnt = opaque_ptr(xn_next);
     f4 zv[1][8];
-    load_z_rows<1>(zv, zrow, z, accumulate);
+    load_z_rows<1>(zv, zrow, zt, accumulate);
     // o block -> [position][channel] rows of the wave's tile
 #pragma unroll
     for (int v = 0; v < 8; v++)
@@ -304,7 +313,7 @@ __global__ __launch_bounds__(64 * TAIL_WAVES) void trimul_tail_f16_k(
 #pragma unroll
       for (int e = 0; e < 4; e++) y[0][cb][e] = (y[0][cb][e] + bp[e]) * (float)gate[cb][e];
     }
-    resid_ln_apply<T, 1>(y, zv, zrow, z, lnw, lnb, eps_next, xn_next);
+    resid_ln_apply<T, 1>(y, zv, zrow, zt, lnw != nullptr ? Lw : nullptr, Lb, eps_next, xnt);
 #pragma unroll
     for (int u = 0; u < 4; u++) ob[u] = obn[u];
 #pragma unroll
@@ -751,7 +760,7 @@ hipError_t launch_trimul_tail(const void* o, const float* now, const float* nob,
                               const void* xn, const void* w_go, float* z, int accumulate, const float* lnw,
                               const float* lnb, float eps_next, void* xn_next, int dt, int64_t N, int64_t ld,
                               hipStream_t st) {
-  if (dt == DT_F16)
+  if (dt == DT_F16 && (int64_t)D * N * ld < (1LL << 31))
     return tm_tail_f16(o, now, nob, eps_out, w_po, xn, w_go, z, accumulate, lnw, lnb, eps_next, xn_next, N, ld, st);
   return dt == DT_F16 ? tm_tail<half_t>(o, now, nob, eps_out, w_po, xn, w_go, z, accumulate, lnw, lnb, eps_next,
                                         xn_next, N, ld, st)

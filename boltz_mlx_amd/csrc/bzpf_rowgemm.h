@@ -156,7 +156,9 @@ __device__ __forceinline__ void st4(half_t* p, f4 v) {
 }
 
 // The residual rows the epilogue below adds to, in the accumulator layout (lane: 4 channels 16 cb + 4 g .. +3 of its
-// row); zeros where accumulate == 0 or the lane has no row. Issued ahead of the MFMAs so the loads overlap them.
+// row); zeros where accumulate == 0. A lane with no row (zrow < 0) loads row 0 instead: its values only enter the
+// reductions of its own row, which is never stored, and the loads stay unconditional (no per-lane branches).
+// Issued ahead of the MFMAs so the loads overlap them.
 template <int RB, typename ZRow>
 __device__ __forceinline__ void load_z_rows(f4 (&zv)[RB][8], ZRow zrow, const float* __restrict__ z, int accumulate) {
   constexpr int D = 128;
@@ -164,15 +166,16 @@ __device__ __forceinline__ void load_z_rows(f4 (&zv)[RB][8], ZRow zrow, const fl
 #pragma unroll
   for (int rb = 0; rb < RB; rb++) {
     const int64_t zr = zrow(rb);
+    const float* zp = z + (zr >= 0 ? zr : 0) * D + 4 * g;  // one row base; column blocks are immediate offsets
 #pragma unroll
-    for (int cb = 0; cb < 8; cb++)
-      zv[rb][cb] = (accumulate && zr >= 0) ? ld4(z + zr * D + 16 * cb + 4 * g) : f4{0.f, 0.f, 0.f, 0.f};
+    for (int cb = 0; cb < 8; cb++) zv[rb][cb] = accumulate ? ld4(zp + 16 * cb) : f4{0.f, 0.f, 0.f, 0.f};
   }
 }
 
 // Residual + LayerNorm epilogue on the transposed accumulator of 8 column blocks (D = 128 channels): for each of the
 // lane's rows, z[zr] = zv + y, then xn_next[zr] = LN(z[zr]) when lnw != nullptr. zrow(rb) returns the z row of the
-// lane's row in block rb (< 0: no row; the lane still joins the cross-lane reductions).
+// lane's row in block rb (< 0: no row; the lane still joins the cross-lane reductions, which only mix the 4 lanes
+// of one row, and stores nothing).
 template <typename TO, int RB, typename ZRow>
 __device__ __forceinline__ void resid_ln_apply(const f4 (&y)[RB][8], const f4 (&zv)[RB][8], ZRow zrow,
                                                float* __restrict__ z, const float* __restrict__ lnw,
@@ -182,14 +185,19 @@ __device__ __forceinline__ void resid_ln_apply(const f4 (&y)[RB][8], const f4 (&
 #pragma unroll
   for (int rb = 0; rb < RB; rb++) {
     const int64_t zr = zrow(rb);
+    // one row base per pointer; the column blocks 16 cb are immediate offsets (no per-block 64-bit addresses)
+    const int64_t rowoff = (zr >= 0 ? zr : 0) * D + 4 * g;
+    float* zp = z + rowoff;
     f4 v[8];
     float s = 0.f;
 #pragma unroll
     for (int cb = 0; cb < 8; cb++) {
-      const int c = 16 * cb + 4 * g;
       v[cb] = y[rb][cb] + zv[rb][cb];
-      if (zr >= 0) st4(z + zr * D + c, v[cb]);
       s += v[cb][0] + v[cb][1] + v[cb][2] + v[cb][3];
+    }
+    if (zr >= 0) {
+#pragma unroll
+      for (int cb = 0; cb < 8; cb++) st4(zp + 16 * cb, v[cb]);
     }
     if (lnw == nullptr) continue;
     const float mean = xgroups_sum(s) * (1.0f / D);
@@ -201,10 +209,11 @@ __device__ __forceinline__ void resid_ln_apply(const f4 (&y)[RB][8], const f4 (&
     }
     const float rstd = 1.0f / sqrtf(xgroups_sum(ss) * (1.0f / D) + eps);
     if (zr < 0) continue;
+    TO* xp = xn_next + rowoff;
 #pragma unroll
     for (int cb = 0; cb < 8; cb++) {
       const int c = 16 * cb + 4 * g;
-      st4(xn_next + zr * D + c, (v[cb] - mean) * rstd * ld4(lnw + c) + ld4(lnb + c));
+      st4(xp + 16 * cb, (v[cb] - mean) * rstd * ld4(lnw + c) + ld4(lnb + c));
     }
   }
 }

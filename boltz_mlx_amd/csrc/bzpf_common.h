@@ -97,14 +97,16 @@ __device__ __forceinline__ void zero_acc(f4 (&acc)[MB][NB]) {
 template <typename T> struct Vec16 { static constexpr int n = 16 / sizeof(T); };
 
 // Triangle-bias layout: element (head h, query j, key k) of the [H][N][N] bias, stored in the order the MFMA
-// attention core consumes it. For a 16-query tile jt and a 64-key block kb, lane l = 16*g + qi of a wave owns the
-// 16 values of query 16*jt + qi at keys 64*kb + 16*t4 + 4*g + e (t4, e < 4), contiguous in that order, so a lane
-// loads its bias with two 16-byte loads and a wave reads 2 KB contiguously. ldk = N rounded up to 64.
+// attention core consumes it (the accumulator layout of v_mfma_f32_32x32x16_f16). For a 32-query tile jt and a
+// 64-key block kb, lane l = 32*hl + q of a wave owns the 32 values of query 32*jt + q at keys
+// 64*kb + 32*kt + 8*p + 4*hl + e (kt < 2, p < 4, e < 4), contiguous in that order, so a lane loads its bias with four
+// 16-byte loads and a wave reads 4 KB contiguously. ldk = N rounded up to 64; 4 consecutive keys 4m .. 4m + 3 are
+// contiguous.
 __host__ __device__ inline int64_t tb_offset(int64_t h, int64_t j, int64_t k, int64_t N, int64_t ldk) {
-  const int64_t njt = (N + 15) / 16, nkb = ldk / 64;
-  const int64_t jt = j >> 4, qi = j & 15, kb = k >> 6, kk = k & 63;
-  const int64_t t4 = kk >> 4, g = (kk >> 2) & 3, e = kk & 3;
-  return (((h * njt + jt) * nkb + kb) * 64 + (g * 16 + qi)) * 16 + t4 * 4 + e;
+  const int64_t njt = (N + 31) / 32, nkb = ldk / 64;
+  const int64_t jt = j >> 5, q = j & 31, kb = k >> 6, kk = k & 63;
+  const int64_t kt = kk >> 5, p = (kk >> 3) & 3, hl = (kk >> 2) & 1, e = kk & 3;
+  return (((h * njt + jt) * nkb + kb) * 64 + (hl * 32 + q)) * 32 + kt * 16 + p * 4 + e;
 }
 struct alignas(16) U128 { uint32_t w[4]; };
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));

@@ -1,17 +1,20 @@
-// fp16 flash triangle-attention core on MFMA (v_mfma_f32_16x16x32_f16), head width C = 32.
+// fp16 flash triangle-attention core on MFMA (v_mfma_f32_32x32x16_f16), head width C = 32.
 //
-// Work unit: one (head h, row i, 128 queries); 4 waves of 32 queries (two 16-query tiles each). The logits are
-// formed transposed, S^T = K Q^T + Cinit (A = a 16-key tile of K from LDS, shared by both query tiles; B = the
-// tile's Q fragment, held in registers for the whole row), so every lane owns one query (l % 16) and 4 keys of each
-// 16-key tile: a query's softmax statistics live in lanes l, l^16, l^32, l^48 and need two cross-lane steps per key
-// block. The MFMA accumulator is initialised with tri_bias - m (plus the key-mask bias in blocks that hold a masked
-// key), so the matrix core adds the bias and subtracts the running maximum. The maximum is raised lazily: only when
-// a block's logits exceed it by more than 2^8 (a wave-uniform branch) are the accumulators rescaled. The
-// probabilities P^T are already laid out as the B operand of O^T = V^T P^T (V^T tiles arrive transposed from the
-// projection), so P never leaves registers, and a third MFMA tile whose A operand is a constant row of ones
-// accumulates the softmax denominator on the matrix cores. The next key block's K, V^T, bias and mask are loaded
-// into registers while the current block computes; the bias arrives in the fragment-ordered layout (tb_offset), two
-// 16-byte loads per lane and tile, without passing through LDS.
+// Work unit: one (head h, row i, 128 queries); 4 waves of 32 queries. The 32 x 32 MFMA form is used throughout: on
+// gfx950 it delivers about 1.6x the FLOP rate of the 16 x 16 x 32 form and overlaps better with the VALU softmax.
+// The logits are formed transposed, S^T = K Q^T + Cinit, one 32-key x 32-query tile per MFMA pair (A = 32 keys of K
+// from LDS, B = the wave's Q fragment, held in registers for the whole row), so lane l owns query l % 32 and 16 keys
+// of each 32-key tile (8 (e / 4) + 4 (l / 32) + e % 4 in accumulator element e): a query's softmax statistics live
+// in lanes l and l ^ 32 and need one cross-lane step per key block. The MFMA accumulator is initialised with
+// tri_bias - m (plus the key-mask bias in blocks that hold a masked key), so the matrix core adds the bias and
+// subtracts the running maximum. The maximum is raised lazily: only when a block's logits exceed it by more than
+// 2^8 (a wave-uniform branch) are the accumulators rescaled. The probabilities P^T, rounded to fp16, are already the
+// B operand of O^T = V^T P^T for the key order the accumulator gives each lane (keys 4h .. 4h + 3, 8 + 4h .. 8 + 4h
+// + 3 of every 16-key slab, h = l / 32); V^T is read from LDS in the same order, so P never leaves registers. The
+// softmax denominator is accumulated from the fp16 probabilities with v_dot2_f32_f16 (exact products by one, fp32
+// sums). The next key block's K, V^T, bias and mask are loaded into registers while the current block computes;
+// the bias arrives in the fragment-ordered layout (tb_offset), four 16-byte loads per lane and block, without
+// passing through LDS.
 // Logits are base 2: the projection stores q * log2(e)/sqrt(C) and tri_bias * log2(e); the key-mask bias is
 // inf*(m-1)*log2(e). A row whose keys are all masked gets uniform weights over its N keys, which is what the
 // reference's rounding gives (every logit rounds to -inf*log2(e); boltz_mlx/kernels.py:579-581). Softmax and
@@ -38,6 +41,20 @@ __device__ __forceinline__ float half_plus(uint32_t pair, float c) {
   else
     asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(pair), "v"(c));
   return r;
+}
+
+typedef _Float16 half2_t __attribute__((ext_vector_type(2)));
+
+// max / sum of a value over the two lanes l and l ^ 32 (the two halves of the wave)
+__device__ __forceinline__ float halves_max(float v) {
+  const unsigned u = __float_as_uint(v);
+  const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(a[0]), __uint_as_float(a[1]));
+}
+__device__ __forceinline__ float halves_sum(float v) {
+  const unsigned u = __float_as_uint(v);
+  const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return __uint_as_float(a[0]) + __uint_as_float(a[1]);
 }
 
 template <int C>
@@ -72,16 +89,15 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
   const int64_t NN = (int64_t)N * N;
   const int t = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63;
-  const int g = l >> 4, qi = l & 15;
+  const int hl = l >> 5, qi = l & 31;  // lane half, query of the lane within the wave's tile
   const half_t* qp = qkg + ((int64_t)h * NN + (int64_t)i * N) * C;
   const half_t* kp = qkg + ((int64_t)(H + h) * NN + (int64_t)i * N) * C;
   const half_t* gp = qkg + ((int64_t)(2 * H + h) * NN + (int64_t)i * N) * C;
   const half_t* vp = vt + ((int64_t)h * N + i) * C * ldk;
   const float* mrow = mask + (int64_t)i * mask_si;
-
-  int jq[2];
-#pragma unroll
-  for (int tq = 0; tq < 2; tq++) jq[tq] = qb * WQ + 32 * wave + 16 * tq + qi;
+  const int jq = qb * WQ + 32 * wave + qi;
+  // channels of the lane's accumulator (O^T rows) and of its gate / output vectors: 8 q + 4 hl + e, q < 4
+  half_t* oq = out + ((int64_t)i * N + jq) * (int64_t)(H * C) + h * C;
 
   // A row whose keys are all masked gets uniform weights over its N keys (every logit rounds to the same value in
   // the reference): out = sigmoid(g) * mean_k v[k], no key loop. The first 64 keys settle it for almost every row;
@@ -103,15 +119,11 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
       if (part == 0) Vmean[d] = sum / (float)N;
     }
     __syncthreads();
+    if (jq < N) {
 #pragma unroll
-    for (int tq = 0; tq < 2; tq++) {
-      if (jq[tq] >= N) continue;
-      const half_t* gq = gp + (int64_t)jq[tq] * C;
-      half_t* oq = out + ((int64_t)i * N + jq[tq]) * (int64_t)(H * C) + h * C;
-#pragma unroll
-      for (int dt = 0; dt < 2; dt++) {
-        const int d0 = 16 * dt + 4 * g;
-        const half4 gv = *reinterpret_cast<const half4*>(gq + d0);
+      for (int q = 0; q < 4; q++) {
+        const int d0 = 8 * q + 4 * hl;
+        const half4 gv = *reinterpret_cast<const half4*>(gp + (int64_t)jq * C + d0);
         half4 ov;
 #pragma unroll
         for (int e = 0; e < 4; e++) ov[e] = (half_t)(Vmean[d0 + e] * sigmoidf_((float)gv[e]));
@@ -121,22 +133,20 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
     return;
   }
 
+  // Q fragments for the two 16-channel slabs: lane (query qi, half hl) holds channels 16 m + 8 hl .. + 7
   half8 qf[2];
-  f4 oacc[2][3];
-  float m[2];
+  {
+    const int jc = jq < N ? jq : N - 1;
 #pragma unroll
-  for (int tq = 0; tq < 2; tq++) {
-    const int jc = jq[tq] < N ? jq[tq] : N - 1;
-    qf[tq] = *reinterpret_cast<const half8*>(qp + (int64_t)jc * C + g * 8);
-#pragma unroll
-    for (int dt = 0; dt < 3; dt++) oacc[tq][dt] = f4{0.f, 0.f, 0.f, 0.f};
-    m[tq] = -INFINITY;
+    for (int m = 0; m < 2; m++) qf[m] = *reinterpret_cast<const half8*>(qp + (int64_t)jc * C + 16 * m + 8 * hl);
   }
+  f16x oacc;
+#pragma unroll
+  for (int e = 0; e < 16; e++) oacc[e] = 0.f;
+  float m_run = -INFINITY, lsum = 0.f;
   const float munset = -0.5f * inf * LOG2E;
   const float infl = inf * LOG2E;  // key-mask bias inf * (m - 1) * log2(e) = m * infl - infl
-  half8 ones;
-#pragma unroll
-  for (int e = 0; e < 8; e++) ones[e] = (half_t)(qi == 0 ? 1.0f : 0.0f);
+  const half2_t one2 = half2_t{(half_t)1.0f, (half_t)1.0f};
 
   // staging roles: K rows (64 keys x 32 channels) and V^T rows (32 channels x 64 keys), one 16-byte vector each;
   // every wave loads the raw mask values of the block's 64 keys (lane l: key k0 + l)
@@ -151,17 +161,16 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
   const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)kp, 0, N * C * 2, RSRC_CFG);
   const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)vp, 0, C * ldk * 2, RSRC_CFG);
   const int koff = (skey * C + sd8) * 2, voff = (vd * ldk + vk8) * 2;
-  // bias fragments (fragment-ordered layout): 16 contiguous values per lane per 16-query tile and 64-key block
-  const int njt = (N + 15) / 16, nkb = ldk / 64;
-  __amdgpu_buffer_rsrc_t brs[2];
-#pragma unroll
-  for (int tq = 0; tq < 2; tq++) {
-    int jt = qb * (WQ / 16) + 2 * wave + tq;
+  // bias fragments (fragment-ordered layout): 32 contiguous values per lane per 32-query tile and 64-key block
+  const int njt = (N + 31) / 32, nkb = ldk / 64;
+  __amdgpu_buffer_rsrc_t brs;
+  {
+    int jt = qb * (WQ / 32) + wave;
     if (jt >= njt) jt = njt - 1;
-    brs[tq] = __builtin_amdgcn_make_buffer_rsrc((void*)(tb + (((int64_t)h * njt + jt) * nkb) * 1024), 0, nkb * 2048,
-                                                RSRC_CFG);
+    brs = __builtin_amdgcn_make_buffer_rsrc((void*)(tb + (((int64_t)h * njt + jt) * nkb) * 2048), 0, nkb * 4096,
+                                            RSRC_CFG);
   }
-  half8 bcur[2][2];
+  half8 bcur[4];  // bias of keys 32 kt + 8 (e / 4) + 4 hl + e % 4: elements 16 kt + e of the lane's 32
   // mask: lane l reads key kb * 64 + l; only the partial last block clamps (to key N - 1)
   const float* mbase = mrow + (int64_t)l * mask_sk;
   const float* mlast = mrow + (int64_t)(N - 1) * mask_sk;
@@ -175,11 +184,8 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
   };
   auto prefetch_bias = [&](int kb) {
 #pragma unroll
-    for (int tq = 0; tq < 2; tq++) {
-      bcur[tq][0] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(brs[tq], l * 32, kb * 2048, 0));
-      bcur[tq][1] =
-          __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(brs[tq], l * 32 + 16, kb * 2048, 0));
-    }
+    for (int v = 0; v < 4; v++)
+      bcur[v] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(brs, l * 64 + 16 * v, kb * 4096, 0));
   };
   // Issue order pinned to the loop's (K, V^T, mask, then bias): the wait counter merges the prologue and the loop
   // back edge at the loop header, and any other order there turns the first wait of every iteration into a wait
@@ -207,116 +213,87 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
     __syncthreads();
     prefetch(kb + 1 < nblk ? kb + 1 : nblk - 1);
 
-    half8 kf[4];
-#pragma unroll
-    for (int t4 = 0; t4 < 4; t4++) kf[t4] = *reinterpret_cast<const half8*>(Kb + (16 * t4 + qi) * LDK + g * 8);
     // the maximum is "unset" until a key that is not masked has been seen (a masked logit is about
     // -inf*log2(e)); subtracting such a maximum would cancel catastrophically
-    float mref[2];
-    bool unset[2];
+    const bool unset = m_run <= munset;
+    const float mref = unset ? 0.0f : m_run;
+    f16x s[2];
 #pragma unroll
-    for (int tq = 0; tq < 2; tq++) {
-      unset[tq] = m[tq] <= munset;
-      mref[tq] = unset[tq] ? 0.0f : m[tq];
-    }
-    f4 s[2][4];
-    if (masked) {
+    for (int kt = 0; kt < 2; kt++) {
+      half8 kf[2];
 #pragma unroll
-      for (int tq = 0; tq < 2; tq++)
+      for (int m = 0; m < 2; m++)
+        kf[m] = *reinterpret_cast<const half8*>(Kb + (32 * kt + qi) * LDK + 16 * m + 8 * hl);
+      f16x c;
+      if (masked) {
 #pragma unroll
-        for (int t4 = 0; t4 < 4; t4++) {
-          const half8 bh = bcur[tq][t4 >> 1];
-          const int o4 = (t4 & 1) * 4;
-          const f4 mbv = *reinterpret_cast<const f4*>(&Mb[wave][16 * t4 + 4 * g]);
-          f4 c;
+        for (int q = 0; q < 4; q++) {
+          const f4 mbv = *reinterpret_cast<const f4*>(&Mb[wave][32 * kt + 8 * q + 4 * hl]);
+          const half8 bh = bcur[2 * kt + (q >> 1)];
 #pragma unroll
-          for (int e = 0; e < 4; e++) c[e] = ((float)bh[o4 + e] + mbv[e]) - mref[tq];
-          s[tq][t4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[t4], qf[tq], c, 0, 0, 0);
+          for (int e = 0; e < 4; e++) c[4 * q + e] = ((float)bh[4 * (q & 1) + e] + mbv[e]) - mref;
         }
-    } else {
+      } else {
 #pragma unroll
-      for (int tq = 0; tq < 2; tq++) {
-        const u32x4_t bw0 = __builtin_bit_cast(u32x4_t, bcur[tq][0]);
-        const u32x4_t bw1 = __builtin_bit_cast(u32x4_t, bcur[tq][1]);
-        const float nm = -mref[tq];
+        for (int v = 0; v < 2; v++) {
+          const u32x4_t bw = __builtin_bit_cast(u32x4_t, bcur[2 * kt + v]);
 #pragma unroll
-        for (int t4 = 0; t4 < 4; t4++) {
-          const u32x4_t bw = t4 < 2 ? bw0 : bw1;
-          const int w = (t4 & 1) * 2;  // 32-bit words holding bias elements 4 (t4 & 1) .. + 3
-          const f4 c = f4{half_plus<0>(bw[w], nm), half_plus<1>(bw[w], nm), half_plus<0>(bw[w + 1], nm),
-                          half_plus<1>(bw[w + 1], nm)};
-          s[tq][t4] = __builtin_amdgcn_mfma_f32_16x16x32_f16(kf[t4], qf[tq], c, 0, 0, 0);
+          for (int w = 0; w < 4; w++) {
+            c[8 * v + 2 * w] = half_plus<0>(bw[w], -mref);
+            c[8 * v + 2 * w + 1] = half_plus<1>(bw[w], -mref);
+          }
         }
       }
+      c = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[0], qf[0], c, 0, 0, 0);
+      s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[1], qf[1], c, 0, 0, 0);
     }
     prefetch_bias(kb + 1 < nblk ? kb + 1 : nblk - 1);  // the bias registers are free once the logits are formed
-    float mloc[2];
+    float mx = fmaxf(s[0][0], s[0][1]);  // a serial chain, so each step is one v_max3 over two new values
 #pragma unroll
-    for (int tq = 0; tq < 2; tq++) {
-      float mx = -INFINITY;
+    for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-      for (int t4 = 0; t4 < 4; t4++)
-        mx = fmaxf(mx, fmaxf(fmaxf(s[tq][t4][0], s[tq][t4][1]), fmaxf(s[tq][t4][2], s[tq][t4][3])));
-      mloc[tq] = xgroups_max(mx);
-    }
+      for (int e = kt == 0 ? 2 : 0; e < 16; e += 2) mx = fmaxf(fmaxf(mx, s[kt][e]), s[kt][e + 1]);
+    const float mloc = halves_max(mx);
     // s holds logit - mref; raise the maximum only when the block exceeds it by more than 2^THRESH
-    const bool need = unset[0] || unset[1] || mloc[0] > THRESH || mloc[1] > THRESH;
-    if (__any(need)) {
+    if (__any(unset || mloc > THRESH)) {
+      const float mn = fmaxf(m_run, mloc + mref);
+      const float corr = __builtin_amdgcn_exp2f(m_run - mn);
+      oacc *= corr;
+      lsum *= corr;
+      const float delta = mref - mn;
 #pragma unroll
-      for (int tq = 0; tq < 2; tq++) {
-        const float mn = fmaxf(m[tq], mloc[tq] + mref[tq]);
-        const float corr = __builtin_amdgcn_exp2f(m[tq] - mn);
-#pragma unroll
-        for (int dt = 0; dt < 3; dt++) oacc[tq][dt] *= corr;
-        const float delta = mref[tq] - mn;
-#pragma unroll
-        for (int t4 = 0; t4 < 4; t4++) s[tq][t4] += delta;
-        m[tq] = mn;
-      }
+      for (int kt = 0; kt < 2; kt++) s[kt] += delta;
+      m_run = mn;
     }
-    // V^T fragments, read after the logits so that their registers reuse those of the K fragments
-    half8 vf[2][2];
 #pragma unroll
-    for (int s2 = 0; s2 < 2; s2++)
+    for (int kt = 0; kt < 2; kt++)
 #pragma unroll
-      for (int dt = 0; dt < 2; dt++) {
-        const half_t* vr = Vb + (16 * dt + qi) * LDV + 32 * s2 + 4 * g;
+      for (int sl = 0; sl < 2; sl++) {
+        // keys 32 kt + 16 sl + {4 hl .. 4 hl + 3, 8 + 4 hl .. 8 + 4 hl + 3}: accumulator elements 8 sl .. 8 sl + 7
+        const half_t* vr = Vb + qi * LDV + 32 * kt + 16 * sl + 4 * hl;
         const half4 lo = *reinterpret_cast<const half4*>(vr);
-        const half4 hi4 = *reinterpret_cast<const half4*>(vr + 16);
-        vf[s2][dt] = half8{lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-      }
-#pragma unroll
-    for (int tq = 0; tq < 2; tq++)
-#pragma unroll
-      for (int s2 = 0; s2 < 2; s2++) {
+        const half4 hi4 = *reinterpret_cast<const half4*>(vr + 8);
+        const half8 vf = half8{lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
         half8 pf;
 #pragma unroll
-        for (int e = 0; e < 4; e++) {
-          pf[e] = (half_t)__builtin_amdgcn_exp2f(s[tq][2 * s2][e]);
-          pf[4 + e] = (half_t)__builtin_amdgcn_exp2f(s[tq][2 * s2 + 1][e]);
-        }
-        oacc[tq][0] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[s2][0], pf, oacc[tq][0], 0, 0, 0);
-        oacc[tq][1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(vf[s2][1], pf, oacc[tq][1], 0, 0, 0);
-        oacc[tq][2] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ones, pf, oacc[tq][2], 0, 0, 0);
+        for (int e = 0; e < 8; e++) pf[e] = (half_t)__builtin_amdgcn_exp2f(s[kt][8 * sl + e]);
+#pragma unroll
+        for (int e = 0; e < 8; e += 2) lsum = __builtin_amdgcn_fdot2(half2_t{pf[e], pf[e + 1]}, one2, lsum, false);
+        oacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, oacc, 0, 0, 0);
       }
   }
-  // oacc[tq][dt][e] = O^T[channel 16*dt + 4g + e][query qi]; the row sum is row 0 of tile 2 (lane qi, e = 0)
+  // oacc[4 q + e] = O^T[channel 8 q + 4 hl + e][query qi]; the denominator is split over the lane halves
+  const float ltot = halves_sum(lsum);
+  if (jq >= N) return;
+  const float inv = 1.0f / ltot;
 #pragma unroll
-  for (int tq = 0; tq < 2; tq++) {
-    const float lsum = __shfl(oacc[tq][2][0], qi, 64);
-    if (jq[tq] >= N) continue;
-    const float inv = 1.0f / lsum;
-    const half_t* gq = gp + (int64_t)jq[tq] * C;
-    half_t* oq = out + ((int64_t)i * N + jq[tq]) * (int64_t)(H * C) + h * C;
+  for (int q = 0; q < 4; q++) {
+    const int d0 = 8 * q + 4 * hl;
+    const half4 gv = *reinterpret_cast<const half4*>(gp + (int64_t)jq * C + d0);
+    half4 ov;
 #pragma unroll
-    for (int dt = 0; dt < 2; dt++) {
-      const int d0 = 16 * dt + 4 * g;
-      const half4 gv = *reinterpret_cast<const half4*>(gq + d0);
-      half4 ov;
-#pragma unroll
-      for (int e = 0; e < 4; e++) ov[e] = (half_t)(oacc[tq][dt][e] * inv * sigmoidf_((float)gv[e]));
-      *reinterpret_cast<half4*>(oq + d0) = ov;
-    }
+    for (int e = 0; e < 4; e++) ov[e] = (half_t)(oacc[4 * q + e] * inv * sigmoidf_((float)gv[e]));
+    *reinterpret_cast<half4*>(oq + d0) = ov;
   }
 }
 

@@ -218,23 +218,24 @@ def triattn_proj(xn, w, trans: bool, N: int, H: int, C: int):
 
 
 def tri_bias_numel(N: int, H: int) -> int:
-    """Elements of the fragment-ordered triangle-bias buffer: H * (N rounded up to 16) * row_pitch(N)."""
-    return H * ((N + 15) // 16) * 16 * row_pitch(N)
+    """Elements of the fragment-ordered triangle-bias buffer: H * (N rounded up to 32) * row_pitch(N)."""
+    return H * ((N + 31) // 32) * 32 * row_pitch(N)
 
 
 def tri_bias_offsets(N: int, H: int):
     """Index of element (h, j, k) of a dense [H, N, N] bias in the fragment-ordered layout the attention core reads
-    (16-query tile, 64-key block, lane 16*g + qi owning keys 16*t4 + 4*g + e contiguously), as an int64 array."""
+    (32-query tile, 64-key block, lane 32*hl + q owning keys 32*kt + 8*p + 4*hl + e contiguously), as an int64
+    array."""
     import numpy as np
 
     ldk = row_pitch(N)
-    njt, nkb = (N + 15) // 16, ldk // 64
+    njt, nkb = (N + 31) // 32, ldk // 64
     h = np.arange(H)[:, None, None]
     j = np.arange(N)[None, :, None]
     k = np.arange(N)[None, None, :]
-    jt, qi, kb, kk = j >> 4, j & 15, k >> 6, k & 63
-    t4, g, e = kk >> 4, (kk >> 2) & 3, kk & 3
-    return (((h * njt + jt) * nkb + kb) * 64 + (g * 16 + qi)) * 16 + t4 * 4 + e
+    jt, q, kb, kk = j >> 5, j & 31, k >> 6, k & 63
+    kt, p, hl, e = kk >> 5, (kk >> 3) & 3, (kk >> 2) & 1, kk & 3
+    return (((h * njt + jt) * nkb + kb) * 64 + (hl * 32 + q)) * 32 + kt * 16 + p * 4 + e
 
 
 TRIATT_IMPL = {"auto": 0, "scalar": 1, "mma": 2}[os.environ.get("BOLTZ_MLX_TRIATT_IMPL", "auto")]

@@ -257,13 +257,13 @@ def _tb_index(N, H):
     from boltz_mlx_amd import kernels as K
 
     ldk = K.row_pitch(N)
-    njt, nkb = (N + 15) // 16, ldk // 64
+    njt, nkb = (N + 31) // 32, ldk // 64
     h = np.arange(H)[:, None, None]
     j = np.arange(N)[None, :, None]
     k = np.arange(ldk)[None, None, :]
-    jt, qi, kb, kk = j >> 4, j & 15, k >> 6, k & 63
-    t4, g, e = kk >> 4, (kk >> 2) & 3, kk & 3
-    return (((h * njt + jt) * nkb + kb) * 64 + (g * 16 + qi)) * 16 + t4 * 4 + e
+    jt, q, kb, kk = j >> 5, j & 31, k >> 6, k & 63
+    kt, p, hl, e = kk >> 5, (kk >> 3) & 3, (kk >> 2) & 1, kk & 3
+    return (((h * njt + jt) * nkb + kb) * 64 + (hl * 32 + q)) * 32 + kt * 16 + p * 4 + e
 
 
 @pytest.mark.parametrize("trans", [False, True])

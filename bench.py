@@ -102,13 +102,9 @@ def make_trunk(N: int, blocks: int, seed: int, device):
 
 
 def run_blocks(m, s, z, tok, pm, start: int, count: int, xn=None):
-    """Apply `count` consecutive blocks of the trunk (cycling) in place; carries the next norm_in output."""
-    n = len(m.layers)
-    for k in range(count):
-        i = (start + k) % n
-        nxt = m.layers[(i + 1) % n].tri_mul_out.norm_in
-        xn = m.layers[i].inplace(s, z, tok, pm, xn_in=xn, next_ln=nxt)
-    return xn
+    """Apply `count` consecutive blocks of the trunk (cycling) in place, as PairformerModule runs them (the s track
+    of each block overlapped with the next block's pair kernels); carries the next norm_in output."""
+    return m.run(s, z, tok, pm, start, count, xn=xn, cycle=True)
 
 
 def cpu_baseline(N_sample: int = 400, N_target: int = 1000) -> dict:

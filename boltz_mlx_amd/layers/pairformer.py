@@ -28,15 +28,16 @@ from boltz_mlx_amd.layers.triangular_attention.attention import (
 from boltz_mlx_amd.layers.triangular_mult import TriangleMultiplicationIncoming, TriangleMultiplicationOutgoing
 
 
-def _pair_chain(layer, z: torch.Tensor, pm: torch.Tensor, xn_in: Optional[torch.Tensor], next_ln):
+def _pair_chain(layer, z: torch.Tensor, pm: torch.Tensor, xn_in: Optional[torch.Tensor], next_ln, hooks=(None, None)):
     """The five pair updates on one batch element z [N, N, D] (fp32, updated in place) with pair mask pm [N, N]
-    fp32. Returns next_ln(z_new) in the storage dtype (or None)."""
+    fp32. Returns next_ln(z_new) in the storage dtype (or None). hooks[0] / hooks[1] are called just before the
+    starting / ending node's attention core is enqueued."""
     N, D = z.shape[0], z.shape[-1]
     xn = layer.tri_mul_out.norm_in.to_storage(z).reshape(N * N, D) if xn_in is None else xn_in
     xn = layer.tri_mul_out.fused(xn, pm, z, True, next_ln=layer.tri_mul_in.norm_in)
     xn = layer.tri_mul_in.fused(xn, pm, z, True, next_ln=layer.tri_att_start.layer_norm)
-    xn = layer.tri_att_start.fused(xn, pm, z, True, next_ln=layer.tri_att_end.layer_norm)
-    xn = layer.tri_att_end.fused(xn, pm, z, True, next_ln=layer.transition_z.norm)
+    xn = layer.tri_att_start.fused(xn, pm, z, True, next_ln=layer.tri_att_end.layer_norm, before_core=hooks[0])
+    xn = layer.tri_att_end.fused(xn, pm, z, True, next_ln=layer.transition_z.norm, before_core=hooks[1])
     return layer.transition_z.fused(xn, z, True, next_ln=next_ln)
 
 
@@ -83,15 +84,25 @@ class PairformerLayer(torch.nn.Module):
             xn_next = _pair_chain(self, z[b], pair_mask[b], xn_in if B == 1 else None,
                                   next_ln if B == 1 else None)
             self._s_track(s[b], z[b], mask[b])
-        if not isinstance(self.s_post_norm, torch.nn.Identity):
-            s.copy_(self.s_post_norm(s))
         return xn_next
 
     def _s_track(self, s: torch.Tensor, z: torch.Tensor, mask: torch.Tensor) -> None:
+        self._s_update(s, self.attention.pair_bias(z), mask)
+
+    def _s_update(self, s: torch.Tensor, bias: torch.Tensor, mask: torch.Tensor) -> None:
+        """s += attention(pre_norm_s(s), pair bias) then s += transition_s(s), in place (one batch element)."""
+        self._s_attention(s, bias, mask)
+        self._s_transition(s)
+
+    def _s_attention(self, s: torch.Tensor, bias: torch.Tensor, mask: torch.Tensor) -> None:
         dt = K.storage_dtype()
         s_n = K.layer_norm(s, self.pre_norm_s.weight, self.pre_norm_s.bias, self.pre_norm_s.eps, out_dtype=dt)
-        self.attention.fused(s_n, s_n, self.attention.pair_bias(z), mask, s, accumulate=True)
+        self.attention.fused(s_n, s_n, bias, mask, s, accumulate=True)
+
+    def _s_transition(self, s: torch.Tensor) -> None:
         self.transition_s.unfused(self.transition_s.norm.to_storage(s), out=s, accumulate=True)
+        if not isinstance(self.s_post_norm, torch.nn.Identity):
+            s.copy_(self.s_post_norm(s))
 
 
 class PairformerModule(torch.nn.Module):
@@ -119,10 +130,58 @@ class PairformerModule(torch.nn.Module):
 
     def inplace(self, s: torch.Tensor, z: torch.Tensor, mask: torch.Tensor, pair_mask: torch.Tensor) -> None:
         """Run every layer on fp32 s, z in place (masks fp32 contiguous)."""
-        n, xn = len(self.layers), None
-        for i, layer in enumerate(self.layers):
-            nxt = self.layers[i + 1].tri_mul_out.norm_in if i + 1 < n else None
-            xn = layer.inplace(s, z, mask, pair_mask, xn_in=xn, next_ln=nxt)
+        self.run(s, z, mask, pair_mask, 0, len(self.layers))
+
+    def run(self, s: torch.Tensor, z: torch.Tensor, mask: torch.Tensor, pair_mask: torch.Tensor, start: int,
+            count: int, xn: Optional[torch.Tensor] = None, cycle: bool = False) -> Optional[torch.Tensor]:
+        """Apply layers start, start + 1, ... (count of them, wrapping modulo the depth when cycle) to fp32 s, z
+        in place; xn is the first layer's tri_mul_out.norm_in(z) when already computed (B = 1). Returns the next
+        layer's norm_in(z) for B = 1 (the carry; None after the last layer unless cycle).
+
+        The z updates of layer i + 1 read only z, so the s track of layer i (attention with the pair bias of layer
+        i's z, then transition_s) runs on a second stream, overlapped with the pair kernels of layer i + 1: its
+        attention half is released when layer i + 1's starting-node attention core starts and its transition half
+        when the ending-node core starts, so it shares the GPU with those two (non-persistent) kernels rather than
+        with the persistent row kernels, whose grids assume the whole GPU. The pair bias is computed on the main
+        stream before z moves on; the main stream waits for the side stream once at the end. (The reference
+        pipelines the same way by submitting layer i + 1 while layer i's tail runs, pairformer.py:145-148.)"""
+        n, B = len(self.layers), z.shape[0]
+        main = torch.cuda.current_stream(z.device)
+        side = torch.cuda.Stream(device=z.device)
+        side.wait_stream(main)  # s, the masks and the weights are ready
+
+        def release(work):
+            ready = torch.cuda.Event()
+            ready.record(main)
+            side.wait_event(ready)
+            with torch.cuda.stream(side):
+                work()
+
+        def hooks_for(pending):
+            if not pending:
+                return (None, None)
+            return (lambda: release(lambda: [lay._s_attention(sb, bias, mb) for lay, sb, bias, mb in pending]),
+                    lambda: release(lambda: [lay._s_transition(sb) for lay, sb, _, _ in pending]))
+
+        xn = xn if B == 1 else None
+        pending = []  # s-track work of the previous layer: (layer, s[b], pair bias, mask[b])
+        for k in range(count):
+            i = (start + k) % n
+            layer = self.layers[i]
+            nxt = self.layers[(i + 1) % n].tri_mul_out.norm_in if (i + 1 < n or cycle) else None
+            done = []
+            for b in range(B):
+                hooks = hooks_for(pending) if b == 0 else (None, None)
+                xn = _pair_chain(layer, z[b], pair_mask[b], xn if B == 1 else None, nxt if B == 1 else None, hooks)
+                bias = layer.attention.pair_bias(z[b])
+                bias.record_stream(side)  # allocated on the main stream, read on the side stream
+                done.append((layer, s[b], bias, mask[b]))
+            pending = done
+        hooks = hooks_for(pending)
+        hooks[0]()
+        hooks[1]()
+        main.wait_stream(side)
+        return xn if B == 1 else None
 
 
 class PairformerNoSeqLayer(torch.nn.Module):

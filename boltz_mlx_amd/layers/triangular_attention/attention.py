@@ -50,9 +50,12 @@ class TriangleAttention(torch.nn.Module):
             out = out.transpose(1, 2).contiguous()
         return out
 
-    def fused(self, xn: torch.Tensor, mask: torch.Tensor, z: torch.Tensor, accumulate: bool = True, next_ln=None):
+    def fused(self, xn: torch.Tensor, mask: torch.Tensor, z: torch.Tensor, accumulate: bool = True, next_ln=None,
+              before_core=None):
         """z (+)= self(z) from xn = layer_norm(z) ([N*N, D], storage dtype, natural layout) and the pair mask [N, N]
-        fp32 (natural layout); returns next_ln(z_new) when next_ln is given."""
+        fp32 (natural layout); returns next_ln(z_new) when next_ln is given. before_core() is called after the
+        projection is enqueued and before the attention core (the point where independent work on another stream
+        overlaps the core rather than a persistent kernel)."""
         N = z.shape[0]
         H, C = self.no_heads, self.mha.c_hidden
         mha = self.mha
@@ -60,6 +63,8 @@ class TriangleAttention(torch.nn.Module):
                      mha.linear_g.weight, self.linear.weight)
         trans = not self.starting
         qkg, vt, tb = K.triattn_proj(xn, w, trans, N, H, C)
+        if before_core is not None:
+            before_core()
         core = K.triattn_core(qkg, vt, tb, mask, trans, self.inf, N, H, C)
         del qkg, vt, tb
         return K.linear_resid_ln(core, K.wcache(self, "w_o", mha.linear_o.weight), trans, z, accumulate, next_ln, N)

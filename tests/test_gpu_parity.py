@@ -320,3 +320,33 @@ def test_triattn_core_mfma_vs_valu(N, trans):
     m = O.metrics(fast, slow)
     print(f"core mfma vs valu N={N} trans={trans}: {m}", flush=True)
     assert m["finite"] and m["max_rel"] <= 5e-3 and m["rel_fro"] <= 2e-3, m
+
+
+@pytest.mark.parametrize("precision", ["f16"], indirect=True)
+def test_pairformer_module_overlap_matches_sequential(precision):
+    """The module runs each block's s track on a second stream, overlapped with the next block's pair kernels; the
+    result must equal running the layers one after the other on one stream, bit for bit (same kernels, same
+    order on each tensor)."""
+    import torch
+
+    from boltz_mlx_amd.layers.pairformer import PairformerModule
+
+    N, cs, cz, H, nb = 40, 384, 128, 16, 3
+    m = PairformerModule(cs, cz, nb, H)
+    p = {}
+    for i in range(nb):
+        p.update({f"layers.{i}.{k}": v for k, v in rand_params(shapes_layer(cs, cz, H), seed=700 + i, std=0.05).items()})
+    m = load(m, p)
+    z, tok, pm = pair_inputs(N, cz, seed=71, n_pad=3)
+    s = np.random.default_rng(72).standard_normal((1, N, cs))
+    s1, z1 = dev(s).float().clone(), dev(z).float().clone()
+    s2, z2 = s1.clone(), z1.clone()
+    tk, pmk = dev(tok).float().contiguous(), dev(pm).float().contiguous()
+    m.run(s1, z1, tk, pmk, 0, nb)
+    xn = None
+    for i, layer in enumerate(m.layers):
+        nxt = m.layers[i + 1].tri_mul_out.norm_in if i + 1 < nb else None
+        xn = layer.inplace(s2, z2, tk, pmk, xn_in=xn, next_ln=nxt)
+    torch.cuda.synchronize()
+    assert torch.equal(z1, z2)
+    assert torch.equal(s1, s2)

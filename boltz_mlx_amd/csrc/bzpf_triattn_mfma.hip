@@ -13,8 +13,8 @@
 // + 3 of every 16-key slab, h = l / 32); V^T is read from LDS in the same order, so P never leaves registers. The
 // softmax denominator is accumulated from the fp16 probabilities with v_dot2_f32_f16 (exact products by one, fp32
 // sums). The next key block's K, V^T, bias and mask are loaded into registers while the current block computes;
-// the bias arrives in the fragment-ordered layout (tb_offset), four 16-byte loads per lane and block, without
-// passing through LDS.
+// the bias arrives in the fragment-ordered layout (tb_offset), four 16-byte loads per lane and block, each of them
+// one contiguous 1 KB across the wave (whole cache lines), without passing through LDS.
 // Logits are base 2: the projection stores q * log2(e)/sqrt(C) and tri_bias * log2(e); the key-mask bias is
 // inf*(m-1)*log2(e). A row whose keys are all masked gets uniform weights over its N keys, which is what the
 // reference's rounding gives (every logit rounds to -inf*log2(e); boltz_mlx/kernels.py:579-581). Softmax and
@@ -185,7 +185,7 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
   auto prefetch_bias = [&](int kb) {
 #pragma unroll
     for (int v = 0; v < 4; v++)
-      bcur[v] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(brs, l * 64 + 16 * v, kb * 4096, 0));
+      bcur[v] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(brs, 1024 * v + 16 * l, kb * 4096, 0));
   };
   // Issue order pinned to the loop's (K, V^T, mask, then bias): the wait counter merges the prologue and the loop
   // back edge at the loop header, and any other order there turns the first wait of every iteration into a wait

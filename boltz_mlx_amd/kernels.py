@@ -224,8 +224,8 @@ def tri_bias_numel(N: int, H: int) -> int:
 
 def tri_bias_offsets(N: int, H: int):
     """Index of element (h, j, k) of a dense [H, N, N] bias in the fragment-ordered layout the attention core reads
-    (32-query tile, 64-key block, lane 32*hl + q owning keys 32*kt + 8*p + 4*hl + e contiguously), as an int64
-    array."""
+    (32-query tile, 64-key block, lane 32*hl + q owning keys 32*kt + 8*p + 4*hl + e, stored so that each of a
+    lane's four 16-byte loads is contiguous across the wave), as an int64 array."""
     import numpy as np
 
     ldk = row_pitch(N)
@@ -235,7 +235,8 @@ def tri_bias_offsets(N: int, H: int):
     k = np.arange(N)[None, None, :]
     jt, q, kb, kk = j >> 5, j & 31, k >> 6, k & 63
     kt, p, hl, e = kk >> 5, (kk >> 3) & 3, (kk >> 2) & 1, kk & 3
-    return (((h * njt + jt) * nkb + kb) * 64 + (hl * 32 + q)) * 32 + kt * 16 + p * 4 + e
+    x = kt * 16 + p * 4 + e
+    return ((h * njt + jt) * nkb + kb) * 2048 + (x >> 3) * 512 + (hl * 32 + q) * 8 + (x & 7)
 
 
 TRIATT_IMPL = {"auto": 0, "scalar": 1, "mma": 2}[os.environ.get("BOLTZ_MLX_TRIATT_IMPL", "auto")]

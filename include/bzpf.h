@@ -80,9 +80,9 @@ int bzpf_trimul_tail(const void* o, const float* norm_out_w, const float* norm_o
  *   qkg [3H][N*N][C]: q * q_scale (planes 0..H-1), k (H..2H-1), g (2H..3H-1);
  *   vt [H][N][C][ldk]: v transposed per row i (vt[h][i][c][j] = v at (i, j)); columns j >= N are not written;
  *   tri_bias: bias_scale * (linear at (j, k)) for head h, query j, key k, in the fragment-ordered layout the
- *     attention core reads: element (h, j, k) at (((h*NJ + j/32)*(ldk/64) + k/64)*64 + 32*((k%8)/4) + j%32)*32
- *     + 16*((k%64)/32) + 4*((k%32)/8) + k%4 with NJ = ceil(N/32) (H*32*NJ*ldk elements); keys N <= k < ldk are
- *     set to 0.
+ *     attention core reads: with x = 16*((k%64)/32) + 4*((k%32)/8) + k%4 and lane = 32*((k%8)/4) + j%32, element
+ *     (h, j, k) is at ((h*NJ + j/32)*(ldk/64) + k/64)*2048 + 512*(x/8) + 8*lane + x%8 with NJ = ceil(N/32)
+ *     (H*32*NJ*ldk elements); keys N <= k < ldk are set to 0.
  * ldk = bzpf_row_pitch(N). bzpf_triattn_core expects q_scale = log2(e)/sqrt(C) and bias_scale = log2(e) (logits
  * in base 2). Replaces the fused projection of TriangleAttention
  * (boltz_mlx/layers/triangular_attention/attention.py:49-69, 100-104) and kernels_nax3.pair_proj16

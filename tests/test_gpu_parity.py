@@ -263,7 +263,8 @@ def _tb_index(N, H):
     k = np.arange(ldk)[None, None, :]
     jt, q, kb, kk = j >> 5, j & 31, k >> 6, k & 63
     kt, p, hl, e = kk >> 5, (kk >> 3) & 3, (kk >> 2) & 1, kk & 3
-    return (((h * njt + jt) * nkb + kb) * 64 + (hl * 32 + q)) * 32 + kt * 16 + p * 4 + e
+    x = kt * 16 + p * 4 + e
+    return ((h * njt + jt) * nkb + kb) * 2048 + (x >> 3) * 512 + (hl * 32 + q) * 8 + (x & 7)
 
 
 @pytest.mark.parametrize("trans", [False, True])

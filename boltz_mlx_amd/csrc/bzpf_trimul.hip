@@ -115,20 +115,25 @@ __global__ __launch_bounds__(256, 2) void trimul_contract_kernel(const T* __rest
   }
 }
 
-// fp16 form on v_mfma_f32_32x32x16_f16, which delivers about 1.6x the FLOP rate of the 16x16x32 form on gfx950
-// (1.9 vs 1.2 PFLOP/s measured for back-to-back independent MFMAs). Same 128 x 128 tile, 4 waves of 64 x 64 = 2 x 2
-// blocks of 32 x 32, 64-element K stages double-buffered in LDS with the next stage prefetched into registers.
+// fp16 form: 256 x 256 tiles on v_mfma_f32_32x32x16_f16, 8 waves of 128 (j) x 64 (i) = 4 x 2 blocks of 32 x 32
+// (128 accumulator registers per lane). The 128 x 128 tile of the fp32 form moves 32 KB from L2 per 2.1 MFLOP;
+// this tile halves that (64 KB per 8.4 MFLOP per 64-element K stage), which is what bounds the contraction: the
+// vector-memory path that feeds LDS, not the matrix cores. K stages (64 elements) are double-buffered in LDS
+// (147 KB, one workgroup per CU) with the next stage loaded into registers while the current one computes.
 // Operand layouts (A = rows of b, B = rows of a, both K-contiguous): lane l holds row l % 32 and 8 consecutive k;
 // in MFMA step s of a stage, lane half h = l / 32 takes k = 32 h + 8 s .. + 7, so over the 4 steps a lane reads 64
 // contiguous bytes of its row (a permutation of the k sum shared by A and B). The accumulator lane holds
 // o^T[j = 8 q + 4 h + e][i = l % 32] in element 4 q + e: 4 runs of 4 consecutive j of one i.
-__global__ __launch_bounds__(256, 2) void trimul_contract_f16_k(const half_t* __restrict__ ab, half_t* __restrict__ o,
-                                                                int64_t N, int64_t ld, int D, int64_t tiles1,
-                                                                int64_t units, int64_t per_xcd) {
-  constexpr int BT = 128, BK = 64;
+constexpr int CT_BT = 256, CT_WAVES = 8;
+
+__global__ __launch_bounds__(64 * CT_WAVES, 1) void trimul_contract_f16_k(const half_t* __restrict__ ab,
+                                                                          half_t* __restrict__ o, int64_t N,
+                                                                          int64_t ld, int D, int64_t tiles1,
+                                                                          int64_t units, int64_t per_xcd) {
+  constexpr int BT = CT_BT, BK = 64, NT = 64 * CT_WAVES;
   constexpr int LDT = BK + 8;              // LDS row pitch (halves): 36 dwords, conflict-free 16-byte row reads
   constexpr int VPR = BK / 8;              // 16-byte vectors per row per stage
-  constexpr int LOADS = 2 * BT * VPR / 256;
+  constexpr int LOADS = 2 * BT * VPR / NT;  // 8
   __shared__ LDS_ALIGN half_t As[2][BT * LDT];  // rows of a (i)
   __shared__ LDS_ALIGN half_t Bs[2][BT * LDT];  // rows of b (j)
 
@@ -140,89 +145,78 @@ __global__ __launch_bounds__(256, 2) void trimul_contract_f16_k(const half_t* __
   const half_t* a = ab + c * N * ld;
   const half_t* b = ab + ((int64_t)D + c) * N * ld;
   const int t = threadIdx.x, wave = t >> 6, l = t & 63, r = l & 31, h = l >> 5;
-  const int wi = wave >> 1, wj = wave & 1;
+  const int wj = wave >> 2, wi = wave & 3;  // wave tile: j = 128 wj .., i = 64 wi ..
 
-  // Two register sets: the loads of stage st + 2 are issued at the start of stage st and stored to LDS at the end of
-  // stage st + 1, so each load has two stages of MFMA work to arrive (one stage does not cover the L2 latency).
-  // The per-thread row pointers are fixed; stages only advance k.
+  // per-thread rows are fixed; stages only advance k (rows past N read row N - 1; their outputs are not stored)
   const half_t* src[LOADS];
   int dst_off[LOADS];
 #pragma unroll
   for (int v = 0; v < LOADS; v++) {
-    const int e = v * 256 + t, rr = e / VPR, col = (e % VPR) * 8;
+    const int e = v * NT + t, rr = e / VPR, col = (e % VPR) * 8;
     const bool isb = rr >= BT;
     int64_t row = (isb ? j0 : i0) + (isb ? rr - BT : rr);
     if (row >= N) row = N - 1;
     src[v] = (isb ? b : a) + row * ld + col;
-    dst_off[v] = (isb ? BT * LDT * 2 : 0) + (isb ? rr - BT : rr) * LDT + col;  // from As[buf] (Bs follows As)
+    dst_off[v] = (isb ? 2 * BT * LDT : 0) + (isb ? rr - BT : rr) * LDT + col;  // from As[buf] (Bs follows As)
   }
-  u32x4_t reg[2][LOADS];
-  auto gload = [&](int set, int64_t k0) {
+  u32x4_t reg[LOADS];
+  auto gload = [&](int64_t k0) {
 #pragma unroll
-    for (int v = 0; v < LOADS; v++) reg[set][v] = *reinterpret_cast<const u32x4_t*>(src[v] + k0);
+    for (int v = 0; v < LOADS; v++) reg[v] = *reinterpret_cast<const u32x4_t*>(src[v] + k0);
   };
-  auto lstore = [&](int set, int buf) {
+  auto lstore = [&](int buf) {
 #pragma unroll
     for (int v = 0; v < LOADS; v++) {
       half_t* base = dst_off[v] >= 2 * BT * LDT ? Bs[buf] + dst_off[v] - 2 * BT * LDT : As[buf] + dst_off[v];
-      *reinterpret_cast<u32x4_t*>(base) = reg[set][v];
+      *reinterpret_cast<u32x4_t*>(base) = reg[v];
     }
   };
 
-  f16x acc[2][2];  // acc[jb][ib]: o^T block (j = 64 wj + 32 jb .., i = 64 wi + 32 ib ..)
+  f16x acc[4][2];  // acc[jb][ib]: o^T block (j = 128 wj + 32 jb .., i = 64 wi + 32 ib ..)
 #pragma unroll
-  for (int jb = 0; jb < 2; jb++)
+  for (int jb = 0; jb < 4; jb++)
 #pragma unroll
     for (int ib = 0; ib < 2; ib++)
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[jb][ib][e] = 0.0f;
   const int nst = (int)(ld / BK);
-  // The loop body has no branches around loads or stores (stages past the end reload the last one and store it to
-  // the idle buffer): with a conditional, the wait-counter merge at the loop header assumes both register sets may
-  // still be in flight and waits for every load before the next batch is issued.
-  gload(0, 0);
-  gload(1, (int64_t)min(1, nst - 1) * BK);
-  lstore(0, 0);
+  gload(0);
+  lstore(0);
   __syncthreads();
-  // buf is a literal at every call site, so the register sets are indexed statically
-  auto stage = [&](int st, int buf) {
-    gload(buf, (int64_t)min(st + 2, nst - 1) * BK);
+  // no branches around the loads or stores in the loop body (the last stage reloads itself into the idle buffer),
+  // so the wait counter sees one load order at the loop header
+  for (int st = 0; st < nst; st++) {
+    const int buf = st & 1;
+    gload((int64_t)min(st + 1, nst - 1) * BK);
     __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs (the scheduler sinks them otherwise)
     const half_t* Ab = As[buf] + (64 * wi + r) * LDT + 32 * h;
-    const half_t* Bb = Bs[buf] + (64 * wj + r) * LDT + 32 * h;
+    const half_t* Bb = Bs[buf] + (128 * wj + r) * LDT + 32 * h;
 #pragma unroll
     for (int s = 0; s < 4; s++) {
-      half8 fa[2], fb[2];
+      half8 fa[2], fb[4];
 #pragma unroll
-      for (int q = 0; q < 2; q++) {
-        fa[q] = *reinterpret_cast<const half8*>(Ab + 32 * q * LDT + 8 * s);
-        fb[q] = *reinterpret_cast<const half8*>(Bb + 32 * q * LDT + 8 * s);
-      }
+      for (int q = 0; q < 2; q++) fa[q] = *reinterpret_cast<const half8*>(Ab + 32 * q * LDT + 8 * s);
 #pragma unroll
-      for (int jb = 0; jb < 2; jb++)
+      for (int q = 0; q < 4; q++) fb[q] = *reinterpret_cast<const half8*>(Bb + 32 * q * LDT + 8 * s);
+#pragma unroll
+      for (int jb = 0; jb < 4; jb++)
 #pragma unroll
         for (int ib = 0; ib < 2; ib++)
           acc[jb][ib] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[jb], fa[ib], acc[jb][ib], 0, 0, 0);
     }
-    lstore(buf ^ 1, buf ^ 1);
+    lstore(buf ^ 1);
     __syncthreads();
-  };
-  int st = 0;
-  for (; st + 1 < nst; st += 2) {
-    stage(st, 0);
-    stage(st + 1, 1);
   }
-  if (st < nst) stage(st, 0);
   half_t* oc = o + c * N * ld;
 #pragma unroll
   for (int ib = 0; ib < 2; ib++) {
     const int64_t i = i0 + 64 * wi + 32 * ib + r;
     if (i >= N) continue;
 #pragma unroll
-    for (int jb = 0; jb < 2; jb++)
+    for (int jb = 0; jb < 4; jb++)
 #pragma unroll
       for (int q = 0; q < 4; q++) {
-        const int64_t j = j0 + 64 * wj + 32 * jb + 8 * q + 4 * h;
+        const int64_t j = j0 + 128 * wj + 32 * jb + 8 * q + 4 * h;
         if (j >= ld) continue;
         const f16x& v = acc[jb][ib];
         *reinterpret_cast<half4*>(oc + i * ld + j) =
@@ -233,14 +227,14 @@ __global__ __launch_bounds__(256, 2) void trimul_contract_f16_k(const half_t* __
 
 template <typename T>
 static hipError_t contract_t(const void* ab, void* o, int64_t N, int64_t ld, int D, hipStream_t st) {
-  constexpr int BT = 128;
+  const int BT = sizeof(T) == 2 ? CT_BT : 128;
   const int64_t tiles1 = (N + BT - 1) / BT;
   const int64_t units = (int64_t)D * tiles1 * tiles1;
   const int64_t per_xcd = (units + 7) / 8;
   const dim3 grid((unsigned)(per_xcd * 8));
   if constexpr (sizeof(T) == 2)
-    trimul_contract_f16_k<<<grid, 256, 0, st>>>(static_cast<const half_t*>(ab), static_cast<half_t*>(o), N, ld, D,
-                                                tiles1, units, per_xcd);
+    trimul_contract_f16_k<<<grid, 64 * CT_WAVES, 0, st>>>(static_cast<const half_t*>(ab), static_cast<half_t*>(o), N,
+                                                          ld, D, tiles1, units, per_xcd);
   else
     trimul_contract_kernel<T><<<grid, 256, 0, st>>>(static_cast<const T*>(ab), static_cast<T*>(o), N, ld, D, tiles1,
                                                     units, per_xcd);

@@ -328,6 +328,21 @@ def seq_attention(q, k, v, g, bias, mask, inf: float, H: int) -> torch.Tensor:
     return out
 
 
+def seq_attention_packed(qkvg, bias, mask, inf: float, H: int) -> torch.Tensor:
+    """seq_attention over one [N, 4*H*hd] buffer holding q | k | v | g per row (the fused projection's output)."""
+    _dev(qkvg, bias, mask)
+    N, HD4 = qkvg.shape
+    HD = HD4 // 4
+    hd = HD // H
+    if bias.shape != (H, N, N) or mask.numel() != N or mask.dtype != torch.float32:
+        raise ValueError("seq_attention: bias must be [H, N, N] and mask fp32 [N]")
+    out = torch.empty((N, HD), dtype=qkvg.dtype, device=qkvg.device)
+    base, es = qkvg.data_ptr(), qkvg.element_size()
+    call("bzpf_seq_attention", base, base + HD * es, base + 2 * HD * es, base + 3 * HD * es, HD4, _p(bias),
+         _p(mask), float(inf), _p(out), HD, _dt(qkvg), N, H, hd, _stream())
+    return out
+
+
 def pair_bias(z: torch.Tensor, ln, w: torch.Tensor) -> torch.Tensor:
     """Linear(LN(z)) for z fp32 [N, N, D] as [H, N, N] in w's dtype."""
     _dev(z, w)

@@ -34,9 +34,26 @@ class AttentionPairBias(torch.nn.Module):
             self.proj_z = torch.nn.Sequential(LayerNorm(c_z), torch.nn.Linear(c_z, num_heads, bias=False))
         self.proj_o = torch.nn.Linear(c_s, c_s, bias=False)
 
+    def prepare(self):
+        """The kernel weights in the storage dtype, cached on the module: [proj_q; proj_k; proj_v; proj_g] with the
+        matching bias (proj_q's, then zeros; fp32), proj_o, and proj_z's linear when the module computes it."""
+        w_qkvg = K.wcache(self, "w_qkvg", self.proj_q.weight, self.proj_k.weight, self.proj_v.weight,
+                          self.proj_g.weight)
+        bq = self.proj_q.bias
+        key = (bq.data_ptr(), bq._version, bq.device)
+        hit = self.__dict__.get("_bzpf_b_qkvg")
+        if hit is None or hit[0] != key:
+            full = torch.zeros(4 * self.c_s, dtype=torch.float32, device=bq.device)
+            with torch.no_grad():
+                full[: self.c_s] = bq.detach().float()
+            hit = (key, full)
+            self.__dict__["_bzpf_b_qkvg"] = hit
+        w_z = K.wcache(self, "w_z", self.proj_z[1].weight) if self.compute_pair_bias else None
+        return w_qkvg, hit[1], K.wcache(self, "w_o", self.proj_o.weight), w_z
+
     def pair_bias(self, z: torch.Tensor) -> torch.Tensor:
         """proj_z(z) as [H, N, N] in the storage dtype, from z [N, N, c_z] fp32."""
-        return K.pair_bias(z, self.proj_z[0], K.wcache(self, "w_z", self.proj_z[1].weight))
+        return K.pair_bias(z, self.proj_z[0], self.prepare()[3])
 
     def forward(self, s: torch.Tensor, z: torch.Tensor, mask: torch.Tensor, k_in: torch.Tensor,
                 multiplicity: int = 1, pair_bias: Optional[torch.Tensor] = None) -> torch.Tensor:
@@ -62,9 +79,15 @@ class AttentionPairBias(torch.nn.Module):
               accumulate: bool = True) -> None:
         """out (+)= attention(s, k_in) for one batch element: s, k_in [N, c_s] and bias [H, N, N] in the storage
         dtype, mask [N] fp32, out [N, c_s] fp32."""
-        q = K.linear(s, K.wcache(self, "w_q", self.proj_q.weight), bias=self.proj_q.bias)
-        k = K.linear(k_in, K.wcache(self, "w_k", self.proj_k.weight))
-        v = K.linear(k_in, K.wcache(self, "w_v", self.proj_v.weight))
-        g = K.linear(s, K.wcache(self, "w_g", self.proj_g.weight))
-        o = K.seq_attention(q, k, v, g, bias, mask, self.inf, self.num_heads)
-        K.linear(o, K.wcache(self, "w_o", self.proj_o.weight), out=out, accumulate=accumulate)
+        w_qkvg, b_qkvg, w_o, _ = self.prepare()
+        c = self.c_s
+        if k_in is s:  # one GEMM for q, k, v, g (the Pairformer's self-attention): [N, 4 c_s]
+            qkvg = K.linear(s, w_qkvg, bias=b_qkvg)
+            o = K.seq_attention_packed(qkvg, bias, mask, self.inf, self.num_heads)
+        else:
+            q = K.linear(s, w_qkvg[:c], bias=b_qkvg[:c])
+            k = K.linear(k_in, w_qkvg[c:2 * c])
+            v = K.linear(k_in, w_qkvg[2 * c:3 * c])
+            g = K.linear(s, w_qkvg[3 * c:])
+            o = K.seq_attention(q, k, v, g, bias, mask, self.inf, self.num_heads)
+        K.linear(o, w_o, out=out, accumulate=accumulate)

@@ -86,6 +86,13 @@ class PairformerLayer(torch.nn.Module):
             self._s_track(s[b], z[b], mask[b])
         return xn_next
 
+    def prepare(self) -> None:
+        """Cache every kernel weight of the layer in the storage dtype (a one-time conversion per precision; the
+        module does it for all layers before the first block, outside the steady-state block loop)."""
+        for mod in (self.attention, self.tri_mul_out, self.tri_mul_in, self.tri_att_start, self.tri_att_end,
+                    self.transition_s, self.transition_z):
+            mod.prepare()
+
     def _s_track(self, s: torch.Tensor, z: torch.Tensor, mask: torch.Tensor) -> None:
         self._s_update(s, self.attention.pair_bias(z), mask)
 
@@ -146,6 +153,12 @@ class PairformerModule(torch.nn.Module):
         stream before z moves on; the main stream waits for the side stream once at the end. (The reference
         pipelines the same way by submitting layer i + 1 while layer i's tail runs, pairformer.py:145-148.)"""
         n, B = len(self.layers), z.shape[0]
+        if self.__dict__.get("_bzpf_prepared") != K.storage_dtype():
+            # first run in this precision: convert every layer's weights now; the per-call caches in the layers
+            # still rebuild any weight that changes afterwards
+            for layer in self.layers:
+                layer.prepare()
+            self.__dict__["_bzpf_prepared"] = K.storage_dtype()
         main = torch.cuda.current_stream(z.device)
         side = torch.cuda.Stream(device=z.device)
         side.wait_stream(main)  # s, the masks and the weights are ready

@@ -42,15 +42,17 @@ class Transition(torch.nn.Module):
             return out
         return self.unfused(xn)
 
+    def prepare(self):
+        """The kernel weights in the storage dtype ([fc1; fc2] and fc3), cached on the module."""
+        return K.wcache(self, "w12", self.fc1.weight, self.fc2.weight), K.wcache(self, "w3", self.fc3.weight)
+
     def fused(self, xn: torch.Tensor, z: torch.Tensor, accumulate: bool = True, next_ln=None):
         """z (+)= transition from xn = norm(z) (storage dtype); returns next_ln(z_new) when next_ln is given."""
-        w12 = K.wcache(self, "w12", self.fc1.weight, self.fc2.weight)
-        w3 = K.wcache(self, "w3", self.fc3.weight)
+        w12, w3 = self.prepare()
         return K.transition(xn, w12, w3, z, accumulate, next_ln)
 
     def unfused(self, xn: torch.Tensor, out: Optional[torch.Tensor] = None, accumulate: bool = False):
         """fc3(SwiGLU(xn fc12^T)) as separate kernels; accumulate adds into the fp32 `out`."""
-        w12 = K.wcache(self, "w12", self.fc1.weight, self.fc2.weight)
-        w3 = K.wcache(self, "w3", self.fc3.weight)
+        w12, w3 = self.prepare()
         a = K.swiglu(K.linear(xn, w12))
         return K.linear(a, w3, out=out, out_dtype=torch.float32, accumulate=accumulate)

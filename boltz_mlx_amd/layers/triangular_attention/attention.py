@@ -58,16 +58,22 @@ class TriangleAttention(torch.nn.Module):
         overlaps the core rather than a persistent kernel)."""
         N = z.shape[0]
         H, C = self.no_heads, self.mha.c_hidden
-        mha = self.mha
-        w = K.wcache(self, "w_qkvgb", mha.linear_q.weight, mha.linear_k.weight, mha.linear_v.weight,
-                     mha.linear_g.weight, self.linear.weight)
+        w, w_o = self.prepare()
         trans = not self.starting
         qkg, vt, tb = K.triattn_proj(xn, w, trans, N, H, C)
         if before_core is not None:
             before_core()
         core = K.triattn_core(qkg, vt, tb, mask, trans, self.inf, N, H, C)
         del qkg, vt, tb
-        return K.linear_resid_ln(core, K.wcache(self, "w_o", mha.linear_o.weight), trans, z, accumulate, next_ln, N)
+        return K.linear_resid_ln(core, w_o, trans, z, accumulate, next_ln, N)
+
+    def prepare(self):
+        """The kernel weights in the storage dtype ([q; k; v; g; triangle bias] and linear_o), cached on the
+        module."""
+        mha = self.mha
+        return (K.wcache(self, "w_qkvgb", mha.linear_q.weight, mha.linear_k.weight, mha.linear_v.weight,
+                         mha.linear_g.weight, self.linear.weight),
+                K.wcache(self, "w_o", mha.linear_o.weight))
 
 
 TriangleAttentionStartingNode = TriangleAttention

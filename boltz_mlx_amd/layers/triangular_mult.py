@@ -46,13 +46,17 @@ class _TriangleMultiplication(torch.nn.Module):
         next_ln(z_new) in the storage dtype when next_ln is given."""
         N = z.shape[0]
         kexp = K.TRIMULT_K if K.f16() else 0
-        w_pg = K.wcache(self, "w_pg", self.p_in.weight, self.g_in.weight)
+        w_pg, w_po, w_go = self.prepare()
         ab = K.trimul_proj(xn, w_pg, mask, 2.0 ** -kexp, not self.outgoing, N)
         o = K.trimul_contract(ab, N)
         del ab
-        return K.trimul_tail(o, self.norm_out, self.norm_out.eps * 2.0 ** (-4 * kexp),
-                             K.wcache(self, "w_po", self.p_out.weight), xn,
-                             K.wcache(self, "w_go", self.g_out.weight), z, accumulate, next_ln, N)
+        return K.trimul_tail(o, self.norm_out, self.norm_out.eps * 2.0 ** (-4 * kexp), w_po, xn, w_go, z,
+                             accumulate, next_ln, N)
+
+    def prepare(self):
+        """The kernel weights in the storage dtype ([p_in; g_in], p_out, g_out), cached on the module."""
+        return (K.wcache(self, "w_pg", self.p_in.weight, self.g_in.weight), K.wcache(self, "w_po", self.p_out.weight),
+                K.wcache(self, "w_go", self.g_out.weight))
 
 
 class TriangleMultiplicationOutgoing(_TriangleMultiplication):

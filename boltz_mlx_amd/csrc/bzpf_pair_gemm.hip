@@ -87,7 +87,7 @@ __global__ __launch_bounds__(64 * PROJ_WAVES) void trimul_proj_k(const T* __rest
         for (int rb = 0; rb < RB; rb++)
 #pragma unroll
           for (int e = 0; e < 4; e++) v[4 * rb + e] = pa[rb][0][e] * sigmoidf_(ga[rb][0][e]) * mo[hh][rb][e];
-        st_run(dst + (int64_t)16 * cb * N * ld + hh * TW, v);
+        st_run_cached(dst + (int64_t)16 * cb * N * ld + hh * TW, v);
       }
       __builtin_amdgcn_sched_barrier(0);
     }

@@ -104,6 +104,15 @@ __device__ __forceinline__ void st_run(half_t* p, const float (&v)[8]) {
 __device__ __forceinline__ void st_run(float* p, const float (&v)[4]) {
   __builtin_nontemporal_store(f4{v[0], v[1], v[2], v[3]}, reinterpret_cast<f4*>(p));
 }
+// The same runs through the default cache policy (the trimul projection: its half-line runs of one channel row
+// merge in L2 before they are written back; measured 7-10% faster there than non-temporal stores).
+__device__ __forceinline__ void st_run_cached(half_t* p, const float (&v)[8]) {
+  *reinterpret_cast<half8*>(p) = half8{(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3], (half_t)v[4],
+                                       (half_t)v[5], (half_t)v[6], (half_t)v[7]};
+}
+__device__ __forceinline__ void st_run_cached(float* p, const float (&v)[4]) {
+  *reinterpret_cast<f4*>(p) = f4{v[0], v[1], v[2], v[3]};
+}
 
 // mma_rows over CB column blocks in groups of G with a scheduling barrier between groups: the compiler otherwise
 // hoists every LDS weight read ahead of the MFMAs (CB * 4 fragments live at once), which spills at 4 waves/SIMD.

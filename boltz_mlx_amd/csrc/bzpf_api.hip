@@ -182,6 +182,29 @@ int bzpf_transition(const void* xn, const void* w12, const void* w3, float* z, i
               "bzpf_transition");
 }
 
+int bzpf_transition_pb(const void* xn, const void* w12, const void* w3, float* z, int accumulate, const float* next_w,
+                       const float* next_b, float next_eps, void* xn_next, const void* pb_w, const float* pb_lnw,
+                       const float* pb_lnb, float pb_eps, void* pb_out, int pb_heads, int dt, int64_t rows, int D,
+                       int hidden, void* stream) {
+  REQUIRE_PTR(xn);
+  REQUIRE_PTR(w12);
+  REQUIRE_PTR(w3);
+  REQUIRE_PTR(z);
+  REQUIRE(pb_w != nullptr && pb_lnw != nullptr && pb_lnb != nullptr && pb_out != nullptr,
+          "bzpf_transition_pb: NULL pair-bias pointer");
+  REQUIRE(next_w == nullptr || (next_b != nullptr && xn_next != nullptr),
+          "bzpf_transition_pb: next LN needs next_b and xn_next");
+  REQUIRE(dt_ok(dt), "bzpf_transition_pb: bad dtype %d", dt);
+  REQUIRE(D == 128 && hidden >= 64 && hidden % 64 == 0,
+          "bzpf_transition_pb: need D=128, hidden %% 64 == 0 (D=%d H=%d)", D, hidden);
+  REQUIRE(pb_heads >= 1 && pb_heads <= 16, "bzpf_transition_pb: 1 <= heads <= 16 (got %d)", pb_heads);
+  REQUIRE(rows >= 0, "bzpf_transition_pb: rows < 0");
+  if (rows == 0) return BZPF_OK;
+  return done(bzpf::launch_transition_pb(xn, w12, w3, z, accumulate, next_w, next_b, next_eps, xn_next, pb_w, pb_lnw,
+                                         pb_lnb, pb_eps, pb_out, pb_heads, dt, rows, hidden, S(stream)),
+              "bzpf_transition_pb");
+}
+
 int bzpf_linear(const void* x, const void* w, const float* bias, void* y, int dt, int y_dt, int64_t rows, int K,
                 int M, int accumulate, void* stream) {
   REQUIRE_PTR(x);

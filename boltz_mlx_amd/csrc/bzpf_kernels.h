@@ -38,6 +38,10 @@ hipError_t launch_linear_resid_ln(const void* x, const void* w, int trans, float
 hipError_t launch_transition(const void* xn, const void* w12, const void* w3, float* z, int accumulate,
                              const float* lnw, const float* lnb, float eps, void* xn_next, int dt, int64_t rows,
                              int hidden, hipStream_t st);
+hipError_t launch_transition_pb(const void* xn, const void* w12, const void* w3, float* z, int accumulate,
+                                const float* lnw, const float* lnb, float eps, void* xn_next, const void* pb_w,
+                                const float* pb_lnw, const float* pb_lnb, float pb_eps, void* pb_out, int pb_heads,
+                                int dt, int64_t rows, int hidden, hipStream_t st);
 
 hipError_t launch_linear(const void* x, const void* w, const float* bias, void* y, int dt, int y_dt, int64_t rows,
                          int K, int M, int epi, hipStream_t st);

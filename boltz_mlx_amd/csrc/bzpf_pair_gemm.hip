@@ -583,6 +583,7 @@ __global__ __launch_bounds__(256) void transition_k(const T* __restrict__ xn, co
 // next tile's rows are loaded during the current tile's last chunk.
 constexpr int TR_WAVES = 8, TR_HCH = 64;
 
+template <bool PB>
 __global__ __launch_bounds__(64 * TR_WAVES) void transition_f16_k(const half_t* __restrict__ xn,
                                                                   const half_t* __restrict__ w12,
                                                                   const half_t* __restrict__ w3,
@@ -590,7 +591,10 @@ __global__ __launch_bounds__(64 * TR_WAVES) void transition_f16_k(const half_t* 
                                                                   const float* __restrict__ lnw,
                                                                   const float* __restrict__ lnb, float eps,
                                                                   half_t* __restrict__ xn_next, int64_t rows_total,
-                                                                  int hidden) {
+                                                                  int hidden, const half_t* __restrict__ pb_w,
+                                                                  const float* __restrict__ pb_lnw,
+                                                                  const float* __restrict__ pb_lnb, float pb_eps,
+                                                                  half_t* __restrict__ pb_out, int pb_heads) {
   using T = half_t;
   constexpr int RB = 2, STEPS = RG<T>::STEPS, LDW = ldw_of<T>(), LDH = TR_HCH + Pad<T>::v, HB = TR_HCH / 16;
   constexpr int TROWS = 16 * RB * TR_WAVES;
@@ -598,12 +602,32 @@ __global__ __launch_bounds__(64 * TR_WAVES) void transition_f16_k(const half_t* 
   __shared__ LDS_ALIGN T W1s[2][TR_HCH * LDW];
   __shared__ LDS_ALIGN T W2s[2][TR_HCH * LDW];
   __shared__ LDS_ALIGN T W3s[2][D * LDH];
+  // pair bias of the s track (PB): W' = W_pb with gamma_pb folded into its columns (heads past pb_heads zero), and
+  // W_pb . beta_pb
+  constexpr int LDP = D + 8;
+  __shared__ LDS_ALIGN T Wpb[PB ? 16 * LDP : 8];
+  __shared__ float Bpb[16];
   const int t = threadIdx.x, l = t & 63, g = l >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int nch = hidden / TR_HCH;
   const int64_t ntiles = (rows_total + TROWS - 1) / TROWS;
   int64_t tile = blockIdx.x;
   if (tile >= ntiles) return;  // whole workgroup
+  if constexpr (PB) {
+    for (int e = t; e < 16 * D; e += 64 * TR_WAVES) {
+      const int h = e >> 7, c = e & (D - 1);
+      Wpb[h * LDP + c] = h < pb_heads ? (half_t)((float)pb_w[h * D + c] * pb_lnw[c]) : (half_t)0.0f;
+    }
+    if (t < 64) {  // 4 lanes per head, 32 channels each
+      const int h = t >> 2, q = t & 3;
+      float acc = 0.f;
+      if (h < pb_heads)
+        for (int c = 32 * q; c < 32 * q + 32; c++) acc += (float)pb_w[h * D + c] * pb_lnb[c];
+      acc += __shfl_xor(acc, 1, 64);
+      acc += __shfl_xor(acc, 2, 64);
+      if (q == 0) Bpb[h] = acc;
+    }
+  }
 
   // chunk staging: vector v of thread t is element e = (v & 1) * 512 + t of matrix v / 2 (fc1, fc2: 64 rows x 16
   // vectors; fc3: 128 rows x 8 vectors of the chunk's 64 columns)
@@ -691,8 +715,12 @@ __global__ __launch_bounds__(64 * TR_WAVES) void transition_f16_k(const half_t* 
       gload(c + 2 < nch ? c + 2 : c + 2 - nch >= nch ? 0 : c + 2 - nch);
     }
     const int64_t row0 = tile * TROWS + wave * 16 * RB + (l & 15);
-    resid_ln_rows<T, RB>(out, [&](int rb) -> int64_t { return row0 + 16 * rb < rows_total ? row0 + 16 * rb : -1; }, z,
-                         accumulate, lnw, lnb, eps, xn_next);
+    const auto zrow = [&](int rb) -> int64_t { return row0 + 16 * rb < rows_total ? row0 + 16 * rb : -1; };
+    if constexpr (PB)
+      resid_ln_pb_rows<RB>(out, zrow, z, accumulate, lnw, lnb, eps, xn_next, Wpb, LDP, Bpb, pb_eps, pb_out,
+                           rows_total, pb_heads);
+    else
+      resid_ln_rows<T, RB>(out, zrow, z, accumulate, lnw, lnb, eps, xn_next);
 #pragma unroll
     for (int rb = 0; rb < RB; rb++)
 #pragma unroll
@@ -828,17 +856,20 @@ static hipError_t trans_t(const void* xn, const void* w12, const void* w3, float
   return hipGetLastError();
 }
 
+template <bool PB>
 static hipError_t trans_f16(const void* xn, const void* w12, const void* w3, float* z, int accumulate,
                             const float* lnw, const float* lnb, float eps, void* xn_next, int64_t rows, int hidden,
-                            hipStream_t st) {
+                            const void* pb_w, const float* pb_lnw, const float* pb_lnb, float pb_eps, void* pb_out,
+                            int pb_heads, hipStream_t st) {
   static int cache[kMaxDevices];
-  const int resident = resident_grid(transition_f16_k, 64 * TR_WAVES, cache);
+  const int resident = resident_grid(transition_f16_k<PB>, 64 * TR_WAVES, cache);
   if (resident <= 0) return hipErrorInvalidDevice;
   const int64_t ntiles = (rows + 16 * 2 * TR_WAVES - 1) / (16 * 2 * TR_WAVES);
   const dim3 grid((unsigned)std::min<int64_t>(resident, ntiles));
-  transition_f16_k<<<grid, 64 * TR_WAVES, 0, st>>>(static_cast<const half_t*>(xn), static_cast<const half_t*>(w12),
-                                                   static_cast<const half_t*>(w3), z, accumulate, lnw, lnb, eps,
-                                                   static_cast<half_t*>(xn_next), rows, hidden);
+  transition_f16_k<PB><<<grid, 64 * TR_WAVES, 0, st>>>(
+      static_cast<const half_t*>(xn), static_cast<const half_t*>(w12), static_cast<const half_t*>(w3), z, accumulate,
+      lnw, lnb, eps, static_cast<half_t*>(xn_next), rows, hidden, static_cast<const half_t*>(pb_w), pb_lnw, pb_lnb,
+      pb_eps, static_cast<half_t*>(pb_out), pb_heads);
   return hipGetLastError();
 }
 
@@ -846,9 +877,25 @@ hipError_t launch_transition(const void* xn, const void* w12, const void* w3, fl
                              const float* lnw, const float* lnb, float eps, void* xn_next, int dt, int64_t rows,
                              int hidden, hipStream_t st) {
   if (dt == DT_F16 && hidden % TR_HCH == 0 && (int64_t)2 * hidden * D < (1LL << 31))
-    return trans_f16(xn, w12, w3, z, accumulate, lnw, lnb, eps, xn_next, rows, hidden, st);
+    return trans_f16<false>(xn, w12, w3, z, accumulate, lnw, lnb, eps, xn_next, rows, hidden, nullptr, nullptr,
+                            nullptr, 0.f, nullptr, 0, st);
   return dt == DT_F16 ? trans_t<half_t, 64>(xn, w12, w3, z, accumulate, lnw, lnb, eps, xn_next, rows, hidden, st)
                       : trans_t<float, 32>(xn, w12, w3, z, accumulate, lnw, lnb, eps, xn_next, rows, hidden, st);
+}
+
+// Transition + the s track's pair bias from the updated z: the fp16 kernel computes it in its epilogue; otherwise
+// the pair-bias kernel runs after the transition (same result definition).
+hipError_t launch_transition_pb(const void* xn, const void* w12, const void* w3, float* z, int accumulate,
+                                const float* lnw, const float* lnb, float eps, void* xn_next, const void* pb_w,
+                                const float* pb_lnw, const float* pb_lnb, float pb_eps, void* pb_out, int pb_heads,
+                                int dt, int64_t rows, int hidden, hipStream_t st) {
+  if (pb_heads < 1 || pb_heads > 16) return hipErrorInvalidValue;
+  if (dt == DT_F16 && hidden % TR_HCH == 0 && (int64_t)2 * hidden * D < (1LL << 31))
+    return trans_f16<true>(xn, w12, w3, z, accumulate, lnw, lnb, eps, xn_next, rows, hidden, pb_w, pb_lnw, pb_lnb,
+                           pb_eps, pb_out, pb_heads, st);
+  const hipError_t e = launch_transition(xn, w12, w3, z, accumulate, lnw, lnb, eps, xn_next, dt, rows, hidden, st);
+  if (e != hipSuccess) return e;
+  return launch_pair_bias(z, pb_lnw, pb_lnb, pb_eps, pb_w, pb_out, dt, rows, pb_heads, st);
 }
 
 }  // namespace bzpf

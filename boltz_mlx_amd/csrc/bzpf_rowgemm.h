@@ -237,6 +237,79 @@ __device__ __forceinline__ void resid_ln_rows(const f4 (&y)[RB][8], ZRow zrow, f
   resid_ln_apply<TO, RB>(y, zv, zrow, z, lnw, lnb, eps, xn_next);
 }
 
+// resid_ln_rows for fp16 rows, plus the pair bias Linear(LN_pb(z_new)) of the s track from the same row statistics:
+// with W' = W ⊙ gamma_pb (fp16, LDS [16][ldp]) and bp = W . beta_pb (LDS, fp32),
+//   pb_out[h][zr] = (x_hat . W'[h]) + bp[h],  x_hat = (z_new - mean) * rstd_pb,
+// on one v_mfma_f32_16x16x32_f16 per 32 channels: the B operand is the lane's own 32 normalised channels of its row
+// (k slot 8 g + t <-> channel 32 s + 16 (t / 4) + 4 g + t % 4 in step s), A the same channels of W' for head l % 16,
+// and the accumulator lane (row, g) receives heads 4 g .. 4 g + 3 of its row. The MFMAs run with every lane active;
+// lanes without a row compute on finite stand-in values and store nothing.
+template <int RB, typename ZRow>
+__device__ __forceinline__ void resid_ln_pb_rows(const f4 (&y)[RB][8], ZRow zrow, float* __restrict__ z, int accumulate,
+                                                 const float* __restrict__ lnw, const float* __restrict__ lnb,
+                                                 float eps, half_t* __restrict__ xn_next, const half_t* Wp, int ldp,
+                                                 const float* Bp, float eps_pb, half_t* __restrict__ pb_out,
+                                                 int64_t pb_stride, int pb_heads) {
+  constexpr int D = 128;
+  const int l = threadIdx.x & 63, g = l >> 4, r = l & 15;
+  f4 zv[RB][8];
+  load_z_rows<RB>(zv, zrow, z, accumulate);
+#pragma unroll
+  for (int rb = 0; rb < RB; rb++) {
+    const int64_t zr = zrow(rb);
+    const int64_t rowoff = (zr >= 0 ? zr : 0) * D + 4 * g;
+    float* zp = z + rowoff;
+    f4 v[8];
+    float s = 0.f;
+#pragma unroll
+    for (int cb = 0; cb < 8; cb++) {
+      v[cb] = y[rb][cb] + zv[rb][cb];
+      s += v[cb][0] + v[cb][1] + v[cb][2] + v[cb][3];
+    }
+    if (zr >= 0) {
+#pragma unroll
+      for (int cb = 0; cb < 8; cb++) st4(zp + 16 * cb, v[cb]);
+    }
+    const float mean = xgroups_sum(s) * (1.0f / D);
+    float ss = 0.f;
+#pragma unroll
+    for (int cb = 0; cb < 8; cb++) {
+      const f4 d = v[cb] - mean;
+      ss += d[0] * d[0] + d[1] * d[1] + d[2] * d[2] + d[3] * d[3];
+    }
+    const float var = xgroups_sum(ss) * (1.0f / D);
+    if (lnw != nullptr && zr >= 0) {
+      const float rstd = 1.0f / sqrtf(var + eps);
+      half_t* xp = xn_next + rowoff;
+#pragma unroll
+      for (int cb = 0; cb < 8; cb++) {
+        const int c = 16 * cb + 4 * g;
+        st4(xp + 16 * cb, (v[cb] - mean) * rstd * ld4(lnw + c) + ld4(lnb + c));
+      }
+    }
+    const float rpb = 1.0f / sqrtf(var + eps_pb);
+    f4 acc = f4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int st = 0; st < 4; st++) {
+      const f4 lo = (v[2 * st] - mean) * rpb, hi = (v[2 * st + 1] - mean) * rpb;
+      const half8 bf = half8{(half_t)lo[0], (half_t)lo[1], (half_t)lo[2], (half_t)lo[3],
+                             (half_t)hi[0], (half_t)hi[1], (half_t)hi[2], (half_t)hi[3]};
+      const half_t* wr = Wp + r * ldp + 32 * st + 4 * g;
+      const half4 wlo = *reinterpret_cast<const half4*>(wr);
+      const half4 whi = *reinterpret_cast<const half4*>(wr + 16);
+      const half8 af = half8{wlo[0], wlo[1], wlo[2], wlo[3], whi[0], whi[1], whi[2], whi[3]};
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf, acc, 0, 0, 0);
+    }
+    if (zr >= 0) {
+#pragma unroll
+      for (int e = 0; e < 4; e++) {
+        const int h = 4 * g + e;
+        if (h < pb_heads) pb_out[(int64_t)h * pb_stride + zr] = (half_t)(acc[e] + Bp[h]);
+      }
+    }
+  }
+}
+
 // Index of the calling wave in the grid as a wave-uniform (scalar) value: the compiler cannot prove threadIdx.x / 64
 // uniform by itself, and tile coordinates derived from it would otherwise live (and be divided) in vector registers.
 __device__ __forceinline__ int grid_wave(int waves_per_block) {

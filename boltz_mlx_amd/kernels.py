@@ -273,7 +273,10 @@ def linear_resid_ln(x, w, trans: bool, z, accumulate: bool, next_ln=None, N: int
     return nxt
 
 
-def transition(xn, w12, w3, z, accumulate: bool, next_ln=None):
+def transition(xn, w12, w3, z, accumulate: bool, next_ln=None, pair_bias=None):
+    """z (+)= fc3(silu(xn fc1^T) * (xn fc2^T)); returns next_ln(z_new) (or None). pair_bias = (ln, w) also computes
+    Linear(ln(z_new)) as [H, rows] in w's dtype (the s track's pair bias, z being [N, N, D]) and returns
+    (next_ln(z_new), bias)."""
     _dev(xn, w12, w3, z)
     D = z.shape[-1]
     rows = z.numel() // D
@@ -285,9 +288,21 @@ def transition(xn, w12, w3, z, accumulate: bool, next_ln=None):
     if next_ln is not None:
         nxt = torch.empty((rows, D), dtype=xn.dtype, device=xn.device)
         nw, nb, neps = f32c(next_ln.weight), f32c(next_ln.bias), next_ln.eps
-    call("bzpf_transition", _p(xn), _p(w12), _p(w3), _p(z), int(accumulate), _p(nw), _p(nb), float(neps), _p(nxt),
-         _dt(xn), rows, D, hidden, _stream())
-    return nxt
+    if pair_bias is None:
+        call("bzpf_transition", _p(xn), _p(w12), _p(w3), _p(z), int(accumulate), _p(nw), _p(nb), float(neps),
+             _p(nxt), _dt(xn), rows, D, hidden, _stream())
+        return nxt
+    ln, w = pair_bias
+    _dev(w)
+    H = w.shape[0]
+    if w.shape != (H, D) or w.dtype != xn.dtype:
+        raise ValueError("transition: pair-bias weight must be [H, D] in the storage dtype")
+    N = z.shape[0]
+    bias = torch.empty((H, N, rows // N), dtype=w.dtype, device=z.device)
+    call("bzpf_transition_pb", _p(xn), _p(w12), _p(w3), _p(z), int(accumulate), _p(nw), _p(nb), float(neps),
+         _p(nxt), _p(w), _p(f32c(ln.weight)), _p(f32c(ln.bias)), float(ln.eps), _p(bias), H, _dt(xn), rows, D, hidden,
+         _stream())
+    return nxt, bias
 
 
 def linear(x, w, bias=None, out=None, out_dtype=None, accumulate: bool = False) -> torch.Tensor:

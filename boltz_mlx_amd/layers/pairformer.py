@@ -28,17 +28,19 @@ from boltz_mlx_amd.layers.triangular_attention.attention import (
 from boltz_mlx_amd.layers.triangular_mult import TriangleMultiplicationIncoming, TriangleMultiplicationOutgoing
 
 
-def _pair_chain(layer, z: torch.Tensor, pm: torch.Tensor, xn_in: Optional[torch.Tensor], next_ln, hooks=(None, None)):
+def _pair_chain(layer, z: torch.Tensor, pm: torch.Tensor, xn_in: Optional[torch.Tensor], next_ln, hooks=(None, None),
+                pair_bias=None):
     """The five pair updates on one batch element z [N, N, D] (fp32, updated in place) with pair mask pm [N, N]
-    fp32. Returns next_ln(z_new) in the storage dtype (or None). hooks[0] / hooks[1] are called just before the
-    starting / ending node's attention core is enqueued."""
+    fp32. Returns next_ln(z_new) in the storage dtype (or None); with pair_bias = (LayerNorm, weight) the
+    transition also returns the s track's pair bias of z_new: (next_ln(z_new), bias [H, N, N]). hooks[0] / hooks[1]
+    are called just before the starting / ending node's attention core is enqueued."""
     N, D = z.shape[0], z.shape[-1]
     xn = layer.tri_mul_out.norm_in.to_storage(z).reshape(N * N, D) if xn_in is None else xn_in
     xn = layer.tri_mul_out.fused(xn, pm, z, True, next_ln=layer.tri_mul_in.norm_in)
     xn = layer.tri_mul_in.fused(xn, pm, z, True, next_ln=layer.tri_att_start.layer_norm)
     xn = layer.tri_att_start.fused(xn, pm, z, True, next_ln=layer.tri_att_end.layer_norm, before_core=hooks[0])
     xn = layer.tri_att_end.fused(xn, pm, z, True, next_ln=layer.transition_z.norm, before_core=hooks[1])
-    return layer.transition_z.fused(xn, z, True, next_ln=next_ln)
+    return layer.transition_z.fused(xn, z, True, next_ln=next_ln, pair_bias=pair_bias)
 
 
 class PairformerLayer(torch.nn.Module):
@@ -81,10 +83,14 @@ class PairformerLayer(torch.nn.Module):
         B = z.shape[0]
         xn_next = None
         for b in range(B):
-            xn_next = _pair_chain(self, z[b], pair_mask[b], xn_in if B == 1 else None,
-                                  next_ln if B == 1 else None)
-            self._s_track(s[b], z[b], mask[b])
+            xn_next, bias = _pair_chain(self, z[b], pair_mask[b], xn_in if B == 1 else None,
+                                        next_ln if B == 1 else None, pair_bias=self._pair_bias_args())
+            self._s_update(s[b], bias, mask[b])
         return xn_next
+
+    def _pair_bias_args(self):
+        """(LayerNorm, weight) of the attention's proj_z, for the transition's pair-bias epilogue."""
+        return self.attention.proj_z[0], self.attention.prepare()[3]
 
     def prepare(self) -> None:
         """Cache every kernel weight of the layer in the storage dtype (a one-time conversion per precision; the
@@ -92,9 +98,6 @@ class PairformerLayer(torch.nn.Module):
         for mod in (self.attention, self.tri_mul_out, self.tri_mul_in, self.tri_att_start, self.tri_att_end,
                     self.transition_s, self.transition_z):
             mod.prepare()
-
-    def _s_track(self, s: torch.Tensor, z: torch.Tensor, mask: torch.Tensor) -> None:
-        self._s_update(s, self.attention.pair_bias(z), mask)
 
     def _s_update(self, s: torch.Tensor, bias: torch.Tensor, mask: torch.Tensor) -> None:
         """s += attention(pre_norm_s(s), pair bias) then s += transition_s(s), in place (one batch element)."""
@@ -150,7 +153,8 @@ class PairformerModule(torch.nn.Module):
         attention half is released when layer i + 1's starting-node attention core starts and its transition half
         when the ending-node core starts, so it shares the GPU with those two (non-persistent) kernels rather than
         with the persistent row kernels, whose grids assume the whole GPU. The pair bias is computed on the main
-        stream before z moves on; the main stream waits for the side stream once at the end. (The reference
+        stream (by the transition's epilogue) before z moves on; the main stream waits for the side stream once at
+        the end. (The reference
         pipelines the same way by submitting layer i + 1 while layer i's tail runs, pairformer.py:145-148.)"""
         n, B = len(self.layers), z.shape[0]
         if self.__dict__.get("_bzpf_prepared") != K.storage_dtype():
@@ -185,8 +189,8 @@ class PairformerModule(torch.nn.Module):
             done = []
             for b in range(B):
                 hooks = hooks_for(pending) if b == 0 else (None, None)
-                xn = _pair_chain(layer, z[b], pair_mask[b], xn if B == 1 else None, nxt if B == 1 else None, hooks)
-                bias = layer.attention.pair_bias(z[b])
+                xn, bias = _pair_chain(layer, z[b], pair_mask[b], xn if B == 1 else None, nxt if B == 1 else None,
+                                       hooks, pair_bias=layer._pair_bias_args())
                 bias.record_stream(side)  # allocated on the main stream, read on the side stream
                 done.append((layer, s[b], bias, mask[b]))
             pending = done

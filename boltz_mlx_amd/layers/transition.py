@@ -46,10 +46,11 @@ class Transition(torch.nn.Module):
         """The kernel weights in the storage dtype ([fc1; fc2] and fc3), cached on the module."""
         return K.wcache(self, "w12", self.fc1.weight, self.fc2.weight), K.wcache(self, "w3", self.fc3.weight)
 
-    def fused(self, xn: torch.Tensor, z: torch.Tensor, accumulate: bool = True, next_ln=None):
-        """z (+)= transition from xn = norm(z) (storage dtype); returns next_ln(z_new) when next_ln is given."""
+    def fused(self, xn: torch.Tensor, z: torch.Tensor, accumulate: bool = True, next_ln=None, pair_bias=None):
+        """z (+)= transition from xn = norm(z) (storage dtype); returns next_ln(z_new) when next_ln is given. With
+        pair_bias = (LayerNorm, weight [H, D]) it also returns Linear(LN(z_new)) as [H, N, N]: (next_ln(z_new), bias)."""
         w12, w3 = self.prepare()
-        return K.transition(xn, w12, w3, z, accumulate, next_ln)
+        return K.transition(xn, w12, w3, z, accumulate, next_ln, pair_bias)
 
     def unfused(self, xn: torch.Tensor, out: Optional[torch.Tensor] = None, accumulate: bool = False):
         """fc3(SwiGLU(xn fc12^T)) as separate kernels; accumulate adds into the fp32 `out`."""

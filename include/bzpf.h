@@ -119,6 +119,16 @@ int bzpf_transition(const void* xn, const void* w12, const void* w3, float* z, i
                     const float* next_b, float next_eps, void* xn_next, int dt, int64_t rows, int D, int hidden,
                     void* stream);
 
+/* bzpf_transition, then the s track's pair bias from the updated z: pb_out[h][r] = Linear(LN_pb(z[r]))[h] over the
+ * same rows ([pb_heads][rows] in dt; pb_w [pb_heads, D] in dt, pb_lnw/pb_lnb fp32 [D], 1 <= pb_heads <= 16), as
+ * bzpf_pair_bias computes it. In fp16 the transition's epilogue computes it from the row statistics it already has
+ * (fp16 MFMA on the normalised row with gamma_pb folded into the weights), so z is not read again. Replaces the
+ * reference's proj_z fusion into the pair transition epilogue (boltz_mlx/kernels_nax3.py:702-768). */
+int bzpf_transition_pb(const void* xn, const void* w12, const void* w3, float* z, int accumulate, const float* next_w,
+                       const float* next_b, float next_eps, void* xn_next, const void* pb_w, const float* pb_lnw,
+                       const float* pb_lnb, float pb_eps, void* pb_out, int pb_heads, int dt, int64_t rows, int D,
+                       int hidden, void* stream);
+
 /* Linear layer y[r] = x[r] . W^T + bias (K % 8 == 0; bias may be NULL); accumulate != 0 adds into an fp32 y.
  * Replaces the nn.Linear / kernels.lin16 calls of the s track (boltz_mlx/layers/attentionv2.py:50-52, 70, 84;
  * boltz_mlx/kernels.py:1360-1370). */

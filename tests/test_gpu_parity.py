@@ -351,3 +351,46 @@ def test_pairformer_module_overlap_matches_sequential(precision):
     torch.cuda.synchronize()
     assert torch.equal(z1, z2)
     assert torch.equal(s1, s2)
+
+
+@pytest.mark.parametrize("precision", ["fp32", "f16"], indirect=True)
+@pytest.mark.parametrize("N", [5, 40, 129])
+def test_transition_pair_bias(precision, N):
+    """The transition with the s track's pair bias in its epilogue (bzpf_transition_pb) against the transition
+    followed by the pair-bias kernel on the same z: z and the next LN bit for bit; the bias within the fp16 storage
+    rounding (gamma folded into the fp16 weights), and against Linear(LN(z_new)) in float64."""
+    import torch
+
+    from boltz_mlx_amd import kernels as K
+    from boltz_mlx_amd.layers.norm import LayerNorm
+    from boltz_mlx_amd.layers.transition import Transition
+
+    D, H = 128, 16
+    rng = np.random.default_rng(900 + N)
+    tr = load(Transition(D, 4 * D), rand_params(shapes_transition(D, 4 * D), seed=910 + N, std=0.1))
+    ln_next, ln_pb = LayerNorm(D).cuda(), LayerNorm(D).cuda()
+    with torch.no_grad():
+        for ln in (ln_next, ln_pb):
+            ln.weight.copy_(torch.tensor(1 + 0.3 * rng.standard_normal(D)))
+            ln.bias.copy_(torch.tensor(0.3 * rng.standard_normal(D)))
+    w_pb = dev(0.2 * rng.standard_normal((H, D)), K.storage_dtype())
+    z0 = dev(3 * rng.standard_normal((N, N, D)))
+    xn = tr.norm.to_storage(z0).reshape(N * N, D)
+    z1, z2 = z0.clone(), z0.clone()
+    xn1, bias1 = tr.fused(xn, z1, True, next_ln=ln_next, pair_bias=(ln_pb, w_pb))
+    xn2 = tr.fused(xn, z2, True, next_ln=ln_next)
+    bias2 = K.pair_bias(z2, ln_pb, w_pb)
+    torch.cuda.synchronize()
+    assert torch.equal(z1, z2)
+    assert torch.equal(xn1, xn2)
+    assert bias1.shape == (H, N, N) and bias1.dtype == bias2.dtype
+    b1, b2 = bias1.float().cpu().numpy(), bias2.float().cpu().numpy()
+    scale = np.abs(b2).max()
+    tol = 1e-6 if precision == "fp32" else 4e-3
+    assert np.abs(b1 - b2).max() <= tol * scale
+    zn = z2.double().cpu().numpy()
+    mu, var = zn.mean(-1, keepdims=True), zn.var(-1, keepdims=True)
+    gam, bet = ln_pb.weight.detach().double().cpu().numpy(), ln_pb.bias.detach().double().cpu().numpy()
+    lnz = (zn - mu) / np.sqrt(var + ln_pb.eps) * gam + bet
+    ref = np.einsum("ijc,hc->hij", lnz, w_pb.double().cpu().numpy())
+    assert np.abs(b1 - ref).max() <= (1e-5 if precision == "fp32" else 6e-3) * np.abs(ref).max()

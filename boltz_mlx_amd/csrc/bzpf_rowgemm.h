@@ -206,7 +206,7 @@ __device__ __forceinline__ void resid_ln_apply(const f4 (&y)[RB][8], const f4 (&
     }
     if (zr >= 0) {
 #pragma unroll
-      for (int cb = 0; cb < 8; cb++) st4(zp + 16 * cb, v[cb]);
+      for (int cb = 0; cb < 8; cb++) __builtin_nontemporal_store(v[cb], reinterpret_cast<f4*>(zp + 16 * cb));
     }
     if (lnw == nullptr) continue;
     const float mean = xgroups_sum(s) * (1.0f / D);
@@ -268,7 +268,7 @@ __device__ __forceinline__ void resid_ln_pb_rows(const f4 (&y)[RB][8], ZRow zrow
     }
     if (zr >= 0) {
 #pragma unroll
-      for (int cb = 0; cb < 8; cb++) st4(zp + 16 * cb, v[cb]);
+      for (int cb = 0; cb < 8; cb++) __builtin_nontemporal_store(v[cb], reinterpret_cast<f4*>(zp + 16 * cb));
     }
     const float mean = xgroups_sum(s) * (1.0f / D);
     float ss = 0.f;

@@ -1,7 +1,8 @@
 // fp16 flash triangle-attention core on MFMA (v_mfma_f32_32x32x16_f16), head width C = 32.
 //
-// Work unit: one (head h, row i, 128 queries); 4 waves of 32 queries. The 32 x 32 MFMA form is used throughout: on
-// gfx950 it delivers about 1.6x the FLOP rate of the 16 x 16 x 32 form and overlaps better with the VALU softmax.
+// Work unit: one (head h, row i, 128 queries); 4 waves of 32 queries. The 32 x 32 MFMA form is used throughout: a
+// 32-query tile per wave keeps a query's softmax statistics in two lanes (one cross-lane step) and frees registers
+// for a fourth wave per SIMD (125 VGPRs).
 // The logits are formed transposed, S^T = K Q^T + Cinit, one 32-key x 32-query tile per MFMA pair (A = 32 keys of K
 // from LDS, B = the wave's Q fragment, held in registers for the whole row), so lane l owns query l % 32 and 16 keys
 // of each 32-key tile (8 (e / 4) + 4 (l / 32) + e % 4 in accumulator element e): a query's softmax statistics live

@@ -115,16 +115,17 @@ __global__ __launch_bounds__(256, 2) void trimul_contract_kernel(const T* __rest
   }
 }
 
-// fp16 form: 256 x 256 tiles on v_mfma_f32_32x32x16_f16, 8 waves of 128 (j) x 64 (i) = 4 x 2 blocks of 32 x 32
-// (128 accumulator registers per lane). The 128 x 128 tile of the fp32 form moves 32 KB from L2 per 2.1 MFLOP;
-// this tile halves that (64 KB per 8.4 MFLOP per 64-element K stage), which is what bounds the contraction: the
-// vector-memory path that feeds LDS, not the matrix cores. K stages (64 elements) are double-buffered in LDS
-// (147 KB, one workgroup per CU) with the next stage loaded into registers while the current one computes.
+// fp16 form: 256 x 256 tiles on v_mfma_f32_32x32x16_f16, 16 waves of 64 (j) x 64 (i) = 2 x 2 blocks of 32 x 32
+// (64 accumulator registers per lane, 4 waves per SIMD). The 128 x 128 tile of the fp32 form moves 32 KB from L2 per
+// 2.1 MFLOP; this tile halves that (64 KB per 8.4 MFLOP per 64-element K stage). K stages (64 elements) are
+// double-buffered in LDS (147 KB, one workgroup per CU) with the next stage loaded into registers while the current
+// one computes; four waves per SIMD (rather than two with 128 x 64 wave tiles) keep the matrix cores busier through
+// each stage's barrier and LDS waits.
 // Operand layouts (A = rows of b, B = rows of a, both K-contiguous): lane l holds row l % 32 and 8 consecutive k;
 // in MFMA step s of a stage, lane half h = l / 32 takes k = 32 h + 8 s .. + 7, so over the 4 steps a lane reads 64
 // contiguous bytes of its row (a permutation of the k sum shared by A and B). The accumulator lane holds
 // o^T[j = 8 q + 4 h + e][i = l % 32] in element 4 q + e: 4 runs of 4 consecutive j of one i.
-constexpr int CT_BT = 256, CT_WAVES = 8;
+constexpr int CT_BT = 256, CT_WAVES = 16;
 
 __global__ __launch_bounds__(64 * CT_WAVES, 1) void trimul_contract_f16_k(const half_t* __restrict__ ab,
                                                                           half_t* __restrict__ o, int64_t N,
@@ -145,7 +146,7 @@ __global__ __launch_bounds__(64 * CT_WAVES, 1) void trimul_contract_f16_k(const 
   const half_t* a = ab + c * N * ld;
   const half_t* b = ab + ((int64_t)D + c) * N * ld;
   const int t = threadIdx.x, wave = t >> 6, l = t & 63, r = l & 31, h = l >> 5;
-  const int wj = wave >> 2, wi = wave & 3;  // wave tile: j = 128 wj .., i = 64 wi ..
+  const int wj = wave >> 2, wi = wave & 3;  // wave tile: j = 64 wj .., i = 64 wi ..
 
   // per-thread rows are fixed; stages only advance k (rows past N read row N - 1; their outputs are not stored)
   const half_t* src[LOADS];
@@ -172,9 +173,9 @@ __global__ __launch_bounds__(64 * CT_WAVES, 1) void trimul_contract_f16_k(const 
     }
   };
 
-  f16x acc[4][2];  // acc[jb][ib]: o^T block (j = 128 wj + 32 jb .., i = 64 wi + 32 ib ..)
+  f16x acc[2][2];  // acc[jb][ib]: o^T block (j = 64 wj + 32 jb .., i = 64 wi + 32 ib ..)
 #pragma unroll
-  for (int jb = 0; jb < 4; jb++)
+  for (int jb = 0; jb < 2; jb++)
 #pragma unroll
     for (int ib = 0; ib < 2; ib++)
 #pragma unroll
@@ -190,16 +191,16 @@ __global__ __launch_bounds__(64 * CT_WAVES, 1) void trimul_contract_f16_k(const 
     gload((int64_t)min(st + 1, nst - 1) * BK);
     __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs (the scheduler sinks them otherwise)
     const half_t* Ab = As[buf] + (64 * wi + r) * LDT + 32 * h;
-    const half_t* Bb = Bs[buf] + (128 * wj + r) * LDT + 32 * h;
+    const half_t* Bb = Bs[buf] + (64 * wj + r) * LDT + 32 * h;
 #pragma unroll
     for (int s = 0; s < 4; s++) {
-      half8 fa[2], fb[4];
+      half8 fa[2], fb[2];
 #pragma unroll
       for (int q = 0; q < 2; q++) fa[q] = *reinterpret_cast<const half8*>(Ab + 32 * q * LDT + 8 * s);
 #pragma unroll
-      for (int q = 0; q < 4; q++) fb[q] = *reinterpret_cast<const half8*>(Bb + 32 * q * LDT + 8 * s);
+      for (int q = 0; q < 2; q++) fb[q] = *reinterpret_cast<const half8*>(Bb + 32 * q * LDT + 8 * s);
 #pragma unroll
-      for (int jb = 0; jb < 4; jb++)
+      for (int jb = 0; jb < 2; jb++)
 #pragma unroll
         for (int ib = 0; ib < 2; ib++)
           acc[jb][ib] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[jb], fa[ib], acc[jb][ib], 0, 0, 0);
@@ -213,10 +214,10 @@ __global__ __launch_bounds__(64 * CT_WAVES, 1) void trimul_contract_f16_k(const 
     const int64_t i = i0 + 64 * wi + 32 * ib + r;
     if (i >= N) continue;
 #pragma unroll
-    for (int jb = 0; jb < 4; jb++)
+    for (int jb = 0; jb < 2; jb++)
 #pragma unroll
       for (int q = 0; q < 4; q++) {
-        const int64_t j = j0 + 128 * wj + 32 * jb + 8 * q + 4 * h;
+        const int64_t j = j0 + 64 * wj + 32 * jb + 8 * q + 4 * h;
         if (j >= ld) continue;
         const f16x& v = acc[jb][ib];
         *reinterpret_cast<half4*>(oc + i * ld + j) =

@@ -255,8 +255,10 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
 #pragma unroll
       for (int e = kt == 0 ? 2 : 0; e < 16; e += 2) mx = fmaxf(fmaxf(mx, s[kt][e]), s[kt][e + 1]);
     const float mloc = halves_max(mx);
-    // s holds logit - mref; raise the maximum only when the block exceeds it by more than 2^THRESH
-    if (__any(unset || mloc > THRESH)) {
+    // s holds logit - mref; raise the maximum only when the block exceeds it by more than 2^THRESH. Lanes of the
+    // padded queries past N (whose bias rows are never written) take no part in the decision, so the result of a
+    // real query never depends on them.
+    if (__any(jq < N && (unset || mloc > THRESH))) {
       const float mn = fmaxf(m_run, mloc + mref);
       const float corr = __builtin_amdgcn_exp2f(m_run - mn);
       oacc *= corr;

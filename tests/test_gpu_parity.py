@@ -323,6 +323,34 @@ def test_triattn_core_mfma_vs_valu(N, trans):
     assert m["finite"] and m["max_rel"] <= 5e-3 and m["rel_fro"] <= 2e-3, m
 
 
+@pytest.mark.parametrize("N", [40, 129])
+def test_triattn_core_ignores_padded_query_slots(N):
+    """The bias slots of the padded queries past N (up to the 32-query tile) are never written by the projection. A
+    real query's output must not depend on them: the core's lazy-rescale decision is taken over the real queries
+    only. Large finite values there (which raise the maximum of the padded lanes in many key blocks) must give the
+    same bits as zeros."""
+    from boltz_mlx_amd import kernels as K
+
+    H, C = 4, 32
+    rng = np.random.default_rng(1000 + N)
+    ldk = K.row_pitch(N)
+    qkg = dev(rng.standard_normal((3 * H, N * N, C)), torch.float16)
+    vt = dev(rng.standard_normal((H, N, C, ldk)), torch.float16)
+    dense = np.zeros((H, N, ldk), dtype=np.float32)
+    dense[:, :, :N] = 2 * rng.standard_normal((H, N, N))
+    outs = []
+    for big in (False, True):
+        tb_np = rng.uniform(-6e4, 6e4, K.tri_bias_numel(N, H)).astype(np.float32) if big else np.zeros(
+            K.tri_bias_numel(N, H), np.float32)
+        tb_np[_tb_index(N, H).ravel()] = dense.ravel()
+        mask = np.ones((N, N), np.float32)
+        mask[:, -3:] = 0
+        outs.append(K.triattn_core(qkg, vt, dev(tb_np, torch.float16), dev(mask), False, 1e9, N, H, C, impl=2))
+    torch.cuda.synchronize()
+    assert torch.isfinite(outs[0]).all()
+    assert torch.equal(outs[0], outs[1])
+
+
 @pytest.mark.parametrize("precision", ["f16"], indirect=True)
 def test_pairformer_module_overlap_matches_sequential(precision):
     """The module runs each block's s track on a second stream, overlapped with the next block's pair kernels; the

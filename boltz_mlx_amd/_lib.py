@@ -22,6 +22,7 @@ SIGNATURES = {
     "bzpf_row_pitch": [i64],
     "bzpf_layernorm": [vp, i32, vp, vp, f32, vp, i32, i64, i32, vp],
     "bzpf_add_ln": [vp, vp, i32, f32, i32, vp, vp, f32, vp, i32, i32, i64, i32, vp],
+    "bzpf_count_nonfinite": [vp, i32, i64, vp, vp],
     "bzpf_trimul_proj": [vp, vp, vp, f32, i32, vp, i32, i64, i64, i32, vp],
     "bzpf_trimul_contract": [vp, vp, i32, i64, i64, i32, vp],
     "bzpf_trimul_tail": [vp, vp, vp, f32, vp, vp, vp, vp, i32, vp, vp, f32, vp, i32, i64, i64, i32, vp],

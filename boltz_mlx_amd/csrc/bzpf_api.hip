@@ -57,6 +57,15 @@ int bzpf_layernorm(const void* x, int x_dt, const float* w, const float* b, floa
   return done(bzpf::launch_layernorm(x, x_dt, w, b, eps, y, y_dt, rows, D, S(stream)), "bzpf_layernorm");
 }
 
+int bzpf_count_nonfinite(const void* x, int dt, int64_t n, int* count, void* stream) {
+  REQUIRE(count != nullptr, "bzpf_count_nonfinite: count is NULL");
+  REQUIRE(dt_ok(dt), "bzpf_count_nonfinite: bad dtype %d", dt);
+  REQUIRE(n >= 0, "bzpf_count_nonfinite: n < 0");
+  if (n == 0) return BZPF_OK;
+  REQUIRE_PTR(x);
+  return done(bzpf::launch_count_nonfinite(x, dt, n, count, S(stream)), "bzpf_count_nonfinite");
+}
+
 int bzpf_add_ln(float* z, const void* y, int y_dt, float y_scale, int trans_y, const float* w, const float* b,
                 float eps, void* ln, int ln_dt, int trans_out, int64_t N, int D, void* stream) {
   REQUIRE_PTR(z);

@@ -12,6 +12,7 @@ hipError_t launch_layernorm(const void* x, int x_dt, const float* w, const float
                             int64_t rows, int D, hipStream_t st);
 hipError_t launch_add_ln(float* z, const void* y, int y_dt, float scale, int trans_y, const float* w, const float* b,
                          float eps, void* ln, int ln_dt, int trans_out, int64_t N, int D, hipStream_t st);
+hipError_t launch_count_nonfinite(const void* x, int dt, int64_t n, int* count, hipStream_t st);
 
 hipError_t launch_trimul_proj(const void* xn, const void* w, const float* mask, float scale, int incoming, void* ab,
                               int dt, int64_t N, int64_t ld, hipStream_t st);

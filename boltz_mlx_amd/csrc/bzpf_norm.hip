@@ -4,6 +4,8 @@
 // y, LN(z_new) with optional transposed write).
 // Layout: 16 lanes per row, each lane holding D/16 values as 4-element vectors (coalesced 64-byte+ row segments);
 // a workgroup of 256 threads covers 16 rows.
+#include <algorithm>
+
 #include "bzpf_common.h"
 #include "bzpf_kernels.h"
 
@@ -159,6 +161,53 @@ hipError_t launch_add_ln(float* z, const void* y, int y_dt, float scale, int tra
   if (y_dt == DT_F16 && ln_dt == DT_F32) return addln_dispatch<half_t, float>(z, y, scale, trans_y, w, b, eps, ln, trans_out, N, D, st);
   if (y_dt == DT_F16 && ln_dt == DT_F16) return addln_dispatch<half_t, half_t>(z, y, scale, trans_y, w, b, eps, ln, trans_out, N, D, st);
   return hipErrorInvalidValue;
+}
+
+// Count of inf / nan elements, added to *count: the fp16 overflow guard's check of the fp32 residual streams
+// (reference: kernels.guard_residual / guard_take, boltz_mlx/kernels.py:1262-1282, applied in model.py:176-193).
+// A value is non-finite when its exponent field is all ones (integer test, independent of the compiler's
+// floating-point assumptions). Grid-stride over 16-byte vectors; one atomic per wave that found any.
+template <typename T>
+__global__ __launch_bounds__(256) void count_nonfinite_k(const T* __restrict__ x, int64_t n, int* __restrict__ count) {
+  constexpr int VEC = 16 / sizeof(T);
+  const int64_t nvec = n / VEC;
+  const int64_t stride = (int64_t)gridDim.x * 256;
+  int c = 0;
+  const auto bad32 = [](uint32_t u) { return (u & 0x7f800000u) == 0x7f800000u; };
+  const auto bad16 = [](uint32_t u) { return (u & 0x7c00u) == 0x7c00u; };
+  for (int64_t v = (int64_t)blockIdx.x * 256 + threadIdx.x; v < nvec; v += stride) {
+    const u32x4_t w = *reinterpret_cast<const u32x4_t*>(x + v * VEC);
+#pragma unroll
+    for (int e = 0; e < 4; e++) {
+      if constexpr (sizeof(T) == 4) {
+        c += bad32(w[e]);
+      } else {
+        c += bad16(w[e] & 0xffffu) + bad16(w[e] >> 16);
+      }
+    }
+  }
+  if (blockIdx.x == 0) {  // the tail past the last whole vector
+    for (int64_t i = nvec * VEC + threadIdx.x; i < n; i += 256) {
+      if constexpr (sizeof(T) == 4) {
+        c += bad32(__float_as_uint(x[i]));
+      } else {
+        c += bad16(__builtin_bit_cast(uint16_t, x[i]));
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) c += __shfl_xor(c, o, 64);
+  if ((threadIdx.x & 63) == 0 && c > 0) atomicAdd(count, c);
+}
+
+hipError_t launch_count_nonfinite(const void* x, int dt, int64_t n, int* count, hipStream_t st) {
+  const int64_t vec = dt == DT_F16 ? 8 : 4;
+  const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>((n / vec + 255) / 256, 2048));
+  if (dt == DT_F16)
+    count_nonfinite_k<half_t><<<(unsigned)blocks, 256, 0, st>>>(static_cast<const half_t*>(x), n, count);
+  else
+    count_nonfinite_k<float><<<(unsigned)blocks, 256, 0, st>>>(static_cast<const float*>(x), n, count);
+  return hipGetLastError();
 }
 
 }  // namespace bzpf

@@ -22,6 +22,10 @@ from boltz_mlx_amd._lib import F16, F32
 from boltz_mlx_amd._lib import call as _call
 
 PRECISION = os.environ.get("BOLTZ_MLX_PRECISION", "fp32")
+# fp16 overflow guard (boltz_mlx/kernels.py:1230-1236): after an f16 pass over the trunk, the fp32 residual streams
+# are checked for inf / nan (one count per stream) and the pass is recomputed in fp32 when any is found.
+# BOLTZ_MLX_GUARDS=0 or BOLTZ_MLX_GUARD_MODE=off turns it off.
+GUARDS = os.environ.get("BOLTZ_MLX_GUARDS", "1") == "1" and os.environ.get("BOLTZ_MLX_GUARD_MODE", "residual") != "off"
 TRIMULT_K = int(os.environ.get("BOLTZ_MLX_TRIMULT_K", "4"))
 
 
@@ -132,6 +136,16 @@ def layer_norm(x: torch.Tensor, weight, bias, eps: float = 1e-5, out_dtype=torch
     b = None if bias is None else f32c(bias)
     call("bzpf_layernorm", _p(x), _dt(x), _p(w), _p(b), float(eps), _p(y), _dt(y), x.numel() // D, D, _stream())
     return y
+
+
+def count_nonfinite(*tensors: torch.Tensor) -> torch.Tensor:
+    """Device int32 [1]: the number of inf / nan elements over the given fp32 / fp16 tensors, without a host sync
+    (the residual-mode overflow guard, boltz_mlx/kernels.py:1262-1282)."""
+    _dev(*tensors)
+    count = torch.zeros((1,), dtype=torch.int32, device=tensors[0].device)
+    for t in tensors:
+        call("bzpf_count_nonfinite", _p(t), _dt(t), t.numel(), _p(count), _stream())
+    return count
 
 
 def add_ln(z: torch.Tensor, y: torch.Tensor, ln=None, scale: float = 1.0, trans_y: bool = False,

@@ -13,6 +13,7 @@ layer's transition (the reference's PAIRLNX carry, pairformer.py:145-148, 243-24
 
 from __future__ import annotations
 
+import sys
 from typing import Optional
 
 import torch
@@ -41,6 +42,28 @@ def _pair_chain(layer, z: torch.Tensor, pm: torch.Tensor, xn_in: Optional[torch.
     xn = layer.tri_att_start.fused(xn, pm, z, True, next_ln=layer.tri_att_end.layer_norm, before_core=hooks[0])
     xn = layer.tri_att_end.fused(xn, pm, z, True, next_ln=layer.transition_z.norm, before_core=hooks[1])
     return layer.transition_z.fused(xn, z, True, next_ln=next_ln, pair_bias=pair_bias)
+
+
+def _guarded(owner: torch.nn.Module, run, outs: tuple, ins: tuple) -> None:
+    """run() writes the fp32 streams `outs` in place, starting from copies of `ins`. In f16 with the guard on, the
+    streams are checked for inf / nan afterwards (one device count, one sync) and, if any is found, the pass is
+    recomputed with the fp32 kernels from `ins` (the reference's per-recycle fallback, boltz_mlx/model.py:176-193,
+    with its stderr line and fallback counter)."""
+    run()
+    if not (K.f16() and K.GUARDS):
+        return
+    if int(K.count_nonfinite(*outs).item()) == 0:
+        return
+    owner.fp16_fallbacks += 1
+    print(f"boltz_mlx_amd: fp16 overflow guard hit; pass recomputed in fp32 (fallback {owner.fp16_fallbacks})",
+          file=sys.stderr)
+    for o, i in zip(outs, ins):
+        o.copy_(i)
+    K.set_precision("fp32")
+    try:
+        run()
+    finally:
+        K.set_precision("f16")
 
 
 class PairformerLayer(torch.nn.Module):
@@ -125,6 +148,7 @@ class PairformerModule(torch.nn.Module):
         self.dropout = dropout
         self.num_heads = num_heads
         self.post_layer_norm = post_layer_norm
+        self.fp16_fallbacks = 0  # passes the fp16 overflow guard recomputed in fp32
         self.layers = torch.nn.ModuleList([
             PairformerLayer(token_s, token_z, num_heads, dropout, pairwise_head_width, pairwise_num_heads,
                             post_layer_norm, v2)
@@ -133,9 +157,13 @@ class PairformerModule(torch.nn.Module):
 
     def forward(self, s: torch.Tensor, z: torch.Tensor, mask: torch.Tensor, pair_mask: torch.Tensor,
                 use_kernels: bool = False) -> tuple[torch.Tensor, torch.Tensor]:
+        """All layers on copies of s, z; in f16 the fp16 overflow guard checks the result and recomputes the pass
+        in fp32 if it holds inf / nan (fp16_fallbacks counts those)."""
+        s_in, z_in = s, z
         s = s.to(torch.float32).clone().contiguous()
         z = z.to(torch.float32).clone().contiguous()
-        self.inplace(s, z, mask.to(torch.float32).contiguous(), pair_mask.to(torch.float32).contiguous())
+        m, pm = mask.to(torch.float32).contiguous(), pair_mask.to(torch.float32).contiguous()
+        _guarded(self, lambda: self.inplace(s, z, m, pm), (s, z), (s_in, z_in))
         return s, z
 
     def inplace(self, s: torch.Tensor, z: torch.Tensor, mask: torch.Tensor, pair_mask: torch.Tensor) -> None:
@@ -238,16 +266,22 @@ class PairformerNoSeqModule(torch.nn.Module):
         self.num_blocks = num_blocks
         self.dropout = dropout
         self.post_layer_norm = post_layer_norm
+        self.fp16_fallbacks = 0  # passes the fp16 overflow guard recomputed in fp32
         self.layers = torch.nn.ModuleList([
             PairformerNoSeqLayer(token_z, dropout, pairwise_head_width, pairwise_num_heads, post_layer_norm)
             for _ in range(num_blocks)
         ])
 
     def forward(self, z: torch.Tensor, pair_mask: torch.Tensor, use_kernels: bool = False) -> torch.Tensor:
+        z_in = z
         z = z.to(torch.float32).clone().contiguous()
         pm = pair_mask.to(torch.float32).contiguous()
-        n, xn = len(self.layers), None
-        for i, layer in enumerate(self.layers):
-            nxt = self.layers[i + 1].tri_mul_out.norm_in if i + 1 < n else None
-            xn = layer.inplace(z, pm, xn_in=xn, next_ln=nxt)
+
+        def run():
+            n, xn = len(self.layers), None
+            for i, layer in enumerate(self.layers):
+                nxt = self.layers[i + 1].tri_mul_out.norm_in if i + 1 < n else None
+                xn = layer.inplace(z, pm, xn_in=xn, next_ln=nxt)
+
+        _guarded(self, run, (z,), (z_in,))
         return z

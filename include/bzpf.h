@@ -45,6 +45,11 @@ int64_t bzpf_row_pitch(int64_t N);
 int bzpf_layernorm(const void* x, int x_dt, const float* w, const float* b, float eps, void* y, int y_dt,
                    int64_t rows, int D, void* stream);
 
+/* *count += the number of inf / nan among the n elements of x (fp32 or fp16; device int counter, no host sync): the
+ * fp16 overflow guard's check of the residual streams. Replaces kernels.guard_residual / guard_take
+ * (boltz_mlx/kernels.py:1262-1282) as used per recycle in boltz_mlx/model.py:176-193. */
+int bzpf_count_nonfinite(const void* x, int dt, int64_t n, int* count, void* stream);
+
 /* z[r] += y[trans_y ? T(r) : r] * y_scale over the N*N rows of z [N, N, D] (T swaps the two token axes); then,
  * when ln != NULL, ln[trans_out ? T(r) : r] = LN(z[r]). Replaces kernels.add_ln (boltz_mlx/kernels.py:1448-1480)
  * and kernels.radd (1305-1310). */

@@ -323,6 +323,62 @@ def test_triattn_core_mfma_vs_valu(N, trans):
     assert m["finite"] and m["max_rel"] <= 5e-3 and m["rel_fro"] <= 2e-3, m
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("n", [1, 7, 4099, 1_000_003])
+def test_count_nonfinite(dtype, n):
+    """bzpf_count_nonfinite against numpy on +inf, -inf and nan planted at seeded positions (the tail past the last
+    16-byte vector and the very last element included), and on a clean tensor."""
+    from boltz_mlx_amd import kernels as K
+
+    rng = np.random.default_rng(n)
+    x = (100 * rng.standard_normal(n)).astype(np.float32)
+    assert int(K.count_nonfinite(dev(x, dtype)).item()) == 0
+    pos = np.unique(np.concatenate([rng.integers(0, n, size=min(n, 37)), [n - 1]]))
+    x[pos] = rng.choice([np.inf, -np.inf, np.nan], size=pos.size)
+    if dtype == torch.float16:
+        x[0] = 7e4 if 0 not in pos else x[0]  # rounds to +inf in fp16
+    with np.errstate(over="ignore"):
+        ref = int((~np.isfinite(x.astype(np.float16 if dtype == torch.float16 else np.float32))).sum())
+    t = dev(x, dtype)
+    assert int(K.count_nonfinite(t).item()) == ref
+    assert int(K.count_nonfinite(t, t).item()) == 2 * ref
+
+
+def test_fp16_guard_recomputes_in_fp32():
+    """A transition whose fp16 hidden activations overflow (fc1/fc2 scaled up): the f16 pass leaves inf/nan in z,
+    the guard sees them and recomputes the pass with the fp32 kernels, so forward returns exactly the fp32 result and
+    counts one fallback (boltz_mlx/model.py:176-193). With the guard off, the f16 result is not finite."""
+    from boltz_mlx_amd import kernels as K
+    from boltz_mlx_amd.layers.pairformer import PairformerModule
+
+    N, cs, cz, H = 24, 384, 128, 16
+    p = {f"layers.0.{k}": v for k, v in rand_params(shapes_layer(cs, cz, H), seed=77, std=0.05).items()}
+    for k in ("layers.0.transition_z.fc1.weight", "layers.0.transition_z.fc2.weight"):
+        p[k] = 300.0 * p[k]
+    z, tok, pm = pair_inputs(N, cz, seed=78, n_pad=2)
+    s = np.random.default_rng(79).standard_normal((1, N, cs))
+    args = (dev(s), dev(z), dev(tok), dev(pm))
+    prev, prev_guard = K.PRECISION, K.GUARDS
+    try:
+        K.set_precision("fp32")
+        ref = load(PairformerModule(cs, cz, 1, H), p)
+        s32, z32 = ref(*args)
+        assert torch.isfinite(z32).all() and torch.isfinite(s32).all()
+        K.set_precision("f16")
+        m = load(PairformerModule(cs, cz, 1, H), p)
+        K.GUARDS = False
+        _, z16 = m(*args)
+        assert not torch.isfinite(z16).all()
+        K.GUARDS = True
+        s_g, z_g = m(*args)
+        assert m.fp16_fallbacks == 1
+        assert K.PRECISION == "f16"
+        assert torch.equal(z_g, z32) and torch.equal(s_g, s32)
+    finally:
+        K.set_precision(prev)
+        K.GUARDS = prev_guard
+
+
 @pytest.mark.parametrize("N", [40, 129])
 def test_triattn_core_ignores_padded_query_slots(N):
     """The bias slots of the padded queries past N (up to the 32-query tile) are never written by the projection. A

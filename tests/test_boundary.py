@@ -115,6 +115,29 @@ def test_safetensors_roundtrip(tmp_path):
     assert torch.equal(t.fc3.weight, torch.tensor(st["pairformer_module.layers.0.transition_z.fc3.weight"]))
 
 
+def test_mixed_fp16_checkpoint_loads_exactly(tmp_path):
+    """A mixed checkpoint (the reference's boltz_mlx/mixed.py: fp16 copies of the GEMM weights, fp32 for the rest)
+    loads through the same strict loader: the fp16 tensors become fp32 parameters exactly, so the fp16 operands the
+    kernels build from them are the file's fp16 bits."""
+    from safetensors.numpy import save_file
+
+    from boltz_mlx_amd.layers.transition import Transition
+    from boltz_mlx_amd.weights import load_safetensors
+
+    full = {k: v.astype(np.float32) for k, v in rand_params(shapes_transition(128, 512), seed=5).items()}
+    mixed = {k: (v.astype(np.float16) if k.endswith("weight") and v.ndim == 2 else v) for k, v in full.items()}
+    p = tmp_path / "mixed.safetensors"
+    save_file(mixed, str(p))
+    t = load_safetensors(Transition(128, 512), str(p))
+    for k, v in mixed.items():
+        got = dict(t.named_parameters())[k].detach()
+        assert got.dtype == torch.float32
+        if v.dtype == np.float16:
+            assert np.array_equal(got.half().numpy().view(np.uint16), v.view(np.uint16)), k
+        else:
+            assert torch.equal(got, torch.tensor(v)), k
+
+
 def test_no_cpu_compute_path():
     """The product path refuses CPU tensors instead of computing them some other way."""
     from boltz_mlx_amd import _lib

@@ -118,9 +118,10 @@ __global__ __launch_bounds__(256, 2) void trimul_contract_kernel(const T* __rest
 // fp16 form: 256 x 256 tiles on v_mfma_f32_32x32x16_f16, 16 waves of 64 (j) x 64 (i) = 2 x 2 blocks of 32 x 32
 // (64 accumulator registers per lane, 4 waves per SIMD). The 128 x 128 tile of the fp32 form moves 32 KB from L2 per
 // 2.1 MFLOP; this tile halves that (64 KB per 8.4 MFLOP per 64-element K stage). K stages (64 elements) are
-// double-buffered in LDS (147 KB, one workgroup per CU) with the next stage loaded into registers while the current
-// one computes; four waves per SIMD (rather than two with 128 x 64 wave tiles) keep the matrix cores busier through
-// each stage's barrier and LDS waits.
+// double-buffered in LDS (147 KB, one workgroup per CU); two register sets carry the next two stages, so each load
+// has two stages of compute to land (one stage, about 1 us, is shorter than the loaded L2/HBM latency); four waves
+// per SIMD (rather than two with 128 x 64 wave tiles) keep the matrix cores busier through each stage's barrier and
+// LDS waits.
 // Operand layouts (A = rows of b, B = rows of a, both K-contiguous): lane l holds row l % 32 and 8 consecutive k;
 // in MFMA step s of a stage, lane half h = l / 32 takes k = 32 h + 8 s .. + 7, so over the 4 steps a lane reads 64
 // contiguous bytes of its row (a permutation of the k sum shared by A and B). The accumulator lane holds
@@ -148,29 +149,28 @@ __global__ __launch_bounds__(64 * CT_WAVES, 1) void trimul_contract_f16_k(const 
   const int t = threadIdx.x, wave = t >> 6, l = t & 63, r = l & 31, h = l >> 5;
   const int wj = wave >> 2, wi = wave & 3;  // wave tile: j = 64 wj .., i = 64 wi ..
 
-  // per-thread rows are fixed; stages only advance k (rows past N read row N - 1; their outputs are not stored)
-  const half_t* src[LOADS];
-  int dst_off[LOADS];
-#pragma unroll
-  for (int v = 0; v < LOADS; v++) {
-    const int e = v * NT + t, rr = e / VPR, col = (e % VPR) * 8;
-    const bool isb = rr >= BT;
-    int64_t row = (isb ? j0 : i0) + (isb ? rr - BT : rr);
-    if (row >= N) row = N - 1;
-    src[v] = (isb ? b : a) + row * ld + col;
-    dst_off[v] = (isb ? 2 * BT * LDT : 0) + (isb ? rr - BT : rr) * LDT + col;  // from As[buf] (Bs follows As)
-  }
-  u32x4_t reg[LOADS];
-  auto gload = [&](int64_t k0) {
-#pragma unroll
-    for (int v = 0; v < LOADS; v++) reg[v] = *reinterpret_cast<const u32x4_t*>(src[v] + k0);
-  };
-  auto lstore = [&](int buf) {
+  // Staging: thread t moves 16-byte vector (t / 8, 8 (t % 8)) of each 128-row quarter: quarters 0, 1 of a (rows
+  // i0 ..), 2, 3 of b (rows j0 ..). Loads go through buffer resources: the lane offset is fixed, the quarter's rows
+  // and the stage's k ride in the scalar offset, and rows past N read as zeros (range check; those outputs are not
+  // stored).
+  constexpr int RSRC_CFG = 0x00020000;  // raw buffer, 32-bit data format
+  const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc((void*)a, 0, (int)(N * ld * 2), RSRC_CFG);
+  const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc((void*)b, 0, (int)(N * ld * 2), RSRC_CFG);
+  const int voff = (int)(((t >> 3) * ld + (t & 7) * 8) * 2);
+  const int loff = (t >> 3) * LDT + (t & 7) * 8;  // LDS element offset inside a quarter
+  // two register sets: stage s + 2 is loaded while stage s computes, so each load has two stages of time to land
+  u32x4_t reg0[LOADS], reg1[LOADS];
+  auto gload = [&](u32x4_t (&reg)[LOADS], int stage) {
 #pragma unroll
     for (int v = 0; v < LOADS; v++) {
-      half_t* base = dst_off[v] >= 2 * BT * LDT ? Bs[buf] + dst_off[v] - 2 * BT * LDT : As[buf] + dst_off[v];
-      *reinterpret_cast<u32x4_t*>(base) = reg[v];
+      const int so = (int)((((v < 2 ? i0 : j0) + 128 * (v & 1)) * ld + (int64_t)stage * BK) * 2);
+      reg[v] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(v < 2 ? ars : brs, voff, so, 0));
     }
+  };
+  auto lstore = [&](const u32x4_t (&reg)[LOADS], int buf) {
+#pragma unroll
+    for (int v = 0; v < LOADS; v++)
+      *reinterpret_cast<u32x4_t*>((v < 2 ? As[buf] : Bs[buf]) + 128 * (v & 1) * LDT + loff) = reg[v];
   };
 
   f16x acc[2][2];  // acc[jb][ib]: o^T block (j = 64 wj + 32 jb .., i = 64 wi + 32 ib ..)
@@ -180,16 +180,7 @@ __global__ __launch_bounds__(64 * CT_WAVES, 1) void trimul_contract_f16_k(const 
     for (int ib = 0; ib < 2; ib++)
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[jb][ib][e] = 0.0f;
-  const int nst = (int)(ld / BK);
-  gload(0);
-  lstore(0);
-  __syncthreads();
-  // no branches around the loads or stores in the loop body (the last stage reloads itself into the idle buffer),
-  // so the wait counter sees one load order at the loop header
-  for (int st = 0; st < nst; st++) {
-    const int buf = st & 1;
-    gload((int64_t)min(st + 1, nst - 1) * BK);
-    __builtin_amdgcn_sched_barrier(0);  // keep the loads ahead of the MFMAs (the scheduler sinks them otherwise)
+  auto compute = [&](int buf) {
     const half_t* Ab = As[buf] + (64 * wi + r) * LDT + 32 * h;
     const half_t* Bb = Bs[buf] + (64 * wj + r) * LDT + 32 * h;
 #pragma unroll
@@ -205,8 +196,33 @@ __global__ __launch_bounds__(64 * CT_WAVES, 1) void trimul_contract_f16_k(const 
         for (int ib = 0; ib < 2; ib++)
           acc[jb][ib] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[jb], fa[ib], acc[jb][ib], 0, 0, 0);
     }
-    lstore(buf ^ 1);
+  };
+  const int nst = (int)(ld / BK);
+  // Stages pair up (buffer 0, buffer 1) per trip; an odd stage count starts with a zero stage in buffer 0 (adds
+  // nothing), so the trip body has no branch and the wait counter sees one load order. Loads past the last stage
+  // reload it into registers that are never stored.
+  const int s0 = -(nst & 1);
+  gload(reg0, 0);
+#pragma unroll
+  for (int v = 0; v < LOADS; v++) reg0[v] = s0 ? u32x4_t{0u, 0u, 0u, 0u} : reg0[v];
+  lstore(reg0, 0);
+  __syncthreads();
+  // issue order pinned (reg0 before reg1, as in the loop): the wait counter then needs only the older set
+  gload(reg0, s0 + 1);
+  __builtin_amdgcn_sched_barrier(0);
+  gload(reg1, min(s0 + 2, nst - 1));
+  __builtin_amdgcn_sched_barrier(0);
+  for (int st = s0; st < nst; st += 2) {
+    compute(0);       // stage st
+    lstore(reg0, 1);  // stage st + 1
     __syncthreads();
+    gload(reg0, min(st + 3, nst - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    compute(1);       // stage st + 1
+    lstore(reg1, 0);  // stage st + 2
+    __syncthreads();
+    gload(reg1, min(st + 4, nst - 1));
+    __builtin_amdgcn_sched_barrier(0);
   }
   half_t* oc = o + c * N * ld;
 #pragma unroll
@@ -243,6 +259,7 @@ static hipError_t contract_t(const void* ab, void* o, int64_t N, int64_t ld, int
 }
 
 hipError_t launch_trimul_contract(const void* ab, void* o, int dt, int64_t N, int64_t ld, int D, hipStream_t st) {
+  if (dt == DT_F16 && 2 * N * ld >= (1LL << 31)) return hipErrorInvalidValue;  // 32-bit buffer offsets per channel
   return dt == DT_F16 ? contract_t<half_t>(ab, o, N, ld, D, st) : contract_t<float>(ab, o, N, ld, D, st);
 }
 

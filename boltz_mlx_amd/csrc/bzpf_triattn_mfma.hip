@@ -146,6 +146,11 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
   for (int e = 0; e < 16; e++) oacc[e] = 0.f;
   float m_run = -INFINITY, lsum = 0.f;
   const float munset = -0.5f * inf * LOG2E;
+  // mref: the reference the logits are formed against (0 until a key that is not masked has been seen, then the
+  // running maximum); thr: a block whose local maximum (relative to mref) exceeds it raises the maximum. Until the
+  // maximum is set thr = -inf (every block raises it); lanes of the padded queries past N (whose bias rows are never
+  // written) have thr = +inf and never ask for a rescale, so the result of a real query never depends on them.
+  float mref = 0.0f, thr = jq < N ? -INFINITY : INFINITY;
   const float infl = inf * LOG2E;  // key-mask bias inf * (m - 1) * log2(e) = m * infl - infl
   const half2_t one2 = half2_t{(half_t)1.0f, (half_t)1.0f};
 
@@ -173,15 +178,15 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
   }
   half8 bcur[4];  // bias of keys 32 kt + 8 (e / 4) + 4 hl + e % 4: elements 16 kt + e of the lane's 32
   // mask: lane l reads key kb * 64 + l; only the partial last block clamps (to key N - 1)
-  const float* mbase = mrow + (int64_t)l * mask_sk;
-  const float* mlast = mrow + (int64_t)(N - 1) * mask_sk;
+  // (as a buffer resource over keys 0 .. N - 1 of the row: keys past N read as 0 and are set to -inf below)
+  const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
+      (void*)mrow, 0, (int)(uint32_t)((N - 1) * mask_sk * 4 + 4), RSRC_CFG);
+  const int mvo = (int)(l * mask_sk * 4);
   // loads of block kb (kb < nblk; the loop clamps, so it issues them unconditionally)
   auto prefetch = [&](int kb) {
     kreg = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(krs, koff, kb * BK * C * 2, 0));
     vreg = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff, kb * BK * 2, 0));
-    const float* mp = mbase + (int64_t)kb * BK * mask_sk;
-    if (kb * BK + BK > N) mp = kb * BK + l < N ? mp : mlast;
-    mraw = *mp;
+    mraw = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(mrs, mvo, (int)(kb * BK * mask_sk * 4), 0));
   };
   auto prefetch_bias = [&](int kb) {
 #pragma unroll
@@ -216,8 +221,6 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
 
     // the maximum is "unset" until a key that is not masked has been seen (a masked logit is about
     // -inf*log2(e)); subtracting such a maximum would cancel catastrophically
-    const bool unset = m_run <= munset;
-    const float mref = unset ? 0.0f : m_run;
     f16x s[2];
 #pragma unroll
     for (int kt = 0; kt < 2; kt++) {
@@ -255,10 +258,8 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
 #pragma unroll
       for (int e = kt == 0 ? 2 : 0; e < 16; e += 2) mx = fmaxf(fmaxf(mx, s[kt][e]), s[kt][e + 1]);
     const float mloc = halves_max(mx);
-    // s holds logit - mref; raise the maximum only when the block exceeds it by more than 2^THRESH. Lanes of the
-    // padded queries past N (whose bias rows are never written) take no part in the decision, so the result of a
-    // real query never depends on them.
-    if (__any(jq < N && (unset || mloc > THRESH))) {
+    // s holds logit - mref; raise the maximum only when the block exceeds it by more than 2^THRESH
+    if (__any(mloc > thr)) {
       const float mn = fmaxf(m_run, mloc + mref);
       const float corr = __builtin_amdgcn_exp2f(m_run - mn);
       oacc *= corr;
@@ -267,6 +268,9 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
 #pragma unroll
       for (int kt = 0; kt < 2; kt++) s[kt] += delta;
       m_run = mn;
+      const bool unset = m_run <= munset;
+      mref = unset ? 0.0f : m_run;
+      thr = jq < N ? (unset ? -INFINITY : THRESH) : INFINITY;
     }
 #pragma unroll
     for (int kt = 0; kt < 2; kt++)
@@ -305,7 +309,9 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
 hipError_t launch_triattn_core_f16_mfma(const void* qkg, const void* vt, const void* tb, const float* mask,
                                         int64_t mask_si, int64_t mask_sk, float inf, void* out, int64_t N,
                                         int64_t ldk, int H, int C, hipStream_t st) {
-  if (C != 32 || ldk % 64 != 0 || ldk < N || N > 65535) return hipErrorInvalidValue;
+  // 32-bit buffer offsets: the mask row (keys 0 .. N - 1 at stride mask_sk floats) and the K / V^T / bias rows
+  if (C != 32 || ldk % 64 != 0 || ldk < N || N > 32767 || mask_sk < 1 || (N - 1) * mask_sk * 4 + 4 > 0x7fffffffLL)
+    return hipErrorInvalidValue;
   const int64_t units = (int64_t)H * N * ((N + 127) / 128);
   const int64_t per_xcd = (units + NXCD - 1) / NXCD;
   const dim3 grid((unsigned)(per_xcd * NXCD));

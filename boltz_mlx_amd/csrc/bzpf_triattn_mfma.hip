@@ -2,14 +2,17 @@
 //
 // Work unit: one (head h, row i, 128 queries); 4 waves of 32 queries. The 32 x 32 MFMA form is used throughout: a
 // 32-query tile per wave keeps a query's softmax statistics in two lanes (one cross-lane step) and frees registers
-// for a fourth wave per SIMD (125 VGPRs).
+// for a fourth wave per SIMD (127 VGPRs).
 // The logits are formed transposed, S^T = K Q^T + Cinit, one 32-key x 32-query tile per MFMA pair (A = 32 keys of K
 // from LDS, B = the wave's Q fragment, held in registers for the whole row), so lane l owns query l % 32 and 16 keys
 // of each 32-key tile (8 (e / 4) + 4 (l / 32) + e % 4 in accumulator element e): a query's softmax statistics live
 // in lanes l and l ^ 32 and need one cross-lane step per key block. The MFMA accumulator is initialised with
 // tri_bias - m (plus the key-mask bias in blocks that hold a masked key), so the matrix core adds the bias and
-// subtracts the running maximum. The maximum is raised lazily: only when a block's logits exceed it by more than
-// 2^8 (a wave-uniform branch) are the accumulators rescaled. The probabilities P^T, rounded to fp16, are already the
+// subtracts the running maximum. The maximum is raised lazily and without a per-block maximum: each 32-key tile's
+// probabilities are formed against the current maximum, and only when a lane's sum of them exceeds 2^15 (some logit
+// above the maximum by more than 15, including an fp16 overflow; a wave-uniform branch) is the tile's maximum taken,
+// the accumulators rescaled and the tile's probabilities formed again. The probabilities P^T, rounded to fp16 (at
+// most 2^16 before a rescale, same relative precision), are already the
 // B operand of O^T = V^T P^T for the key order the accumulator gives each lane (keys 4h .. 4h + 3, 8 + 4h .. 8 + 4h
 // + 3 of every 16-key slab, h = l / 32); V^T is read from LDS in the same order, so P never leaves registers. The
 // softmax denominator is accumulated from the fp16 probabilities with v_dot2_f32_f16 (exact products by one, fp32
@@ -71,7 +74,7 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
   constexpr int LDK = C + 8;    // Ks row pitch (halves)
   constexpr int LDV = BK + 8;   // Vs row pitch (halves)
   constexpr float LOG2E = 1.4426950408889634f;
-  constexpr float THRESH = 8.0f;  // lazy rescale threshold (base-2 units)
+  constexpr float PLIM = 32768.0f;  // lazy rescale: a lane's tile sum above 2^15 (some logit > mref + 15)
   // K and V^T tiles double-buffered: block kb is written to buffer kb & 1 before the one barrier of iteration kb,
   // and that buffer was last read in iteration kb - 2, which every wave finished before the barrier of kb - 1.
   __shared__ LDS_ALIGN half_t Ks[2][BK * LDK];
@@ -147,10 +150,11 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
   float m_run = -INFINITY, lsum = 0.f;
   const float munset = -0.5f * inf * LOG2E;
   // mref: the reference the logits are formed against (0 until a key that is not masked has been seen, then the
-  // running maximum); thr: a block whose local maximum (relative to mref) exceeds it raises the maximum. Until the
-  // maximum is set thr = -inf (every block raises it); lanes of the padded queries past N (whose bias rows are never
-  // written) have thr = +inf and never ask for a rescale, so the result of a real query never depends on them.
-  float mref = 0.0f, thr = jq < N ? -INFINITY : INFINITY;
+  // running maximum); plim: a tile whose probabilities (relative to mref) sum to more than it in some lane raises
+  // the maximum. Until the maximum is set plim = -inf (every tile raises it); lanes of the padded queries past N
+  // (whose bias rows are never written) have plim = +inf and never ask for a rescale, so the result of a real query
+  // never depends on them.
+  float mref = 0.0f, plim = jq < N ? -INFINITY : INFINITY;
   const float infl = inf * LOG2E;  // key-mask bias inf * (m - 1) * log2(e) = m * infl - infl
   const half2_t one2 = half2_t{(half_t)1.0f, (half_t)1.0f};
 
@@ -252,28 +256,50 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
       s[kt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(kf[1], qf[1], c, 0, 0, 0);
     }
     prefetch_bias(kb + 1 < nblk ? kb + 1 : nblk - 1);  // the bias registers are free once the logits are formed
-    float mx = fmaxf(s[0][0], s[0][1]);  // a serial chain, so each step is one v_max3 over two new values
+    float sref = mref;  // s holds logit - sref (a rescale moves it to the new maximum for the block's later tiles)
 #pragma unroll
-    for (int kt = 0; kt < 2; kt++)
+    for (int kt = 0; kt < 2; kt++) {
+      // P = 2^(logit - mref) in fp16 for the tile's 32 keys, and the lane's sum of them
+      half8 pf[2];
+      float psum = 0.f;
+      const auto probs = [&]() {
+        psum = 0.f;
 #pragma unroll
-      for (int e = kt == 0 ? 2 : 0; e < 16; e += 2) mx = fmaxf(fmaxf(mx, s[kt][e]), s[kt][e + 1]);
-    const float mloc = halves_max(mx);
-    // s holds logit - mref; raise the maximum only when the block exceeds it by more than 2^THRESH
-    if (__any(mloc > thr)) {
-      const float mn = fmaxf(m_run, mloc + mref);
-      const float corr = __builtin_amdgcn_exp2f(m_run - mn);
-      oacc *= corr;
-      lsum *= corr;
-      const float delta = mref - mn;
+        for (int sl = 0; sl < 2; sl++) {
 #pragma unroll
-      for (int kt = 0; kt < 2; kt++) s[kt] += delta;
-      m_run = mn;
-      const bool unset = m_run <= munset;
-      mref = unset ? 0.0f : m_run;
-      thr = jq < N ? (unset ? -INFINITY : THRESH) : INFINITY;
-    }
+          for (int e = 0; e < 8; e++) pf[sl][e] = (half_t)__builtin_amdgcn_exp2f(s[kt][8 * sl + e]);
 #pragma unroll
-    for (int kt = 0; kt < 2; kt++)
+          for (int e = 0; e < 8; e += 2)
+            psum = __builtin_amdgcn_fdot2(half2_t{pf[sl][e], pf[sl][e + 1]}, one2, psum, false);
+        }
+      };
+      probs();
+      // a lane's sum above plim (2^15 once the maximum is set) means some logit exceeds mref by more than 15 (or
+      // an fp16 overflow): raise the maximum to the block's remaining tiles, rescale, and form P again
+      if (__any(psum > plim)) {
+        float mx = fmaxf(s[kt][0], s[kt][1]);
+#pragma unroll
+        for (int e = 2; e < 16; e += 2) mx = fmaxf(fmaxf(mx, s[kt][e]), s[kt][e + 1]);
+        if (kt == 0) {
+#pragma unroll
+          for (int e = 0; e < 16; e += 2) mx = fmaxf(fmaxf(mx, s[1][e]), s[1][e + 1]);
+        }
+        const float mloc = halves_max(mx);
+        const float mn = fmaxf(m_run, mloc + sref);
+        const float corr = __builtin_amdgcn_exp2f(m_run - mn);
+        oacc *= corr;
+        lsum *= corr;
+        const float delta = sref - mn;
+#pragma unroll
+        for (int k2 = kt; k2 < 2; k2++) s[k2] += delta;
+        sref = mn;
+        m_run = mn;
+        const bool unset = m_run <= munset;
+        mref = unset ? 0.0f : m_run;
+        plim = jq < N ? (unset ? -INFINITY : PLIM) : INFINITY;
+        probs();
+      }
+      lsum += psum;
 #pragma unroll
       for (int sl = 0; sl < 2; sl++) {
         // keys 32 kt + 16 sl + {4 hl .. 4 hl + 3, 8 + 4 hl .. 8 + 4 hl + 3}: accumulator elements 8 sl .. 8 sl + 7
@@ -281,13 +307,9 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
         const half4 lo = *reinterpret_cast<const half4*>(vr);
         const half4 hi4 = *reinterpret_cast<const half4*>(vr + 8);
         const half8 vf = half8{lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-        half8 pf;
-#pragma unroll
-        for (int e = 0; e < 8; e++) pf[e] = (half_t)__builtin_amdgcn_exp2f(s[kt][8 * sl + e]);
-#pragma unroll
-        for (int e = 0; e < 8; e += 2) lsum = __builtin_amdgcn_fdot2(half2_t{pf[e], pf[e + 1]}, one2, lsum, false);
-        oacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf, oacc, 0, 0, 0);
+        oacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[sl], oacc, 0, 0, 0);
       }
+    }
   }
   // oacc[4 q + e] = O^T[channel 8 q + 4 hl + e][query qi]; the denominator is split over the lane halves
   const float ltot = halves_sum(lsum);

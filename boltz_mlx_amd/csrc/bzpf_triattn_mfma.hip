@@ -12,7 +12,7 @@
 // probabilities are formed against the current maximum, and only when a lane's sum of them exceeds 2^15 (some logit
 // above the maximum by more than 15, including an fp16 overflow; a wave-uniform branch) is the tile's maximum taken,
 // the accumulators rescaled and the tile's probabilities formed again. The probabilities P^T, rounded to fp16 (at
-// most 2^16 before a rescale, same relative precision), are already the
+// most 2^15 once accepted, with the same relative precision as below 1), are already the
 // B operand of O^T = V^T P^T for the key order the accumulator gives each lane (keys 4h .. 4h + 3, 8 + 4h .. 8 + 4h
 // + 3 of every 16-key slab, h = l / 32); V^T is read from LDS in the same order, so P never leaves registers. The
 // softmax denominator is accumulated from the fp16 probabilities with v_dot2_f32_f16 (exact products by one, fp32

@@ -235,6 +235,40 @@ int bzpf_swiglu(const void* h, void* a, int dt, int64_t rows, int hidden, void* 
   return done(bzpf::launch_swiglu(h, a, dt, rows, hidden, S(stream)), "bzpf_swiglu");
 }
 
+int bzpf_linear_gated(const void* x, const void* w, const float* bias, const float* gate, int64_t ld_gate,
+                      int64_t gate_rows, float* y, int dt, int64_t rows, int K, int M, void* stream) {
+  REQUIRE_PTR(x);
+  REQUIRE_PTR(w);
+  REQUIRE(gate != nullptr && y != nullptr, "bzpf_linear_gated: NULL pointer");
+  REQUIRE(dt_ok(dt), "bzpf_linear_gated: bad dtype");
+  REQUIRE(K >= 8 && K % 8 == 0 && M >= 1, "bzpf_linear_gated: need K %% 8 == 0, M >= 1 (K=%d M=%d)", K, M);
+  REQUIRE(rows >= 0 && gate_rows >= 1 && ld_gate >= M, "bzpf_linear_gated: bad sizes");
+  if (rows == 0) return BZPF_OK;
+  return done(bzpf::launch_linear_gated(x, w, bias, gate, ld_gate, gate_rows, y, dt, rows, K, M, S(stream)),
+              "bzpf_linear_gated");
+}
+
+int bzpf_swiglu3(const void* h, void* a, int dt, int64_t rows, int hidden, void* stream) {
+  REQUIRE(h != nullptr && a != nullptr, "bzpf_swiglu3: NULL pointer");
+  REQUIRE(dt_ok(dt), "bzpf_swiglu3: bad dtype");
+  REQUIRE(rows >= 0 && hidden >= 1, "bzpf_swiglu3: bad sizes");
+  if (rows == 0) return BZPF_OK;
+  return done(bzpf::launch_swiglu3(h, a, dt, rows, hidden, S(stream)), "bzpf_swiglu3");
+}
+
+int bzpf_adaln(const float* a, const float* scale, const float* shift, int64_t ld_cond, int64_t cond_rows, float eps,
+               void* out, int out_dt, int64_t rows, int D, void* stream) {
+  REQUIRE(a != nullptr && scale != nullptr && shift != nullptr && out != nullptr, "bzpf_adaln: NULL pointer");
+  REQUIRE(dt_ok(out_dt), "bzpf_adaln: bad dtype");
+  REQUIRE(D % 64 == 0 && D >= 64 && D <= 1024 && (D / 64 <= 4 || D / 64 == 6 || D / 64 == 8 || D / 64 == 12 ||
+                                                  D / 64 == 16),
+          "bzpf_adaln: unsupported D=%d", D);
+  REQUIRE(rows >= 0 && cond_rows >= 1 && ld_cond >= D, "bzpf_adaln: bad sizes");
+  if (rows == 0) return BZPF_OK;
+  return done(bzpf::launch_adaln(a, scale, shift, ld_cond, cond_rows, eps, out, out_dt, rows, D, S(stream)),
+              "bzpf_adaln");
+}
+
 int bzpf_seq_attention(const void* q, const void* k, const void* v, const void* g, int64_t ld_in, const void* bias,
                        const float* mask, float inf, void* out, int64_t ld_out, int dt, int64_t N, int H, int hd,
                        void* stream) {

@@ -335,6 +335,52 @@ def linear(x, w, bias=None, out=None, out_dtype=None, accumulate: bool = False) 
     return out
 
 
+def linear_gated(x, w, gate: torch.Tensor, out: torch.Tensor, bias=None) -> torch.Tensor:
+    """out (fp32) += sigmoid(gate) * (x w^T + bias) over the rows of x; gate is an fp32 [rows_g, M] view whose
+    rows may have a pitch (a slice of the precomputed conditioning), row r using gate row r % rows_g
+    (transformersv2.py:96-99, 63-66)."""
+    _dev(x, w, out)
+    K = x.shape[-1]
+    M = w.shape[0]
+    rows = x.numel() // K
+    if w.shape[1] != K or w.dtype != x.dtype or out.dtype != torch.float32 or out.numel() != rows * M:
+        raise ValueError("linear_gated: shape/dtype mismatch")
+    if not gate.is_cuda or gate.dtype != torch.float32 or gate.dim() != 2 or gate.shape[1] != M or gate.stride(1) != 1:
+        raise ValueError("linear_gated: gate must be an fp32 [rows, M] view with unit column stride")
+    b = None if bias is None else f32c(bias)
+    call("bzpf_linear_gated", _p(x), _p(w), _p(b), _p(gate), gate.stride(0), gate.shape[0], _p(out), _dt(x), rows,
+         K, M, _stream())
+    return out
+
+
+def adaln(a: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, out_dtype, eps: float = 1e-5) -> torch.Tensor:
+    """sigmoid(scale) * LN(a) + shift (LN without affine) for fp32 a [rows, D]; scale and shift are fp32 [rows_c, D]
+    views of one pitch (slices of the precomputed conditioning), row r using row r % rows_c
+    (transformersv2.py:27-41, 218, 252)."""
+    _dev(a)
+    D = a.shape[-1]
+    rows = a.numel() // D
+    if a.dtype != torch.float32 or scale.shape != shift.shape or scale.dim() != 2 or scale.shape[1] != D:
+        raise ValueError("adaln: shape/dtype mismatch")
+    if (not scale.is_cuda or not shift.is_cuda or scale.stride() != shift.stride() or scale.stride(1) != 1
+            or scale.dtype != torch.float32 or shift.dtype != torch.float32):
+        raise ValueError("adaln: scale and shift must be fp32 views with one row pitch and unit column stride")
+    out = torch.empty(a.shape, dtype=out_dtype, device=a.device)
+    call("bzpf_adaln", _p(a), _p(scale), _p(shift), scale.stride(0), scale.shape[0], float(eps), _p(out), _dt(out),
+         rows, D, _stream())
+    return out
+
+
+def swiglu3(h: torch.Tensor) -> torch.Tensor:
+    """silu(h[:, :H]) * h[:, H:2H] * h[:, 2H:] for h [rows, 3H] (the conditioned transition's gated product)."""
+    _dev(h)
+    H = h.shape[-1] // 3
+    rows = h.numel() // (3 * H)
+    a = torch.empty(h.shape[:-1] + (H,), dtype=h.dtype, device=h.device)
+    call("bzpf_swiglu3", _p(h), _p(a), _dt(h), rows, H, _stream())
+    return a
+
+
 def swiglu(h: torch.Tensor) -> torch.Tensor:
     _dev(h)
     H = h.shape[-1] // 2
@@ -357,15 +403,19 @@ def seq_attention(q, k, v, g, bias, mask, inf: float, H: int) -> torch.Tensor:
     return out
 
 
-def seq_attention_packed(qkvg, bias, mask, inf: float, H: int) -> torch.Tensor:
-    """seq_attention over one [N, 4*H*hd] buffer holding q | k | v | g per row (the fused projection's output)."""
+def seq_attention_packed(qkvg, bias, mask, inf: float, H: int, out=None) -> torch.Tensor:
+    """seq_attention over one [N, 4*H*hd] buffer holding q | k | v | g per row (the fused projection's output);
+    writes `out` [N, H*hd] when given."""
     _dev(qkvg, bias, mask)
     N, HD4 = qkvg.shape
     HD = HD4 // 4
     hd = HD // H
     if bias.shape != (H, N, N) or mask.numel() != N or mask.dtype != torch.float32:
         raise ValueError("seq_attention: bias must be [H, N, N] and mask fp32 [N]")
-    out = torch.empty((N, HD), dtype=qkvg.dtype, device=qkvg.device)
+    if out is None:
+        out = torch.empty((N, HD), dtype=qkvg.dtype, device=qkvg.device)
+    elif out.shape != (N, HD) or out.dtype != qkvg.dtype or not out.is_contiguous():
+        raise ValueError("seq_attention: out must be a contiguous [N, H*hd] tensor of qkvg's dtype")
     base, es = qkvg.data_ptr(), qkvg.element_size()
     call("bzpf_seq_attention", base, base + HD * es, base + 2 * HD * es, base + 3 * HD * es, HD4, _p(bias),
          _p(mask), float(inf), _p(out), HD, _dt(qkvg), N, H, hd, _stream())

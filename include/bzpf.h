@@ -144,6 +144,23 @@ int bzpf_linear(const void* x, const void* w, const float* bias, void* y, int dt
  * (boltz_mlx/layers/transition.py:148-154; kernels.swiglu16, boltz_mlx/kernels.py:1378-1386). */
 int bzpf_swiglu(const void* h, void* a, int dt, int64_t rows, int hidden, void* stream);
 
+/* y[r][m] += sigmoid(gate[(r % gate_rows) * ld_gate + m]) * (x[r] . W[m] + bias[m]) with y fp32 (bias may be
+ * NULL): a gated residual update. Replaces the diffusion transformer's a + sigmoid(output_projection(s)) * proj_o(..)
+ * and a + sigmoid(output_projection(s)) * b_to_a(..) (boltz_mlx/modules/transformersv2.py:63-66, 96-99, 239, 261). */
+int bzpf_linear_gated(const void* x, const void* w, const float* bias, const float* gate, int64_t ld_gate,
+                      int64_t gate_rows, float* y, int dt, int64_t rows, int K, int M, void* stream);
+
+/* a[r][c] = silu(h[r][c]) * h[r][hidden + c] * h[r][2 hidden + c] (rows of h: 3 hidden). Replaces the conditioned
+ * transition's SwiGLU(swish_gate(a)) * a_to_b(a) with the GEMM rows ordered [gates; x; a_to_b]
+ * (boltz_mlx/modules/transformersv2.py:15-18, 55-66, 254-261). */
+int bzpf_swiglu3(const void* h, void* a, int dt, int64_t rows, int hidden, void* stream);
+
+/* AdaLN: out[r][c] = sigmoid(scale[q][c]) * LN(a[r])[c] + shift[q][c] with q = r % cond_rows (conditioning rows of
+ * pitch ld_cond, fp32, pre-sigmoid scale), LN without affine over D channels, a fp32. Replaces AdaLN.__call__ and
+ * the fast path's attn_scale * LN(a) + attn_shift (boltz_mlx/modules/transformersv2.py:27-41, 218, 252). */
+int bzpf_adaln(const float* a, const float* scale, const float* shift, int64_t ld_cond, int64_t cond_rows, float eps,
+               void* out, int out_dt, int64_t rows, int D, void* stream);
+
 /* Sequence attention with pair bias: for head h and query j,
  *   out[j][h*hd + c] = sigmoid(g[j][h*hd + c]) * sum_k softmax_k(q.k/sqrt(hd) + bias[h][j][k]
  *                                                                 + (1 - mask[k]) * (-inf)) v[k][h*hd + c]

@@ -78,6 +78,38 @@ def shapes_layer(token_s: int, token_z: int, heads: int = 16, pw: int = 32, phea
     return out
 
 
+def shapes_adaln(dim: int, dim_cond: int) -> dict:
+    return {"s_norm.weight": (dim_cond,), "s_scale.weight": (dim, dim_cond), "s_scale.bias": (dim,),
+            "s_bias.weight": (dim, dim_cond)}
+
+
+def shapes_diffusion_layer(dim: int, dim_cond: int | None = None, expansion: int = 2) -> dict:
+    """One DiffusionTransformerLayer (transformersv2.py:69-86). The output projection is one Linear registered under
+    two names (output_projection_linear and output_projection.0); only the first is listed here, and
+    with_shared_alias() adds the second with the same values."""
+    dc = dim if dim_cond is None else dim_cond
+    inner = dim * expansion
+    out = _prefixed("adaln", shapes_adaln(dim, dc))
+    out.update(_prefixed("pair_bias_attn", {
+        "proj_q.weight": (dim, dim), "proj_q.bias": (dim,), "proj_k.weight": (dim, dim),
+        "proj_v.weight": (dim, dim), "proj_g.weight": (dim, dim), "proj_o.weight": (dim, dim)}))
+    out.update({"output_projection_linear.weight": (dim, dc), "output_projection_linear.bias": (dim,)})
+    out.update(_prefixed("transition.adaln", shapes_adaln(dim, dc)))
+    out.update({"transition.swish_gate.0.weight": (2 * inner, dim), "transition.a_to_b.weight": (inner, dim),
+                "transition.b_to_a.weight": (dim, inner), "transition.output_projection.0.weight": (dim, dc),
+                "transition.output_projection.0.bias": (dim,)})
+    return out
+
+
+def with_shared_alias(params: dict) -> dict:
+    """Adds `...output_projection.0.*` = `...output_projection_linear.*` (the shared Linear's second name)."""
+    out = dict(params)
+    for k, v in params.items():
+        if "output_projection_linear." in k:
+            out[k.replace("output_projection_linear.", "output_projection.0.")] = v
+    return out
+
+
 def rand_params(shapes: dict, seed: int, std: float = 0.02, ln_random: bool = True,
                 dtype=np.float64) -> dict:
     """Seeded parameters in sorted-name order: matrices and biases ~ N(0, std); LayerNorm weights

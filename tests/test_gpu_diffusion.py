@@ -1,0 +1,144 @@
+"""GPU parity of the diffusion token transformer (boltz_mlx_amd/layers/transformersv2.py) and its kernels against
+the numpy oracle (oracle/diffusion.py): fp32 within 1e-5 of the float32 oracle, f16 within the module gate of the
+float64 oracle (max_rel 2e-2, rel_fro 5e-3)."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from conftest import rand_params, shapes_diffusion_layer, with_shared_alias
+from oracle import diffusion as OD
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _device():
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    from boltz_mlx_amd import _lib
+
+    _lib.load()
+    yield
+
+
+@pytest.fixture
+def precision(request):
+    from boltz_mlx_amd import kernels as K
+
+    old = K.PRECISION
+    K.set_precision(request.param)
+    yield request.param
+    K.set_precision(old)
+
+
+def dev(x, dtype=torch.float32):
+    return torch.tensor(np.asarray(x), dtype=dtype, device="cuda")
+
+
+@pytest.mark.parametrize("D", [384, 768])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
+def test_adaln_kernel(D, out_dtype):
+    """sigmoid(scale) * LN(a) + shift with scale/shift strided views of a wider conditioning buffer whose rows are
+    shared by consecutive groups of rows (row r uses r % rows_c)."""
+    from boltz_mlx_amd import kernels as K
+
+    rng = np.random.default_rng(D)
+    rows, rows_c = 60, 20
+    a = 2 * rng.standard_normal((rows, D)) + 0.5
+    cond = rng.standard_normal((rows_c, 3, 2, D))
+    c = dev(cond)
+    got = K.adaln(dev(a), c[:, 1, 0], c[:, 1, 1], out_dtype).float().cpu().numpy()
+    q = np.arange(rows) % rows_c
+    ref = OD.sigmoid(cond[q, 1, 0]) * O.layer_norm(a) + cond[q, 1, 1]
+    tol = 1e-5 if out_dtype == torch.float32 else 2e-3
+    assert O.metrics(got, ref)["max_rel"] <= tol
+
+
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16])
+def test_linear_gated_and_swiglu3(dt):
+    from boltz_mlx_amd import kernels as K
+
+    rng = np.random.default_rng(3)
+    rows, Kd, M, rows_g = 70, 96, 80, 35
+    x = rng.standard_normal((rows, Kd))
+    w = 0.1 * rng.standard_normal((M, Kd))
+    b = rng.standard_normal(M)
+    gate = rng.standard_normal((rows_g, 2, M))
+    y0 = rng.standard_normal((rows, M))
+    y = dev(y0)
+    g = dev(gate)
+    xg, wg = dev(x, dt), dev(w, dt)
+    K.linear_gated(xg, wg, g[:, 1], y, bias=dev(b))
+    xr, wr = xg.double().cpu().numpy(), wg.double().cpu().numpy()
+    ref = y0 + OD.sigmoid(gate[np.arange(rows) % rows_g, 1]) * (xr @ wr.T + b)
+    assert O.metrics(y.cpu().numpy(), ref)["max_rel"] <= (1e-5 if dt == torch.float32 else 2e-3)
+    h = dev(rng.standard_normal((rows, 3 * 48)), dt)
+    hr = h.double().cpu().numpy()
+    ref3 = OD.silu(hr[:, :48]) * hr[:, 48:96] * hr[:, 96:]
+    got3 = K.swiglu3(h).double().cpu().numpy()
+    assert O.metrics(got3, ref3)["max_rel"] <= (1e-5 if dt == torch.float32 else 3e-3)
+
+
+def _params(D, depth, std, seed):
+    p = {}
+    for i in range(depth):
+        p.update({f"layers.{i}.{k}": v
+                  for k, v in with_shared_alias(rand_params(shapes_diffusion_layer(D), seed=seed + i, std=std)).items()})
+    return p
+
+
+@pytest.mark.parametrize("precision", ["fp32", "f16"], indirect=True)
+@pytest.mark.parametrize("D,H,N,mult,std", [(64, 4, 13, 2, 0.2), (768, 16, 24, 2, 0.04)])
+def test_diffusion_transformer(precision, D, H, N, mult, std):
+    from boltz_mlx_amd.layers.transformersv2 import DiffusionTransformer
+    from boltz_mlx_amd.weights import load_module
+
+    depth, B = 2, 1
+    p = _params(D, depth, std, seed=D)
+    rng = np.random.default_rng(N)
+    a = rng.standard_normal((B * mult, N, D))
+    s = rng.standard_normal((B * mult, N, D))
+    bias = rng.standard_normal((B, N, N, depth * H))
+    mask = np.ones((B * mult, N))
+    mask[:, -3:] = 0
+    mask[1, 2] = 0
+    odt = np.float32 if precision == "fp32" else np.float64
+    ref = OD.diffusion_transformer(a.astype(odt), s.astype(odt), bias.astype(odt), mask.astype(odt),
+                                   {k: v.astype(odt) for k, v in p.items()}, depth, H, mult)
+    m = load_module(DiffusionTransformer(depth=depth, heads=H, dim=D), p).cuda()
+    got = m(dev(a), dev(s), dev(bias), dev(mask), multiplicity=mult).cpu().numpy()
+    # compare the updates (the residual a dominates the output)
+    mt = O.metrics(got - a, ref - a)
+    print(f"diffusion transformer D={D} [{precision}]: {mt}", flush=True)
+    assert mt["finite"]
+    if precision == "fp32":
+        assert mt["max_rel"] <= 1e-5, mt
+    else:
+        assert mt["max_rel"] <= 2e-2 and mt["rel_fro"] <= 5e-3, mt
+
+
+@pytest.mark.parametrize("precision", ["fp32"], indirect=True)
+def test_diffusion_layer_forward_and_shared_conditioning(precision):
+    """A layer called on its own equals layer 0 of the stack, and conditioning s shared by the samples (one row
+    group) gives the same result as s repeated per sample."""
+    from boltz_mlx_amd.layers.transformersv2 import DiffusionTransformer
+    from boltz_mlx_amd.weights import load_module
+
+    D, H, N, mult = 64, 4, 9, 3
+    p = _params(D, 1, 0.2, seed=5)
+    rng = np.random.default_rng(6)
+    a = rng.standard_normal((mult, N, D))
+    s1 = rng.standard_normal((1, N, D))
+    bias = rng.standard_normal((1, N, N, H))
+    mask = np.ones((mult, N))
+    m = load_module(DiffusionTransformer(depth=1, heads=H, dim=D), p).cuda()
+    full = m(dev(a), dev(np.repeat(s1, mult, 0)), dev(bias), dev(mask), multiplicity=mult)
+    shared = m(dev(a), dev(np.repeat(s1, mult, 0)), dev(bias), dev(mask), multiplicity=mult,
+               cond=m.precompute_cond(dev(s1)))
+    one = m.layers[0](dev(a), dev(np.repeat(s1, mult, 0)), dev(bias), dev(mask), multiplicity=mult)
+    torch.cuda.synchronize()
+    assert torch.equal(full, shared)
+    assert torch.equal(full, one)

@@ -109,6 +109,52 @@ def run_blocks(m, s, z, tok, pm, start: int, count: int, xn=None):
     return m.run(s, z, tok, pm, start, count, xn=xn, cycle=True)
 
 
+def c5_flops_per_step(N: int = 400, samples: int = 5, depth: int = 24, D: int = 768) -> float:
+    """Diffusion token transformer, one step: per layer and sample 2 N D (4D + D + 6D) + 2 N 2D D + 4 N^2 D
+    (q|k|v|g, output, [gates; x; a_to_b] and b_to_a GEMMs, q k^T and P v); the conditioning GEMMs are step-invariant."""
+    return float(depth * samples * (2 * N * D * (4 * D + D + 6 * D) + 2 * N * 2 * D * D + 4 * N * N * D))
+
+
+def diffusion_transformer_leg(steps: int, device) -> dict:
+    """The diffusion-transformer stack (24 layers, D 768, 16 heads x 48, N 400, 5 samples sharing one pair bias)
+    timed over `steps` sampler steps, each a full pass of the stack with the output fed back as the next input;
+    the pair bias (LN(z) W, z [400, 400, 128] -> 24 x 16 heads, laid out per layer) and the s conditioning are
+    computed once."""
+    import torch
+
+    from boltz_mlx_amd import kernels as K
+    from boltz_mlx_amd.layers.transformersv2 import DiffusionTransformer
+    from boltz_mlx_amd.weights import load_module, synthetic_state
+
+    N, D, H, L, S = 400, 768, 16, 24, 5
+    m = DiffusionTransformer(depth=L, heads=H, dim=D)
+    load_module(m, synthetic_state(m, seed=5, std=0.02))
+    m = m.to(device)
+    g = torch.Generator(device=device).manual_seed(5)
+    a = torch.randn((S, N, D), generator=g, device=device)
+    s = torch.randn((S, N, D), generator=g, device=device)
+    z = torch.randn((N * N, 128), generator=g, device=device)
+    w_z = (0.02 * torch.randn((L * H, 128), generator=g, device=device)).to(K.storage_dtype())
+    bias = K.linear(K.layer_norm(z, None, None, 1e-5, out_dtype=K.storage_dtype()), w_z).view(1, N, N, L * H)
+    mask = torch.ones((S, N), device=device)
+    mask[:, N - N // 20:] = 0
+    cond = m.precompute_cond(s)
+    prepared = m.prepare(bias)
+    for _ in range(2):
+        a = m(a, s, bias, mask, multiplicity=S, cond=cond, prepared=prepared)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        a = m(a, s, bias, mask, multiplicity=S, cond=cond, prepared=prepared)
+    torch.cuda.synchronize()
+    dt = time.perf_counter() - t0
+    fl = c5_flops_per_step(N, S, L, D)
+    return {"workload": "diffusion_transformer_24L_D768_N400_5samples_fp16", "steps": steps,
+            "steps_per_s": round(steps / dt, 3), "ms_per_step": round(1e3 * dt / steps, 3),
+            "tflops_effective": round(fl * steps / dt / 1e12, 2), "flop_per_step": fl,
+            "finite": bool(torch.isfinite(a).all().item())}
+
+
 def cpu_baseline(N_sample: int = 400, N_target: int = 1000) -> dict:
     import numpy as np
 
@@ -146,6 +192,10 @@ def main() -> int:
     ap.add_argument("--n-small", type=int, default=400)
     ap.add_argument("--blocks", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--c5-steps", type=int, default=20,
+                    help="diffusion-transformer sampler steps timed after the trunk (0: skip)")
+    ap.add_argument("--c5-only", action="store_true",
+                    help="time only the diffusion-transformer leg (for profiling it) and print its JSON line")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="end with one 512 MiB device-to-device copy (the known-size kernel that scales the "
                          "FETCH_SIZE / WRITE_SIZE counters of rocprofv3 --pmc)")
@@ -164,6 +214,10 @@ def main() -> int:
     K.set_precision("f16")
     dev = torch.device("cuda:0")
     torch.backends.cuda.matmul.allow_tf32 = False
+    if args.c5_only:
+        with torch.no_grad():
+            print(json.dumps({"diffusion_transformer": diffusion_transformer_leg(args.c5_steps, dev)}), flush=True)
+        return 0
     result_small = None
     with torch.no_grad():
         # N = 400 blocks/s (secondary figure)
@@ -231,6 +285,9 @@ def main() -> int:
         "kernel_roofline": per_kernel_roof,
         "timed_with_events_s": round(dt_ev, 4),
     }
+    if args.c5_steps:
+        with torch.no_grad():
+            out["diffusion_transformer"] = diffusion_transformer_leg(args.c5_steps, dev)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)

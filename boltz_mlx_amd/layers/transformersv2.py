@@ -180,18 +180,26 @@ class DiffusionTransformer(torch.nn.Module):
             self.__dict__["_bzpf_cond_w"] = hit
         return _precompute_cond(self.layers, s, hit[1])
 
+    def prepare(self, bias):
+        """The step-invariant per-layer pair biases [B, H, N, M] in the storage dtype from bias [B, N, M, L * H]
+        (transformersv2.py:267-282)."""
+        L = len(self.layers)
+        H = self.layers[0].pair_bias_attn.num_heads
+        return [_layer_bias(bias, i, L, H) for i in range(L)]
+
     def forward(self, a, s, bias=None, mask=None, to_keys=None, multiplicity: int = 1, cond=None, fast: bool = True,
                 prepared=None):
         """a [B*mult, N, D], s [B*mult, N, Dc] (or [B', N, Dc] shared by consecutive groups of rows), bias
         [B, N, N, L * H] (shared by `multiplicity` consecutive samples), mask [B*mult, N]. Returns the new a (fp32).
-        `cond` may hold a precomputed (h1, h2) from precompute_cond, as the reference's step loop does."""
+        `cond` may hold a precomputed (h1, h2) from precompute_cond and `prepared` the per-layer biases from
+        prepare(bias), as the reference's step loop does."""
         if to_keys is not None or not self.pair_bias_attn:
             raise NotImplementedError("only the full-attention token transformer with pair bias is built")
         L = len(self.layers)
-        H = self.layers[0].pair_bias_attn.num_heads
         h1, h2 = cond if cond is not None else self.precompute_cond(s)
+        biases = prepared if prepared is not None else self.prepare(bias)
         out = a.to(torch.float32).clone().contiguous()
         m = mask.to(torch.float32).contiguous()
         for i, layer in enumerate(self.layers):
-            _layer_fast(layer, out, h1, h2, i, L, _layer_bias(bias, i, L, H), m, multiplicity)
+            _layer_fast(layer, out, h1, h2, i, L, biases[i], m, multiplicity)
         return out

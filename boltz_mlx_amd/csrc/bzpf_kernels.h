@@ -52,6 +52,9 @@ hipError_t launch_linear_gated(const void* x, const void* w, const float* bias, 
                                int64_t gate_rows, float* y, int dt, int64_t rows, int K, int M, hipStream_t st);
 hipError_t launch_adaln(const float* a, const float* scale, const float* shift, int64_t ldc, int64_t cond_rows,
                         float eps, void* out, int out_dt, int64_t R, int D, hipStream_t st);
+hipError_t launch_seq_attention_f16_mfma(const void* q, const void* k, const void* v, const void* g, int64_t ld_in,
+                                         const void* bias, const float* mask, float inf, void* out, int64_t ld_out,
+                                         int64_t N, int H, int hd, hipStream_t st);
 hipError_t launch_seq_attention(const void* q, const void* k, const void* v, const void* g, int64_t ld_in,
                                 const void* bias, const float* mask, float inf, void* out, int64_t ld_out, int dt,
                                 int64_t N, int H, int hd, hipStream_t st);

@@ -142,3 +142,46 @@ def test_diffusion_layer_forward_and_shared_conditioning(precision):
     torch.cuda.synchronize()
     assert torch.equal(full, shared)
     assert torch.equal(full, one)
+
+
+@pytest.mark.parametrize("hd", [16, 32, 48, 64])
+@pytest.mark.parametrize("N", [64, 132])
+@pytest.mark.parametrize("all_masked", [False, True])
+def test_seq_attention_mfma_vs_valu(hd, N, all_masked):
+    """The fp16 MFMA sequence attention (head widths 16-64, N % 4 == 0, 16-byte rows) against the VALU kernel on the
+    same fp16 values (the VALU kernel is forced by a row pitch that is not a multiple of 8), within the reference's
+    MMA-vs-scalar gate (5e-3), and against the float64 definition. Keys past N - 3 are masked; all_masked masks
+    every key, which leaves the softmax of the unmasked logits (checked against the float64 definition only)."""
+    from boltz_mlx_amd import kernels as K
+
+    H = 3
+    HD = H * hd
+    rng = np.random.default_rng(hd * 1000 + N)
+    qkvg = rng.standard_normal((N, 4 * HD)).astype(np.float16)
+    bias = (2 * rng.standard_normal((H, N, N))).astype(np.float16)
+    mask = np.ones(N, np.float32)
+    mask[-3:] = 0
+    if all_masked:
+        mask[:] = 0
+    a, bg, mg = dev(qkvg, torch.float16), dev(bias, torch.float16), dev(mask)
+    fast = K.seq_attention_packed(a, bg, mg, 1e6, H)
+    wide = torch.zeros((N, 4 * HD + 4), dtype=torch.float16, device="cuda")
+    wide[:, :4 * HD] = a
+    base, es = wide.data_ptr(), wide.element_size()
+    slow = torch.empty((N, HD), dtype=torch.float16, device="cuda")
+    K.call("bzpf_seq_attention", base, base + HD * es, base + 2 * HD * es, base + 3 * HD * es, 4 * HD + 4,
+           bg.data_ptr(), mg.data_ptr(), 1e6, slow.data_ptr(), HD, K.F16, N, H, hd,
+           K._stream())
+    torch.cuda.synchronize()
+    f, sl = fast.float().cpu().numpy(), slow.float().cpu().numpy()
+    if not all_masked:  # all keys masked: the fp32 VALU kernel keeps the rounding of logits near -1e6
+        m = O.metrics(f, sl)
+        assert m["finite"] and m["max_rel"] <= 5e-3, m
+    x = qkvg.astype(np.float64)
+    ref = np.empty((N, HD))
+    for h in range(H):
+        q, k, v, g = (x[:, c * HD + h * hd: c * HD + (h + 1) * hd] for c in range(4))
+        lg = q @ k.T / np.sqrt(hd) + bias[h].astype(np.float64) + (1 - mask.astype(np.float64))[None, :] * -1e6
+        ref[:, h * hd:(h + 1) * hd] = OD.sigmoid(g) * (O.softmax(lg, -1) @ v)
+    m2 = O.metrics(f, ref)
+    assert m2["max_rel"] <= 1e-2, m2

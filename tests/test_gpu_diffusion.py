@@ -82,6 +82,41 @@ def test_linear_gated_and_swiglu3(dt):
     assert O.metrics(got3, ref3)["max_rel"] <= (1e-5 if dt == torch.float32 else 3e-3)
 
 
+@pytest.mark.parametrize("R,Kd,M", [(1, 64, 4), (130, 192, 260), (300, 768, 132), (257, 1536, 388)])
+def test_gemm_f16_tiles(R, Kd, M):
+    """The fp16 128 x 128 GEMM (K % 64 == 0, 16-byte aligned operands; odd and even K-stage counts, row and column
+    tiles cut short) in all four epilogues against float64 on the same fp16 values, and against the fp32-operand
+    kernel on those values."""
+    from boltz_mlx_amd import kernels as K
+
+    rng = np.random.default_rng(R + Kd + M)
+    x = dev(rng.standard_normal((R, Kd)), torch.float16)
+    w = dev(rng.standard_normal((M, Kd)) / np.sqrt(Kd), torch.float16)
+    b = rng.standard_normal(M)
+    gate = rng.standard_normal((7, 2, M))
+    y0 = rng.standard_normal((R, M))
+    xr, wr = x.double().cpu().numpy(), w.double().cpu().numpy()
+    ref = xr @ wr.T + b
+    sig = OD.sigmoid(gate[np.arange(R) % 7, 0])
+    g = dev(gate)
+    outs = []
+    for x_in, w_in in ((x, w), (x.float(), w.float())):
+        y16 = K.linear(x_in, w_in, bias=dev(b), out_dtype=torch.float16)
+        y32 = K.linear(x_in, w_in, bias=dev(b), out_dtype=torch.float32)
+        yacc = dev(y0)
+        K.linear(x_in, w_in, bias=dev(b), out=yacc, accumulate=True)
+        ygat = dev(y0)
+        K.linear_gated(x_in, w_in, g[:, 0], ygat, bias=dev(b))
+        torch.cuda.synchronize()
+        assert O.metrics(y16.double().cpu().numpy(), ref)["max_rel"] <= 2e-3
+        assert O.metrics(y32.cpu().numpy(), ref)["max_rel"] <= 1e-5
+        assert O.metrics(yacc.cpu().numpy(), y0 + ref)["max_rel"] <= 1e-5
+        assert O.metrics(ygat.cpu().numpy(), y0 + sig * ref)["max_rel"] <= 1e-5
+        outs.append((y16, y32, yacc, ygat))
+    for f, s in zip(*outs):
+        assert O.metrics(f.double().cpu().numpy(), s.double().cpu().numpy())["max_rel"] <= 2e-3
+
+
 def _params(D, depth, std, seed):
     p = {}
     for i in range(depth):

@@ -59,10 +59,12 @@ hipError_t launch_linear_gated(const void* x, const void* w, const float* bias, 
 hipError_t launch_adaln(const float* a, const float* scale, const float* shift, int64_t ldc, int64_t cond_rows,
                         float eps, void* out, int out_dt, int64_t R, int D, hipStream_t st);
 hipError_t launch_seq_attention_f16_mfma(const void* q, const void* k, const void* v, const void* g, int64_t ld_in,
-                                         const void* bias, const float* mask, float inf, void* out, int64_t ld_out,
-                                         int64_t N, int H, int hd, hipStream_t st);
+                                         int64_t s_in, const void* bias, int64_t s_bias, int mult, const float* mask,
+                                         int64_t s_mask, float inf, void* out, int64_t ld_out, int64_t s_out,
+                                         int S, int64_t N, int H, int hd, hipStream_t st);
 hipError_t launch_seq_attention(const void* q, const void* k, const void* v, const void* g, int64_t ld_in,
-                                const void* bias, const float* mask, float inf, void* out, int64_t ld_out, int dt,
+                                int64_t s_in, const void* bias, int64_t s_bias, int mult, const float* mask,
+                                int64_t s_mask, float inf, void* out, int64_t ld_out, int64_t s_out, int dt, int S,
                                 int64_t N, int H, int hd, hipStream_t st);
 hipError_t launch_pair_bias(const float* z, const float* lnw, const float* lnb, float eps, const void* w, void* out,
                             int dt, int64_t rows, int H, hipStream_t st);

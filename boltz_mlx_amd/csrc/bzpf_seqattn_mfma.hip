@@ -6,7 +6,8 @@
 //
 // The structure is the triangle-attention core's (bzpf_triattn_mfma.hip), with the layouts of this path:
 // - q, k, v, g are rows of pitch ld_in (the fused q|k|v|g projection), the bias a plain [H][N][N] array and the key
-//   mask one fp32 row [N];
+//   mask one fp32 row [N]; grid.y runs over samples (row sets s_in elements apart, mask rows s_mask, output rows
+//   s_out), consecutive groups of mult samples sharing one bias (s_bias apart), as the diffusion samples do;
 // - a workgroup owns (head h, 128 queries), 4 waves of 32 queries; S^T = K Q^T + Cinit over HD / 16 MFMA steps per
 //   32-key tile (Q pre-scaled by log2(e)/sqrt(HD) in the fragments, so logits are base 2), with the accumulator
 //   initialised to bias * log2(e) - m (one v_fma_mix_f32 per element from the fp16 bias) plus the key-mask bias in
@@ -54,7 +55,9 @@ __global__ __launch_bounds__(256, 2) void seq_attn_mfma(const half_t* __restrict
                                                         const half_t* __restrict__ v, const half_t* __restrict__ g,
                                                         int64_t ld_in, const half_t* __restrict__ bias,
                                                         const float* __restrict__ mask, float inf,
-                                                        half_t* __restrict__ out, int64_t ld_out, int N, int H) {
+                                                        half_t* __restrict__ out, int64_t ld_out, int N, int H,
+                                                        int64_t s_in, int64_t s_bias, int mult, int64_t s_mask,
+                                                        int64_t s_out) {
   static_assert(HD % 16 == 0 && HD >= 16 && HD <= 64, "head width 16, 32, 48 or 64");
   constexpr int BK = 64;                  // keys per LDS stage
   constexpr int WQ = 128;                 // queries per workgroup
@@ -72,6 +75,17 @@ __global__ __launch_bounds__(256, 2) void seq_attn_mfma(const half_t* __restrict
   __shared__ LDS_ALIGN half_t Vs[2][32 * NT * LDV];
   __shared__ LDS_ALIGN float Mb[4][BK];
 
+  // sample blockIdx.y: its own q / k / v / g rows, mask row and output rows; the bias of sample group smp / mult
+  {
+    const int smp = (int)blockIdx.y;
+    q += smp * s_in;
+    k += smp * s_in;
+    v += smp * s_in;
+    g += smp * s_in;
+    bias += (int64_t)(smp / mult) * s_bias;
+    mask += smp * s_mask;
+    out += smp * s_out;
+  }
   const int nqb = (N + WQ - 1) / WQ;
   const int qb = (int)(blockIdx.x % nqb);
   const int h = (int)(blockIdx.x / nqb);
@@ -288,19 +302,20 @@ __global__ __launch_bounds__(256, 2) void seq_attn_mfma(const half_t* __restrict
 }  // namespace
 
 hipError_t launch_seq_attention_f16_mfma(const void* q, const void* k, const void* v, const void* g, int64_t ld_in,
-                                         const void* bias, const float* mask, float inf, void* out, int64_t ld_out,
-                                         int64_t N, int H, int hd, hipStream_t st) {
+                                         int64_t s_in, const void* bias, int64_t s_bias, int mult, const float* mask,
+                                         int64_t s_mask, float inf, void* out, int64_t ld_out, int64_t s_out,
+                                         int S, int64_t N, int H, int hd, hipStream_t st) {
   // 32-bit buffer offsets over a head's K / V rows (block offsets included) and bias plane; 8-byte bias loads need
   // N % 4 == 0, 16-byte row loads ld_in % 8 == 0
   if (N < 1 || N > 32767 || N % 4 || ld_in % 8 || ld_out % 4 || (N + 64) * ld_in * 2 > 0x7fffffffLL ||
-      N * N * 2 > 0x7fffffffLL)
+      N * N * 2 > 0x7fffffffLL || S < 1 || S > 65535 || mult < 1)
     return hipErrorInvalidValue;
-  const dim3 grid((unsigned)(((N + 127) / 128) * H));
+  const dim3 grid((unsigned)(((N + 127) / 128) * H), (unsigned)S);
 #define BZ_SEQ_MFMA(HDV)                                                                                          \
   seq_attn_mfma<HDV><<<grid, 256, 0, st>>>(static_cast<const half_t*>(q), static_cast<const half_t*>(k),         \
                                            static_cast<const half_t*>(v), static_cast<const half_t*>(g), ld_in,  \
                                            static_cast<const half_t*>(bias), mask, inf, static_cast<half_t*>(out), \
-                                           ld_out, (int)N, H)
+                                           ld_out, (int)N, H, s_in, s_bias, mult, s_mask, s_out)
   switch (hd) {
     case 16: BZ_SEQ_MFMA(16); break;
     case 32: BZ_SEQ_MFMA(32); break;

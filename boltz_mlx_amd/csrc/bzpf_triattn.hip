@@ -211,17 +211,33 @@ hipError_t launch_triattn_core_simple(const void* qkg, const void* vt, const voi
 }
 
 // fp16 with head width 16, 32, 48 or 64 (and the alignment its vector loads need) runs on the MFMA kernel
-// (bzpf_seqattn_mfma.hip); other widths (the s track's 24) and fp32 on the VALU kernel above.
+// (bzpf_seqattn_mfma.hip), all S samples in one launch; other widths (the s track's 24) and fp32 on the VALU kernel
+// above, one launch per sample.
 hipError_t launch_seq_attention(const void* q, const void* k, const void* v, const void* g, int64_t ld_in,
-                                const void* bias, const float* mask, float inf, void* out, int64_t ld_out, int dt,
+                                int64_t s_in, const void* bias, int64_t s_bias, int mult, const float* mask,
+                                int64_t s_mask, float inf, void* out, int64_t ld_out, int64_t s_out, int dt, int S,
                                 int64_t N, int H, int hd, hipStream_t st) {
   const auto al = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; };
+  if (S < 1 || mult < 1) return hipErrorInvalidValue;
   if (dt == DT_F16 && (hd == 16 || hd == 32 || hd == 48 || hd == 64) && N % 4 == 0 && ld_in % 8 == 0 &&
-      ld_out % 4 == 0 && al(q, 16) && al(k, 16) && al(v, 16) && al(g, 16) && al(bias, 8) && al(out, 8) &&
-      N <= 32767 && (N + 64) * ld_in * 2 <= 0x7fffffffLL && N * N * 2 <= 0x7fffffffLL)
-    return launch_seq_attention_f16_mfma(q, k, v, g, ld_in, bias, mask, inf, out, ld_out, N, H, hd, st);
-  return dt == DT_F16 ? seq_attn_t<half_t>(q, k, v, g, ld_in, bias, mask, inf, out, ld_out, N, H, hd, st)
-                      : seq_attn_t<float>(q, k, v, g, ld_in, bias, mask, inf, out, ld_out, N, H, hd, st);
+      ld_out % 4 == 0 && s_in % 8 == 0 && s_bias % 4 == 0 && s_out % 4 == 0 && al(q, 16) && al(k, 16) &&
+      al(v, 16) && al(g, 16) && al(bias, 8) && al(out, 8) && N <= 32767 && S <= 65535 &&
+      (N + 64) * ld_in * 2 <= 0x7fffffffLL && N * N * 2 <= 0x7fffffffLL)
+    return launch_seq_attention_f16_mfma(q, k, v, g, ld_in, s_in, bias, s_bias, mult, mask, s_mask, inf, out, ld_out,
+                                         s_out, S, N, H, hd, st);
+  const int64_t es = dt == DT_F16 ? 2 : 4;
+  for (int smp = 0; smp < S; smp++) {
+    const int64_t oi = smp * s_in * es, ob = (int64_t)(smp / mult) * s_bias * es, oo = smp * s_out * es;
+    const auto at = [](const void* p, int64_t off) { return static_cast<const void*>(static_cast<const char*>(p) + off); };
+    const hipError_t e =
+        dt == DT_F16
+            ? seq_attn_t<half_t>(at(q, oi), at(k, oi), at(v, oi), at(g, oi), ld_in, at(bias, ob), mask + smp * s_mask,
+                                 inf, static_cast<char*>(out) + oo, ld_out, N, H, hd, st)
+            : seq_attn_t<float>(at(q, oi), at(k, oi), at(v, oi), at(g, oi), ld_in, at(bias, ob), mask + smp * s_mask,
+                                inf, static_cast<char*>(out) + oo, ld_out, N, H, hd, st);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 // Core dispatch (impl mirrors the reference's scalar / mma choice, boltz_mlx/kernels.py:902-945): 0 = MFMA for

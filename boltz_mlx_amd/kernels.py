@@ -403,22 +403,31 @@ def seq_attention(q, k, v, g, bias, mask, inf: float, H: int) -> torch.Tensor:
     return out
 
 
-def seq_attention_packed(qkvg, bias, mask, inf: float, H: int, out=None) -> torch.Tensor:
-    """seq_attention over one [N, 4*H*hd] buffer holding q | k | v | g per row (the fused projection's output);
-    writes `out` [N, H*hd] when given."""
+def seq_attention_packed(qkvg, bias, mask, inf: float, H: int, out=None, multiplicity: int = 1) -> torch.Tensor:
+    """seq_attention over [N, 4*H*hd] or [S, N, 4*H*hd] buffers holding q | k | v | g per row (the fused
+    projection's output), one launch for all S samples; bias [H, N, N] or [S / multiplicity, H, N, N] (consecutive
+    groups of `multiplicity` samples share one), mask [N] or [S, N] fp32. Writes `out` [(S,) N, H*hd] when given."""
     _dev(qkvg, bias, mask)
-    N, HD4 = qkvg.shape
+    batched = qkvg.dim() == 3
+    q3 = qkvg if batched else qkvg[None]
+    S, N, HD4 = q3.shape
     HD = HD4 // 4
     hd = HD // H
-    if bias.shape != (H, N, N) or mask.numel() != N or mask.dtype != torch.float32:
-        raise ValueError("seq_attention: bias must be [H, N, N] and mask fp32 [N]")
+    b4 = bias if bias.dim() == 4 else bias[None]
+    m2 = mask.reshape(S, N) if mask.numel() == S * N else mask
+    if (b4.shape[1:] != (H, N, N) or b4.shape[0] * multiplicity != S or m2.shape != (S, N)
+            or mask.dtype != torch.float32 or not (q3.is_contiguous() and b4.is_contiguous() and m2.is_contiguous())):
+        raise ValueError("seq_attention: need contiguous qkvg [S, N, 4HD], bias [S / multiplicity, H, N, N] and "
+                         "mask fp32 [S, N]")
+    shape = (S, N, HD) if batched else (N, HD)
     if out is None:
-        out = torch.empty((N, HD), dtype=qkvg.dtype, device=qkvg.device)
-    elif out.shape != (N, HD) or out.dtype != qkvg.dtype or not out.is_contiguous():
-        raise ValueError("seq_attention: out must be a contiguous [N, H*hd] tensor of qkvg's dtype")
-    base, es = qkvg.data_ptr(), qkvg.element_size()
-    call("bzpf_seq_attention", base, base + HD * es, base + 2 * HD * es, base + 3 * HD * es, HD4, _p(bias),
-         _p(mask), float(inf), _p(out), HD, _dt(qkvg), N, H, hd, _stream())
+        out = torch.empty(shape, dtype=qkvg.dtype, device=qkvg.device)
+    elif out.shape != shape or out.dtype != qkvg.dtype or not out.is_contiguous():
+        raise ValueError("seq_attention: out must be a contiguous [(S,) N, H*hd] tensor of qkvg's dtype")
+    base, es = q3.data_ptr(), q3.element_size()
+    call("bzpf_seq_attention_batched", base, base + HD * es, base + 2 * HD * es, base + 3 * HD * es, HD4, N * HD4,
+         _p(b4), H * N * N, int(multiplicity), _p(m2), N, float(inf), _p(out), HD, N * HD, _dt(qkvg), S, N, H, hd,
+         _stream())
     return out
 
 

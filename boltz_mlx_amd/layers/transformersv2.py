@@ -10,7 +10,7 @@ Forward pass (the reference's fast path, transformersv2.py:199-264 and 376-420):
 layer are computed once per call in two GEMMs (the s_norm weight folded into the AdaLN linears); each layer then runs
   b = sigmoid(attn_scale) * LN(a) + attn_shift                         bzpf_adaln
   q|k|v|g = b W_qkvg^T (+ q bias)                                      bzpf_linear
-  o = sigmoid(g) * softmax(q k^T / sqrt(hd) + bias + mask) v            bzpf_seq_attention (per sample)
+  o = sigmoid(g) * softmax(q k^T / sqrt(hd) + bias + mask) v            bzpf_seq_attention_batched
   a += sigmoid(out_gate) * (o W_o^T)                                   bzpf_linear_gated
   t = sigmoid(tr_scale) * LN(a) + tr_shift                             bzpf_adaln
   u = silu(t W_g^T) * (t W_x^T) * (t W_ab^T)                           bzpf_linear + bzpf_swiglu3
@@ -145,11 +145,8 @@ def _layer_fast(layer, a, h1, h2, i: int, L: int, bias_l, mask, multiplicity: in
     c2 = h2.view(-1, L, 2, D)[:, i]
     b = K.adaln(a2, c1[:, 0], c1[:, 1], dt)
     qkvg = K.linear(b, w_qkvg, bias=b_qkvg)
-    o = torch.empty((rows, D), dtype=dt, device=a.device)
-    for smp in range(Bm):
-        r = slice(smp * N, (smp + 1) * N)
-        K.seq_attention_packed(qkvg[r], bias_l[smp // multiplicity], mask[smp], at.inf, H, out=o[r])
-    K.linear_gated(o, w_o, c2[:, 0], a2)
+    o = K.seq_attention_packed(qkvg.view(Bm, N, 4 * D), bias_l, mask, at.inf, H, multiplicity=multiplicity)
+    K.linear_gated(o.view(rows, D), w_o, c2[:, 0], a2)
     t = K.adaln(a2, c1[:, 2], c1[:, 3], dt)
     u = K.swiglu3(K.linear(t, w_ff))
     K.linear_gated(u, w_ba, c2[:, 1], a2)
@@ -203,3 +200,33 @@ class DiffusionTransformer(torch.nn.Module):
         for i, layer in enumerate(self.layers):
             _layer_fast(layer, out, h1, h2, i, L, biases[i], m, multiplicity)
         return out
+
+
+class DiffusionStepGraph:
+    """One pass of a DiffusionTransformer over fixed conditioning (cond from precompute_cond, per-layer biases from
+    prepare, mask, multiplicity) captured in a HIP graph and replayed per sampler step, so the twelve launches of each
+    layer run without host work between them (the reference compiles its step loop instead,
+    boltz_mlx/modules/transformersv2.py:259-297). The graph holds the weights, conditioning and work buffers of the
+    capture: build a new one after any of them changes. __call__(a) copies a [B*mult, N, D] into the graph's input
+    and replays; the result is the graph's output buffer, overwritten by the next call."""
+
+    def __init__(self, module: DiffusionTransformer, a, cond, prepared, mask, multiplicity: int = 1) -> None:
+        self.a_in = a.to(torch.float32).clone().contiguous()
+        self.mask = mask.to(torch.float32).contiguous()
+
+        def run():
+            return module(self.a_in, None, None, self.mask, multiplicity=multiplicity, cond=cond, prepared=prepared)
+
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            run()  # weight caches and the library are set up outside the capture
+        torch.cuda.current_stream().wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.out = run()
+
+    def __call__(self, a: torch.Tensor) -> torch.Tensor:
+        self.a_in.copy_(a)
+        self.graph.replay()
+        return self.out

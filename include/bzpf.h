@@ -170,6 +170,15 @@ int bzpf_seq_attention(const void* q, const void* k, const void* v, const void* 
                        const float* mask, float inf, void* out, int64_t ld_out, int dt, int64_t N, int H, int hd,
                        void* stream);
 
+/* bzpf_seq_attention over n_samples samples in one call: sample i reads q/k/v/g rows from q + i*s_in (elements),
+ * the mask row mask + i*s_mask, the bias bias + (i / mult)*s_bias (mult consecutive samples share one [H, N, N]
+ * bias) and writes out + i*s_out. Replaces the batched attention of the diffusion transformer's AttentionPairBias
+ * over B * multiplicity samples (boltz_mlx/modules/transformersv2.py:218-239, boltz_mlx/layers/attentionv2.py:59-83). */
+int bzpf_seq_attention_batched(const void* q, const void* k, const void* v, const void* g, int64_t ld_in,
+                               int64_t s_in, const void* bias, int64_t s_bias, int mult, const float* mask,
+                               int64_t s_mask, float inf, void* out, int64_t ld_out, int64_t s_out, int dt,
+                               int n_samples, int64_t N, int H, int hd, void* stream);
+
 /* Pair bias out[h][r] = LN(z[r]; ln_w, ln_b, eps) . W[h] for r < rows (z fp32 [rows, D = 128], W [H, D], H <= 16).
  * Replaces proj_z of AttentionPairBias (boltz_mlx/layers/attentionv2.py:37-39, 57-66) and the pair-bias epilogue of
  * kernels_nax3.transition_lnx (boltz_mlx/kernels_nax3.py:713-768). */

@@ -6,10 +6,11 @@
 // Reference behaviour: the nn.Linear / lin16 calls these replace (boltz_mlx/kernels.py:1360-1370;
 // boltz_mlx/modules/transformersv2.py:199-264).
 //
-// A 256-thread workgroup owns a 128 x 128 tile of y, 4 waves of 64 x 64 on v_mfma_f32_32x32x16_f16. The tile is
-// computed transposed (y^T = W x^T: A = rows of W, B = rows of x), so an accumulator lane holds 4 runs of 4
-// consecutive output columns of one row and stores 8- or 16-byte vectors. K stages of 64 are double-buffered in LDS
-// (72 KB, two workgroups per CU) and two register sets carry the next two stages, as in the triangle contraction.
+// A 256-thread workgroup owns a BM x BR tile of y^T (BM, BR = 64 or 128; gemm_tile_choice picks), 4 waves of
+// BM / 2 x BR / 2 on v_mfma_f32_32x32x16_f16. The tile is computed transposed (y^T = W x^T: A = rows of W, B = rows
+// of x), so an accumulator lane holds 4 runs of 4 consecutive output columns of one row and stores 8- or 16-byte
+// vectors. K stages of 64 are double-buffered in LDS (36-72 KB) and two register sets carry the next two stages, as
+// in the triangle contraction.
 // Rows of x past R and rows of W past M read as zeros through the buffer range check; their outputs are not stored.
 #include "bzpf_common.h"
 #include "bzpf_kernels.h"
@@ -18,65 +19,72 @@ namespace bzpf {
 
 namespace {
 
-template <typename TY>
+template <int BM, int BR, typename TY>
 __global__ __launch_bounds__(256, 2) void gemm_nt_f16_k(const half_t* __restrict__ x, const half_t* __restrict__ w,
                                                         const float* __restrict__ bias, TY* __restrict__ y, int64_t R,
                                                         int K, int M, int epi, const float* __restrict__ gate,
                                                         int64_t ld_gate, int64_t gate_rows) {
-  constexpr int BT = 128, BK = 64, LDT = BK + 8, LOADS = 4;  // 16-byte vectors per thread per operand and stage
-  __shared__ LDS_ALIGN half_t As[2][BT * LDT];  // rows of W (m)
-  __shared__ LDS_ALIGN half_t Bs[2][BT * LDT];  // rows of x (r)
-  const int64_t r0 = (int64_t)blockIdx.x * BT;
-  const int m0 = blockIdx.y * BT;
+  static_assert((BM == 64 || BM == 128) && (BR == 64 || BR == 128), "64- or 128-row tiles");
+  constexpr int BK = 64, LDT = BK + 8;
+  constexpr int LA = BM / 32, LB = BR / 32;  // 16-byte vectors per thread per stage: rows of W, rows of x
+  constexpr int MB = BM / 64, RB = BR / 64;  // 32 x 32 MFMA blocks per wave along m and r
+  __shared__ LDS_ALIGN half_t As[2][BM * LDT];  // rows of W (m)
+  __shared__ LDS_ALIGN half_t Bs[2][BR * LDT];  // rows of x (r)
+  const int64_t r0 = (int64_t)blockIdx.x * BR;
+  const int m0 = blockIdx.y * BM;
   const int t = threadIdx.x, wave = t >> 6, l = t & 63, rr = l & 31, hh = l >> 5;
-  const int wm = wave >> 1, wr = wave & 1;  // wave tile: m = 64 wm .., r = 64 wr ..
+  const int wm = wave >> 1, wr = wave & 1;  // wave tile: m = BM / 2 wm .., r = BR / 2 wr ..
 
   constexpr int RSRC_CFG = 0x00020000;
-  const int64_t xrows = R - r0 < BT ? R - r0 : BT;
-  const int wrows = M - m0 < BT ? M - m0 : BT;
+  const int64_t xrows = R - r0 < BR ? R - r0 : BR;
+  const int wrows = M - m0 < BM ? M - m0 : BM;
   const __amdgpu_buffer_rsrc_t xrs =
       __builtin_amdgcn_make_buffer_rsrc((void*)(x + r0 * K), 0, (int)(xrows * K * 2), RSRC_CFG);
   const __amdgpu_buffer_rsrc_t wrs =
       __builtin_amdgcn_make_buffer_rsrc((void*)(w + (int64_t)m0 * K), 0, (int)((int64_t)wrows * K * 2), RSRC_CFG);
-  // staging: vector v of thread t is row 32 v + t / 8 of the tile, k 8 (t % 8) .. + 7 of the stage
+  // staging: vector v of thread t is row 32 v + t / 8 of its operand's tile, k 8 (t % 8) .. + 7 of the stage
   const int lrow = t >> 3, lcol = (t & 7) * 8;
-  u32x4_t ra0[LOADS], rb0[LOADS], ra1[LOADS], rb1[LOADS];
-  auto gload = [&](u32x4_t (&ra)[LOADS], u32x4_t (&rb)[LOADS], int stage) {
+  u32x4_t ra0[LA], rb0[LB], ra1[LA], rb1[LB];
+  auto gload = [&](u32x4_t (&ra)[LA], u32x4_t (&rb)[LB], int stage) {
 #pragma unroll
-    for (int v = 0; v < LOADS; v++) {
+    for (int v = 0; v < LA; v++) {
       const int off = (int)(((int64_t)(32 * v + lrow) * K + stage * BK + lcol) * 2);
       ra[v] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0));
+    }
+#pragma unroll
+    for (int v = 0; v < LB; v++) {
+      const int off = (int)(((int64_t)(32 * v + lrow) * K + stage * BK + lcol) * 2);
       rb[v] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0));
     }
   };
-  auto lstore = [&](const u32x4_t (&ra)[LOADS], const u32x4_t (&rb)[LOADS], int buf) {
+  auto lstore = [&](const u32x4_t (&ra)[LA], const u32x4_t (&rb)[LB], int buf) {
 #pragma unroll
-    for (int v = 0; v < LOADS; v++) {
-      *reinterpret_cast<u32x4_t*>(As[buf] + (32 * v + lrow) * LDT + lcol) = ra[v];
-      *reinterpret_cast<u32x4_t*>(Bs[buf] + (32 * v + lrow) * LDT + lcol) = rb[v];
-    }
+    for (int v = 0; v < LA; v++) *reinterpret_cast<u32x4_t*>(As[buf] + (32 * v + lrow) * LDT + lcol) = ra[v];
+#pragma unroll
+    for (int v = 0; v < LB; v++) *reinterpret_cast<u32x4_t*>(Bs[buf] + (32 * v + lrow) * LDT + lcol) = rb[v];
   };
-  f16x acc[2][2];  // acc[mb][rb]: y^T block (m = 64 wm + 32 mb .., r = 64 wr + 32 rb ..)
+  f16x acc[MB][RB];  // acc[mb][rb]: y^T block (m = BM / 2 wm + 32 mb .., r = BR / 2 wr + 32 rb ..)
 #pragma unroll
-  for (int mb = 0; mb < 2; mb++)
+  for (int mb = 0; mb < MB; mb++)
 #pragma unroll
-    for (int rb = 0; rb < 2; rb++)
+    for (int rb = 0; rb < RB; rb++)
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[mb][rb][e] = 0.0f;
+  // MFMA step s of a stage: lane half hh takes k = 32 hh + 8 s .. + 7 of both operands (a permutation of the k sum)
   auto compute = [&](int buf) {
-    const half_t* Ab = As[buf] + (64 * wm + rr) * LDT + 32 * hh;
-    const half_t* Bb = Bs[buf] + (64 * wr + rr) * LDT + 32 * hh;
+    const half_t* Ab = As[buf] + (BM / 2 * wm + rr) * LDT + 32 * hh;
+    const half_t* Bb = Bs[buf] + (BR / 2 * wr + rr) * LDT + 32 * hh;
 #pragma unroll
     for (int s = 0; s < 4; s++) {
-      half8 fa[2], fb[2];
+      half8 fa[MB], fb[RB];
 #pragma unroll
-      for (int q = 0; q < 2; q++) fa[q] = *reinterpret_cast<const half8*>(Ab + 32 * q * LDT + 8 * s);
+      for (int q = 0; q < MB; q++) fa[q] = *reinterpret_cast<const half8*>(Ab + 32 * q * LDT + 8 * s);
 #pragma unroll
-      for (int q = 0; q < 2; q++) fb[q] = *reinterpret_cast<const half8*>(Bb + 32 * q * LDT + 8 * s);
+      for (int q = 0; q < RB; q++) fb[q] = *reinterpret_cast<const half8*>(Bb + 32 * q * LDT + 8 * s);
 #pragma unroll
-      for (int mb = 0; mb < 2; mb++)
+      for (int mb = 0; mb < MB; mb++)
 #pragma unroll
-        for (int rb = 0; rb < 2; rb++)
+        for (int rb = 0; rb < RB; rb++)
           acc[mb][rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[mb], fb[rb], acc[mb][rb], 0, 0, 0);
     }
   };
@@ -85,10 +93,9 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_f16_k(const half_t* __restrict
   const int s0 = -(nst & 1);
   gload(ra0, rb0, 0);
 #pragma unroll
-  for (int v = 0; v < LOADS; v++) {
-    ra0[v] = s0 ? u32x4_t{0u, 0u, 0u, 0u} : ra0[v];
-    rb0[v] = s0 ? u32x4_t{0u, 0u, 0u, 0u} : rb0[v];
-  }
+  for (int v = 0; v < LA; v++) ra0[v] = s0 ? u32x4_t{0u, 0u, 0u, 0u} : ra0[v];
+#pragma unroll
+  for (int v = 0; v < LB; v++) rb0[v] = s0 ? u32x4_t{0u, 0u, 0u, 0u} : rb0[v];
   lstore(ra0, rb0, 0);
   __syncthreads();
   gload(ra0, rb0, s0 + 1);
@@ -107,17 +114,17 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_f16_k(const half_t* __restrict
     gload(ra1, rb1, min(st + 4, nst - 1));
     __builtin_amdgcn_sched_barrier(0);
   }
-  // epilogue: lane (rr, hh) of block (mb, rb) holds y[r][m .. m + 3] for r = 64 wr + 32 rb + rr and
-  // m = 64 wm + 32 mb + 8 q + 4 hh, q < 4
+  // epilogue: lane (rr, hh) of block (mb, rb) holds y[r][m .. m + 3] for r = BR / 2 wr + 32 rb + rr and
+  // m = BM / 2 wm + 32 mb + 8 q + 4 hh, q < 4
 #pragma unroll
-  for (int rb = 0; rb < 2; rb++) {
-    const int64_t r = r0 + 64 * wr + 32 * rb + rr;
+  for (int rb = 0; rb < RB; rb++) {
+    const int64_t r = r0 + BR / 2 * wr + 32 * rb + rr;
     if (r >= R) continue;
 #pragma unroll
-    for (int mb = 0; mb < 2; mb++)
+    for (int mb = 0; mb < MB; mb++)
 #pragma unroll
       for (int q = 0; q < 4; q++) {
-        const int m = m0 + 64 * wm + 32 * mb + 8 * q + 4 * hh;
+        const int m = m0 + BM / 2 * wm + 32 * mb + 8 * q + 4 * hh;
         if (m >= M) continue;  // M % 4 == 0: a run of 4 is in or out whole
         f4 v4 = f4{acc[mb][rb][4 * q], acc[mb][rb][4 * q + 1], acc[mb][rb][4 * q + 2], acc[mb][rb][4 * q + 3]};
         if (bias != nullptr) v4 += *reinterpret_cast<const f4*>(bias + m);
@@ -137,6 +144,31 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_f16_k(const half_t* __restrict
   }
 }
 
+template <int BM, int BR>
+hipError_t gemm_t(const void* x, const void* w, const float* bias, void* y, int y_dt, int64_t R, int K, int M,
+                  int epi, const float* gate, int64_t ld_gate, int64_t gate_rows, hipStream_t st) {
+  const dim3 grid((unsigned)((R + BR - 1) / BR), (unsigned)((M + BM - 1) / BM));
+  if (y_dt == DT_F16)
+    gemm_nt_f16_k<BM, BR, half_t><<<grid, 256, 0, st>>>(static_cast<const half_t*>(x), static_cast<const half_t*>(w),
+                                                        bias, static_cast<half_t*>(y), R, K, M, epi, gate, ld_gate,
+                                                        gate_rows);
+  else
+    gemm_nt_f16_k<BM, BR, float><<<grid, 256, 0, st>>>(static_cast<const half_t*>(x), static_cast<const half_t*>(w),
+                                                       bias, static_cast<float*>(y), R, K, M, epi, gate, ld_gate,
+                                                       gate_rows);
+  return hipGetLastError();
+}
+
+// Tile choice (W rows x x rows per workgroup): 0 = 128 x 128, 1 = 128 x 64, 2 = 64 x 128, 3 = 64 x 64. The loop
+// is latency-bound at these sizes (each stage's loads have two stages of compute to land), so more, smaller
+// workgroups per CU win up to the 2000 x 768 x 4608 projections (64 x 64: 403-434 TF/s against 373-393 for
+// 128 x 128, and 1.5-2.3x faster on the 768-wide outputs); 128 x 128 wins only on grids of thousands of its tiles
+// (2000 x 768 x 36864: 454 against 378 TF/s).
+int gemm_tile_choice(int64_t R, int M) {
+  const int64_t n128 = ((R + 127) / 128) * ((M + 127) / 128);
+  return n128 >= 2048 ? 0 : 3;
+}
+
 }  // namespace
 
 bool gemm_nt_f16_ok(const void* x, const void* w, const float* bias, const void* y, int64_t R, int K, int M,
@@ -151,14 +183,12 @@ hipError_t launch_gemm_nt_f16(const void* x, const void* w, const float* bias, v
   if (!gemm_nt_f16_ok(x, w, bias, y, R, K, M, gate, ld_gate) || epi < 0 || epi > 2 ||
       (epi >= 1 && y_dt != DT_F32) || (epi == 2 && (gate == nullptr || gate_rows < 1)))
     return hipErrorInvalidValue;
-  const dim3 grid((unsigned)((R + 127) / 128), (unsigned)((M + 127) / 128));
-  if (y_dt == DT_F16)
-    gemm_nt_f16_k<half_t><<<grid, 256, 0, st>>>(static_cast<const half_t*>(x), static_cast<const half_t*>(w), bias,
-                                                static_cast<half_t*>(y), R, K, M, epi, gate, ld_gate, gate_rows);
-  else
-    gemm_nt_f16_k<float><<<grid, 256, 0, st>>>(static_cast<const half_t*>(x), static_cast<const half_t*>(w), bias,
-                                               static_cast<float*>(y), R, K, M, epi, gate, ld_gate, gate_rows);
-  return hipGetLastError();
+  switch (gemm_tile_choice(R, M)) {
+    case 0: return gemm_t<128, 128>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st);
+    case 1: return gemm_t<128, 64>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st);
+    case 2: return gemm_t<64, 128>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st);
+    default: return gemm_t<64, 64>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st);
+  }
 }
 
 }  // namespace bzpf

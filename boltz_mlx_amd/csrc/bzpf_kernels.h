@@ -46,7 +46,7 @@ hipError_t launch_transition_pb(const void* xn, const void* w12, const void* w3,
 
 hipError_t launch_linear(const void* x, const void* w, const float* bias, void* y, int dt, int y_dt, int64_t rows,
                          int K, int M, int epi, hipStream_t st);
-// fp16 128 x 128 MFMA GEMM behind launch_linear / launch_linear_gated when K % 64 == 0, M % 4 == 0 and the operands
+// fp16 tiled MFMA GEMM (64- or 128-row tiles) behind launch_linear / launch_linear_gated when K % 64 == 0, M % 4 == 0 and the operands
 // are 16-byte aligned (gemm_nt_f16_ok)
 bool gemm_nt_f16_ok(const void* x, const void* w, const float* bias, const void* y, int64_t R, int K, int M,
                     const float* gate, int64_t ld_gate);

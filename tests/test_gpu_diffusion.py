@@ -117,6 +117,31 @@ def test_gemm_f16_tiles(R, Kd, M):
         assert O.metrics(f.double().cpu().numpy(), s.double().cpu().numpy())["max_rel"] <= 2e-3
 
 
+def test_gemm_f16_large_grid_tiles():
+    """A grid of 2048+ 128 x 128 tiles takes the 128 x 128 kernel (smaller grids the 64 x 64 one): its rows equal
+    the 64 x 64 kernel's on the same rows bit for bit (same k order per element), and the last row tile, cut short,
+    and a gated update match float64."""
+    from boltz_mlx_amd import kernels as K
+
+    R, Kd, M = 4000, 192, 8192
+    rng = np.random.default_rng(21)
+    x = dev(rng.standard_normal((R, Kd)), torch.float16)
+    w = dev(rng.standard_normal((M, Kd)) / np.sqrt(Kd), torch.float16)
+    b = dev(rng.standard_normal(M))
+    big = K.linear(x, w, bias=b, out_dtype=torch.float32)
+    small = K.linear(x[:100].contiguous(), w, bias=b, out_dtype=torch.float32)
+    gate = dev(rng.standard_normal((3, M)))
+    y = torch.ones((R, M), device="cuda")
+    K.linear_gated(x, w, gate, y, bias=b)
+    torch.cuda.synchronize()
+    assert torch.equal(big[:100], small)
+    xr, wr = x[-72:].double().cpu().numpy(), w.double().cpu().numpy()
+    ref = xr @ wr.T + b.double().cpu().numpy()
+    assert O.metrics(big[-72:].cpu().numpy(), ref)["max_rel"] <= 1e-5
+    g = OD.sigmoid(gate.double().cpu().numpy()[np.arange(R - 72, R) % 3])
+    assert O.metrics(y[-72:].cpu().numpy(), 1 + g * ref)["max_rel"] <= 1e-5
+
+
 def _params(D, depth, std, seed):
     p = {}
     for i in range(depth):

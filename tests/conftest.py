@@ -101,6 +101,39 @@ def shapes_diffusion_layer(dim: int, dim_cond: int | None = None, expansion: int
     return out
 
 
+def shapes_opm(c_in: int = 64, c_hidden: int = 32, c_out: int = 128) -> dict:
+    """OuterProductMean (outer_product_mean.py:15-21)."""
+    return {"norm.weight": (c_in,), "norm.bias": (c_in,), "proj_a.weight": (c_hidden, c_in),
+            "proj_b.weight": (c_hidden, c_in), "proj_o.weight": (c_out, c_hidden * c_hidden), "proj_o.bias": (c_out,)}
+
+
+def shapes_pwa(c_m: int = 64, c_z: int = 128, c_h: int = 32, heads: int = 8) -> dict:
+    """PairWeightedAveraging (pair_averaging.py:13-28)."""
+    return {"norm_m.weight": (c_m,), "norm_m.bias": (c_m,), "norm_z.weight": (c_z,), "norm_z.bias": (c_z,),
+            "proj_m.weight": (c_h * heads, c_m), "proj_g.weight": (c_h * heads, c_m), "proj_z.weight": (heads, c_z),
+            "proj_o.weight": (c_m, c_h * heads)}
+
+
+def shapes_noseq_layer(token_z: int, pw: int = 32, pheads: int = 4) -> dict:
+    out = {}
+    out.update(_prefixed("tri_mul_out", shapes_tri_mul(token_z)))
+    out.update(_prefixed("tri_mul_in", shapes_tri_mul(token_z)))
+    out.update(_prefixed("tri_att_start", shapes_tri_att(token_z, pw, pheads)))
+    out.update(_prefixed("tri_att_end", shapes_tri_att(token_z, pw, pheads)))
+    out.update(_prefixed("transition_z", shapes_transition(token_z, 4 * token_z)))
+    return out
+
+
+def shapes_msa_layer(msa_s: int = 64, token_z: int = 128) -> dict:
+    """MSALayer (trunkv2.py:205-227)."""
+    out = {}
+    out.update(_prefixed("msa_transition", shapes_transition(msa_s, 4 * msa_s)))
+    out.update(_prefixed("pair_weighted_averaging", shapes_pwa(msa_s, token_z)))
+    out.update(_prefixed("pairformer_layer", shapes_noseq_layer(token_z)))
+    out.update(_prefixed("outer_product_mean", shapes_opm(msa_s, 32, token_z)))
+    return out
+
+
 def with_shared_alias(params: dict) -> dict:
     """Adds `...output_projection.0.*` = `...output_projection_linear.*` (the shared Linear's second name)."""
     out = dict(params)

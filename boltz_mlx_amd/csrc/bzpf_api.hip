@@ -292,6 +292,37 @@ int bzpf_seq_attention(const void* q, const void* k, const void* v, const void* 
                                     stream);
 }
 
+int bzpf_opm_outer(const float* ab, int64_t ld_ab, const float* mask, void* out, int out_dt, int n_seq, int N,
+                   int i_base, int n_i, void* stream) {
+  REQUIRE(ab && mask && out, "bzpf_opm_outer: NULL pointer");
+  REQUIRE(dt_ok(out_dt), "bzpf_opm_outer: bad dtype");
+  REQUIRE(reinterpret_cast<uintptr_t>(ab) % 16 == 0 && ld_ab >= 64 && ld_ab % 4 == 0,
+          "bzpf_opm_outer: ab must be 16-byte aligned with a row pitch >= 64 and a multiple of 4 (ld_ab=%lld)",
+          (long long)ld_ab);
+  REQUIRE(n_seq >= 1 && N >= 1 && i_base >= 0 && n_i >= 1 && i_base + n_i <= N,
+          "bzpf_opm_outer: bad sizes (n_seq=%d N=%d i_base=%d n_i=%d)", n_seq, N, i_base, n_i);
+  return done(bzpf::launch_opm_outer(ab, ld_ab, mask, out, out_dt, n_seq, N, i_base, n_i, S(stream)), "bzpf_opm_outer");
+}
+
+int bzpf_pwa_softmax(const float* logits, const float* pair_mask, float inf, float* w, int N, int64_t ldw, int H,
+                     void* stream) {
+  REQUIRE(logits && pair_mask && w, "bzpf_pwa_softmax: NULL pointer");
+  REQUIRE(N >= 1 && H >= 1 && ldw >= N && ldw % 16 == 0, "bzpf_pwa_softmax: bad sizes (N=%d H=%d ldw=%lld)", N, H,
+          (long long)ldw);
+  return done(bzpf::launch_pwa_softmax(logits, pair_mask, inf, w, N, ldw, H, S(stream)), "bzpf_pwa_softmax");
+}
+
+int bzpf_pwa_avg(const float* w, int64_t ldw, const float* v, int64_t ldv, const float* g, int64_t ldg, float* out,
+                 int64_t ldo, int n_seq, int N, int H, void* stream) {
+  REQUIRE(w && v && g && out, "bzpf_pwa_avg: NULL pointer");
+  REQUIRE(reinterpret_cast<uintptr_t>(w) % 16 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0 && ldv % 4 == 0,
+          "bzpf_pwa_avg: w and v must be 16-byte aligned and ldv a multiple of 4");
+  REQUIRE(n_seq >= 1 && n_seq <= 4 * 65535 && N >= 1 && H >= 1 && H <= 65535 && ldw >= N && ldw % 16 == 0 &&
+              ldv >= 32 * H && ldg >= 32 * H && ldo >= 32 * H,
+          "bzpf_pwa_avg: bad sizes (n_seq=%d N=%d H=%d)", n_seq, N, H);
+  return done(bzpf::launch_pwa_avg(w, ldw, v, ldv, g, ldg, out, ldo, n_seq, N, H, S(stream)), "bzpf_pwa_avg");
+}
+
 int bzpf_pair_bias(const float* z, const float* ln_w, const float* ln_b, float eps, const void* w, void* out, int dt,
                    int64_t rows, int D, int H, void* stream) {
   REQUIRE_PTR(z);

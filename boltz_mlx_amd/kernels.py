@@ -431,6 +431,52 @@ def seq_attention_packed(qkvg, bias, mask, inf: float, H: int, out=None, multipl
     return out
 
 
+def opm_outer(ab: torch.Tensor, mask: torch.Tensor, i_base: int = 0, n_i: int | None = None,
+              out_dtype=torch.float16) -> torch.Tensor:
+    """OuterProductMean's outer sum for one MSA: ab fp32 [S, N, 64] (LN(m) [W_a; W_b]^T, unmasked), mask fp32
+    [S, N] -> [n_i * N, 1024] with row (i - i_base) * N + j and column c * 32 + d holding
+    sum_s mask_si mask_sj a[s, i, c] b[s, j, d] / max(sum_s mask_si mask_sj, 1) (outer_product_mean.py:37-45)."""
+    _dev(ab, mask)
+    S, N, C2 = ab.shape
+    n_i = N - i_base if n_i is None else n_i
+    if ab.dtype != torch.float32 or C2 < 64 or not ab.is_contiguous() or mask.shape != (S, N) \
+            or mask.dtype != torch.float32 or not mask.is_contiguous():
+        raise ValueError("opm_outer: need contiguous fp32 ab [S, N, 64] and mask [S, N]")
+    out = torch.empty((n_i * N, 1024), dtype=out_dtype, device=ab.device)
+    call("bzpf_opm_outer", _p(ab), C2, _p(mask), _p(out), _dt(out), S, N, int(i_base), int(n_i), _stream())
+    return out
+
+
+def pwa_softmax(logits: torch.Tensor, pair_mask: torch.Tensor, inf: float) -> torch.Tensor:
+    """softmax_j(logits[h, i, j] + (1 - pair_mask[i, j]) * -inf) for fp32 logits [H, N, N] as [H, N, ldw] with
+    ldw = N rounded up to 16 and zeros past N (pair_averaging.py:43-49)."""
+    _dev(logits, pair_mask)
+    H, N, _ = logits.shape
+    if logits.dtype != torch.float32 or not logits.is_contiguous() or pair_mask.shape != (N, N) \
+            or pair_mask.dtype != torch.float32 or not pair_mask.is_contiguous():
+        raise ValueError("pwa_softmax: need contiguous fp32 logits [H, N, N] and pair_mask [N, N]")
+    ldw = (N + 15) // 16 * 16
+    w = torch.empty((H, N, ldw), dtype=torch.float32, device=logits.device)
+    call("bzpf_pwa_softmax", _p(logits), _p(pair_mask), float(inf), _p(w), N, ldw, H, _stream())
+    return w
+
+
+def pwa_avg(w: torch.Tensor, v: torch.Tensor, g: torch.Tensor, S: int, N: int) -> torch.Tensor:
+    """sigmoid(g) * (sum_j w[h, i, j] v[s, j, h*32 + d]) for w [H, N, ldw] from pwa_softmax and fp32 v, g
+    [S * N, >= 32 H] row views with unit column stride (pair_averaging.py:50-57) -> [S * N, 32 H] fp32."""
+    _dev(w)
+    H, Nw, ldw = w.shape
+    HC = 32 * H
+    for t in (v, g):
+        if not t.is_cuda or t.dtype != torch.float32 or t.dim() != 2 or t.shape[0] != S * N or t.shape[1] < HC or t.stride(1) != 1:
+            raise ValueError("pwa_avg: v and g must be fp32 [S * N, >= 32 H] views with unit column stride")
+    if Nw != N or not w.is_contiguous():
+        raise ValueError("pwa_avg: w must be the contiguous [H, N, ldw] output of pwa_softmax")
+    out = torch.empty((S * N, HC), dtype=torch.float32, device=v.device)
+    call("bzpf_pwa_avg", _p(w), ldw, _p(v), v.stride(0), _p(g), g.stride(0), _p(out), HC, S, N, H, _stream())
+    return out
+
+
 def pair_bias(z: torch.Tensor, ln, w: torch.Tensor) -> torch.Tensor:
     """Linear(LN(z)) for z fp32 [N, N, D] as [H, N, N] in w's dtype."""
     _dev(z, w)

@@ -1,0 +1,55 @@
+"""OuterProductMean on the bzpf kernels: same constructor, parameter names and call signature as
+boltz_mlx/layers/outer_product_mean.py:12-50 (inference).
+
+  ab = LN(m) [W_a; W_b]^T                                  bzpf_layernorm + bzpf_linear (fp32)
+  z16 = (sum_s mask_si mask_sj a_si (x) b_sj) / max(count, 1)  bzpf_opm_outer (fp32 MFMA; fp16 out in f16 mode)
+  out (+)= z16 W_o^T + bias                                bzpf_linear (fp16 GEMM in f16 mode, fp32 accumulate)
+The outer sum runs over all MSA rows in one kernel per block of token rows i (at most OPM_PAIRS_PER_CHUNK pairs),
+as the reference's fused f16 path does (outer_product_mean.py:52-84); the reference's re-associated form for very
+few MSA rows (outer_product_mean.py:86-114) computes the same linear map and is not separate here.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from boltz_mlx_amd import kernels as K
+from boltz_mlx_amd.layers.norm import LayerNorm
+
+OPM_PAIRS_PER_CHUNK = 1 << 20  # (i, j) pairs per outer-sum launch: 2 GiB of fp16 z rows of 1024
+
+
+class OuterProductMean(torch.nn.Module):
+    def __init__(self, c_in: int, c_hidden: int, c_out: int) -> None:
+        super().__init__()
+        if c_hidden != 32:
+            raise NotImplementedError("the outer-sum kernel is built for c_hidden = 32 (the model's value)")
+        self.c_hidden = c_hidden
+        self.norm = LayerNorm(c_in)
+        self.proj_a = torch.nn.Linear(c_in, c_hidden, bias=False)
+        self.proj_b = torch.nn.Linear(c_in, c_hidden, bias=False)
+        self.proj_o = torch.nn.Linear(c_hidden * c_hidden, c_out)
+
+    def forward(self, m: torch.Tensor, mask: torch.Tensor, chunk_size=None) -> torch.Tensor:
+        """m [B, S, N, c_in], mask [B, S, N] -> [B, N, N, c_out] fp32. chunk_size is accepted and ignored."""
+        B, S, N, _ = m.shape
+        out = torch.empty((B, N, N, self.proj_o.out_features), dtype=torch.float32, device=m.device)
+        for b in range(B):
+            self.accumulate(out[b], m[b], mask[b], accumulate=False)
+        return out
+
+    def accumulate(self, z: torch.Tensor, m: torch.Tensor, mask: torch.Tensor, accumulate: bool = True) -> None:
+        """z [N, N, c_out] fp32 contiguous (+)= the layer's output for one MSA m [S, N, c_in], mask [S, N]."""
+        S, N, c_in = m.shape
+        co = self.proj_o.out_features
+        w_ab = K.wcache(self, "w_ab", self.proj_a.weight, self.proj_b.weight, dtype=torch.float32)
+        w_o = K.wcache(self, "w_o", self.proj_o.weight)
+        mn = K.layer_norm(m.reshape(S * N, c_in).to(torch.float32), self.norm.weight, self.norm.bias, self.norm.eps)
+        ab = K.linear(mn, w_ab).view(S, N, 2 * self.c_hidden)
+        mk = mask.to(torch.float32).reshape(S, N).contiguous()
+        z2 = z.view(N * N, co)
+        step = max(1, min(N, OPM_PAIRS_PER_CHUNK // N))
+        for i0 in range(0, N, step):
+            n = min(step, N - i0)
+            zz = K.opm_outer(ab, mk, i0, n, out_dtype=w_o.dtype)
+            K.linear(zz, w_o, bias=self.proj_o.bias, out=z2[i0 * N:(i0 + n) * N], accumulate=accumulate)

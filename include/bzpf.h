@@ -179,6 +179,29 @@ int bzpf_seq_attention_batched(const void* q, const void* k, const void* v, cons
                                int64_t s_mask, float inf, void* out, int64_t ld_out, int64_t s_out, int dt,
                                int n_samples, int64_t N, int H, int hd, void* stream);
 
+/* Outer-product-mean outer sum for MSA rows s < n_seq over tokens (fp32 ab [n_seq, N, ld_ab]: a = ab[.., 0:32],
+ * b = ab[.., 32:64], unmasked; mask fp32 [n_seq, N]): for i_base <= i < i_base + n_i and j < N,
+ *   out[(i - i_base) * N + j][c * 32 + d] = sum_s mask[s][i] mask[s][j] a[s][i][c] b[s][j][d] / max(count_ij, 1),
+ * count_ij = sum_s mask[s][i] mask[s][j]; out fp16 or fp32 [n_i * N, 1024] (fp32 MFMA accumulation). Replaces
+ * kernels_msa.opm_outer and the module path's outer sum (boltz_mlx/kernels_msa.py:292-343,
+ * boltz_mlx/layers/outer_product_mean.py:37-45). */
+int bzpf_opm_outer(const float* ab, int64_t ld_ab, const float* mask, void* out, int out_dt, int n_seq, int N,
+                   int i_base, int n_i, void* stream);
+
+/* Pair-weighted-averaging weights: w[h][i][j] = softmax_j(logits[h][i][j] + (1 - pair_mask[i][j]) * -inf) for
+ * logits fp32 [H, N, N], pair_mask fp32 [N, N]; w fp32 [H, N, ldw] with zeros for N <= j < ldw (ldw a multiple of
+ * 16 and >= N). Replaces the softmax of kernels_msa.pwa_weights (boltz_mlx/kernels_msa.py:461-500,
+ * boltz_mlx/layers/pair_averaging.py:43-49); the logits are bzpf_pair_bias of z with the fp32 proj_z weight. */
+int bzpf_pwa_softmax(const float* logits, const float* pair_mask, float inf, float* w, int N, int64_t ldw, int H,
+                     void* stream);
+
+/* Pair-weighted average with its gate: out[s][i][h*32 + d] = sigmoid(g[s][i][h*32 + d]) *
+ * sum_j w[h][i][j] v[s][j][h*32 + d] for w from bzpf_pwa_softmax and v, g, out fp32 rows (s, i) of pitch
+ * ldv / ldg / ldo (fp32 MFMA accumulation). Replaces kernels_msa.pwa_avg (boltz_mlx/kernels_msa.py:620-653,
+ * boltz_mlx/layers/pair_averaging.py:50-57). */
+int bzpf_pwa_avg(const float* w, int64_t ldw, const float* v, int64_t ldv, const float* g, int64_t ldg, float* out,
+                 int64_t ldo, int n_seq, int N, int H, void* stream);
+
 /* Pair bias out[h][r] = LN(z[r]; ln_w, ln_b, eps) . W[h] for r < rows (z fp32 [rows, D = 128], W [H, D], H <= 16).
  * Replaces proj_z of AttentionPairBias (boltz_mlx/layers/attentionv2.py:37-39, 57-66) and the pair-bias epilogue of
  * kernels_nax3.transition_lnx (boltz_mlx/kernels_nax3.py:713-768). */

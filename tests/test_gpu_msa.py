@@ -1,0 +1,195 @@
+"""GPU parity of the MSA-block kernels and modules (boltz_mlx_amd/layers/outer_product_mean.py, pair_averaging.py,
+msa.py) against the numpy oracle (oracle/msa.py). Gates follow the reference's own MSA kernel tests
+(tests/test_msa_kernels.py): the fp32 reductions within 1e-5 (relative Frobenius) / 1e-4 (max) of float64 on the
+same fp32 operands, the fp16-stored outer sum within one fp16 rounding (2^-10 of the largest value), modules in fp32
+within 1e-5 relative Frobenius and in f16 mode within 3e-3."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+import oracle as O
+from conftest import pair_inputs, rand_params, shapes_msa_layer, shapes_opm, shapes_pwa
+from oracle import msa as OM
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module", autouse=True)
+def _device():
+    assert torch.cuda.is_available(), "GPU tests need a ROCm device"
+    from boltz_mlx_amd import _lib
+
+    _lib.load()
+    yield
+
+
+@pytest.fixture
+def precision(request):
+    from boltz_mlx_amd import kernels as K
+
+    old = K.PRECISION
+    K.set_precision(request.param)
+    yield request.param
+    K.set_precision(old)
+
+
+def dev(x, dtype=torch.float32):
+    return torch.tensor(np.asarray(x), dtype=dtype, device="cuda")
+
+
+def _opm_inputs(S, N, seed):
+    rng = np.random.default_rng(seed)
+    ab = rng.standard_normal((S, N, 64)).astype(np.float32)
+    mask = (rng.random((S, N)) > 0.2).astype(np.float32)
+    mask[0] = 1
+    return ab, mask
+
+
+@pytest.mark.parametrize("S,N,i_base,n_i", [(249, 37, 0, 37), (40, 13, 3, 7), (33, 5, 0, 5), (64, 70, 64, 6),
+                                            (17, 130, 5, 120)])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.float16])
+def test_opm_outer(S, N, i_base, n_i, out_dtype):
+    from boltz_mlx_amd import kernels as K
+
+    ab, mask = _opm_inputs(S, N, S + N)
+    got = K.opm_outer(dev(ab), dev(mask), i_base, n_i, out_dtype=out_dtype).double().cpu().numpy()
+    ref = OM.opm_outer(ab.astype(np.float64), mask.astype(np.float64))[i_base:i_base + n_i].reshape(n_i * N, 1024)
+    m = O.metrics(got, ref)
+    assert m["finite"]
+    if out_dtype == torch.float32:
+        assert m["rel_fro"] < 1e-5 and m["max_rel"] < 1e-5, m
+    else:
+        assert np.abs(got - ref).max() <= np.abs(ref).max() * 2.0 ** -10, m
+
+
+def test_opm_outer_zero_count_pair():
+    """Two tokens that never share an unmasked MSA row: their pair's count is 0, clamped to 1, and z is 0."""
+    from boltz_mlx_amd import kernels as K
+
+    ab, mask = _opm_inputs(20, 9, 3)
+    mask[:, 2] = np.arange(20) % 2
+    mask[:, 6] = 1 - np.arange(20) % 2
+    got = K.opm_outer(dev(ab), dev(mask), out_dtype=torch.float32).cpu().numpy().reshape(9, 9, 1024)
+    ref = OM.opm_outer(ab.astype(np.float64), mask.astype(np.float64))
+    assert np.all(got[2, 6] == 0) and np.all(got[6, 2] == 0)
+    assert O.metrics(got, ref)["max_rel"] < 1e-5
+
+
+@pytest.mark.parametrize("N", [5, 37, 130])
+@pytest.mark.parametrize("wdt", [torch.float16, torch.float32])
+def test_pwa_weights(N, wdt):
+    from boltz_mlx_amd import kernels as K
+
+    rng = np.random.default_rng(N)
+    z = (rng.standard_normal((N, N, 128)) * 3 + 1).astype(np.float32)
+    pm = (rng.random((N, N)) > 0.2).astype(np.float32)
+    pm[:, 0] = 1
+    pm[1] = 0  # a row with every key masked
+    p = rand_params(shapes_pwa(), seed=N, std=128 ** -0.5)
+    wz = torch.tensor(p["proj_z.weight"], dtype=wdt).float()
+
+    class LN:
+        weight, bias, eps = dev(p["norm_z.weight"]), dev(p["norm_z.bias"]), 1e-5
+
+    logits = K.pair_bias(dev(z), LN, wz.cuda())
+    w = K.pwa_softmax(logits, dev(pm), 1e6).cpu().numpy()
+    ref = OM.pwa_weights(z.astype(np.float64), pm.astype(np.float64),
+                         {**p, "proj_z.weight": wz.double().numpy()})
+    assert w.shape == (8, N, (N + 15) // 16 * 16) and np.all(w[:, :, N:] == 0)
+    assert np.isfinite(w).all() and np.abs(w.sum(-1) - 1).max() < 1e-5
+    # row 1 masks every key: its fp32 logits - 1e6 round to multiples of 1/16 (as the reference's fp32 logits do),
+    # which the float64 definition does not; the other rows are compared exactly
+    keep = np.arange(N) != 1
+    m = O.metrics(w[:, keep, :N], ref[:, keep])
+    assert m["rel_fro"] < 1e-5 and m["max_rel"] < 1e-5, m
+
+
+@pytest.mark.parametrize("S,N", [(249, 37), (1, 130), (7, 64), (6, 200)])
+def test_pwa_avg(S, N):
+    from boltz_mlx_amd import kernels as K
+
+    rng = np.random.default_rng(S * N)
+    H = 8
+    ldw = (N + 15) // 16 * 16
+    w = np.zeros((H, N, ldw), np.float32)
+    x = rng.random((H, N, N)).astype(np.float32)
+    w[:, :, :N] = x / x.sum(-1, keepdims=True)
+    vg = rng.standard_normal((S * N, 2 * H * 32)).astype(np.float32)
+    vgd = dev(vg)
+    got = K.pwa_avg(dev(w), vgd[:, :256], vgd[:, 256:], S, N).cpu().numpy()
+    ref = OM.pwa_avg(w[:, :, :N].astype(np.float64), vg[:, :256].reshape(S, N, 256).astype(np.float64),
+                     vg[:, 256:].reshape(S, N, 256).astype(np.float64)).reshape(S * N, 256)
+    m = O.metrics(got, ref)
+    assert m["rel_fro"] < 1e-5 and m["max_rel"] < 1e-4, m
+
+
+@pytest.mark.parametrize("precision", ["fp32", "f16"], indirect=True)
+@pytest.mark.parametrize("S,N", [(249, 37), (64, 130)])
+def test_opm_module(precision, S, N):
+    from boltz_mlx_amd.layers.outer_product_mean import OuterProductMean
+    from boltz_mlx_amd.weights import load_module
+
+    p = rand_params(shapes_opm(), seed=S + N, std=0.1)
+    rng = np.random.default_rng(S)
+    m = rng.standard_normal((1, S, N, 64))
+    mask = (rng.random((1, S, N)) > 0.2).astype(np.float64)
+    mask[:, 0] = 1
+    mod = load_module(OuterProductMean(64, 32, 128), p).cuda()
+    got = mod(dev(m), dev(mask)).cpu().numpy()
+    ref = OM.outer_product_mean(m, mask, p)
+    mt = O.metrics(got, ref)
+    assert mt["finite"]
+    assert mt["rel_fro"] < (1e-5 if precision == "fp32" else 3e-3), mt
+
+
+@pytest.mark.parametrize("precision", ["fp32", "f16"], indirect=True)
+@pytest.mark.parametrize("S,N", [(249, 37), (1, 130), (17, 64)])
+def test_pwa_module(precision, S, N):
+    from boltz_mlx_amd.layers.pair_averaging import PairWeightedAveraging
+    from boltz_mlx_amd.weights import load_module
+
+    p = rand_params(shapes_pwa(), seed=S * 7 + N, std=0.1)
+    rng = np.random.default_rng(S + 1)
+    m = rng.standard_normal((1, S, N, 64))
+    z = rng.standard_normal((1, N, N, 128)) * 3
+    pm = (rng.random((1, N, N)) > 0.15).astype(np.float64)
+    pm[:, :, 0] = 1
+    mod = load_module(PairWeightedAveraging(64, 128, 32, 8), p).cuda()
+    got = mod(dev(m), dev(z), dev(pm)).cpu().numpy()
+    if precision == "f16":
+        p = {**p, "proj_z.weight": p["proj_z.weight"].astype(np.float16).astype(np.float64)}
+    ref = OM.pair_weighted_averaging(m, z, pm, p)
+    mt = O.metrics(got, ref)
+    assert mt["finite"] and mt["rel_fro"] < 1e-5, mt
+
+
+@pytest.mark.parametrize("precision", ["fp32", "f16"], indirect=True)
+def test_msa_layer(precision):
+    from boltz_mlx_amd.layers.msa import MSALayer
+    from boltz_mlx_amd.weights import load_module
+
+    N, S = 40, 23
+    p = rand_params(shapes_msa_layer(), seed=31, std=0.05)
+    z, _, pm = pair_inputs(N, 128, seed=32, n_pad=3)
+    rng = np.random.default_rng(33)
+    m = rng.standard_normal((1, S, N, 64))
+    msa_mask = (rng.random((1, S, N)) > 0.1).astype(np.float64)
+    mod = load_module(MSALayer(64, 128), p).cuda()
+    zg, mg = mod(dev(z), dev(m), dev(pm), dev(msa_mask))
+    zr, mr = OM.msa_layer(z, m, pm, msa_mask, p)
+    # the 3 padded tokens mask every key of their PWA rows, whose fp32 logits - 1e6 round to multiples of 1/16 (as
+    # the reference's do); the masked pair updates keep that out of the valid tokens, which are compared
+    v = N - 3
+    zg, mg = zg.cpu().numpy(), mg.cpu().numpy()
+    assert np.isfinite(zg).all() and np.isfinite(mg).all()
+    mz = O.metrics(zg[:, :v, :v] - z[:, :v, :v], zr[:, :v, :v] - z[:, :v, :v])
+    mm = O.metrics(mg[:, :, :v] - m[:, :, :v], mr[:, :, :v] - m[:, :, :v])
+    print(f"msa layer [{precision}]: z {mz} m {mm}", flush=True)
+    assert mz["finite"] and mm["finite"]
+    if precision == "fp32":
+        assert mz["rel_fro"] < 1e-5 and mm["rel_fro"] < 1e-5, (mz, mm)
+    else:
+        assert mz["rel_fro"] < 5e-3 and mm["rel_fro"] < 5e-3, (mz, mm)

@@ -166,6 +166,41 @@ def diffusion_transformer_leg(steps: int, device) -> dict:
             "finite": bool(torch.isfinite(a).all().item())}
 
 
+def msa_layer_leg(steps: int, device, N: int = 400, S: int = 1024) -> dict:
+    """One MSA block (MSALayer: pair-weighted averaging, transition on m, outer-product mean, NoSeq pair layer) at
+    N tokens and S MSA rows (5 % padded tokens, 10 % masked MSA entries), random-init weights, timed over `steps`
+    layer calls. The outer sum and the weighted average are fp32 MFMA reductions (the reference's numerics policy);
+    their FLOPs are reported with the fraction of the fp32 MFMA peak they reach together."""
+    import torch
+
+    from boltz_mlx_amd.layers.msa import MSALayer
+    from boltz_mlx_amd.weights import load_module, synthetic_state
+
+    m = MSALayer(64, 128)
+    load_module(m, synthetic_state(m, seed=7, std=0.02))
+    m = m.to(device)
+    g = torch.Generator(device=device).manual_seed(7)
+    z = torch.randn((1, N, N, 128), generator=g, device=device)
+    msa = torch.randn((1, S, N, 64), generator=g, device=device)
+    tok = torch.ones((1, N), device=device)
+    tok[:, N - N // 20:] = 0
+    pm = tok[:, :, None] * tok[:, None, :]
+    msa_mask = (torch.rand((1, S, N), generator=g, device=device) > 0.1).float() * tok[:, None, :]
+    for _ in range(2):
+        zo, mo = m(z, msa, pm, msa_mask)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        zo, mo = m(z, msa, pm, msa_mask)
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / steps
+    fl_opm = 2.0 * (32 * N) ** 2 * S
+    fl_pwa = 2.0 * 8 * N * N * S * 32
+    return {"workload": f"msa_layer_N{N}_S{S}_fp16", "steps": steps, "ms_per_layer": round(1e3 * dt, 3),
+            "fp32_reduction_flop": fl_opm + fl_pwa,
+            "finite": bool(torch.isfinite(zo).all().item() and torch.isfinite(mo).all().item())}
+
+
 def cpu_baseline(N_sample: int = 400, N_target: int = 1000) -> dict:
     import numpy as np
 
@@ -205,6 +240,8 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--c5-steps", type=int, default=20,
                     help="diffusion-transformer sampler steps timed after the trunk (0: skip)")
+    ap.add_argument("--msa-steps", type=int, default=5, help="MSA-block layer calls timed after the trunk (0: skip)")
+    ap.add_argument("--msa-only", action="store_true", help="time only the MSA-block leg and print its JSON line")
     ap.add_argument("--c5-only", action="store_true",
                     help="time only the diffusion-transformer leg (for profiling it) and print its JSON line")
     ap.add_argument("--calibrate-copy", action="store_true",
@@ -228,6 +265,10 @@ def main() -> int:
     if args.c5_only:
         with torch.no_grad():
             print(json.dumps({"diffusion_transformer": diffusion_transformer_leg(args.c5_steps, dev)}), flush=True)
+        return 0
+    if args.msa_only:
+        with torch.no_grad():
+            print(json.dumps({"msa_layer": msa_layer_leg(args.msa_steps, dev)}), flush=True)
         return 0
     result_small = None
     with torch.no_grad():
@@ -299,6 +340,9 @@ def main() -> int:
     if args.c5_steps:
         with torch.no_grad():
             out["diffusion_transformer"] = diffusion_transformer_leg(args.c5_steps, dev)
+    if args.msa_steps:
+        with torch.no_grad():
+            out["msa_layer"] = msa_layer_leg(args.msa_steps, dev)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)

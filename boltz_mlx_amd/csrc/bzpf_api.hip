@@ -292,6 +292,38 @@ int bzpf_seq_attention(const void* q, const void* k, const void* v, const void* 
                                     stream);
 }
 
+int bzpf_trimul_pack(const void* P, const float* mask, float scale, int incoming, void* ab, int dt, int64_t N,
+                     int64_t ld, int D, void* stream) {
+  REQUIRE(P && mask && ab, "bzpf_trimul_pack: NULL pointer");
+  REQUIRE(dt_ok(dt), "bzpf_trimul_pack: bad dtype %d", dt);
+  REQUIRE(N >= 1 && N <= 65535 && ld == bzpf_row_pitch(N), "bzpf_trimul_pack: N=%lld ld=%lld", (long long)N,
+          (long long)ld);
+  REQUIRE(D >= 1 && D <= 4096, "bzpf_trimul_pack: need 1 <= D <= 4096 (D=%d)", D);
+  return done(bzpf::launch_trimul_pack(P, mask, scale, incoming, ab, dt, N, ld, D, S(stream)), "bzpf_trimul_pack");
+}
+
+int bzpf_channels_to_rows(const void* o, int o_dt, void* out, int out_dt, int64_t N, int64_t ld, int D,
+                          void* stream) {
+  REQUIRE(o && out, "bzpf_channels_to_rows: NULL pointer");
+  REQUIRE(dt_ok(o_dt) && dt_ok(out_dt), "bzpf_channels_to_rows: bad dtype");
+  REQUIRE(N >= 1 && N <= 65535 && ld == bzpf_row_pitch(N), "bzpf_channels_to_rows: N=%lld ld=%lld", (long long)N,
+          (long long)ld);
+  REQUIRE(D >= 1 && D <= 252, "bzpf_channels_to_rows: need 1 <= D <= 252 (D=%d)", D);
+  return done(bzpf::launch_channels_to_rows(o, o_dt, out, out_dt, N, ld, D, S(stream)), "bzpf_channels_to_rows");
+}
+
+int bzpf_triattn_pack(const void* P, int trans, float q_scale, float bias_scale, void* qkg, void* vt, void* tri_bias,
+                      int dt, int64_t N, int64_t ldk, int H, int C, void* stream) {
+  REQUIRE(P && qkg && vt && tri_bias, "bzpf_triattn_pack: NULL pointer");
+  REQUIRE(dt_ok(dt), "bzpf_triattn_pack: bad dtype %d", dt);
+  REQUIRE(N >= 1 && N <= 65535 && ldk == bzpf_row_pitch(N), "bzpf_triattn_pack: N=%lld ldk=%lld", (long long)N,
+          (long long)ldk);
+  REQUIRE(H >= 1 && C >= 1 && H * C + H <= 252, "bzpf_triattn_pack: need H*C + H <= 252 (H=%d C=%d)", H, C);
+  return done(bzpf::launch_triattn_pack(P, trans, q_scale, bias_scale, qkg, vt, tri_bias, dt, N, ldk, H, C,
+                                        S(stream)),
+              "bzpf_triattn_pack");
+}
+
 int bzpf_opm_outer(const float* ab, int64_t ld_ab, const float* mask, void* out, int out_dt, int n_seq, int N,
                    int i_base, int n_i, void* stream) {
   REQUIRE(ab && mask && out, "bzpf_opm_outer: NULL pointer");

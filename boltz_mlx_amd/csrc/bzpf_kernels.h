@@ -72,6 +72,12 @@ hipError_t launch_pwa_softmax(const float* logits, const float* pm, float inf, f
                               hipStream_t st);
 hipError_t launch_pwa_avg(const float* w, int64_t ldw, const float* v, int64_t ldv, const float* g, int64_t ldg,
                           float* out, int64_t ldo, int S, int N, int H, hipStream_t st);
+hipError_t launch_trimul_pack(const void* P, const float* mask, float scale, int incoming, void* ab, int dt,
+                              int64_t N, int64_t ld, int D, hipStream_t st);
+hipError_t launch_channels_to_rows(const void* o, int o_dt, void* out, int out_dt, int64_t N, int64_t ld, int D,
+                                   hipStream_t st);
+hipError_t launch_triattn_pack(const void* P, int trans, float q_scale, float b_scale, void* qkg, void* vt, void* tb,
+                               int dt, int64_t N, int64_t ldk, int H, int C, hipStream_t st);
 hipError_t launch_pair_bias(const float* z, const float* lnw, const float* lnb, float eps, const void* w, void* out,
                             int dt, int64_t rows, int H, hipStream_t st);
 

@@ -27,6 +27,8 @@ PRECISION = os.environ.get("BOLTZ_MLX_PRECISION", "fp32")
 # BOLTZ_MLX_GUARDS=0 or BOLTZ_MLX_GUARD_MODE=off turns it off.
 GUARDS = os.environ.get("BOLTZ_MLX_GUARDS", "1") == "1" and os.environ.get("BOLTZ_MLX_GUARD_MODE", "residual") != "off"
 TRIMULT_K = int(os.environ.get("BOLTZ_MLX_TRIMULT_K", "4"))
+# fp16 transition hidden down-scale exponent at 64 channels (boltz_mlx/kernels.py:1327, layers/transition.py:60-92)
+TRANS64_K = int(os.environ.get("BOLTZ_MLX_TRANS64_K", "2"))
 
 
 # Per-entry-point HIP event timing (off unless a dict is installed with start_timing()).
@@ -181,6 +183,44 @@ def trimul_proj(xn, w_pg, mask, scale: float, incoming: bool, N: int) -> torch.T
     call("bzpf_trimul_proj", _p(xn), _p(w_pg), _p(mask), float(scale), int(incoming), _p(ab), _dt(xn), N, ld, D,
          _stream())
     return ab
+
+
+def trimul_pack(P: torch.Tensor, mask: torch.Tensor, scale: float, incoming: bool, N: int) -> torch.Tensor:
+    """ab [2D, N, ld] from P = xn [p_in; g_in]^T ([N*N, 4D]) at any D (the fused trimul_proj is built for 128)."""
+    _dev(P, mask)
+    D = P.shape[-1] // 4
+    if P.shape != (N * N, 4 * D) or mask.dtype != torch.float32 or mask.numel() != N * N:
+        raise ValueError("trimul_pack: need P [N*N, 4D] and an fp32 mask [N, N]")
+    ld = row_pitch(N)
+    ab = torch.empty((2 * D, N, ld), dtype=P.dtype, device=P.device)
+    call("bzpf_trimul_pack", _p(P), _p(mask), float(scale), int(incoming), _p(ab), _dt(P), N, ld, D, _stream())
+    return ab
+
+
+def channels_to_rows(o: torch.Tensor, N: int, out_dtype=None) -> torch.Tensor:
+    """[N*N, D] rows from the contraction output o [D, N, ld]."""
+    _dev(o)
+    D = o.shape[0]
+    ld = row_pitch(N)
+    if o.shape != (D, N, ld):
+        raise ValueError("channels_to_rows: o must be [D, N, ld]")
+    out = torch.empty((N * N, D), dtype=out_dtype or o.dtype, device=o.device)
+    call("bzpf_channels_to_rows", _p(o), _dt(o), _p(out), _dt(out), N, ld, D, _stream())
+    return out
+
+
+def triattn_pack(P: torch.Tensor, trans: bool, N: int, H: int, C: int):
+    """(qkg, vt, tb) as triattn_proj returns them, from P = xn [q; k; v; g; bias]^T ([N*N, 4HC + H]) at any c_in."""
+    _dev(P)
+    if P.shape != (N * N, 4 * H * C + H):
+        raise ValueError("triattn_pack: P must be [N*N, 4HC + H]")
+    ldk = row_pitch(N)
+    qkg = torch.empty((3 * H, N * N, C), dtype=P.dtype, device=P.device)
+    vt = torch.empty((H, N, C, ldk), dtype=P.dtype, device=P.device)
+    tb = torch.zeros((tri_bias_numel(N, H),), dtype=P.dtype, device=P.device)
+    call("bzpf_triattn_pack", _p(P), int(trans), LOG2E / C ** 0.5, LOG2E, _p(qkg), _p(vt), _p(tb), _dt(P), N, ldk, H,
+         C, _stream())
+    return qkg, vt, tb
 
 
 def trimul_contract(ab: torch.Tensor, N: int) -> torch.Tensor:

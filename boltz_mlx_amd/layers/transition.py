@@ -43,12 +43,31 @@ class Transition(torch.nn.Module):
         return self.unfused(xn)
 
     def prepare(self):
-        """The kernel weights in the storage dtype ([fc1; fc2] and fc3), cached on the module."""
-        return K.wcache(self, "w12", self.fc1.weight, self.fc2.weight), K.wcache(self, "w3", self.fc3.weight)
+        """The kernel weights in the storage dtype ([fc1; fc2] and fc3), cached on the module. In f16 mode at 64
+        channels the hidden activations are scaled by 2^-TRANS64_K before their fp16 store and the output by
+        2^TRANS64_K (the reference's fp16 overflow margin, boltz_mlx/kernels.py:1327, layers/transition.py:60-92):
+        folded exactly into the weights as fc2 * 2^-k and fc3 * 2^k."""
+        w12, w3 = K.wcache(self, "w12", self.fc1.weight, self.fc2.weight), K.wcache(self, "w3", self.fc3.weight)
+        k = K.TRANS64_K if (K.f16() and self.fc1.in_features == 64) else 0
+        if not k:
+            return w12, w3
+        hit = self.__dict__.get("_bzpf_scaled")
+        if hit is None or hit[0] is not w12 or hit[1] is not w3 or hit[2] != k:
+            w12s = w12.clone()
+            w12s[self.hidden:] *= 2.0 ** -k
+            hit = (w12, w3, k, w12s, (w3 * 2.0 ** k).contiguous())
+            self.__dict__["_bzpf_scaled"] = hit
+        return hit[3], hit[4]
 
     def fused(self, xn: torch.Tensor, z: torch.Tensor, accumulate: bool = True, next_ln=None, pair_bias=None):
         """z (+)= transition from xn = norm(z) (storage dtype); returns next_ln(z_new) when next_ln is given. With
         pair_bias = (LayerNorm, weight [H, D]) it also returns Linear(LN(z_new)) as [H, N, N]: (next_ln(z_new), bias)."""
+        if not self._pair_kernel():  # other channel counts: GEMMs + SwiGLU, residual in the second GEMM
+            if pair_bias is not None:
+                raise NotImplementedError("the pair-bias epilogue needs the 128-channel transition kernel")
+            z2 = z.view(-1, z.shape[-1])
+            self.unfused(xn, out=z2, accumulate=accumulate)
+            return None if next_ln is None else next_ln.to_storage(z2).reshape(z2.shape)
         w12, w3 = self.prepare()
         return K.transition(xn, w12, w3, z, accumulate, next_ln, pair_bias)
 

@@ -56,10 +56,21 @@ class TriangleAttention(torch.nn.Module):
         fp32 (natural layout); returns next_ln(z_new) when next_ln is given. before_core() is called after the
         projection is enqueued and before the attention core (the point where independent work on another stream
         overlaps the core rather than a persistent kernel)."""
-        N = z.shape[0]
+        N, D = z.shape[0], z.shape[-1]
         H, C = self.no_heads, self.mha.c_hidden
         w, w_o = self.prepare()
         trans = not self.starting
+        if D != 128:  # the projection and output kernels are built for 128 channels: GEMMs plus layout kernels
+            qkg, vt, tb = K.triattn_pack(K.linear(xn, w), trans, N, H, C)
+            if before_core is not None:
+                before_core()
+            core = K.triattn_core(qkg, vt, tb, mask, trans, self.inf, N, H, C)
+            del qkg, vt, tb
+            y = K.linear(core, w_o, out_dtype=torch.float32).view(N, N, D)
+            if not accumulate:
+                z.zero_()
+            nxt = K.add_ln(z, y, ln=next_ln, trans_y=trans, out_dtype=K.storage_dtype())
+            return None if nxt is None else nxt.view(N * N, D)
         qkg, vt, tb = K.triattn_proj(xn, w, trans, N, H, C)
         if before_core is not None:
             before_core()

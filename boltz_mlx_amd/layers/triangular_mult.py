@@ -44,9 +44,21 @@ class _TriangleMultiplication(torch.nn.Module):
               next_ln=None):
         """z (+)= self(z) from xn = norm_in(z) ([N*N, D], storage dtype) and mask [N, N] fp32; returns
         next_ln(z_new) in the storage dtype when next_ln is given."""
-        N = z.shape[0]
+        N, D = z.shape[0], z.shape[-1]
         kexp = K.TRIMULT_K if K.f16() else 0
         w_pg, w_po, w_go = self.prepare()
+        if D != 128:  # the projection and tail kernels are built for 128 channels: GEMMs plus layout kernels
+            ab = K.trimul_pack(K.linear(xn, w_pg), mask, 2.0 ** -kexp, not self.outgoing, N)
+            o = K.trimul_contract(ab, N)
+            del ab
+            on = K.layer_norm(K.channels_to_rows(o, N), self.norm_out.weight, self.norm_out.bias,
+                              self.norm_out.eps * 2.0 ** (-4 * kexp), out_dtype=K.storage_dtype())
+            del o
+            z2 = z.view(N * N, D)
+            if not accumulate:
+                z2.zero_()
+            K.linear_gated(on, w_po, K.linear(xn, w_go, out_dtype=torch.float32), z2)
+            return None if next_ln is None else next_ln.to_storage(z).reshape(N * N, D)
         ab = K.trimul_proj(xn, w_pg, mask, 2.0 ** -kexp, not self.outgoing, N)
         o = K.trimul_contract(ab, N)
         del ab

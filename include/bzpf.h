@@ -179,6 +179,30 @@ int bzpf_seq_attention_batched(const void* q, const void* k, const void* v, cons
                                int64_t s_mask, float inf, void* out, int64_t ld_out, int64_t s_out, int dt,
                                int n_samples, int64_t N, int H, int hd, void* stream);
 
+/* Pair updates at channel counts other than 128 (the template stack's c_z = 64): the projections run as bzpf_linear
+ * GEMMs over xn [N*N, D] and these three calls move their outputs into the layouts bzpf_trimul_contract and
+ * bzpf_triattn_core read (the fused bzpf_trimul_proj / bzpf_triattn_proj / bzpf_trimul_tail need D = 128).
+ *
+ * bzpf_trimul_pack: P [N*N, 4D] = xn [p_in; g_in]^T -> ab [2D][N][ld] with
+ *   ab[c][i][k] = P[p][c] * sigmoid(P[p][2D + c]) * mask[p] * scale, p = i*N + k (outgoing) or k*N + i (incoming),
+ * zeros for N <= k < ld; mask fp32 [N, N], ld = bzpf_row_pitch(N), D <= 4096. Replaces the projection of the
+ * reference's TriangleMultiplication (boltz_mlx/layers/triangular_mult.py:40-65, 143-170). */
+int bzpf_trimul_pack(const void* P, const float* mask, float scale, int incoming, void* ab, int dt, int64_t N,
+                     int64_t ld, int D, void* stream);
+
+/* bzpf_channels_to_rows: out[i*N + j][c] = o[c][i][j] for o [D][N][ld] (the contraction output) -> out [N*N, D]
+ * (dtypes independent), the operand of norm_out (boltz_mlx/layers/triangular_mult.py:93-98). D <= 252. */
+int bzpf_channels_to_rows(const void* o, int o_dt, void* out, int out_dt, int64_t N, int64_t ld, int D,
+                          void* stream);
+
+/* bzpf_triattn_pack: P [N*N, 4*H*C + H] = xn [linear_q; linear_k; linear_v; linear_g; linear]^T -> the qkg, vt and
+ * fragment-ordered tri_bias buffers of bzpf_triattn_proj (same layouts, q * q_scale, bias * bias_scale), P read at
+ * (j, i) when trans (the ending node). tri_bias rows of padded queries (N <= j < 32*ceil(N/32)) are not written:
+ * the caller zeroes the buffer. H*C + H <= 252. Replaces the projection of the reference's TriangleAttention
+ * (boltz_mlx/layers/triangular_attention/attention.py:49-69, 100-104) at any c_in. */
+int bzpf_triattn_pack(const void* P, int trans, float q_scale, float bias_scale, void* qkg, void* vt, void* tri_bias,
+                      int dt, int64_t N, int64_t ldk, int H, int C, void* stream);
+
 /* Outer-product-mean outer sum for MSA rows s < n_seq over tokens (fp32 ab [n_seq, N, ld_ab]: a = ab[.., 0:32],
  * b = ab[.., 32:64], unmasked; mask fp32 [n_seq, N]): for i_base <= i < i_base + n_i and j < N,
  *   out[(i - i_base) * N + j][c * 32 + d] = sum_s mask[s][i] mask[s][j] a[s][i][c] b[s][j][d] / max(count_ij, 1),

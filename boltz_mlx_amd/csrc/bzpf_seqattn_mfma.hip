@@ -1,4 +1,5 @@
-// fp16 sequence attention with pair bias on MFMA (v_mfma_f32_32x32x16_f16), head width HD in {16, 32, 48, 64}:
+// fp16 sequence attention with pair bias on MFMA (v_mfma_f32_32x32x16_f16), head width HD in {16, 24, 32, 48, 64}
+// (24, the s track's 384 / 16, runs its QK product as 32 with zero Q and K dims 24..31):
 //   out[j][h*HD + c] = sigmoid(g[j][h*HD + c]) * sum_k softmax_k(q_j.k_k / sqrt(HD) + bias[h][j][k]
 //                                                                 + (1 - mask[k]) * -inf) v[k][h*HD + c]
 // for the attention of AttentionPairBias (boltz_mlx/layers/attentionv2.py:59-83), the s track's and the diffusion
@@ -58,15 +59,16 @@ __global__ __launch_bounds__(256, 2) void seq_attn_mfma(const half_t* __restrict
                                                         half_t* __restrict__ out, int64_t ld_out, int N, int H,
                                                         int64_t s_in, int64_t s_bias, int mult, int64_t s_mask,
                                                         int64_t s_out) {
-  static_assert(HD % 16 == 0 && HD >= 16 && HD <= 64, "head width 16, 32, 48 or 64");
-  constexpr int BK = 64;                  // keys per LDS stage
-  constexpr int WQ = 128;                 // queries per workgroup
-  constexpr int KS = HD / 16;             // QK MFMA steps per 32-key tile
-  constexpr int NT = (HD + 31) / 32;      // 32-channel output tiles
-  constexpr int LDK = HD + 8;             // Ks row pitch (halves)
-  constexpr int LDV = BK + 8;             // Vs row pitch (halves)
-  constexpr int VPR = HD / 8;             // 16-byte vectors per K / V row
-  constexpr int NV = 2 * BK * VPR / 256;  // staged vectors per thread and block (K then V)
+  static_assert((HD % 16 == 0 || HD == 24) && HD >= 16 && HD <= 64, "head width 16, 24, 32, 48 or 64");
+  constexpr int BK = 64;                   // keys per LDS stage
+  constexpr int WQ = 128;                  // queries per workgroup
+  constexpr int KS = (HD + 15) / 16;       // QK MFMA steps per 32-key tile (24 runs as 32 with zero dims 24..31)
+  constexpr int NT = (HD + 31) / 32;       // 32-channel output tiles
+  constexpr int LDK = 16 * KS + 8;         // Ks row pitch (halves)
+  constexpr int LDV = BK + 8;              // Vs row pitch (halves)
+  constexpr int VPR = HD / 8;              // 16-byte vectors per K / V row
+  constexpr int NSTAGE = 2 * BK * VPR;     // staged vectors per block (K then V), a multiple of 64
+  constexpr int NV = (NSTAGE + 255) / 256;  // per thread
   constexpr float LOG2E = 1.4426950408889634f;
   constexpr float PLIM = 32768.0f;
   // K and V^T tiles double-buffered: block kb is written to buffer kb & 1 before the one barrier of iteration kb,
@@ -115,7 +117,8 @@ __global__ __launch_bounds__(256, 2) void seq_attn_mfma(const half_t* __restrict
     const float qs = LOG2E / sqrtf((float)HD);
 #pragma unroll
     for (int m = 0; m < KS; m++) {
-      const half8 raw = *reinterpret_cast<const half8*>(qh + (int64_t)jc * ld_in + 16 * m + 8 * hl);
+      const half8 raw = 16 * m + 8 * hl < HD ? *reinterpret_cast<const half8*>(qh + (int64_t)jc * ld_in + 16 * m + 8 * hl)
+                                             : half8{0, 0, 0, 0, 0, 0, 0, 0};
 #pragma unroll
       for (int e = 0; e < 8; e++) qf[m][e] = (half_t)((float)raw[e] * qs);
     }
@@ -154,6 +157,7 @@ __global__ __launch_bounds__(256, 2) void seq_attn_mfma(const half_t* __restrict
 #pragma unroll
     for (int n = 0; n < NV; n++) {
       const int e = t + 256 * n;
+      if (e >= NSTAGE) break;  // wave-uniform
       const bool isk = e < BK * VPR;
       const int ee = isk ? e : e - BK * VPR;
       const int off = (int)(((int64_t)(ee / VPR) * ld_in + (ee % VPR) * 8) * 2);
@@ -170,6 +174,10 @@ __global__ __launch_bounds__(256, 2) void seq_attn_mfma(const half_t* __restrict
         bcur[kt][gq] = __builtin_bit_cast(
             half4, __builtin_amdgcn_raw_buffer_load_b64(brs, bo + (32 * kt + 8 * gq) * 2, 0, 0));
   };
+  if constexpr (16 * KS > HD) {  // K dims HD .. 16 KS - 1 meet zero Q dims: keep them finite (zero) in both buffers
+    for (int r = t; r < 2 * BK; r += 256)
+      *reinterpret_cast<half8*>(Ks[r / BK] + (r % BK) * LDK + HD) = half8{0, 0, 0, 0, 0, 0, 0, 0};
+  }
   prefetch(0);
   __builtin_amdgcn_sched_barrier(0);
   prefetch_bias(0);
@@ -182,6 +190,7 @@ __global__ __launch_bounds__(256, 2) void seq_attn_mfma(const half_t* __restrict
 #pragma unroll
     for (int n = 0; n < NV; n++) {
       const int e = t + 256 * n;
+      if (e >= NSTAGE) break;  // wave-uniform
       if (e < BK * VPR) {  // wave-uniform: BK * VPR is a multiple of 64
         *reinterpret_cast<half8*>(Kb + (e / VPR) * LDK + (e % VPR) * 8) = sreg[n];
       } else {
@@ -318,6 +327,7 @@ hipError_t launch_seq_attention_f16_mfma(const void* q, const void* k, const voi
                                            ld_out, (int)N, H, s_in, s_bias, mult, s_mask, s_out)
   switch (hd) {
     case 16: BZ_SEQ_MFMA(16); break;
+    case 24: BZ_SEQ_MFMA(24); break;
     case 32: BZ_SEQ_MFMA(32); break;
     case 48: BZ_SEQ_MFMA(48); break;
     case 64: BZ_SEQ_MFMA(64); break;

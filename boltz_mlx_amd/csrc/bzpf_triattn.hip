@@ -210,8 +210,8 @@ hipError_t launch_triattn_core_simple(const void* qkg, const void* vt, const voi
                       : core_valu_t<float>(qkg, vt, tb, mask, mask_si, mask_sk, inf, out, N, ldk, H, C, st);
 }
 
-// fp16 with head width 16, 32, 48 or 64 (and the alignment its vector loads need) runs on the MFMA kernel
-// (bzpf_seqattn_mfma.hip), all S samples in one launch; other widths (the s track's 24) and fp32 on the VALU kernel
+// fp16 with head width 16, 24, 32, 48 or 64 (and the alignment its vector loads need) runs on the MFMA kernel
+// (bzpf_seqattn_mfma.hip), all S samples in one launch; fp32 and other widths on the VALU kernel
 // above, one launch per sample.
 hipError_t launch_seq_attention(const void* q, const void* k, const void* v, const void* g, int64_t ld_in,
                                 int64_t s_in, const void* bias, int64_t s_bias, int mult, const float* mask,
@@ -219,7 +219,7 @@ hipError_t launch_seq_attention(const void* q, const void* k, const void* v, con
                                 int64_t N, int H, int hd, hipStream_t st) {
   const auto al = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; };
   if (S < 1 || mult < 1) return hipErrorInvalidValue;
-  if (dt == DT_F16 && (hd == 16 || hd == 32 || hd == 48 || hd == 64) && N % 4 == 0 && ld_in % 8 == 0 &&
+  if (dt == DT_F16 && (hd == 16 || hd == 24 || hd == 32 || hd == 48 || hd == 64) && N % 4 == 0 && ld_in % 8 == 0 &&
       ld_out % 4 == 0 && s_in % 8 == 0 && s_bias % 4 == 0 && s_out % 4 == 0 && al(q, 16) && al(k, 16) &&
       al(v, 16) && al(g, 16) && al(bias, 8) && al(out, 8) && N <= 32767 && S <= 65535 &&
       (N + 64) * ld_in * 2 <= 0x7fffffffLL && N * N * 2 <= 0x7fffffffLL)

@@ -204,11 +204,11 @@ def test_diffusion_layer_forward_and_shared_conditioning(precision):
     assert torch.equal(full, one)
 
 
-@pytest.mark.parametrize("hd", [16, 32, 48, 64])
+@pytest.mark.parametrize("hd", [16, 24, 32, 48, 64])
 @pytest.mark.parametrize("N", [64, 132])
 @pytest.mark.parametrize("all_masked", [False, True])
 def test_seq_attention_mfma_vs_valu(hd, N, all_masked):
-    """The fp16 MFMA sequence attention (head widths 16-64, N % 4 == 0, 16-byte rows) against the VALU kernel on the
+    """The fp16 MFMA sequence attention (head widths 16-64, N % 4 == 0, 16-byte rows; 24 as 32 with zero dims) against the VALU kernel on the
     same fp16 values (the VALU kernel is forced by a row pitch that is not a multiple of 8), within the reference's
     MMA-vs-scalar gate (5e-3), and against the float64 definition. Keys past N - 3 are masked; all_masked masks
     every key, which leaves the softmax of the unmasked logits (checked against the float64 definition only)."""

@@ -292,6 +292,15 @@ int bzpf_seq_attention(const void* q, const void* k, const void* v, const void* 
                                     stream);
 }
 
+int bzpf_linear_swiglu3(const void* x, const void* w, void* u, int64_t rows, int K, int H, void* stream) {
+  REQUIRE(x && w && u, "bzpf_linear_swiglu3: NULL pointer");
+  REQUIRE(aligned16(x) && aligned16(w) && reinterpret_cast<uintptr_t>(u) % 8 == 0,
+          "bzpf_linear_swiglu3: x and w must be 16-byte aligned, u 8-byte aligned");
+  REQUIRE(rows >= 1 && K >= 64 && K % 64 == 0 && K <= (1 << 22) && H >= 32 && H % 32 == 0,
+          "bzpf_linear_swiglu3: need K %% 64 == 0, H %% 32 == 0 (rows=%lld K=%d H=%d)", (long long)rows, K, H);
+  return done(bzpf::launch_gemm_swiglu3_f16(x, w, u, rows, K, H, S(stream)), "bzpf_linear_swiglu3");
+}
+
 int bzpf_trimul_pack(const void* P, const float* mask, float scale, int incoming, void* ab, int dt, int64_t N,
                      int64_t ld, int D, void* stream) {
   REQUIRE(P && mask && ab, "bzpf_trimul_pack: NULL pointer");

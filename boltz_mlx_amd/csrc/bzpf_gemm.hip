@@ -144,6 +144,100 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_f16_k(const half_t* __restrict
   }
 }
 
+// Feed-forward GEMM with the gated product in its epilogue: u[r][c] = silu(x[r] . Wg[c]) * (x[r] . Wx[c]) *
+// (x[r] . Wab[c]) (the conditioned transition's silu(gates) * x * a_to_b, transformersv2.py:44-66) without the
+// [R, 3H] intermediate. W is stored in 96-row groups [Wg[32 q .. +31]; Wx[..]; Wab[..]] per 32 output columns q, so
+// a workgroup tile of 96 W rows x 128 x rows holds all three products of its 32 columns; its 4 waves own 32 x rows
+// each (3 MFMA blocks of 32 x 32), and each lane ends with the three values of 4 x 4 outputs of one row.
+__global__ __launch_bounds__(256, 2) void gemm_swiglu3_f16_k(const half_t* __restrict__ x, const half_t* __restrict__ w,
+                                                            half_t* __restrict__ u, int64_t R, int K, int H) {
+  constexpr int BM = 96, BR = 128, BK = 64, LDT = BK + 8, LA = BM / 32, LB = BR / 32;
+  __shared__ LDS_ALIGN half_t As[2][BM * LDT];
+  __shared__ LDS_ALIGN half_t Bs[2][BR * LDT];
+  const int64_t r0 = (int64_t)blockIdx.x * BR;
+  const int q = blockIdx.y;  // output columns 32 q .. 32 q + 31
+  const int t = threadIdx.x, wave = t >> 6, l = t & 63, rr = l & 31, hh = l >> 5;
+  constexpr int RSRC_CFG = 0x00020000;
+  const int64_t xrows = R - r0 < BR ? R - r0 : BR;
+  const __amdgpu_buffer_rsrc_t xrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(x + r0 * K), 0, (int)(xrows * K * 2), RSRC_CFG);
+  const __amdgpu_buffer_rsrc_t wrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(w + (int64_t)q * BM * K), 0, (int)((int64_t)BM * K * 2), RSRC_CFG);
+  const int lrow = t >> 3, lcol = (t & 7) * 8;
+  u32x4_t ra0[LA], rb0[LB], ra1[LA], rb1[LB];
+  auto gload = [&](u32x4_t (&ra)[LA], u32x4_t (&rb)[LB], int stage) {
+#pragma unroll
+    for (int v = 0; v < LA; v++) {
+      const int off = (int)(((int64_t)(32 * v + lrow) * K + stage * BK + lcol) * 2);
+      ra[v] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0));
+    }
+#pragma unroll
+    for (int v = 0; v < LB; v++) {
+      const int off = (int)(((int64_t)(32 * v + lrow) * K + stage * BK + lcol) * 2);
+      rb[v] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0));
+    }
+  };
+  auto lstore = [&](const u32x4_t (&ra)[LA], const u32x4_t (&rb)[LB], int buf) {
+#pragma unroll
+    for (int v = 0; v < LA; v++) *reinterpret_cast<u32x4_t*>(As[buf] + (32 * v + lrow) * LDT + lcol) = ra[v];
+#pragma unroll
+    for (int v = 0; v < LB; v++) *reinterpret_cast<u32x4_t*>(Bs[buf] + (32 * v + lrow) * LDT + lcol) = rb[v];
+  };
+  f16x acc[3];
+#pragma unroll
+  for (int mb = 0; mb < 3; mb++)
+#pragma unroll
+    for (int e = 0; e < 16; e++) acc[mb][e] = 0.0f;
+  auto compute = [&](int buf) {
+    const half_t* Ab = As[buf] + rr * LDT + 32 * hh;
+    const half_t* Bb = Bs[buf] + (32 * wave + rr) * LDT + 32 * hh;
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      half8 fa[3];
+#pragma unroll
+      for (int mb = 0; mb < 3; mb++) fa[mb] = *reinterpret_cast<const half8*>(Ab + 32 * mb * LDT + 8 * s);
+      const half8 fb = *reinterpret_cast<const half8*>(Bb + 8 * s);
+#pragma unroll
+      for (int mb = 0; mb < 3; mb++) acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[mb], fb, acc[mb], 0, 0, 0);
+    }
+  };
+  const int nst = K / BK;
+  const int s0 = -(nst & 1);
+  gload(ra0, rb0, 0);
+#pragma unroll
+  for (int v = 0; v < LA; v++) ra0[v] = s0 ? u32x4_t{0u, 0u, 0u, 0u} : ra0[v];
+#pragma unroll
+  for (int v = 0; v < LB; v++) rb0[v] = s0 ? u32x4_t{0u, 0u, 0u, 0u} : rb0[v];
+  lstore(ra0, rb0, 0);
+  __syncthreads();
+  gload(ra0, rb0, s0 + 1);
+  __builtin_amdgcn_sched_barrier(0);
+  gload(ra1, rb1, min(s0 + 2, nst - 1));
+  __builtin_amdgcn_sched_barrier(0);
+  for (int st = s0; st < nst; st += 2) {
+    compute(0);
+    lstore(ra0, rb0, 1);
+    __syncthreads();
+    gload(ra0, rb0, min(st + 3, nst - 1));
+    __builtin_amdgcn_sched_barrier(0);
+    compute(1);
+    lstore(ra1, rb1, 0);
+    __syncthreads();
+    gload(ra1, rb1, min(st + 4, nst - 1));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // lane (rr, hh): row r0 + 32 wave + rr, columns 32 q + 8 j + 4 hh .. + 3 in elements 4 j .. 4 j + 3 of each block
+  const int64_t r = r0 + 32 * wave + rr;
+  if (r >= R) return;
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    half4 o;
+#pragma unroll
+    for (int e = 0; e < 4; e++) o[e] = (half_t)(siluf_(acc[0][4 * j + e]) * acc[1][4 * j + e] * acc[2][4 * j + e]);
+    *reinterpret_cast<half4*>(u + r * H + 32 * q + 8 * j + 4 * hh) = o;
+  }
+}
+
 template <int BM, int BR>
 hipError_t gemm_t(const void* x, const void* w, const float* bias, void* y, int y_dt, int64_t R, int K, int M,
                   int epi, const float* gate, int64_t ld_gate, int64_t gate_rows, hipStream_t st) {
@@ -170,6 +264,17 @@ int gemm_tile_choice(int64_t R, int M) {
 }
 
 }  // namespace
+
+hipError_t launch_gemm_swiglu3_f16(const void* x, const void* w, void* u, int64_t R, int K, int H, hipStream_t st) {
+  const auto al = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; };
+  if (R < 1 || K % 64 || K < 64 || H % 32 || H < 32 || (int64_t)128 * K * 2 > 0x7fffffffLL || !al(x, 16) ||
+      !al(w, 16) || !al(u, 8) || (R + 127) / 128 > 0x7fffffffLL)
+    return hipErrorInvalidValue;
+  const dim3 grid((unsigned)((R + 127) / 128), (unsigned)(H / 32));
+  gemm_swiglu3_f16_k<<<grid, 256, 0, st>>>(static_cast<const half_t*>(x), static_cast<const half_t*>(w),
+                                           static_cast<half_t*>(u), R, K, H);
+  return hipGetLastError();
+}
 
 bool gemm_nt_f16_ok(const void* x, const void* w, const float* bias, const void* y, int64_t R, int K, int M,
                     const float* gate, int64_t ld_gate) {

@@ -393,6 +393,26 @@ def linear_gated(x, w, gate: torch.Tensor, out: torch.Tensor, bias=None) -> torc
     return out
 
 
+def linear_swiglu3(x: torch.Tensor, w_grouped: torch.Tensor) -> torch.Tensor:
+    """silu(x Wg^T) * (x Wx^T) * (x Wab^T) in one fp16 GEMM for w_grouped from group_swiglu3_rows (fp16 only)."""
+    _dev(x, w_grouped)
+    Kd = x.shape[-1]
+    H = w_grouped.shape[0] // 3
+    rows = x.numel() // Kd
+    if x.dtype != torch.float16 or w_grouped.dtype != torch.float16 or w_grouped.shape != (3 * H, Kd):
+        raise ValueError("linear_swiglu3: need fp16 x [rows, K] and grouped fp16 w [3H, K]")
+    u = torch.empty(x.shape[:-1] + (H,), dtype=torch.float16, device=x.device)
+    call("bzpf_linear_swiglu3", _p(x), _p(w_grouped), _p(u), rows, Kd, H, _stream())
+    return u
+
+
+def group_swiglu3_rows(wg: torch.Tensor, wx: torch.Tensor, wab: torch.Tensor) -> torch.Tensor:
+    """[Wg; Wx; Wab] regrouped as 96-row blocks [Wg[32q:32q+32]; Wx[..]; Wab[..]] (the fused kernel's layout)."""
+    H, Kd = wg.shape
+    return torch.stack([wg.view(H // 32, 32, Kd), wx.view(H // 32, 32, Kd), wab.view(H // 32, 32, Kd)], 1) \
+        .reshape(3 * H, Kd).contiguous()
+
+
 def adaln(a: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, out_dtype, eps: float = 1e-5) -> torch.Tensor:
     """sigmoid(scale) * LN(a) + shift (LN without affine) for fp32 a [rows, D]; scale and shift are fp32 [rows_c, D]
     views of one pitch (slices of the precomputed conditioning), row r using row r % rows_c

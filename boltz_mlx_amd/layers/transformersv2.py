@@ -13,7 +13,8 @@ layer are computed once per call in two GEMMs (the s_norm weight folded into the
   o = sigmoid(g) * softmax(q k^T / sqrt(hd) + bias + mask) v            bzpf_seq_attention_batched
   a += sigmoid(out_gate) * (o W_o^T)                                   bzpf_linear_gated
   t = sigmoid(tr_scale) * LN(a) + tr_shift                             bzpf_adaln
-  u = silu(t W_g^T) * (t W_x^T) * (t W_ab^T)                           bzpf_linear + bzpf_swiglu3
+  u = silu(t W_g^T) * (t W_x^T) * (t W_ab^T)                           bzpf_linear_swiglu3 (fp16; else
+                                                                       bzpf_linear + bzpf_swiglu3)
   a += sigmoid(tr_gate) * (u W_ba^T)                                   bzpf_linear_gated
 with a fp32 throughout; in f16 mode the GEMM operands and intermediates are fp16 (fp32 accumulation, LayerNorm
 statistics and softmax).
@@ -87,6 +88,15 @@ class DiffusionTransformerLayer(torch.nn.Module):
         w_ba = K.wcache(self, "w_ba", tr.b_to_a.weight)
         return w_qkvg, b_qkvg, w_o, w_ff, w_ba
 
+    def ff_grouped(self, w_ff):
+        """w_ff regrouped for the fused fp16 feed-forward kernel (K.linear_swiglu3), cached with its source."""
+        hit = self.__dict__.get("_bzpf_ffg")
+        if hit is None or hit[0] is not w_ff:
+            H = w_ff.shape[0] // 3
+            hit = (w_ff, K.group_swiglu3_rows(w_ff[:H], w_ff[H:2 * H], w_ff[2 * H:]))
+            self.__dict__["_bzpf_ffg"] = hit
+        return hit[1]
+
     def forward(self, a, s, bias=None, mask=None, to_keys=None, multiplicity: int = 1, cond=None, attn_bias=None):
         """One layer on its own (a [B*mult, N, D], s [B*mult, N, Dc], bias [B, N, N, H], mask [B*mult, N])."""
         if to_keys is not None:
@@ -148,7 +158,11 @@ def _layer_fast(layer, a, h1, h2, i: int, L: int, bias_l, mask, multiplicity: in
     o = K.seq_attention_packed(qkvg.view(Bm, N, 4 * D), bias_l, mask, at.inf, H, multiplicity=multiplicity)
     K.linear_gated(o.view(rows, D), w_o, c2[:, 0], a2)
     t = K.adaln(a2, c1[:, 2], c1[:, 3], dt)
-    u = K.swiglu3(K.linear(t, w_ff))
+    H3 = w_ff.shape[0]
+    if dt == torch.float16 and D % 64 == 0 and (H3 // 3) % 32 == 0:
+        u = K.linear_swiglu3(t, layer.ff_grouped(w_ff))
+    else:
+        u = K.swiglu3(K.linear(t, w_ff))
     K.linear_gated(u, w_ba, c2[:, 1], a2)
     if layer.post_layer_norm:
         a2.copy_(layer.post_lnorm(a2))

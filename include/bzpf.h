@@ -203,6 +203,15 @@ int bzpf_channels_to_rows(const void* o, int o_dt, void* out, int out_dt, int64_
 int bzpf_triattn_pack(const void* P, int trans, float q_scale, float bias_scale, void* qkg, void* vt, void* tri_bias,
                       int dt, int64_t N, int64_t ldk, int H, int C, void* stream);
 
+/* The conditioned transition's feed-forward GEMM with its gated product fused (fp16 only):
+ *   u[r][c] = silu(x[r] . Wg[c]) * (x[r] . Wx[c]) * (x[r] . Wab[c])   for r < rows, c < H,
+ * x fp16 [rows, K] (K % 64 == 0), u fp16 [rows, H] (H % 32 == 0), fp32 accumulation; w fp16 [3H, K] in 96-row groups
+ * [Wg[32 q .. 32 q + 31]; Wx[same]; Wab[same]] for q < H / 32 (Wg = the second half of swish_gate.0.weight, Wx its
+ * first half, Wab = a_to_b.weight). Replaces swish_gate + SwiGLU + a_to_b of ConditionedTransitionBlock
+ * (boltz_mlx/modules/transformersv2.py:44-66, kernels_nax3.py:447-700): bzpf_linear + bzpf_swiglu3 without the
+ * [rows, 3H] intermediate. */
+int bzpf_linear_swiglu3(const void* x, const void* w, void* u, int64_t rows, int K, int H, void* stream);
+
 /* Outer-product-mean outer sum for MSA rows s < n_seq over tokens (fp32 ab [n_seq, N, ld_ab]: a = ab[.., 0:32],
  * b = ab[.., 32:64], unmasked; mask fp32 [n_seq, N]): for i_base <= i < i_base + n_i and j < N,
  *   out[(i - i_base) * N + j][c * 32 + d] = sum_s mask[s][i] mask[s][j] a[s][i][c] b[s][j][d] / max(count_ij, 1),

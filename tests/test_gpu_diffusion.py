@@ -295,3 +295,21 @@ def test_step_graph_replays_equal_eager(precision):
         torch.cuda.synchronize()
         assert torch.equal(x_graph, x_eager), f"replay {it}"
         _ = (torch.randn(1000, device="cuda") * 2).sum().item()  # unrelated eager work between replays
+
+
+@pytest.mark.parametrize("R,Kd,H", [(70, 64, 32), (300, 768, 1536), (129, 192, 96)])
+def test_linear_swiglu3_fused(R, Kd, H):
+    """The fused feed-forward GEMM (gated product in the epilogue, grouped weight rows) against float64 on the same
+    fp16 values, and against the unfused linear + swiglu3 (which rounds the [R, 3H] product to fp16 first)."""
+    from boltz_mlx_amd import kernels as K
+
+    rng = np.random.default_rng(R + H)
+    x = dev(rng.standard_normal((R, Kd)), torch.float16)
+    w = dev(rng.standard_normal((3 * H, Kd)) / np.sqrt(Kd), torch.float16)
+    fused = K.linear_swiglu3(x, K.group_swiglu3_rows(w[:H], w[H:2 * H], w[2 * H:]))
+    unfused = K.swiglu3(K.linear(x, w))
+    torch.cuda.synchronize()
+    h = x.double().cpu().numpy() @ w.double().cpu().numpy().T
+    ref = OD.silu(h[:, :H]) * h[:, H:2 * H] * h[:, 2 * H:]
+    assert O.metrics(fused.double().cpu().numpy(), ref)["max_rel"] <= 2e-3
+    assert O.metrics(fused.double().cpu().numpy(), unfused.double().cpu().numpy())["max_rel"] <= 5e-3

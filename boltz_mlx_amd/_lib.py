@@ -38,6 +38,7 @@ SIGNATURES = {
     "bzpf_swiglu": [vp, vp, i32, i64, i32, vp],
     "bzpf_seq_attention": [vp, vp, vp, vp, i64, vp, vp, f32, vp, i64, i32, i64, i32, i32, vp],
     "bzpf_linear_swiglu3": [vp, vp, vp, i64, i32, i32, vp],
+    "bzpf_linear_swiglu": [vp, vp, vp, i64, i32, i32, vp],
     "bzpf_trimul_pack": [vp, vp, f32, i32, vp, i32, i64, i64, i32, vp],
     "bzpf_channels_to_rows": [vp, i32, vp, i32, i64, i64, i32, vp],
     "bzpf_triattn_pack": [vp, i32, f32, f32, vp, vp, vp, i32, i64, i64, i32, i32, vp],

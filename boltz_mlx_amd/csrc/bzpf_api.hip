@@ -298,7 +298,16 @@ int bzpf_linear_swiglu3(const void* x, const void* w, void* u, int64_t rows, int
           "bzpf_linear_swiglu3: x and w must be 16-byte aligned, u 8-byte aligned");
   REQUIRE(rows >= 1 && K >= 64 && K % 64 == 0 && K <= (1 << 22) && H >= 32 && H % 32 == 0,
           "bzpf_linear_swiglu3: need K %% 64 == 0, H %% 32 == 0 (rows=%lld K=%d H=%d)", (long long)rows, K, H);
-  return done(bzpf::launch_gemm_swiglu3_f16(x, w, u, rows, K, H, S(stream)), "bzpf_linear_swiglu3");
+  return done(bzpf::launch_gemm_swiglu_f16(x, w, u, rows, K, H, 3, S(stream)), "bzpf_linear_swiglu3");
+}
+
+int bzpf_linear_swiglu(const void* x, const void* w, void* u, int64_t rows, int K, int H, void* stream) {
+  REQUIRE(x && w && u, "bzpf_linear_swiglu: NULL pointer");
+  REQUIRE(aligned16(x) && aligned16(w) && reinterpret_cast<uintptr_t>(u) % 8 == 0,
+          "bzpf_linear_swiglu: x and w must be 16-byte aligned, u 8-byte aligned");
+  REQUIRE(rows >= 1 && K >= 64 && K % 64 == 0 && K <= (1 << 22) && H >= 32 && H % 32 == 0,
+          "bzpf_linear_swiglu: need K %% 64 == 0, H %% 32 == 0 (rows=%lld K=%d H=%d)", (long long)rows, K, H);
+  return done(bzpf::launch_gemm_swiglu_f16(x, w, u, rows, K, H, 2, S(stream)), "bzpf_linear_swiglu");
 }
 
 int bzpf_trimul_pack(const void* P, const float* mask, float scale, int incoming, void* ab, int dt, int64_t N,

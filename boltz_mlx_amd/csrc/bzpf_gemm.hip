@@ -144,14 +144,16 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_f16_k(const half_t* __restrict
   }
 }
 
-// Feed-forward GEMM with the gated product in its epilogue: u[r][c] = silu(x[r] . Wg[c]) * (x[r] . Wx[c]) *
-// (x[r] . Wab[c]) (the conditioned transition's silu(gates) * x * a_to_b, transformersv2.py:44-66) without the
-// [R, 3H] intermediate. W is stored in 96-row groups [Wg[32 q .. +31]; Wx[..]; Wab[..]] per 32 output columns q, so
-// a workgroup tile of 96 W rows x 128 x rows holds all three products of its 32 columns; its 4 waves own 32 x rows
-// each (3 MFMA blocks of 32 x 32), and each lane ends with the three values of 4 x 4 outputs of one row.
-__global__ __launch_bounds__(256, 2) void gemm_swiglu3_f16_k(const half_t* __restrict__ x, const half_t* __restrict__ w,
-                                                            half_t* __restrict__ u, int64_t R, int K, int H) {
-  constexpr int BM = 96, BR = 128, BK = 64, LDT = BK + 8, LA = BM / 32, LB = BR / 32;
+// Feed-forward GEMM with the gated product in its epilogue, NP = 3: u[r][c] = silu(x[r] . Wg[c]) * (x[r] . Wx[c]) *
+// (x[r] . Wab[c]) (the conditioned transition's silu(gates) * x * a_to_b, transformersv2.py:44-66); NP = 2:
+// u[r][c] = silu(x[r] . W1[c]) * (x[r] . W2[c]) (Transition's SwiGLU, transition.py:27-54), without the [R, NP H]
+// intermediate. W is stored in 32 NP-row groups [Wg[32 q .. +31]; Wx[..] (; Wab[..])] per 32 output columns q, so a
+// workgroup tile of 32 NP W rows x 128 x rows holds all products of its 32 columns; its 4 waves own 32 x rows each
+// (NP MFMA blocks of 32 x 32), and each lane ends with the NP values of 4 x 4 outputs of one row.
+template <int NP>
+__global__ __launch_bounds__(256, 2) void gemm_swiglu_f16_k(const half_t* __restrict__ x, const half_t* __restrict__ w,
+                                                           half_t* __restrict__ u, int64_t R, int K, int H) {
+  constexpr int BM = 32 * NP, BR = 128, BK = 64, LDT = BK + 8, LA = BM / 32, LB = BR / 32;
   __shared__ LDS_ALIGN half_t As[2][BM * LDT];
   __shared__ LDS_ALIGN half_t Bs[2][BR * LDT];
   const int64_t r0 = (int64_t)blockIdx.x * BR;
@@ -183,9 +185,9 @@ __global__ __launch_bounds__(256, 2) void gemm_swiglu3_f16_k(const half_t* __res
 #pragma unroll
     for (int v = 0; v < LB; v++) *reinterpret_cast<u32x4_t*>(Bs[buf] + (32 * v + lrow) * LDT + lcol) = rb[v];
   };
-  f16x acc[3];
+  f16x acc[NP];
 #pragma unroll
-  for (int mb = 0; mb < 3; mb++)
+  for (int mb = 0; mb < NP; mb++)
 #pragma unroll
     for (int e = 0; e < 16; e++) acc[mb][e] = 0.0f;
   auto compute = [&](int buf) {
@@ -193,12 +195,12 @@ __global__ __launch_bounds__(256, 2) void gemm_swiglu3_f16_k(const half_t* __res
     const half_t* Bb = Bs[buf] + (32 * wave + rr) * LDT + 32 * hh;
 #pragma unroll
     for (int s = 0; s < 4; s++) {
-      half8 fa[3];
+      half8 fa[NP];
 #pragma unroll
-      for (int mb = 0; mb < 3; mb++) fa[mb] = *reinterpret_cast<const half8*>(Ab + 32 * mb * LDT + 8 * s);
+      for (int mb = 0; mb < NP; mb++) fa[mb] = *reinterpret_cast<const half8*>(Ab + 32 * mb * LDT + 8 * s);
       const half8 fb = *reinterpret_cast<const half8*>(Bb + 8 * s);
 #pragma unroll
-      for (int mb = 0; mb < 3; mb++) acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[mb], fb, acc[mb], 0, 0, 0);
+      for (int mb = 0; mb < NP; mb++) acc[mb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[mb], fb, acc[mb], 0, 0, 0);
     }
   };
   const int nst = K / BK;
@@ -233,7 +235,11 @@ __global__ __launch_bounds__(256, 2) void gemm_swiglu3_f16_k(const half_t* __res
   for (int j = 0; j < 4; j++) {
     half4 o;
 #pragma unroll
-    for (int e = 0; e < 4; e++) o[e] = (half_t)(siluf_(acc[0][4 * j + e]) * acc[1][4 * j + e] * acc[2][4 * j + e]);
+    for (int e = 0; e < 4; e++) {
+      float v = siluf_(acc[0][4 * j + e]) * acc[1][4 * j + e];
+      if constexpr (NP == 3) v *= acc[NP - 1][4 * j + e];
+      o[e] = (half_t)v;
+    }
     *reinterpret_cast<half4*>(u + r * H + 32 * q + 8 * j + 4 * hh) = o;
   }
 }
@@ -265,14 +271,19 @@ int gemm_tile_choice(int64_t R, int M) {
 
 }  // namespace
 
-hipError_t launch_gemm_swiglu3_f16(const void* x, const void* w, void* u, int64_t R, int K, int H, hipStream_t st) {
+hipError_t launch_gemm_swiglu_f16(const void* x, const void* w, void* u, int64_t R, int K, int H, int np,
+                                  hipStream_t st) {
   const auto al = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; };
   if (R < 1 || K % 64 || K < 64 || H % 32 || H < 32 || (int64_t)128 * K * 2 > 0x7fffffffLL || !al(x, 16) ||
-      !al(w, 16) || !al(u, 8) || (R + 127) / 128 > 0x7fffffffLL)
+      !al(w, 16) || !al(u, 8) || (R + 127) / 128 > 0x7fffffffLL || (np != 2 && np != 3))
     return hipErrorInvalidValue;
   const dim3 grid((unsigned)((R + 127) / 128), (unsigned)(H / 32));
-  gemm_swiglu3_f16_k<<<grid, 256, 0, st>>>(static_cast<const half_t*>(x), static_cast<const half_t*>(w),
-                                           static_cast<half_t*>(u), R, K, H);
+  if (np == 3)
+    gemm_swiglu_f16_k<3><<<grid, 256, 0, st>>>(static_cast<const half_t*>(x), static_cast<const half_t*>(w),
+                                               static_cast<half_t*>(u), R, K, H);
+  else
+    gemm_swiglu_f16_k<2><<<grid, 256, 0, st>>>(static_cast<const half_t*>(x), static_cast<const half_t*>(w),
+                                               static_cast<half_t*>(u), R, K, H);
   return hipGetLastError();
 }
 

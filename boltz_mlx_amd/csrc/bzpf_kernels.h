@@ -52,7 +52,8 @@ bool gemm_nt_f16_ok(const void* x, const void* w, const float* bias, const void*
                     const float* gate, int64_t ld_gate);
 hipError_t launch_gemm_nt_f16(const void* x, const void* w, const float* bias, void* y, int y_dt, int64_t R, int K,
                               int M, int epi, const float* gate, int64_t ld_gate, int64_t gate_rows, hipStream_t st);
-hipError_t launch_gemm_swiglu3_f16(const void* x, const void* w, void* u, int64_t R, int K, int H, hipStream_t st);
+hipError_t launch_gemm_swiglu_f16(const void* x, const void* w, void* u, int64_t R, int K, int H, int np,
+                                  hipStream_t st);
 hipError_t launch_swiglu(const void* h, void* a, int dt, int64_t R, int H, hipStream_t st);
 hipError_t launch_swiglu3(const void* h, void* a, int dt, int64_t R, int H, hipStream_t st);
 hipError_t launch_linear_gated(const void* x, const void* w, const float* bias, const float* gate, int64_t ld_gate,

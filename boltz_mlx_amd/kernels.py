@@ -406,11 +406,28 @@ def linear_swiglu3(x: torch.Tensor, w_grouped: torch.Tensor) -> torch.Tensor:
     return u
 
 
+def linear_swiglu(x: torch.Tensor, w_grouped: torch.Tensor) -> torch.Tensor:
+    """silu(x W1^T) * (x W2^T) in one fp16 GEMM for w_grouped = group_swiglu_rows(W1, W2) (fp16 only)."""
+    _dev(x, w_grouped)
+    Kd = x.shape[-1]
+    H = w_grouped.shape[0] // 2
+    rows = x.numel() // Kd
+    if x.dtype != torch.float16 or w_grouped.dtype != torch.float16 or w_grouped.shape != (2 * H, Kd):
+        raise ValueError("linear_swiglu: need fp16 x [rows, K] and grouped fp16 w [2H, K]")
+    u = torch.empty(x.shape[:-1] + (H,), dtype=torch.float16, device=x.device)
+    call("bzpf_linear_swiglu", _p(x), _p(w_grouped), _p(u), rows, Kd, H, _stream())
+    return u
+
+
+def group_swiglu_rows(*ws: torch.Tensor) -> torch.Tensor:
+    """[W_0; W_1 (; W_2)] regrouped as blocks [W_0[32q:32q+32]; W_1[..] (; W_2[..])] per 32 output columns q (the
+    fused kernels' layout)."""
+    H, Kd = ws[0].shape
+    return torch.stack([w.view(H // 32, 32, Kd) for w in ws], 1).reshape(len(ws) * H, Kd).contiguous()
+
+
 def group_swiglu3_rows(wg: torch.Tensor, wx: torch.Tensor, wab: torch.Tensor) -> torch.Tensor:
-    """[Wg; Wx; Wab] regrouped as 96-row blocks [Wg[32q:32q+32]; Wx[..]; Wab[..]] (the fused kernel's layout)."""
-    H, Kd = wg.shape
-    return torch.stack([wg.view(H // 32, 32, Kd), wx.view(H // 32, 32, Kd), wab.view(H // 32, 32, Kd)], 1) \
-        .reshape(3 * H, Kd).contiguous()
+    return group_swiglu_rows(wg, wx, wab)
 
 
 def adaln(a: torch.Tensor, scale: torch.Tensor, shift: torch.Tensor, out_dtype, eps: float = 1e-5) -> torch.Tensor:

@@ -72,7 +72,15 @@ class Transition(torch.nn.Module):
         return K.transition(xn, w12, w3, z, accumulate, next_ln, pair_bias)
 
     def unfused(self, xn: torch.Tensor, out: Optional[torch.Tensor] = None, accumulate: bool = False):
-        """fc3(SwiGLU(xn fc12^T)) as separate kernels; accumulate adds into the fp32 `out`."""
+        """fc3(SwiGLU(xn fc12^T)) as row GEMMs (in fp16 the up-projection carries the SwiGLU product in its
+        epilogue); accumulate adds into the fp32 `out`."""
         w12, w3 = self.prepare()
-        a = K.swiglu(K.linear(xn, w12))
+        if xn.dtype == torch.float16 and xn.shape[-1] % 64 == 0 and self.hidden % 32 == 0:
+            hit = self.__dict__.get("_bzpf_w12g")
+            if hit is None or hit[0] is not w12:
+                hit = (w12, K.group_swiglu_rows(w12[:self.hidden], w12[self.hidden:]))
+                self.__dict__["_bzpf_w12g"] = hit
+            a = K.linear_swiglu(xn.contiguous(), hit[1])
+        else:
+            a = K.swiglu(K.linear(xn, w12))
         return K.linear(a, w3, out=out, out_dtype=torch.float32, accumulate=accumulate)

@@ -212,6 +212,12 @@ int bzpf_triattn_pack(const void* P, int trans, float q_scale, float bias_scale,
  * [rows, 3H] intermediate. */
 int bzpf_linear_swiglu3(const void* x, const void* w, void* u, int64_t rows, int K, int H, void* stream);
 
+/* The same for Transition's SwiGLU: u[r][c] = silu(x[r] . W1[c]) * (x[r] . W2[c]) with w fp16 [2H, K] in 64-row
+ * groups [W1[32 q .. 32 q + 31]; W2[same]] (W1 = fc1.weight, W2 = fc2.weight). Replaces fc1 / fc2 and the SwiGLU of
+ * Transition (boltz_mlx/layers/transition.py:27-92): bzpf_linear + bzpf_swiglu without the [rows, 2H]
+ * intermediate. */
+int bzpf_linear_swiglu(const void* x, const void* w, void* u, int64_t rows, int K, int H, void* stream);
+
 /* Outer-product-mean outer sum for MSA rows s < n_seq over tokens (fp32 ab [n_seq, N, ld_ab]: a = ab[.., 0:32],
  * b = ab[.., 32:64], unmasked; mask fp32 [n_seq, N]): for i_base <= i < i_base + n_i and j < N,
  *   out[(i - i_base) * N + j][c * 32 + d] = sum_s mask[s][i] mask[s][j] a[s][i][c] b[s][j][d] / max(count_ij, 1),

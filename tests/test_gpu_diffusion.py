@@ -313,3 +313,20 @@ def test_linear_swiglu3_fused(R, Kd, H):
     ref = OD.silu(h[:, :H]) * h[:, H:2 * H] * h[:, 2 * H:]
     assert O.metrics(fused.double().cpu().numpy(), ref)["max_rel"] <= 2e-3
     assert O.metrics(fused.double().cpu().numpy(), unfused.double().cpu().numpy())["max_rel"] <= 5e-3
+
+
+@pytest.mark.parametrize("R,Kd,H", [(70, 64, 32), (300, 384, 1536), (257, 64, 256)])
+def test_linear_swiglu_fused(R, Kd, H):
+    """The two-factor form (Transition's SwiGLU, 64-row weight groups) against float64 and the unfused kernels."""
+    from boltz_mlx_amd import kernels as K
+
+    rng = np.random.default_rng(R * 3 + H)
+    x = dev(rng.standard_normal((R, Kd)), torch.float16)
+    w = dev(rng.standard_normal((2 * H, Kd)) / np.sqrt(Kd), torch.float16)
+    fused = K.linear_swiglu(x, K.group_swiglu_rows(w[:H], w[H:]))
+    unfused = K.swiglu(K.linear(x, w))
+    torch.cuda.synchronize()
+    h = x.double().cpu().numpy() @ w.double().cpu().numpy().T
+    ref = OD.silu(h[:, :H]) * h[:, H:]
+    assert O.metrics(fused.double().cpu().numpy(), ref)["max_rel"] <= 2e-3
+    assert O.metrics(fused.double().cpu().numpy(), unfused.double().cpu().numpy())["max_rel"] <= 5e-3

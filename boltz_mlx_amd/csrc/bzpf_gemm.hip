@@ -1,8 +1,8 @@
-// fp16 row GEMM with fused epilogues for the linear layers of the s track and the diffusion transformer:
+// Row GEMM (fp16 or fp32 operands) with fused epilogues for the linear layers of the s track and the diffusion transformer:
 //   y[r][m] = x[r] . W[m] + bias[m]                     (epi 0: stored as fp16 or fp32)
 //   y[r][m] += x[r] . W[m] + bias[m]                    (epi 1: fp32 y)
 //   y[r][m] += sigmoid(gate[r % gate_rows][m]) * (..)   (epi 2: fp32 y, the diffusion transformer's gated residuals)
-// with x [R][K] and W [M][K] both K-contiguous (nn.Linear), K % 64 == 0.
+// with x [R][K] and W [M][K] both K-contiguous (nn.Linear), K a multiple of 128 bytes (64 fp16 / 32 fp32 elements).
 // Reference behaviour: the nn.Linear / lin16 calls these replace (boltz_mlx/kernels.py:1360-1370;
 // boltz_mlx/modules/transformersv2.py:199-264).
 //
@@ -19,17 +19,18 @@ namespace bzpf {
 
 namespace {
 
-template <int BM, int BR, typename TY>
-__global__ __launch_bounds__(256, 2) void gemm_nt_f16_k(const half_t* __restrict__ x, const half_t* __restrict__ w,
-                                                        const float* __restrict__ bias, TY* __restrict__ y, int64_t R,
-                                                        int K, int M, int epi, const float* __restrict__ gate,
-                                                        int64_t ld_gate, int64_t gate_rows) {
+template <int BM, int BR, typename TX, typename TY>
+__global__ __launch_bounds__(256, 2) void gemm_nt_k(const TX* __restrict__ x, const TX* __restrict__ w,
+                                                    const float* __restrict__ bias, TY* __restrict__ y, int64_t R,
+                                                    int K, int M, int epi, const float* __restrict__ gate,
+                                                    int64_t ld_gate, int64_t gate_rows) {
   static_assert((BM == 64 || BM == 128) && (BR == 64 || BR == 128), "64- or 128-row tiles");
-  constexpr int BK = 64, LDT = BK + 8;
+  constexpr int ES = sizeof(TX), VE = 16 / ES;  // element size, elements per 16-byte vector
+  constexpr int BK = 128 / ES, LDT = BK + VE;   // a stage is 128 bytes of each row (64 fp16 or 32 fp32 elements)
   constexpr int LA = BM / 32, LB = BR / 32;  // 16-byte vectors per thread per stage: rows of W, rows of x
   constexpr int MB = BM / 64, RB = BR / 64;  // 32 x 32 MFMA blocks per wave along m and r
-  __shared__ LDS_ALIGN half_t As[2][BM * LDT];  // rows of W (m)
-  __shared__ LDS_ALIGN half_t Bs[2][BR * LDT];  // rows of x (r)
+  __shared__ LDS_ALIGN TX As[2][BM * LDT];  // rows of W (m)
+  __shared__ LDS_ALIGN TX Bs[2][BR * LDT];  // rows of x (r)
   const int64_t r0 = (int64_t)blockIdx.x * BR;
   const int m0 = blockIdx.y * BM;
   const int t = threadIdx.x, wave = t >> 6, l = t & 63, rr = l & 31, hh = l >> 5;
@@ -39,21 +40,21 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_f16_k(const half_t* __restrict
   const int64_t xrows = R - r0 < BR ? R - r0 : BR;
   const int wrows = M - m0 < BM ? M - m0 : BM;
   const __amdgpu_buffer_rsrc_t xrs =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(x + r0 * K), 0, (int)(xrows * K * 2), RSRC_CFG);
+      __builtin_amdgcn_make_buffer_rsrc((void*)(x + r0 * K), 0, (int)(xrows * K * ES), RSRC_CFG);
   const __amdgpu_buffer_rsrc_t wrs =
-      __builtin_amdgcn_make_buffer_rsrc((void*)(w + (int64_t)m0 * K), 0, (int)((int64_t)wrows * K * 2), RSRC_CFG);
-  // staging: vector v of thread t is row 32 v + t / 8 of its operand's tile, k 8 (t % 8) .. + 7 of the stage
-  const int lrow = t >> 3, lcol = (t & 7) * 8;
+      __builtin_amdgcn_make_buffer_rsrc((void*)(w + (int64_t)m0 * K), 0, (int)((int64_t)wrows * K * ES), RSRC_CFG);
+  // staging: vector v of thread t is row 32 v + t / 8 of its operand's tile, 16 bytes at k VE (t % 8) of the stage
+  const int lrow = t >> 3, lcol = (t & 7) * VE;
   u32x4_t ra0[LA], rb0[LB], ra1[LA], rb1[LB];
   auto gload = [&](u32x4_t (&ra)[LA], u32x4_t (&rb)[LB], int stage) {
 #pragma unroll
     for (int v = 0; v < LA; v++) {
-      const int off = (int)(((int64_t)(32 * v + lrow) * K + stage * BK + lcol) * 2);
+      const int off = (int)(((int64_t)(32 * v + lrow) * K + stage * BK + lcol) * ES);
       ra[v] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(wrs, off, 0, 0));
     }
 #pragma unroll
     for (int v = 0; v < LB; v++) {
-      const int off = (int)(((int64_t)(32 * v + lrow) * K + stage * BK + lcol) * 2);
+      const int off = (int)(((int64_t)(32 * v + lrow) * K + stage * BK + lcol) * ES);
       rb[v] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(xrs, off, 0, 0));
     }
   };
@@ -70,22 +71,39 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_f16_k(const half_t* __restrict
     for (int rb = 0; rb < RB; rb++)
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[mb][rb][e] = 0.0f;
-  // MFMA step s of a stage: lane half hh takes k = 32 hh + 8 s .. + 7 of both operands (a permutation of the k sum)
+  // Lane half hh takes the contiguous half k = BK / 2 hh .. of each stage for both operands (a permutation of the
+  // k sum): fp16, MFMA step s takes k = 32 hh + 8 s .. + 7 (v_mfma_f32_32x32x16_f16); fp32, step 4 s + e takes
+  // k = 16 hh + 4 s + e (v_mfma_f32_32x32x2f32, one element per lane), read as one 16-byte vector per s.
   auto compute = [&](int buf) {
-    const half_t* Ab = As[buf] + (BM / 2 * wm + rr) * LDT + 32 * hh;
-    const half_t* Bb = Bs[buf] + (BR / 2 * wr + rr) * LDT + 32 * hh;
+    const TX* Ab = As[buf] + (BM / 2 * wm + rr) * LDT + BK / 2 * hh;
+    const TX* Bb = Bs[buf] + (BR / 2 * wr + rr) * LDT + BK / 2 * hh;
 #pragma unroll
     for (int s = 0; s < 4; s++) {
-      half8 fa[MB], fb[RB];
+      if constexpr (ES == 2) {
+        half8 fa[MB], fb[RB];
 #pragma unroll
-      for (int q = 0; q < MB; q++) fa[q] = *reinterpret_cast<const half8*>(Ab + 32 * q * LDT + 8 * s);
+        for (int q = 0; q < MB; q++) fa[q] = *reinterpret_cast<const half8*>(Ab + 32 * q * LDT + 8 * s);
 #pragma unroll
-      for (int q = 0; q < RB; q++) fb[q] = *reinterpret_cast<const half8*>(Bb + 32 * q * LDT + 8 * s);
+        for (int q = 0; q < RB; q++) fb[q] = *reinterpret_cast<const half8*>(Bb + 32 * q * LDT + 8 * s);
 #pragma unroll
-      for (int mb = 0; mb < MB; mb++)
+        for (int mb = 0; mb < MB; mb++)
 #pragma unroll
-        for (int rb = 0; rb < RB; rb++)
-          acc[mb][rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[mb], fb[rb], acc[mb][rb], 0, 0, 0);
+          for (int rb = 0; rb < RB; rb++)
+            acc[mb][rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[mb], fb[rb], acc[mb][rb], 0, 0, 0);
+      } else {
+        f4 fa[MB], fb[RB];
+#pragma unroll
+        for (int q = 0; q < MB; q++) fa[q] = *reinterpret_cast<const f4*>(Ab + 32 * q * LDT + 4 * s);
+#pragma unroll
+        for (int q = 0; q < RB; q++) fb[q] = *reinterpret_cast<const f4*>(Bb + 32 * q * LDT + 4 * s);
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+#pragma unroll
+          for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++)
+              acc[mb][rb] = __builtin_amdgcn_mfma_f32_32x32x2f32(fa[mb][e], fb[rb][e], acc[mb][rb], 0, 0, 0);
+      }
     }
   };
   const int nst = K / BK;
@@ -244,17 +262,17 @@ __global__ __launch_bounds__(256, 2) void gemm_swiglu_f16_k(const half_t* __rest
   }
 }
 
-template <int BM, int BR>
+template <int BM, int BR, typename TX>
 hipError_t gemm_t(const void* x, const void* w, const float* bias, void* y, int y_dt, int64_t R, int K, int M,
                   int epi, const float* gate, int64_t ld_gate, int64_t gate_rows, hipStream_t st) {
   const dim3 grid((unsigned)((R + BR - 1) / BR), (unsigned)((M + BM - 1) / BM));
   if (y_dt == DT_F16)
-    gemm_nt_f16_k<BM, BR, half_t><<<grid, 256, 0, st>>>(static_cast<const half_t*>(x), static_cast<const half_t*>(w),
-                                                        bias, static_cast<half_t*>(y), R, K, M, epi, gate, ld_gate,
+    gemm_nt_k<BM, BR, TX, half_t><<<grid, 256, 0, st>>>(static_cast<const TX*>(x), static_cast<const TX*>(w), bias,
+                                                        static_cast<half_t*>(y), R, K, M, epi, gate, ld_gate,
                                                         gate_rows);
   else
-    gemm_nt_f16_k<BM, BR, float><<<grid, 256, 0, st>>>(static_cast<const half_t*>(x), static_cast<const half_t*>(w),
-                                                       bias, static_cast<float*>(y), R, K, M, epi, gate, ld_gate,
+    gemm_nt_k<BM, BR, TX, float><<<grid, 256, 0, st>>>(static_cast<const TX*>(x), static_cast<const TX*>(w), bias,
+                                                       static_cast<float*>(y), R, K, M, epi, gate, ld_gate,
                                                        gate_rows);
   return hipGetLastError();
 }
@@ -287,23 +305,28 @@ hipError_t launch_gemm_swiglu_f16(const void* x, const void* w, void* u, int64_t
   return hipGetLastError();
 }
 
-bool gemm_nt_f16_ok(const void* x, const void* w, const float* bias, const void* y, int64_t R, int K, int M,
-                    const float* gate, int64_t ld_gate) {
+bool gemm_nt_ok(int x_dt, const void* x, const void* w, const float* bias, const void* y, int64_t R, int K, int M,
+                const float* gate, int64_t ld_gate) {
   const auto al = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; };
-  return K % 64 == 0 && M % 4 == 0 && R >= 1 && (int64_t)128 * K * 2 <= 0x7fffffffLL && al(x, 16) && al(w, 16) &&
-         al(y, 16) && (bias == nullptr || al(bias, 16)) && (gate == nullptr || (al(gate, 16) && ld_gate % 4 == 0));
+  const int es = x_dt == DT_F16 ? 2 : 4;
+  return K % (128 / es) == 0 && M % 4 == 0 && R >= 1 && (int64_t)128 * K * es <= 0x7fffffffLL && al(x, 16) &&
+         al(w, 16) && al(y, 16) && (bias == nullptr || al(bias, 16)) &&
+         (gate == nullptr || (al(gate, 16) && ld_gate % 4 == 0));
 }
 
-hipError_t launch_gemm_nt_f16(const void* x, const void* w, const float* bias, void* y, int y_dt, int64_t R, int K,
-                              int M, int epi, const float* gate, int64_t ld_gate, int64_t gate_rows, hipStream_t st) {
-  if (!gemm_nt_f16_ok(x, w, bias, y, R, K, M, gate, ld_gate) || epi < 0 || epi > 2 ||
-      (epi >= 1 && y_dt != DT_F32) || (epi == 2 && (gate == nullptr || gate_rows < 1)))
+hipError_t launch_gemm_nt(const void* x, const void* w, const float* bias, void* y, int x_dt, int y_dt, int64_t R,
+                          int K, int M, int epi, const float* gate, int64_t ld_gate, int64_t gate_rows,
+                          hipStream_t st) {
+  if ((x_dt != DT_F16 && x_dt != DT_F32) || !gemm_nt_ok(x_dt, x, w, bias, y, R, K, M, gate, ld_gate) || epi < 0 ||
+      epi > 2 || (epi >= 1 && y_dt != DT_F32) || (epi == 2 && (gate == nullptr || gate_rows < 1)))
     return hipErrorInvalidValue;
+  if (x_dt == DT_F32)  // fp32 operands: 64 x 64 tiles (the m track's 409,600-row projections)
+    return gemm_t<64, 64, float>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st);
   switch (gemm_tile_choice(R, M)) {
-    case 0: return gemm_t<128, 128>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st);
-    case 1: return gemm_t<128, 64>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st);
-    case 2: return gemm_t<64, 128>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st);
-    default: return gemm_t<64, 64>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st);
+    case 0: return gemm_t<128, 128, half_t>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st);
+    case 1: return gemm_t<128, 64, half_t>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st);
+    case 2: return gemm_t<64, 128, half_t>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st);
+    default: return gemm_t<64, 64, half_t>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st);
   }
 }
 

@@ -46,12 +46,13 @@ hipError_t launch_transition_pb(const void* xn, const void* w12, const void* w3,
 
 hipError_t launch_linear(const void* x, const void* w, const float* bias, void* y, int dt, int y_dt, int64_t rows,
                          int K, int M, int epi, hipStream_t st);
-// fp16 tiled MFMA GEMM (64- or 128-row tiles) behind launch_linear / launch_linear_gated when K % 64 == 0, M % 4 == 0 and the operands
-// are 16-byte aligned (gemm_nt_f16_ok)
-bool gemm_nt_f16_ok(const void* x, const void* w, const float* bias, const void* y, int64_t R, int K, int M,
-                    const float* gate, int64_t ld_gate);
-hipError_t launch_gemm_nt_f16(const void* x, const void* w, const float* bias, void* y, int y_dt, int64_t R, int K,
-                              int M, int epi, const float* gate, int64_t ld_gate, int64_t gate_rows, hipStream_t st);
+// Tiled MFMA GEMM (64- or 128-row tiles; fp16 or fp32 operands) behind launch_linear / launch_linear_gated when K
+// is a multiple of 128 bytes, M % 4 == 0 and the operands are 16-byte aligned (gemm_nt_ok)
+bool gemm_nt_ok(int x_dt, const void* x, const void* w, const float* bias, const void* y, int64_t R, int K, int M,
+                const float* gate, int64_t ld_gate);
+hipError_t launch_gemm_nt(const void* x, const void* w, const float* bias, void* y, int x_dt, int y_dt, int64_t R,
+                          int K, int M, int epi, const float* gate, int64_t ld_gate, int64_t gate_rows,
+                          hipStream_t st);
 hipError_t launch_gemm_swiglu_f16(const void* x, const void* w, void* u, int64_t R, int K, int H, int np,
                                   hipStream_t st);
 hipError_t launch_swiglu(const void* h, void* a, int dt, int64_t R, int H, hipStream_t st);

@@ -75,9 +75,9 @@ hipError_t launch_linear(const void* x, const void* w, const float* bias, void* 
                          int K, int M, int epi, hipStream_t st) {
   if (K % 8 || epi < 0 || epi > 1) return hipErrorInvalidValue;
   if (epi == 1 && y_dt != DT_F32) return hipErrorInvalidValue;
+  if (gemm_nt_ok(dt, x, w, bias, y, rows, K, M, nullptr, 0))
+    return launch_gemm_nt(x, w, bias, y, dt, y_dt, rows, K, M, epi, nullptr, 0, 1, st);
   if (dt == DT_F16) {
-    if (gemm_nt_f16_ok(x, w, bias, y, rows, K, M, nullptr, 0))
-      return launch_gemm_nt_f16(x, w, bias, y, y_dt, rows, K, M, epi, nullptr, 0, 1, st);
     return y_dt == DT_F16 ? linear_t<half_t, half_t>(x, w, bias, y, rows, K, M, epi, nullptr, 0, 1, st)
                           : linear_t<half_t, float>(x, w, bias, y, rows, K, M, epi, nullptr, 0, 1, st);
   }
@@ -88,8 +88,8 @@ hipError_t launch_linear(const void* x, const void* w, const float* bias, void* 
 hipError_t launch_linear_gated(const void* x, const void* w, const float* bias, const float* gate, int64_t ld_gate,
                                int64_t gate_rows, float* y, int dt, int64_t rows, int K, int M, hipStream_t st) {
   if (K % 8 || gate_rows < 1) return hipErrorInvalidValue;
-  if (dt == DT_F16 && gemm_nt_f16_ok(x, w, bias, y, rows, K, M, gate, ld_gate))
-    return launch_gemm_nt_f16(x, w, bias, y, DT_F32, rows, K, M, 2, gate, ld_gate, gate_rows, st);
+  if (gemm_nt_ok(dt, x, w, bias, y, rows, K, M, gate, ld_gate))
+    return launch_gemm_nt(x, w, bias, y, dt, DT_F32, rows, K, M, 2, gate, ld_gate, gate_rows, st);
   return dt == DT_F16 ? linear_t<half_t, float>(x, w, bias, y, rows, K, M, 2, gate, ld_gate, gate_rows, st)
                       : linear_t<float, float>(x, w, bias, y, rows, K, M, 2, gate, ld_gate, gate_rows, st);
 }

@@ -1,7 +1,8 @@
 // MSA-block pair kernels (fp32 operands and MFMA accumulation, the reference's numerics policy for the reductions
 // over MSA rows and tokens):
-//   opm_outer   : z[(i - i_base) N + j][c 32 + d] = sum_s mask[s][i] mask[s][j] a[s][i][c] b[s][j][d] / max(count, 1)
-//                 with count = sum_s mask[s][i] mask[s][j] and a | b = ab[s][i][0:32] | ab[s][j][32:64]
+//   opm_outer   : z[(i - i_base) N + j][c 32 + d] = sum_s mask[s][i] mask[s][j] a[s][i][c] b[s][j][d] / max(num, 1)
+//                 with num[i][j] = sum_s mask[s][i] mask[s][j] given (mask^T mask, one small GEMM) and
+//                 a | b = ab[s][i][0:32] | ab[s][j][32:64]
 //                 (OuterProductMean's outer sum, boltz_mlx/layers/outer_product_mean.py:37-45,
 //                 boltz_mlx/kernels_msa.py:292-343), stored fp16 (the proj_o GEMM's operand) or fp32;
 //   pwa_softmax : w[h][i][j] = softmax_j(logit[h][i][j] + (1 - pair_mask[i][j]) * -inf), rows padded with zeros
@@ -22,16 +23,14 @@ constexpr int MBK = 16;  // K (MSA rows s for the outer sum, tokens j for the av
 
 // ---------------------------------------------------------------- outer product mean
 // Workgroup tile: tokens i0 .. i0 + 3 (A rows (i, c)) x j0 .. j0 + 3 (B columns (j, d)). LDS holds each stage
-// K-major (As[s][i 32 + c]), the layout the loads arrive in, and the stage's mask values for the pair counts.
+// K-major (As[s][i 32 + c]), the layout the loads arrive in.
 template <typename TO>
 __global__ __launch_bounds__(256, 2) void opm_outer_k(const float* __restrict__ ab, int64_t ld_ab,
-                                                      const float* __restrict__ mask, TO* __restrict__ out, int S,
-                                                      int N, int i_base, int n_i) {
+                                                      const float* __restrict__ mask, const float* __restrict__ num,
+                                                      TO* __restrict__ out, int S, int N, int i_base, int n_i) {
   constexpr int LD = 128 + 16;
   __shared__ LDS_ALIGN float As[2][MBK * LD];
   __shared__ LDS_ALIGN float Bs[2][MBK * LD];
-  __shared__ float Ms[2][MBK][8];  // mask[s][i0 + 0..3], mask[s][j0 + 0..3]
-  __shared__ float Cs[16];
   const int t = threadIdx.x, wave = t >> 6, l = t & 63;
   const int wm = wave >> 1, wn = wave & 1;
   const int i0 = i_base + 4 * (int)blockIdx.y, j0 = 4 * (int)blockIdx.x;
@@ -57,10 +56,6 @@ __global__ __launch_bounds__(256, 2) void opm_outer_k(const float* __restrict__ 
       const int e = t + 256 * v, s = e >> 5, tk = (e >> 3) & 3, q = e & 7;
       *reinterpret_cast<f4*>(As[buf] + s * LD + 32 * tk + 4 * q) = ra[v] * ma[v];
       *reinterpret_cast<f4*>(Bs[buf] + s * LD + 32 * tk + 4 * q) = rb[v] * mb_[v];
-      if (q == 0) {
-        Ms[buf][s][tk] = ma[v];
-        Ms[buf][s][4 + tk] = mb_[v];
-      }
     }
   };
   f4 acc[4][4];
@@ -68,7 +63,6 @@ __global__ __launch_bounds__(256, 2) void opm_outer_k(const float* __restrict__ 
   for (int a = 0; a < 4; a++)
 #pragma unroll
     for (int b = 0; b < 4; b++) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
-  float cnt = 0.0f;  // thread t < 16: count of pair (i0 + t / 4, j0 + t % 4)
   auto compute = [&](int buf) {
     const float* Ab = As[buf] + (l >> 4) * LD + 64 * wm + (l & 15);
     const float* Bb = Bs[buf] + (l >> 4) * LD + 64 * wn + (l & 15);
@@ -84,10 +78,6 @@ __global__ __launch_bounds__(256, 2) void opm_outer_k(const float* __restrict__ 
 #pragma unroll
         for (int b = 0; b < 4; b++) acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[a], fb[b], acc[a][b], 0, 0, 0);
     }
-    if (t < 16) {
-#pragma unroll
-      for (int s = 0; s < MBK; s++) cnt += Ms[buf][s][t >> 2] * Ms[buf][s][4 + (t & 3)];
-    }
   };
   const int nst = (S + MBK - 1) / MBK;
   gload(0);
@@ -99,8 +89,6 @@ __global__ __launch_bounds__(256, 2) void opm_outer_k(const float* __restrict__ 
     if (st + 1 < nst) lstore((st + 1) & 1);
     __syncthreads();
   }
-  if (t < 16) Cs[t] = fmaxf(cnt, 1.0f);
-  __syncthreads();
   // block (a, b) of wave (wm, wn): rows 64 wm + 16 a + 4 (l / 16) + e = (token, c), columns 64 wn + 16 b + l % 16
 #pragma unroll
   for (int a = 0; a < 4; a++)
@@ -109,13 +97,13 @@ __global__ __launch_bounds__(256, 2) void opm_outer_k(const float* __restrict__ 
       const int ti = 2 * wm + (a >> 1), tj = 2 * wn + (b >> 1);
       const int i = i0 + ti, j = j0 + tj;
       if (i >= i_end || j >= N) continue;
-      const float num = Cs[4 * ti + tj];
+      const float cnt = fmaxf(num[(int64_t)i * N + j], 1.0f);
       const int d = 16 * (b & 1) + (l & 15);
       TO* op = out + ((int64_t)(i - i_base) * N + j) * 1024 + d;
 #pragma unroll
       for (int e = 0; e < 4; e++) {
         const int c = 16 * (a & 1) + 4 * (l >> 4) + e;
-        op[c * 32] = (TO)(acc[a][b][e] / num);
+        op[c * 32] = (TO)(acc[a][b][e] / cnt);
       }
     }
 }
@@ -232,16 +220,16 @@ __global__ __launch_bounds__(256, 2) void pwa_avg_k(const float* __restrict__ w,
 
 }  // namespace
 
-hipError_t launch_opm_outer(const float* ab, int64_t ld_ab, const float* mask, void* out, int out_dt, int S, int N,
-                            int i_base, int n_i, hipStream_t st) {
+hipError_t launch_opm_outer(const float* ab, int64_t ld_ab, const float* mask, const float* num, void* out,
+                            int out_dt, int S, int N, int i_base, int n_i, hipStream_t st) {
   const auto al = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; };
   if (S < 1 || N < 1 || i_base < 0 || n_i < 1 || i_base + n_i > N || ld_ab < 64 || ld_ab % 4 || !al(ab, 16))
     return hipErrorInvalidValue;
   const dim3 grid((unsigned)((N + 3) / 4), (unsigned)((n_i + 3) / 4));
   if (out_dt == DT_F16)
-    opm_outer_k<half_t><<<grid, 256, 0, st>>>(ab, ld_ab, mask, static_cast<half_t*>(out), S, N, i_base, n_i);
+    opm_outer_k<half_t><<<grid, 256, 0, st>>>(ab, ld_ab, mask, num, static_cast<half_t*>(out), S, N, i_base, n_i);
   else
-    opm_outer_k<float><<<grid, 256, 0, st>>>(ab, ld_ab, mask, static_cast<float*>(out), S, N, i_base, n_i);
+    opm_outer_k<float><<<grid, 256, 0, st>>>(ab, ld_ab, mask, num, static_cast<float*>(out), S, N, i_base, n_i);
   return hipGetLastError();
 }
 

@@ -508,8 +508,17 @@ def seq_attention_packed(qkvg, bias, mask, inf: float, H: int, out=None, multipl
     return out
 
 
+def opm_counts(mask: torch.Tensor) -> torch.Tensor:
+    """num = mask^T mask ([N, N] fp32: the pair counts sum_s mask_si mask_sj, exact integers) for mask fp32 [S, N],
+    as one fp32 GEMM over the transposed mask (MSA rows padded with zeros to a multiple of 32)."""
+    S, N = mask.shape
+    mt = torch.zeros((N, (S + 31) // 32 * 32), dtype=torch.float32, device=mask.device)
+    mt[:, :S] = mask.t()
+    return linear(mt, mt)
+
+
 def opm_outer(ab: torch.Tensor, mask: torch.Tensor, i_base: int = 0, n_i: int | None = None,
-              out_dtype=torch.float16) -> torch.Tensor:
+              out_dtype=torch.float16, num: torch.Tensor | None = None) -> torch.Tensor:
     """OuterProductMean's outer sum for one MSA: ab fp32 [S, N, 64] (LN(m) [W_a; W_b]^T, unmasked), mask fp32
     [S, N] -> [n_i * N, 1024] with row (i - i_base) * N + j and column c * 32 + d holding
     sum_s mask_si mask_sj a[s, i, c] b[s, j, d] / max(sum_s mask_si mask_sj, 1) (outer_product_mean.py:37-45)."""
@@ -519,8 +528,11 @@ def opm_outer(ab: torch.Tensor, mask: torch.Tensor, i_base: int = 0, n_i: int | 
     if ab.dtype != torch.float32 or C2 < 64 or not ab.is_contiguous() or mask.shape != (S, N) \
             or mask.dtype != torch.float32 or not mask.is_contiguous():
         raise ValueError("opm_outer: need contiguous fp32 ab [S, N, 64] and mask [S, N]")
+    num = opm_counts(mask) if num is None else num
+    if num.shape != (N, N) or num.dtype != torch.float32 or not num.is_contiguous():
+        raise ValueError("opm_outer: num must be the contiguous fp32 [N, N] pair counts")
     out = torch.empty((n_i * N, 1024), dtype=out_dtype, device=ab.device)
-    call("bzpf_opm_outer", _p(ab), C2, _p(mask), _p(out), _dt(out), S, N, int(i_base), int(n_i), _stream())
+    call("bzpf_opm_outer", _p(ab), C2, _p(mask), _p(num), _p(out), _dt(out), S, N, int(i_base), int(n_i), _stream())
     return out
 
 

@@ -220,12 +220,13 @@ int bzpf_linear_swiglu(const void* x, const void* w, void* u, int64_t rows, int 
 
 /* Outer-product-mean outer sum for MSA rows s < n_seq over tokens (fp32 ab [n_seq, N, ld_ab]: a = ab[.., 0:32],
  * b = ab[.., 32:64], unmasked; mask fp32 [n_seq, N]): for i_base <= i < i_base + n_i and j < N,
- *   out[(i - i_base) * N + j][c * 32 + d] = sum_s mask[s][i] mask[s][j] a[s][i][c] b[s][j][d] / max(count_ij, 1),
- * count_ij = sum_s mask[s][i] mask[s][j]; out fp16 or fp32 [n_i * N, 1024] (fp32 MFMA accumulation). Replaces
+ *   out[(i - i_base) * N + j][c * 32 + d] = sum_s mask[s][i] mask[s][j] a[s][i][c] b[s][j][d] / max(num[i][j], 1),
+ * num fp32 [N, N] = mask^T mask (the pair counts; one bzpf_linear of the transposed mask with itself, as the
+ * reference's num input); out fp16 or fp32 [n_i * N, 1024] (fp32 MFMA accumulation). Replaces
  * kernels_msa.opm_outer and the module path's outer sum (boltz_mlx/kernels_msa.py:292-343,
  * boltz_mlx/layers/outer_product_mean.py:37-45). */
-int bzpf_opm_outer(const float* ab, int64_t ld_ab, const float* mask, void* out, int out_dt, int n_seq, int N,
-                   int i_base, int n_i, void* stream);
+int bzpf_opm_outer(const float* ab, int64_t ld_ab, const float* mask, const float* num, void* out, int out_dt,
+                   int n_seq, int N, int i_base, int n_i, void* stream);
 
 /* Pair-weighted-averaging weights: w[h][i][j] = softmax_j(logits[h][i][j] + (1 - pair_mask[i][j]) * -inf) for
  * logits fp32 [H, N, N], pair_mask fp32 [N, N]; w fp32 [H, N, ldw] with zeros for N <= j < ldw (ldw a multiple of

@@ -247,13 +247,14 @@ def test_seq_attention_mfma_vs_valu(hd, N, all_masked):
     assert m2["max_rel"] <= 1e-2, m2
 
 
-@pytest.mark.parametrize("dt", [torch.float16, torch.float32])
-def test_seq_attention_batched_samples(dt):
+@pytest.mark.parametrize("dt,N", [(torch.float16, 68), (torch.float32, 68), (torch.float16, 67)])
+def test_seq_attention_batched_samples(dt, N):
     """All samples in one launch (sample groups of `multiplicity` sharing a bias, a mask row each) equal one call per
-    sample: the MFMA kernel in fp16 (one grid over the samples), the VALU kernel in fp32 (one launch per sample)."""
+    sample: the MFMA kernel in fp16 (one grid over the samples), the VALU kernel in fp32 and for N % 4 != 0 (one
+    launch per sample)."""
     from boltz_mlx_amd import kernels as K
 
-    S, mult, N, H, hd = 6, 3, 68, 4, 48
+    S, mult, H, hd = 6, 3, 4, 48
     rng = np.random.default_rng(11)
     qkvg = dev(rng.standard_normal((S, N, 4 * H * hd)), dt)
     bias = dev(2 * rng.standard_normal((S // mult, H, N, N)), dt)

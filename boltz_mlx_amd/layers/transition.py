@@ -17,6 +17,9 @@ from boltz_mlx_amd import kernels as K
 from boltz_mlx_amd.layers.norm import LayerNorm
 
 
+FUSED_MIN_ROWS = 16384  # rows from which the fp16 up-projection carries the SwiGLU product (bzpf_linear_swiglu)
+
+
 class Transition(torch.nn.Module):
     def __init__(self, dim: int = 128, hidden: int = 512, out_dim: Optional[int] = None) -> None:
         super().__init__()
@@ -75,7 +78,10 @@ class Transition(torch.nn.Module):
         """fc3(SwiGLU(xn fc12^T)) as row GEMMs (in fp16 the up-projection carries the SwiGLU product in its
         epilogue); accumulate adds into the fp32 `out`."""
         w12, w3 = self.prepare()
-        if xn.dtype == torch.float16 and xn.shape[-1] % 64 == 0 and self.hidden % 32 == 0:
+        # fused for the large row counts (MSA rows x tokens, pairs); the s track's N rows run on a side stream next
+        # to the triangle core, where the separate small kernels find free slots more easily
+        if xn.dtype == torch.float16 and xn.shape[-1] % 64 == 0 and self.hidden % 32 == 0 \
+                and xn.numel() // xn.shape[-1] >= FUSED_MIN_ROWS:
             hit = self.__dict__.get("_bzpf_w12g")
             if hit is None or hit[0] is not w12:
                 hit = (w12, K.group_swiglu_rows(w12[:self.hidden], w12[self.hidden:]))

@@ -9,8 +9,8 @@
 // - q, k, v, g are rows of pitch ld_in (the fused q|k|v|g projection), the bias a plain [H][N][N] array and the key
 //   mask one fp32 row [N]; grid.y runs over samples (row sets s_in elements apart, mask rows s_mask, output rows
 //   s_out), consecutive groups of mult samples sharing one bias (s_bias apart), as the diffusion samples do;
-// - a workgroup owns (head h, 128 queries), 4 waves of 32 queries; S^T = K Q^T + Cinit over HD / 16 MFMA steps per
-//   32-key tile (Q pre-scaled by log2(e)/sqrt(HD) in the fragments, so logits are base 2), with the accumulator
+// - a workgroup owns (head h, 32 NW queries), NW = 4 waves of 32 queries (2 when the grid is small); S^T = K Q^T
+//   + Cinit over HD / 16 MFMA steps per 32-key tile (Q pre-scaled by log2(e)/sqrt(HD) in the fragments, so logits are base 2), with the accumulator
 //   initialised to bias * log2(e) - m (one v_fma_mix_f32 per element from the fp16 bias) plus the key-mask bias in
 //   blocks that mask a key;
 // - O^T = V^T P^T in 32-channel tiles (ceil(HD / 32) of them; the rows past HD of a partial tile read unused LDS
@@ -51,8 +51,8 @@ __device__ __forceinline__ float halves_sum(float v) {
   return __uint_as_float(a[0]) + __uint_as_float(a[1]);
 }
 
-template <int HD>
-__global__ __launch_bounds__(256, 2) void seq_attn_mfma(const half_t* __restrict__ q, const half_t* __restrict__ k,
+template <int HD, int NW>
+__global__ __launch_bounds__(64 * NW, 2) void seq_attn_mfma(const half_t* __restrict__ q, const half_t* __restrict__ k,
                                                         const half_t* __restrict__ v, const half_t* __restrict__ g,
                                                         int64_t ld_in, const half_t* __restrict__ bias,
                                                         const float* __restrict__ mask, float inf,
@@ -61,14 +61,15 @@ __global__ __launch_bounds__(256, 2) void seq_attn_mfma(const half_t* __restrict
                                                         int64_t s_out) {
   static_assert((HD % 16 == 0 || HD == 24) && HD >= 16 && HD <= 64, "head width 16, 24, 32, 48 or 64");
   constexpr int BK = 64;                   // keys per LDS stage
-  constexpr int WQ = 128;                  // queries per workgroup
+  constexpr int NTH = 64 * NW;             // threads: NW waves of 32 queries
+  constexpr int WQ = 32 * NW;              // queries per workgroup
   constexpr int KS = (HD + 15) / 16;       // QK MFMA steps per 32-key tile (24 runs as 32 with zero dims 24..31)
   constexpr int NT = (HD + 31) / 32;       // 32-channel output tiles
   constexpr int LDK = 16 * KS + 8;         // Ks row pitch (halves)
   constexpr int LDV = BK + 8;              // Vs row pitch (halves)
   constexpr int VPR = HD / 8;              // 16-byte vectors per K / V row
   constexpr int NSTAGE = 2 * BK * VPR;     // staged vectors per block (K then V), a multiple of 64
-  constexpr int NV = (NSTAGE + 255) / 256;  // per thread
+  constexpr int NV = (NSTAGE + NTH - 1) / NTH;  // per thread
   constexpr float LOG2E = 1.4426950408889634f;
   constexpr float PLIM = 32768.0f;
   // K and V^T tiles double-buffered: block kb is written to buffer kb & 1 before the one barrier of iteration kb,
@@ -107,7 +108,7 @@ __global__ __launch_bounds__(256, 2) void seq_attn_mfma(const half_t* __restrict
   bool any_key = __syncthreads_or(l < N && mask[l] != 0.0f) != 0;
   if (!any_key) {
     int found = 0;
-    for (int kk = 64 + t; kk < N; kk += 256) found |= (mask[kk] != 0.0f);
+    for (int kk = 64 + t; kk < N; kk += NTH) found |= (mask[kk] != 0.0f);
     any_key = __syncthreads_or(found) != 0;
   }
 
@@ -149,14 +150,14 @@ __global__ __launch_bounds__(256, 2) void seq_attn_mfma(const half_t* __restrict
   half8 sreg[NV];
   half4 bcur[2][4];  // bias of keys 32 kt + 8 gq + 4 hl + e: accumulator elements 4 gq + e of tile kt
   float mraw;
-  // staged vector n of thread t: index e = t + 256 n; e < BK * VPR is K row e / VPR, else V row (e - BK VPR) / VPR
+  // staged vector n of thread t: index e = t + NTH n; e < BK * VPR is K row e / VPR, else V row (e - BK VPR) / VPR
   // The block offset is added to the lane (VGPR) offset, which the buffer range check covers, so keys past N
   // (and the bias of the last query row past its N keys) read as zeros rather than past the allocations.
   auto prefetch = [&](int kb) {
     const int blk = (int)((int64_t)kb * BK * ld_in * 2);
 #pragma unroll
     for (int n = 0; n < NV; n++) {
-      const int e = t + 256 * n;
+      const int e = t + NTH * n;
       if (e >= NSTAGE) break;  // wave-uniform
       const bool isk = e < BK * VPR;
       const int ee = isk ? e : e - BK * VPR;
@@ -175,7 +176,7 @@ __global__ __launch_bounds__(256, 2) void seq_attn_mfma(const half_t* __restrict
             half4, __builtin_amdgcn_raw_buffer_load_b64(brs, bo + (32 * kt + 8 * gq) * 2, 0, 0));
   };
   if constexpr (16 * KS > HD) {  // K dims HD .. 16 KS - 1 meet zero Q dims: keep them finite (zero) in both buffers
-    for (int r = t; r < 2 * BK; r += 256)
+    for (int r = t; r < 2 * BK; r += NTH)
       *reinterpret_cast<half8*>(Ks[r / BK] + (r % BK) * LDK + HD) = half8{0, 0, 0, 0, 0, 0, 0, 0};
   }
   prefetch(0);
@@ -189,7 +190,7 @@ __global__ __launch_bounds__(256, 2) void seq_attn_mfma(const half_t* __restrict
     half_t* Vb = Vs[buf];
 #pragma unroll
     for (int n = 0; n < NV; n++) {
-      const int e = t + 256 * n;
+      const int e = t + NTH * n;
       if (e >= NSTAGE) break;  // wave-uniform
       if (e < BK * VPR) {  // wave-uniform: BK * VPR is a multiple of 64
         *reinterpret_cast<half8*>(Kb + (e / VPR) * LDK + (e % VPR) * 8) = sreg[n];
@@ -319,12 +320,24 @@ hipError_t launch_seq_attention_f16_mfma(const void* q, const void* k, const voi
   if (N < 1 || N > 32767 || N % 4 || ld_in % 8 || ld_out % 4 || (N + 64) * ld_in * 2 > 0x7fffffffLL ||
       N * N * 2 > 0x7fffffffLL || S < 1 || S > 65535 || mult < 1)
     return hipErrorInvalidValue;
-  const dim3 grid((unsigned)(((N + 127) / 128) * H), (unsigned)S);
+  // 64-query workgroups (2 waves) when 128-query ones would not give two per CU: more of them per CU hide each
+  // key block's load latency, and the last query block of a sequence wastes fewer lanes
+  const bool small = ((N + 127) / 128) * H * (int64_t)S < 512;
+  const int wq = small ? 64 : 128;
+  const dim3 grid((unsigned)(((N + wq - 1) / wq) * H), (unsigned)S);
 #define BZ_SEQ_MFMA(HDV)                                                                                          \
-  seq_attn_mfma<HDV><<<grid, 256, 0, st>>>(static_cast<const half_t*>(q), static_cast<const half_t*>(k),         \
-                                           static_cast<const half_t*>(v), static_cast<const half_t*>(g), ld_in,  \
-                                           static_cast<const half_t*>(bias), mask, inf, static_cast<half_t*>(out), \
-                                           ld_out, (int)N, H, s_in, s_bias, mult, s_mask, s_out)
+  if (small)                                                                                                     \
+    seq_attn_mfma<HDV, 2><<<grid, 128, 0, st>>>(static_cast<const half_t*>(q), static_cast<const half_t*>(k),    \
+                                                static_cast<const half_t*>(v), static_cast<const half_t*>(g), ld_in, \
+                                                static_cast<const half_t*>(bias), mask, inf,                     \
+                                                static_cast<half_t*>(out), ld_out, (int)N, H, s_in, s_bias, mult, \
+                                                s_mask, s_out);                                                  \
+  else                                                                                                           \
+    seq_attn_mfma<HDV, 4><<<grid, 256, 0, st>>>(static_cast<const half_t*>(q), static_cast<const half_t*>(k),    \
+                                                static_cast<const half_t*>(v), static_cast<const half_t*>(g), ld_in, \
+                                                static_cast<const half_t*>(bias), mask, inf,                     \
+                                                static_cast<half_t*>(out), ld_out, (int)N, H, s_in, s_bias, mult, \
+                                                s_mask, s_out)
   switch (hd) {
     case 16: BZ_SEQ_MFMA(16); break;
     case 24: BZ_SEQ_MFMA(24); break;

@@ -331,3 +331,22 @@ def test_linear_swiglu_fused(R, Kd, H):
     ref = OD.silu(h[:, :H]) * h[:, H:]
     assert O.metrics(fused.double().cpu().numpy(), ref)["max_rel"] <= 2e-3
     assert O.metrics(fused.double().cpu().numpy(), unfused.double().cpu().numpy())["max_rel"] <= 5e-3
+
+
+def test_seq_attention_wave_count_variants_agree():
+    """A grid of 512+ 128-query blocks runs 4-wave workgroups, a smaller one 2-wave workgroups; a query's result does
+    not depend on how many query tiles share its workgroup: 32 samples in one call equal 32 single-sample calls
+    bit for bit."""
+    from boltz_mlx_amd import kernels as K
+
+    S, mult, N, H, hd = 32, 4, 200, 8, 32
+    rng = np.random.default_rng(31)
+    qkvg = dev(rng.standard_normal((S, N, 4 * H * hd)), torch.float16)
+    bias = dev(rng.standard_normal((S // mult, H, N, N)), torch.float16)
+    mask = np.ones((S, N), np.float32)
+    mask[:, -9:] = 0
+    mg = dev(mask)
+    batched = K.seq_attention_packed(qkvg, bias, mg, 1e6, H, multiplicity=mult)
+    single = torch.stack([K.seq_attention_packed(qkvg[i], bias[i // mult], mg[i], 1e6, H) for i in range(S)])
+    torch.cuda.synchronize()
+    assert torch.equal(batched, single)

@@ -20,6 +20,8 @@
 //   AttentionPairBias inf of 1e6 the reference's fp32 logits keep their differences, unlike the triangle
 //   attention's 1e9, which rounds them all to one value).
 // Each lane's bias for a 64-key block is eight 8-byte loads (4 consecutive keys each) from its query's row.
+#include <type_traits>
+
 #include "bzpf_common.h"
 #include "bzpf_kernels.h"
 
@@ -147,13 +149,17 @@ __global__ __launch_bounds__(64 * NW, 2) void seq_attn_mfma(const half_t* __rest
                                                                        RSRC_CFG);
   const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc((void*)mask, 0, N * 4, RSRC_CFG);
   const int boff = (jc * N + 4 * hl) * 2, mvo = l * 4;
-  half8 sreg[NV];
-  half4 bcur[2][4];  // bias of keys 32 kt + 8 gq + 4 hl + e: accumulator elements 4 gq + e of tile kt
-  float mraw;
+  // PF register sets: block kb is loaded PF blocks ahead into set kb % PF (two for 4-wave workgroups, whose VGPR
+  // budget holds a second set; one for 2-wave workgroups, which stage twice the vectors per thread)
+  constexpr int PF = NW == 4 ? 2 : 1;
+  half8 sreg[PF][NV];
+  half4 bcur[PF][2][4];  // bias of keys 32 kt + 8 gq + 4 hl + e: accumulator elements 4 gq + e of tile kt
+  float mraw[PF];
   // staged vector n of thread t: index e = t + NTH n; e < BK * VPR is K row e / VPR, else V row (e - BK VPR) / VPR
   // The block offset is added to the lane (VGPR) offset, which the buffer range check covers, so keys past N
   // (and the bias of the last query row past its N keys) read as zeros rather than past the allocations.
-  auto prefetch = [&](int kb) {
+  auto prefetch = [&](auto si, int kb) {
+    constexpr int SI = decltype(si)::value;
     const int blk = (int)((int64_t)kb * BK * ld_in * 2);
 #pragma unroll
     for (int n = 0; n < NV; n++) {
@@ -162,29 +168,39 @@ __global__ __launch_bounds__(64 * NW, 2) void seq_attn_mfma(const half_t* __rest
       const bool isk = e < BK * VPR;
       const int ee = isk ? e : e - BK * VPR;
       const int off = (int)(((int64_t)(ee / VPR) * ld_in + (ee % VPR) * 8) * 2);
-      sreg[n] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(isk ? krs : vrs, off + blk, 0, 0));
+      sreg[SI][n] =
+          __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(isk ? krs : vrs, off + blk, 0, 0));
     }
-    mraw = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(mrs, mvo + kb * BK * 4, 0, 0));
+    mraw[SI] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(mrs, mvo + kb * BK * 4, 0, 0));
   };
-  auto prefetch_bias = [&](int kb) {
+  auto prefetch_bias = [&](auto si, int kb) {
+    constexpr int SI = decltype(si)::value;
     const int bo = boff + kb * BK * 2;
 #pragma unroll
     for (int kt = 0; kt < 2; kt++)
 #pragma unroll
       for (int gq = 0; gq < 4; gq++)
-        bcur[kt][gq] = __builtin_bit_cast(
+        bcur[SI][kt][gq] = __builtin_bit_cast(
             half4, __builtin_amdgcn_raw_buffer_load_b64(brs, bo + (32 * kt + 8 * gq) * 2, 0, 0));
   };
   if constexpr (16 * KS > HD) {  // K dims HD .. 16 KS - 1 meet zero Q dims: keep them finite (zero) in both buffers
     for (int r = t; r < 2 * BK; r += NTH)
       *reinterpret_cast<half8*>(Ks[r / BK] + (r % BK) * LDK + HD) = half8{0, 0, 0, 0, 0, 0, 0, 0};
   }
-  prefetch(0);
+  prefetch(std::integral_constant<int, 0>{}, 0);
   __builtin_amdgcn_sched_barrier(0);
-  prefetch_bias(0);
+  prefetch_bias(std::integral_constant<int, 0>{}, 0);
   __builtin_amdgcn_sched_barrier(0);
+  if constexpr (PF == 2) {
+    prefetch(std::integral_constant<int, 1>{}, nblk > 1 ? 1 : 0);
+    __builtin_amdgcn_sched_barrier(0);
+    prefetch_bias(std::integral_constant<int, 1>{}, nblk > 1 ? 1 : 0);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 
-  for (int kb = 0; kb < nblk; kb++) {
+  // one key block: stage set kb % PF into LDS buffer kb & 1, load block kb + PF into that set, compute
+  auto block = [&](auto si, int kb) {
+    constexpr int SI = decltype(si)::value;
     const int k0 = kb * BK, buf = kb & 1;
     half_t* Kb = Ks[buf];
     half_t* Vb = Vs[buf];
@@ -193,18 +209,18 @@ __global__ __launch_bounds__(64 * NW, 2) void seq_attn_mfma(const half_t* __rest
       const int e = t + NTH * n;
       if (e >= NSTAGE) break;  // wave-uniform
       if (e < BK * VPR) {  // wave-uniform: BK * VPR is a multiple of 64
-        *reinterpret_cast<half8*>(Kb + (e / VPR) * LDK + (e % VPR) * 8) = sreg[n];
+        *reinterpret_cast<half8*>(Kb + (e / VPR) * LDK + (e % VPR) * 8) = sreg[SI][n];
       } else {
         const int ee = e - BK * VPR, key = ee / VPR, c0 = (ee % VPR) * 8;
 #pragma unroll
-        for (int u = 0; u < 8; u++) Vb[(c0 + u) * LDV + key] = sreg[n][u];
+        for (int u = 0; u < 8; u++) Vb[(c0 + u) * LDV + key] = sreg[SI][n][u];
       }
     }
-    const float mbias = k0 + l < N ? (any_key ? fmaf(mraw, infl, -infl) : 0.0f) : -INFINITY;
+    const float mbias = k0 + l < N ? (any_key ? fmaf(mraw[SI], infl, -infl) : 0.0f) : -INFINITY;
     const bool masked = __any(mbias != 0.0f);
     if (masked) Mb[wave][l] = mbias;
     __syncthreads();
-    prefetch(kb + 1 < nblk ? kb + 1 : nblk - 1);
+    prefetch(si, kb + PF < nblk ? kb + PF : nblk - 1);
 
     f16x s[2];
 #pragma unroll
@@ -215,12 +231,12 @@ __global__ __launch_bounds__(64 * NW, 2) void seq_attn_mfma(const half_t* __rest
         for (int gq = 0; gq < 4; gq++) {
           const f4 mbv = *reinterpret_cast<const f4*>(&Mb[wave][32 * kt + 8 * gq + 4 * hl]);
 #pragma unroll
-          for (int e = 0; e < 4; e++) c[4 * gq + e] = ((float)bcur[kt][gq][e] * LOG2E + mbv[e]) - mref;
+          for (int e = 0; e < 4; e++) c[4 * gq + e] = ((float)bcur[SI][kt][gq][e] * LOG2E + mbv[e]) - mref;
         }
       } else {
 #pragma unroll
         for (int gq = 0; gq < 4; gq++) {
-          const uint2 bw = __builtin_bit_cast(uint2, bcur[kt][gq]);
+          const uint2 bw = __builtin_bit_cast(uint2, bcur[SI][kt][gq]);
           c[4 * gq + 0] = half_fma<0>(bw.x, log2e, -mref);
           c[4 * gq + 1] = half_fma<1>(bw.x, log2e, -mref);
           c[4 * gq + 2] = half_fma<0>(bw.y, log2e, -mref);
@@ -234,7 +250,7 @@ __global__ __launch_bounds__(64 * NW, 2) void seq_attn_mfma(const half_t* __rest
       }
       s[kt] = c;
     }
-    prefetch_bias(kb + 1 < nblk ? kb + 1 : nblk - 1);
+    prefetch_bias(si, kb + PF < nblk ? kb + PF : nblk - 1);
     float sref = mref;
 #pragma unroll
     for (int kt = 0; kt < 2; kt++) {
@@ -289,6 +305,12 @@ __global__ __launch_bounds__(64 * NW, 2) void seq_attn_mfma(const half_t* __rest
           oacc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[sl], oacc[tt], 0, 0, 0);
         }
       }
+    }
+    };
+  for (int kb = 0; kb < nblk; kb += PF) {
+    block(std::integral_constant<int, 0>{}, kb);
+    if constexpr (PF == 2) {
+      if (kb + 1 < nblk) block(std::integral_constant<int, 1>{}, kb + 1);
     }
   }
   // oacc[tt][4 qq + e] = O^T[channel 32 tt + 8 qq + 4 hl + e][query qi]

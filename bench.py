@@ -8,7 +8,8 @@ full trunk pass. Inputs and weights are resident in HBM before the timed region.
 
 Prints one JSON line. `roofline` is for the kernel with the largest share of the timed region, from HIP events
 recorded around every launch on the launch stream; `cpu_baseline` times the numpy oracle (reference-equivalent
-fp32 CPU path) on one block at N=400 and scales it to N=1000 by the FLOP ratio.
+fp32 CPU path) on the N=128 block, N=400 triangle attention and N=800 triangle multiplication configurations and
+estimates one N=1000 block from row samples and FLOP ratios (see cpu_baseline).
 """
 
 from __future__ import annotations
@@ -201,7 +202,44 @@ def msa_layer_leg(steps: int, device, N: int = 400, S: int = 1024) -> dict:
             "finite": bool(torch.isfinite(zo).all().item() and torch.isfinite(mo).all().item())}
 
 
-def cpu_baseline(N_sample: int = 400, N_target: int = 1000) -> dict:
+def _median_time(fn, reps: int, budget_s: float):
+    """1 warm-up call, then up to `reps` timed calls (fewer when the warm-up shows they would exceed budget_s;
+    at least 1); returns (median seconds, timed calls)."""
+    import statistics
+
+    t0 = time.perf_counter()
+    fn()
+    warm = time.perf_counter() - t0
+    n = max(1, min(reps, int(budget_s / max(warm, 1e-9))))
+    ts = []
+    for _ in range(n):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return statistics.median(ts), n
+
+
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(budget_s: float = 25.0) -> dict:
+    """The numpy float32 oracle (reference-equivalent fp32 CPU path) on the host cores: each configuration gets
+    1 warm-up and the median of up to 5 timed runs (fewer if 5 would exceed budget_s), on the BLAS thread pool the
+    environment gives (OMP_NUM_THREADS; numpy's elementwise work is single-threaded).
+      C1: one PairformerLayer, N = 128;  C2: triangle attention N = 400 (last 40 padded), starting + ending node;
+      C3: triangle multiplication N = 800, outgoing + incoming.
+    value: blocks/s at N = 1000 (ESTIMATE): triangle attention from a row sample at N = 1000 (rows are independent:
+    fixed + per-row cost from two sample sizes, times 1000 rows, both nodes), triangle multiplication from C3 scaled
+    by its module FLOP ratio 800 -> 1000, the pair transition from a 10^5-row sample (row-wise, times 10), and the s
+    track (pre-norm, AttentionPairBias with the pair bias from z, transition_s) timed at N = 1000."""
     import numpy as np
 
     import oracle as O
@@ -213,20 +251,67 @@ def cpu_baseline(N_sample: int = 400, N_target: int = 1000) -> dict:
         threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
     except Exception:  # threadpoolctl absent: report the visible cores
         threads = os.cpu_count()
+    f32 = np.float32
     p = synthetic_state(PairformerLayer(384, 128, 16), seed=0)
     rng = np.random.default_rng(1)
-    z = rng.standard_normal((1, N_sample, N_sample, 128), dtype=np.float32)
-    s = rng.standard_normal((1, N_sample, 384), dtype=np.float32)
-    tok = np.ones((1, N_sample), np.float32)
-    tok[:, N_sample - int(round(0.05 * N_sample)):] = 0
-    pm = tok[:, :, None] * tok[:, None, :]
+
+    def inputs(N, n_pad):
+        z = rng.standard_normal((1, N, N, 128), dtype=f32)
+        tok = np.ones((1, N), f32)
+        if n_pad:
+            tok[:, N - n_pad:] = 0
+        return z, tok, tok[:, :, None] * tok[:, None, :]
+
+    cfg = {}
+    z, tok, pm = inputs(128, 0)
+    s = rng.standard_normal((1, 128, 384), dtype=f32)
+    t, n = _median_time(lambda: O.pairformer_layer(s, z, tok, pm, p, 16), 5, budget_s)
+    cfg["C1_block_N128_fp32"] = {"s": round(t, 4), "runs": n}
+    z, tok, pm = inputs(400, 40)
+    pa, pe = O.sub(p, "tri_att_start"), O.sub(p, "tri_att_end")
+    t, n = _median_time(lambda: (O.tri_att(z, pm, pa, True), O.tri_att(z, pm, pe, False)), 5, budget_s)
+    cfg["C2_tri_att_N400_start_end"] = {"s": round(t, 4), "runs": n}
+    z, tok, pm = inputs(800, 0)
+    po, pi = O.sub(p, "tri_mul_out"), O.sub(p, "tri_mul_in")
+    t_c3, n = _median_time(lambda: (O.tri_mul(z, pm, po, True), O.tri_mul(z, pm, pi, False)), 5, budget_s)
+    cfg["C3_tri_mul_N800_out_in"] = {"s": round(t_c3, 4), "runs": n}
+    del z, tok, pm
+    # C4 estimate at N = 1000
+    N = 1000
+    z, tok, pm = inputs(N, 50)
+    r1, r2 = 8, 24
+    t1 = min(_time_once(lambda: O.tri_att(z, pm, pa, True, row_chunk=8, rows=r1)) for _ in range(2))
+    t2 = min(_time_once(lambda: O.tri_att(z, pm, pa, True, row_chunk=8, rows=r2)) for _ in range(2))
+    per_row = max(t2 - t1, 0.0) / (r2 - r1)
+    t_att = 2 * (max(t1 - r1 * per_row, 0.0) + N * per_row)
+    fl = lambda n: 256.0 * n ** 3 + 196608.0 * n ** 2  # noqa: E731  (module FLOP per direction)
+    t_mul = t_c3 * fl(N) / fl(800)
+    rows = 100_000
+    xr = z.reshape(-1, 128)[:rows]
+    t_tr = min(_time_once(lambda: O.transition(xr, O.sub(p, "transition_z"))) for _ in range(2)) * (N * N / rows)
+    s = rng.standard_normal((1, N, 384), dtype=f32)
+
+    def s_track():
+        s_n = O.layer_norm(s, p["pre_norm_s.weight"], p["pre_norm_s.bias"])
+        s1 = s + O.attention_pair_bias(s_n, z, tok, s_n, O.sub(p, "attention"), 16)
+        return s1 + O.transition(s1, O.sub(p, "transition_s"))
+
+    t_s = _time_once(s_track)
+    t_block = t_att + t_mul + t_tr + t_s
+    return {"value": round(1.0 / t_block, 6), "unit": "blocks/s", "cores": int(threads), "kind": "port",
+            "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(),
+            "sample": (f"numpy float32 oracle, {threads} BLAS threads; configs (1 warm-up + median): "
+                       + ", ".join(f"{k} {v['s']} s (median of {v['runs']})" for k, v in cfg.items())
+                       + f"; value = ESTIMATE of one N=1000 block ({t_block:.1f} s): tri-att {t_att:.1f} s "
+                         f"(rows {r1}/{r2} sampled), tri-mul {t_mul:.1f} s (C3 x FLOP ratio), transition "
+                         f"{t_tr:.1f} s (1e5-row sample), s track {t_s:.1f} s"),
+            "configs": cfg}
+
+
+def _time_once(fn) -> float:
     t0 = time.perf_counter()
-    O.pairformer_layer(s, z, tok, pm, p, 16)
-    dt = time.perf_counter() - t0
-    scale = block_flops(N_target) / block_flops(N_sample)
-    return {"value": round(1.0 / (dt * scale), 6), "unit": "blocks/s", "cores": int(threads), "kind": "port",
-            "sample": f"one PairformerLayer at N={N_sample} (numpy float32 oracle, 5% padded) in {dt:.2f} s, "
-                      f"scaled by the block FLOP ratio {scale:.2f} to N={N_target} (estimate)"}
+    fn()
+    return time.perf_counter() - t0
 
 
 def main() -> int:
@@ -236,6 +321,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=4)
     ap.add_argument("--n", type=int, default=1000)
     ap.add_argument("--n-small", type=int, default=400)
+    ap.add_argument("--small-warmup", type=int, default=16, help="untimed blocks before the N=400 figure")
+    ap.add_argument("--small-steps", type=int, default=128, help="timed blocks for the N=400 figure")
+    ap.add_argument("--cpu-budget", type=float, default=25.0,
+                    help="seconds per CPU-baseline configuration (bounds the timed runs after the warm-up)")
     ap.add_argument("--blocks", type=int, default=64)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--c5-steps", type=int, default=20,
@@ -275,12 +364,12 @@ def main() -> int:
         # N = 400 blocks/s (secondary figure)
         if args.n_small:
             m, s, z, tok, pm = make_trunk(args.n_small, args.blocks, 0, dev)
-            xn = run_blocks(m, s, z, tok, pm, 0, 2)
+            xn = run_blocks(m, s, z, tok, pm, 0, args.small_warmup)
             torch.cuda.synchronize()
             t0 = time.perf_counter()
-            run_blocks(m, s, z, tok, pm, 2, 16, xn)
+            run_blocks(m, s, z, tok, pm, args.small_warmup, args.small_steps, xn)
             torch.cuda.synchronize()
-            result_small = 16 / (time.perf_counter() - t0)
+            result_small = args.small_steps / (time.perf_counter() - t0)
             del m, s, z, tok, pm
             torch.cuda.empty_cache()
         m, s, z, tok, pm = make_trunk(args.n, args.blocks, 0, dev)
@@ -344,7 +433,7 @@ def main() -> int:
         with torch.no_grad():
             out["msa_layer"] = msa_layer_leg(args.msa_steps, dev)
     if not args.no_cpu:
-        out["cpu_baseline"] = cpu_baseline()
+        out["cpu_baseline"] = cpu_baseline(args.cpu_budget)
     print(json.dumps(out), flush=True)
     return 0
 

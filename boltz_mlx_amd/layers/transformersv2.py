@@ -145,6 +145,11 @@ def _layer_bias(bias, i: int, L: int, H: int):
 def _layer_fast(layer, a, h1, h2, i: int, L: int, bias_l, mask, multiplicity: int) -> None:
     """Layer i of L on a [B*mult, N, D] fp32 in place from the precomputed conditioning h1, h2."""
     Bm, N, D = a.shape
+    rows_c = h1.shape[0]
+    if rows_c not in (N, Bm * N):
+        # the kernels pair row r with conditioning row r % rows_c: valid for one shared group or one per sample
+        raise ValueError(f"conditioning s must have 1 or {Bm} samples of {N} tokens (a is [{Bm}, {N}, {D}]); got "
+                         f"{rows_c} rows")
     dt = K.storage_dtype()
     at = layer.pair_bias_attn
     H = at.num_heads

@@ -37,8 +37,13 @@ class Transition(torch.nn.Module):
     def forward(self, x: torch.Tensor, chunk_size: Optional[int] = None,
                 xn: Optional[torch.Tensor] = None) -> torch.Tensor:
         """x: [..., dim] fp32 -> [..., out_dim] fp32. chunk_size is accepted and ignored (the fused kernel keeps
-        no [rows, hidden] intermediate)."""
-        xn = self.norm.to_storage(x) if xn is None else xn.contiguous()
+        no [rows, hidden] intermediate). xn: norm(x) already computed, used in f16 mode only, as the reference
+        uses it (transition.py:27-31, 56-60); otherwise the LayerNorm is computed from x."""
+        use_xn = xn is not None and K.f16()
+        if use_xn and (tuple(xn.shape) != tuple(x.shape) or xn.dtype != K.storage_dtype()):
+            raise ValueError(f"xn must be the fp16 norm output of shape {tuple(x.shape)}, got "
+                             f"{tuple(xn.shape)} {xn.dtype}")
+        xn = xn.contiguous() if use_xn else self.norm.to_storage(x)
         if self._pair_kernel():
             out = torch.empty(x.shape, dtype=torch.float32, device=x.device)
             self.fused(xn, out, accumulate=False)

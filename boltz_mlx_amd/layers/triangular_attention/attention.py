@@ -6,8 +6,10 @@ use_kernels=False, xn=None, keep_t=False)`` returns the update). Three kernels p
 q|k|v|g|tri-bias projection (reading positions transposed for the ending node), the flash core, and linear_o +
 residual (+ next LN) writing back at the un-transposed position.
 
-Difference from the reference: ``xn`` is the LayerNorm output in the natural (un-transposed) layout for both
-nodes, since the projection kernel reads the ending node's positions transposed itself.
+``xn`` follows the reference's contract (attention.py:95-100): it is used in f16 mode only (the fp32 path computes
+the LayerNorm itself), and for the ending node it is the LayerNorm output already transposed, so its projection
+reads it in place. Inside the layer chain (``fused``) the carried LayerNorm output stays in the natural layout and
+the projection kernel reads the ending node's positions transposed instead.
 """
 
 from __future__ import annotations
@@ -35,7 +37,8 @@ class TriangleAttention(torch.nn.Module):
     def forward(self, x: torch.Tensor, mask: Optional[torch.Tensor] = None, chunk_size: Optional[int] = None,
                 use_kernels: bool = False, xn: Optional[torch.Tensor] = None, keep_t: bool = False) -> torch.Tensor:
         """x: [B, I, J, C_in] fp32; mask: [B, I, J]. chunk_size / use_kernels are accepted and ignored (the core is
-        flash-style and never materialises the logits)."""
+        flash-style and never materialises the logits). xn (f16 mode): layer_norm(x) in fp16, for the ending node
+        transposed ([B, J, I, C_in]), as the reference's f16 path takes it; outside f16 mode it is ignored."""
         B, N, M, D = x.shape
         if N != M:
             raise ValueError("triangle attention needs a square pair representation")
@@ -43,25 +46,32 @@ class TriangleAttention(torch.nn.Module):
             mask = torch.ones(x.shape[:-1], dtype=torch.float32, device=x.device)
         mask = mask.to(torch.float32).contiguous()
         out = torch.empty(x.shape, dtype=torch.float32, device=x.device)
+        use_xn = xn is not None and K.f16()
+        if use_xn and (tuple(xn.shape) != tuple(x.shape) or xn.dtype != K.storage_dtype()):
+            raise ValueError(f"xn must be the fp16 layer_norm output of shape {tuple(x.shape)}, got "
+                             f"{tuple(xn.shape)} {xn.dtype}")
         for b in range(B):
-            xb = self.layer_norm.to_storage(x[b]) if xn is None else xn[b].contiguous()
-            self.fused(xb.reshape(N * N, D), mask[b], out[b], accumulate=False)
+            xb = xn[b].contiguous() if use_xn else self.layer_norm.to_storage(x[b])
+            self.fused(xb.reshape(N * N, D), mask[b], out[b], accumulate=False, xn_transposed=use_xn)
         if keep_t and not self.starting:
             out = out.transpose(1, 2).contiguous()
         return out
 
     def fused(self, xn: torch.Tensor, mask: torch.Tensor, z: torch.Tensor, accumulate: bool = True, next_ln=None,
-              before_core=None):
-        """z (+)= self(z) from xn = layer_norm(z) ([N*N, D], storage dtype, natural layout) and the pair mask [N, N]
-        fp32 (natural layout); returns next_ln(z_new) when next_ln is given. before_core() is called after the
-        projection is enqueued and before the attention core (the point where independent work on another stream
-        overlaps the core rather than a persistent kernel)."""
+              before_core=None, xn_transposed: bool = False):
+        """z (+)= self(z) from xn = layer_norm(z) ([N*N, D], storage dtype; natural layout, or for the ending node
+        transposed when xn_transposed) and the pair mask [N, N] fp32 (natural layout); returns next_ln(z_new) when
+        next_ln is given. before_core() is called after the projection is enqueued and before the attention core
+        (the point where independent work on another stream overlaps the core rather than a persistent kernel)."""
         N, D = z.shape[0], z.shape[-1]
         H, C = self.no_heads, self.mha.c_hidden
         w, w_o = self.prepare()
         trans = not self.starting
+        # the projection reads xn at the attention frame's position: transposed for the ending node unless the
+        # caller already transposed it
+        proj_trans = trans and not xn_transposed
         if D != 128:  # the projection and output kernels are built for 128 channels: GEMMs plus layout kernels
-            qkg, vt, tb = K.triattn_pack(K.linear(xn, w), trans, N, H, C)
+            qkg, vt, tb = K.triattn_pack(K.linear(xn, w), proj_trans, N, H, C)
             if before_core is not None:
                 before_core()
             core = K.triattn_core(qkg, vt, tb, mask, trans, self.inf, N, H, C)
@@ -71,7 +81,7 @@ class TriangleAttention(torch.nn.Module):
                 z.zero_()
             nxt = K.add_ln(z, y, ln=next_ln, trans_y=trans, out_dtype=K.storage_dtype())
             return None if nxt is None else nxt.view(N * N, D)
-        qkg, vt, tb = K.triattn_proj(xn, w, trans, N, H, C)
+        qkg, vt, tb = K.triattn_proj(xn, w, proj_trans, N, H, C)
         if before_core is not None:
             before_core()
         core = K.triattn_core(qkg, vt, tb, mask, trans, self.inf, N, H, C)

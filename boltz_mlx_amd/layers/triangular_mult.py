@@ -29,14 +29,19 @@ class _TriangleMultiplication(torch.nn.Module):
     def forward(self, x: torch.Tensor, mask: torch.Tensor, use_kernels: bool = False,
                 xn: torch.Tensor | None = None) -> torch.Tensor:
         """x: [B, N, N, D] fp32; mask: [B, N, N]. `use_kernels` is accepted and ignored. xn: norm_in(x) already
-        computed (storage dtype, [B, N, N, D])."""
+        computed, used as the reference uses it (triangular_mult.py:23-29): in f16 mode with B = 1 (fp16
+        [1, N, N, D]); otherwise the LayerNorm is computed from x."""
         B, N, M, D = x.shape
         if N != M:
             raise ValueError("triangle multiplication needs a square pair representation")
         out = torch.empty(x.shape, dtype=torch.float32, device=x.device)
         mask = mask.to(torch.float32).contiguous()
+        use_xn = xn is not None and B == 1 and K.f16()
+        if use_xn and (tuple(xn.shape) != tuple(x.shape) or xn.dtype != K.storage_dtype()):
+            raise ValueError(f"xn must be the fp16 norm_in output of shape {tuple(x.shape)}, got "
+                             f"{tuple(xn.shape)} {xn.dtype}")
         for b in range(B):
-            xb = self.norm_in.to_storage(x[b]) if xn is None else xn[b].contiguous()
+            xb = xn[b].contiguous() if use_xn else self.norm_in.to_storage(x[b])
             self.fused(xb.reshape(N * N, D), mask[b], out[b], accumulate=False)
         return out
 

@@ -55,12 +55,13 @@ def layer_norm(x, w=None, b=None, eps=1e-5):
     mean = x.mean(axis=-1, keepdims=True)
     d = x - mean
     var = (d * d).mean(axis=-1, keepdims=True)
-    y = d / np.sqrt(var + x.dtype.type(eps))
+    # in place from here (the values equal d / sqrt(var + eps) * w + b; fewer large temporaries at N^2 rows)
+    d /= np.sqrt(var + x.dtype.type(eps))
     if w is not None:
-        y = y * w
+        d *= w
     if b is not None:
-        y = y + b
-    return y
+        d += b
+    return d
 
 
 def linear(x, w, b=None):
@@ -70,7 +71,11 @@ def linear(x, w, b=None):
 
 
 def sigmoid(x):
-    return 1.0 / (1.0 + np.exp(-x))
+    """1 / (1 + exp(-x)), evaluated in place on one temporary."""
+    e = np.negative(x)
+    np.exp(e, out=e)
+    e += 1.0
+    return np.divide(1.0, e, out=e)
 
 
 def silu(x):
@@ -79,8 +84,10 @@ def silu(x):
 
 def softmax(a, axis=-1):
     m = a.max(axis=axis, keepdims=True)
-    e = np.exp(a - m)
-    return e / e.sum(axis=axis, keepdims=True)
+    e = np.subtract(a, m)
+    np.exp(e, out=e)
+    e /= e.sum(axis=axis, keepdims=True)
+    return e
 
 
 def tri_mul(x, mask, p: dict, outgoing: bool):
@@ -90,8 +97,9 @@ def tri_mul(x, mask, p: dict, outgoing: bool):
     out = p_out(norm_out(o)) * sigmoid(g_out(xn))."""
     D = p["p_out.weight"].shape[0]
     xn = layer_norm(x, p["norm_in.weight"], p["norm_in.bias"], 1e-5)
-    ab = linear(xn, p["p_in.weight"]) * sigmoid(linear(xn, p["g_in.weight"]))
-    ab = ab * mask[..., None]
+    ab = linear(xn, p["p_in.weight"])
+    ab *= sigmoid(linear(xn, p["g_in.weight"]))
+    ab *= mask[..., None]
     a, b = ab[..., :D], ab[..., D:]
     at = np.ascontiguousarray(a.transpose(0, 3, 1, 2))  # [B, D, N, N]
     bt = np.ascontiguousarray(b.transpose(0, 3, 1, 2))
@@ -101,15 +109,19 @@ def tri_mul(x, mask, p: dict, outgoing: bool):
         o = at.transpose(0, 1, 3, 2) @ bt  # sum_k a[d,k,i] b[d,k,j]
     o = o.transpose(0, 2, 3, 1)
     g_out = sigmoid(linear(xn, p["g_out.weight"]))
-    return linear(layer_norm(o, p["norm_out.weight"], p["norm_out.bias"], 1e-5), p["p_out.weight"]) * g_out
+    out = linear(layer_norm(o, p["norm_out.weight"], p["norm_out.bias"], 1e-5), p["p_out.weight"])
+    out *= g_out
+    return out
 
 
-def tri_att(x, mask, p: dict, starting: bool, inf: float = 1e9, row_chunk: int = 64):
+def tri_att(x, mask, p: dict, starting: bool, inf: float = 1e9, row_chunk: int = 64, rows=None):
     """Triangle attention update for x [B, I, J, C_in], mask [B, I, J] (attention.py:27-93; primitives.py:40-75).
     For row i, head h: logits[j,k] = (q[i,j]/sqrt(c)) . k[i,k] + inf*(mask[i,k]-1) + tri_bias[h,j,k],
     tri_bias = linear(xn)[j,k,h]; out = linear_o(sigmoid(g) * softmax(logits) v). The ending node runs the same
     on x and mask with the two token axes swapped and swaps the output back (attention.py:40-42, 91-92).
-    Rows are processed `row_chunk` at a time (same math; bounds the [rows, H, J, K] logits)."""
+    Rows are processed `row_chunk` at a time (same math; bounds the [rows, H, J, K] logits). `rows` (a count)
+    restricts the attention to the first `rows` rows of the (swapped) frame and returns only those, the tri bias
+    still coming from every row: rows are independent, so this times a sample of a large case."""
     if mask is None:
         mask = np.ones(x.shape[:-1], dtype=x.dtype)
     if not starting:
@@ -122,11 +134,15 @@ def tri_att(x, mask, p: dict, starting: bool, inf: float = 1e9, row_chunk: int =
     xn = layer_norm(x, p["layer_norm.weight"], p["layer_norm.bias"], 1e-5)
     B, I, J, _ = x.shape
     tri_bias = linear(xn, p["linear.weight"]).transpose(0, 3, 1, 2)  # [B, H, J, K]
+    if rows is not None:
+        if not starting:
+            raise ValueError("a row sample is defined for the starting node's frame")
+        I = min(I, int(rows))
     scale = x.dtype.type(1.0 / np.sqrt(C))
     out = np.empty((B, I, J, HC), dtype=x.dtype)
     for b in range(B):
         for i0 in range(0, I, row_chunk):
-            xs = xn[b, i0:i0 + row_chunk]  # [r, J, Cin]
+            xs = xn[b, i0:min(i0 + row_chunk, I)]  # [r, J, Cin]
             r = xs.shape[0]
             q = linear(xs, Hq).reshape(r, J, H, C).transpose(0, 2, 1, 3) * scale
             k = linear(xs, p["mha.linear_k.weight"]).reshape(r, J, H, C).transpose(0, 2, 1, 3)

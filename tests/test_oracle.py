@@ -218,6 +218,17 @@ def test_tri_att_symmetry_and_masks():
     assert np.abs(a - b).max() < 1e-12
 
 
+def test_tri_att_row_sample():
+    """The row sample used to time large cases is the first rows of the full result (rows are independent; the tri
+    bias comes from every row)."""
+    p = rand_params(shapes_tri_att(16, 4, 2), seed=16, std=0.3)
+    x, _, pm = pair_inputs(11, 16, seed=17, n_pad=2)
+    full = O.tri_att(x, pm, p, True, row_chunk=4)
+    part = O.tri_att(x, pm, p, True, row_chunk=4, rows=6)
+    assert part.shape == (1, 6, 11, 16)
+    assert np.abs(part - full[:, :6]).max() < 1e-13
+
+
 # ---------------------------------------------------------------- transition
 
 def test_transition_vs_torch():
@@ -287,6 +298,99 @@ def test_layer_order():
         else:
             ref = z + O.transition(z, q)
         assert np.abs(z2 - ref).max() < 1e-12
+
+
+def _torch_transition(x, p):
+    xn = F.layer_norm(x, (x.shape[-1],), T(p["norm.weight"]), T(p["norm.bias"]), 1e-5)
+    return F.linear(F.silu(F.linear(xn, T(p["fc1.weight"]))) * F.linear(xn, T(p["fc2.weight"])), T(p["fc3.weight"]))
+
+
+def _torch_apb(s_n, z, mask, p, H, inf=1e6):
+    """AttentionPairBias on torch SDPA: q from s_n (biased), k / v from k_in = s_n, pair bias Linear(LN(z))."""
+    B, N, Cs = s_n.shape
+    hd = Cs // H
+    q = F.linear(s_n, T(p["proj_q.weight"]), T(p["proj_q.bias"])).reshape(B, N, H, hd).transpose(1, 2)
+    k = F.linear(s_n, T(p["proj_k.weight"])).reshape(B, N, H, hd).transpose(1, 2)
+    v = F.linear(s_n, T(p["proj_v.weight"])).reshape(B, N, H, hd).transpose(1, 2)
+    zb = F.linear(F.layer_norm(z, (z.shape[-1],), T(p["proj_z.0.weight"]), T(p["proj_z.0.bias"]), 1e-5),
+                  T(p["proj_z.1.weight"]))
+    bias = zb.permute(0, 3, 1, 2) + (1 - mask)[:, None, None, :] * -inf
+    o = F.scaled_dot_product_attention(q, k, v, attn_mask=bias).transpose(1, 2).reshape(B, N, Cs)
+    return F.linear(torch.sigmoid(F.linear(s_n, T(p["proj_g.weight"]))) * o, T(p["proj_o.weight"]))
+
+
+def test_layer_s_track_composition():
+    """The s track reads the pair bias from the z every pair update has produced, takes q and k_in from
+    pre_norm_s(s), and runs transition_s on s after the attention residual (pairformer.py:90-93). transition_z is
+    the only non-zero pair module, so the pre- and post-update z differ; a bias from the old z, transition_s on
+    pre_norm_s(s) or on the pre-attention s would each fail."""
+    cs, cz, H = 48, 32, 4
+    base = rand_params(shapes_layer(cs, cz, heads=H, pw=8, pheads=2), seed=46, std=0.3)
+    keep = ("attention", "transition_s", "transition_z")
+    p = {k: (v if (k.startswith(keep) or v.ndim == 1 and not k.endswith("proj_q.bias")) else np.zeros_like(v))
+         for k, v in base.items()}
+    z, tok, pm = pair_inputs(7, cz, seed=47, n_pad=2)
+    s = np.random.default_rng(48).standard_normal((1, 7, cs)) * 2 + 0.5
+    s2, z2 = O.pairformer_layer(s, z, tok, pm, p, num_heads=H)
+    zt, st, mt = T(z), T(s), T(tok)
+    z1 = zt + _torch_transition(zt, O.sub(p, "transition_z"))
+    s_n = F.layer_norm(st, (cs,), T(p["pre_norm_s.weight"]), T(p["pre_norm_s.bias"]), 1e-5)
+    s1 = st + _torch_apb(s_n, z1, mt, O.sub(p, "attention"), H)
+    ref_s = s1 + _torch_transition(s1, O.sub(p, "transition_s"))
+    assert np.abs(z2 - z1.numpy()).max() < 1e-12
+    assert np.abs(s2 - ref_s.numpy()).max() < 1e-11
+    # the alternatives a misreading would compute are far from it
+    wrong_bias = st + _torch_apb(s_n, zt, mt, O.sub(p, "attention"), H)
+    wrong_bias = wrong_bias + _torch_transition(wrong_bias, O.sub(p, "transition_s"))
+    wrong_tr = s1 + _torch_transition(s_n, O.sub(p, "transition_s"))
+    for w in (wrong_bias, wrong_tr):
+        assert np.abs(s2 - w.numpy()).max() > 1e-4
+
+
+def test_layer_transition_s_alone():
+    """Only transition_s non-zero: s' = s + transition(s) on the un-normalised s, z unchanged."""
+    cs, cz, H = 48, 32, 4
+    base = rand_params(shapes_layer(cs, cz, heads=H, pw=8, pheads=2), seed=49, std=0.3)
+    p = {k: (v if (k.startswith("transition_s") or v.ndim == 1 and not k.endswith("proj_q.bias"))
+             else np.zeros_like(v)) for k, v in base.items()}
+    z, tok, pm = pair_inputs(5, cz, seed=50)
+    s = np.random.default_rng(51).standard_normal((1, 5, cs)) * 3 - 1
+    s2, z2 = O.pairformer_layer(s, z, tok, pm, p, num_heads=H)
+    ref = T(s) + _torch_transition(T(s), O.sub(p, "transition_s"))
+    assert np.array_equal(z2, z)
+    assert np.abs(s2 - ref.numpy()).max() < 1e-12
+
+
+def _zeroed(p):
+    return {k: (np.zeros_like(v) if (v.ndim == 2 or k.endswith("proj_q.bias")) else v) for k, v in p.items()}
+
+
+def test_module_runs_layers_in_order():
+    """PairformerModule applies layers.0, then layers.1, ... (pairformer.py:145-148): with block 1 zeroed the
+    module equals layer 0 alone, with block 0 zeroed it equals layer 1 alone, and with both live it is layer 1 after
+    layer 0 (which differs from the reverse order)."""
+    cs, cz, H = 48, 32, 4
+    p0 = rand_params(shapes_layer(cs, cz, heads=H, pw=8, pheads=2), seed=52, std=0.2)
+    p1 = rand_params(shapes_layer(cs, cz, heads=H, pw=8, pheads=2), seed=53, std=0.2)
+    z, tok, pm = pair_inputs(6, cz, seed=54, n_pad=1)
+    s = np.random.default_rng(55).standard_normal((1, 6, cs))
+
+    def stack(a, b):
+        out = {f"layers.0.{k}": v for k, v in a.items()}
+        out.update({f"layers.1.{k}": v for k, v in b.items()})
+        return out
+
+    one = O.pairformer_layer(s, z, tok, pm, p0, H)
+    got = O.pairformer_module(s, z, tok, pm, stack(p0, _zeroed(p1)), 2, H)
+    assert all(np.abs(g - r).max() < 1e-12 for g, r in zip(got, one))
+    one = O.pairformer_layer(s, z, tok, pm, p1, H)
+    got = O.pairformer_module(s, z, tok, pm, stack(_zeroed(p0), p1), 2, H)
+    assert all(np.abs(g - r).max() < 1e-12 for g, r in zip(got, one))
+    fwd = O.pairformer_layer(*O.pairformer_layer(s, z, tok, pm, p0, H), tok, pm, p1, H)
+    rev = O.pairformer_layer(*O.pairformer_layer(s, z, tok, pm, p1, H), tok, pm, p0, H)
+    got = O.pairformer_module(s, z, tok, pm, stack(p0, p1), 2, H)
+    assert all(np.abs(g - r).max() < 1e-12 for g, r in zip(got, fwd))
+    assert np.abs(got[1] - rev[1]).max() > 1e-4
 
 
 def test_metrics_definition():

@@ -7,6 +7,7 @@
 // contraction's k loop and the 64-wide position tiles of proj/tail never straddle a row.
 #include "bzpf_common.h"
 #include "bzpf_kernels.h"
+#include "bzpf_rowgemm.h"
 
 namespace bzpf {
 
@@ -115,146 +116,211 @@ __global__ __launch_bounds__(256, 2) void trimul_contract_kernel(const T* __rest
   }
 }
 
-// fp16 form: 256 x 256 tiles on v_mfma_f32_32x32x16_f16, 16 waves of 64 (j) x 64 (i) = 2 x 2 blocks of 32 x 32
-// (64 accumulator registers per lane, 4 waves per SIMD). The 128 x 128 tile of the fp32 form moves 32 KB from L2 per
-// 2.1 MFLOP; this tile halves that (64 KB per 8.4 MFLOP per 64-element K stage). K stages (64 elements) are
-// double-buffered in LDS (147 KB, one workgroup per CU); two register sets carry the next two stages, so each load
-// has two stages of compute to land (one stage, about 1 us, is shorter than the loaded L2/HBM latency); four waves
-// per SIMD (rather than two with 128 x 64 wave tiles) keep the matrix cores busier through each stage's barrier and
-// LDS waits.
-// Operand layouts (A = rows of b, B = rows of a, both K-contiguous): lane l holds row l % 32 and 8 consecutive k;
-// in MFMA step s of a stage, lane half h = l / 32 takes k = 32 h + 8 s .. + 7, so over the 4 steps a lane reads 64
-// contiguous bytes of its row (a permutation of the k sum shared by A and B). The accumulator lane holds
-// o^T[j = 8 q + 4 h + e][i = l % 32] in element 4 q + e: 4 runs of 4 consecutive j of one i.
-constexpr int CT_BT = 256, CT_WAVES = 16;
+// fp16 form, persistent and LDS-direct. One 512-thread workgroup per CU walks its tiles (256 x 256 of one channel) as
+// one stream of K stages, so the next tile's first stages load while the current tile's last stages compute. A tile
+// is 8 waves of 128 (j) x 64 (i) = 4 x 2 blocks of 32 x 32 on v_mfma_f32_32x32x16_f16 (128 accumulator registers per
+// lane, 2 waves per SIMD). K stages of BK elements go from memory straight into LDS (buffer_load ... lds: no staging
+// registers, no LDS store instructions), NS stages deep. A wave's load instruction fills 1 KB of LDS in lane order,
+// so the LDS row layout is fixed; each lane picks its global 16-byte chunk so that LDS chunk p of row R holds the
+// row's chunk p ^ swz(R), which makes the fragment reads (16 lanes on 16 rows at one logical chunk) hit distinct
+// banks. The fragments of MFMA step g + 1 are read while step g computes (two register sets, across stage
+// boundaries too) and the reads are interleaved with the MFMAs. The output tile leaves through a small LDS buffer so
+// that each store instruction writes whole 128-byte row segments (scattered 8-byte stores took a third of the time).
+// The lane-to-k assignment (lane half h takes k = 32 h + 8 s .. + 7 of a 64-element stage in step s) is the one the
+// earlier register-staged kernel used, so the accumulation order, and the result, are unchanged.
+template <int BK>
+__device__ __forceinline__ int ct_swz(int row) {
+  if constexpr (BK == 64) return (row & 7) ^ ((row >> 3) & 1);       // 8 chunks of a 128-byte row
+  else return ((row >> 1) & 3) ^ ((row >> 3) & 1);                     // 4 chunks of a 64-byte row
+}
 
-__global__ __launch_bounds__(64 * CT_WAVES, 1) void trimul_contract_f16_k(const half_t* __restrict__ ab,
-                                                                          half_t* __restrict__ o, int64_t N,
-                                                                          int64_t ld, int D, int64_t tiles1,
-                                                                          int64_t units, int64_t per_xcd) {
-  constexpr int BT = CT_BT, BK = 64, NT = 64 * CT_WAVES;
-  constexpr int LDT = BK + 8;              // LDS row pitch (halves): 36 dwords, conflict-free 16-byte row reads
-  constexpr int VPR = BK / 8;              // 16-byte vectors per row per stage
-  constexpr int LOADS = 2 * BT * VPR / NT;  // 8
-  __shared__ LDS_ALIGN half_t As[2][BT * LDT];  // rows of a (i)
-  __shared__ LDS_ALIGN half_t Bs[2][BT * LDT];  // rows of b (j)
+template <int BK, int NS>
+__global__ __launch_bounds__(512, 1) void trimul_contract_f16_k(const half_t* __restrict__ ab, half_t* __restrict__ o,
+                                                                int64_t N, int64_t ld, int D, int64_t tiles1,
+                                                                int64_t units, int64_t per_xcd, int wg_per_xcd) {
+  constexpr int BT = 256, NW = 8;
+  constexpr int ROWB = BK * 2;               // bytes of a row per stage
+  constexpr int CPR = ROWB / 16;             // 16-byte chunks per row
+  constexpr int RPI = 1024 / ROWB;           // rows per load instruction
+  constexpr int STAGE = 2 * BT * ROWB;       // a rows, then b rows
+  constexpr int LPW = 2 * BT / RPI / NW;     // load instructions per wave per stage (first half a, second half b)
+  constexpr int STEPS = BK / 16;
+  // the stage slots, then one 4 KB output staging buffer per wave (160 KB)
+  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE + NW * 4096];
 
-  const int64_t u = (int64_t)(blockIdx.x % 8) * per_xcd + blockIdx.x / 8;
-  if (u >= units) return;
-  const int64_t c = u / (tiles1 * tiles1);
-  const int64_t tt = u - c * tiles1 * tiles1;
-  const int64_t i0 = (tt / tiles1) * BT, j0 = (tt % tiles1) * BT;
-  const half_t* a = ab + c * N * ld;
-  const half_t* b = ab + ((int64_t)D + c) * N * ld;
-  const int t = threadIdx.x, wave = t >> 6, l = t & 63, r = l & 31, h = l >> 5;
-  const int wj = wave >> 2, wi = wave & 3;  // wave tile: j = 64 wj .., i = 64 wi ..
+  // this workgroup's tiles: u = first + wg_per_xcd * k, k < cnt, inside its XCD's contiguous range of units (the
+  // XCD's CUs work on consecutive tiles, so one channel's a and b stay in its L2)
+  const int xcd = blockIdx.x % 8;
+  const int64_t first = (int64_t)xcd * per_xcd + blockIdx.x / 8;
+  const int64_t end = min(units, (int64_t)(xcd + 1) * per_xcd);
+  if (first >= end) return;
+  const int cnt = (int)((end - first + wg_per_xcd - 1) / wg_per_xcd);
+  const int nst = (int)(ld / BK);
+  const int total = cnt * nst;
 
-  // Staging: thread t moves 16-byte vector (t / 8, 8 (t % 8)) of each 128-row quarter: quarters 0, 1 of a (rows
-  // i0 ..), 2, 3 of b (rows j0 ..). Loads go through buffer resources: the lane offset is fixed, the quarter's rows
-  // and the stage's k ride in the scalar offset, and rows past N read as zeros (range check; those outputs are not
-  // stored).
-  constexpr int RSRC_CFG = 0x00020000;  // raw buffer, 32-bit data format
-  const __amdgpu_buffer_rsrc_t ars = __builtin_amdgcn_make_buffer_rsrc((void*)a, 0, (int)(N * ld * 2), RSRC_CFG);
-  const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc((void*)b, 0, (int)(N * ld * 2), RSRC_CFG);
-  const int voff = (int)(((t >> 3) * ld + (t & 7) * 8) * 2);
-  const int loff = (t >> 3) * LDT + (t & 7) * 8;  // LDS element offset inside a quarter
-  // two register sets: stage s + 2 is loaded while stage s computes, so each load has two stages of time to land
-  u32x4_t reg0[LOADS], reg1[LOADS];
-  auto gload = [&](u32x4_t (&reg)[LOADS], int stage) {
+  const int t = threadIdx.x, w = t >> 6, l = t & 63, r = l & 31, h = l >> 5;
+  const int wj = w >> 2, wi = w & 3;  // wave tile: j = 128 wj .., i = 64 wi ..
+  struct Tile { int64_t c, i0, j0; };
+  auto tile = [&](int k) {
+    const int64_t u = first + (int64_t)wg_per_xcd * k;
+    const int64_t c = u / (tiles1 * tiles1);
+    const int64_t tt = u - c * tiles1 * tiles1;
+    return Tile{c, (tt / tiles1) * BT, (tt % tiles1) * BT};
+  };
+
+  constexpr int RSRC_CFG = 0x00020000;
+  const int chan_bytes = (int)(N * ld * 2);
+  // lane part of every load: row w * RPI + l / CPR of its 8-wave group, logical chunk (l % CPR) ^ swz(row)
+  const int lrow = w * RPI + l / CPR;
+  const int voff = (int)(((int64_t)lrow * ld + 8 * ((l % CPR) ^ ct_swz<BK>(lrow))) * 2);
+  // The row part of the offset rides in the lane offset, which the buffer range check covers: rows past N read as
+  // zeros (their outputs are not stored) and nothing is read past the end of a channel. The stage's k rides in the
+  // scalar offset. Global stage gs = k * nst + stage; issues past the last one reload it (into a slot never read).
+  auto issue = [&](int gs, int slot) {
+    gs = min(gs, total - 1);
+    const int k = gs / nst, stage = gs - k * nst;
+    const Tile tl = tile(k);
+    const __amdgpu_buffer_rsrc_t ars =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(ab + tl.c * N * ld), 0, chan_bytes, RSRC_CFG);
+    const __amdgpu_buffer_rsrc_t brs =
+        __builtin_amdgcn_make_buffer_rsrc((void*)(ab + ((int64_t)D + tl.c) * N * ld), 0, chan_bytes, RSRC_CFG);
+    char* dst = lds + slot * STAGE + w * 1024;
 #pragma unroll
-    for (int v = 0; v < LOADS; v++) {
-      const int so = (int)((((v < 2 ? i0 : j0) + 128 * (v & 1)) * ld + (int64_t)stage * BK) * 2);
-      reg[v] = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(v < 2 ? ars : brs, voff, so, 0));
+    for (int v = 0; v < LPW; v++) {
+      const bool isa = v < LPW / 2;
+      const int64_t row0 = (isa ? tl.i0 : tl.j0) + (int64_t)(v % (LPW / 2)) * NW * RPI;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(isa ? ars : brs,
+                                               (__attribute__((address_space(3))) void*)(dst + v * NW * 1024), 16,
+                                               voff + (int)(row0 * ld * 2), stage * BK * 2, 0, 0);
     }
   };
-  auto lstore = [&](const u32x4_t (&reg)[LOADS], int buf) {
-#pragma unroll
-    for (int v = 0; v < LOADS; v++)
-      *reinterpret_cast<u32x4_t*>((v < 2 ? As[buf] : Bs[buf]) + 128 * (v & 1) * LDT + loff) = reg[v];
-  };
 
-  f16x acc[2][2];  // acc[jb][ib]: o^T block (j = 64 wj + 32 jb .., i = 64 wi + 32 ib ..)
+  f16x acc[4][2];  // acc[jb][ib]: o^T block (j = 128 wj + 32 jb .., i = 64 wi + 32 ib ..)
+  auto zero = [&]() {
 #pragma unroll
-  for (int jb = 0; jb < 2; jb++)
+    for (int jb = 0; jb < 4; jb++)
+#pragma unroll
+      for (int ib = 0; ib < 2; ib++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[jb][ib][e] = 0.0f;
+  };
+  // acc[jb][ib][4 q + e] = o[i = i0 + 64 wi + 32 ib + r][j = j0 + 128 wj + 32 jb + 8 q + 4 h + e]
+  // Stores through a wave-private LDS buffer: each 32 (i) x 64 (j) piece of the wave's tile is written in the
+  // accumulator layout (16-byte chunks XOR-swizzled by row) and read back as 16 bytes of one row per lane, so a
+  // store instruction covers 8 rows x 128 contiguous bytes rather than 32 rows x 16 bytes.
+  char* ob = lds + NS * STAGE + w * 4096;
+  auto store = [&](int k) {
+    const Tile tl = tile(k);
+    half_t* oc = o + tl.c * N * ld;
 #pragma unroll
     for (int ib = 0; ib < 2; ib++)
 #pragma unroll
-      for (int e = 0; e < 16; e++) acc[jb][ib][e] = 0.0f;
-  auto compute = [&](int buf) {
-    const half_t* Ab = As[buf] + (64 * wi + r) * LDT + 32 * h;
-    const half_t* Bb = Bs[buf] + (64 * wj + r) * LDT + 32 * h;
+      for (int jp = 0; jp < 2; jp++) {
 #pragma unroll
-    for (int s = 0; s < 4; s++) {
-      half8 fa[2], fb[2];
+        for (int jj = 0; jj < 2; jj++)
 #pragma unroll
-      for (int q = 0; q < 2; q++) fa[q] = *reinterpret_cast<const half8*>(Ab + 32 * q * LDT + 8 * s);
+          for (int q = 0; q < 4; q++) {
+            const f16x& v = acc[2 * jp + jj][ib];
+            *reinterpret_cast<half4*>(ob + r * 128 + (((4 * jj + q) ^ (r & 7)) * 16) + 8 * h) =
+                half4{(half_t)v[4 * q], (half_t)v[4 * q + 1], (half_t)v[4 * q + 2], (half_t)v[4 * q + 3]};
+          }
 #pragma unroll
-      for (int q = 0; q < 2; q++) fb[q] = *reinterpret_cast<const half8*>(Bb + 32 * q * LDT + 8 * s);
-#pragma unroll
-      for (int jb = 0; jb < 2; jb++)
-#pragma unroll
-        for (int ib = 0; ib < 2; ib++)
-          acc[jb][ib] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fb[jb], fa[ib], acc[jb][ib], 0, 0, 0);
-    }
-  };
-  const int nst = (int)(ld / BK);
-  // Stages pair up (buffer 0, buffer 1) per trip; an odd stage count starts with a zero stage in buffer 0 (adds
-  // nothing), so the trip body has no branch and the wait counter sees one load order. Loads past the last stage
-  // reload it into registers that are never stored.
-  const int s0 = -(nst & 1);
-  gload(reg0, 0);
-#pragma unroll
-  for (int v = 0; v < LOADS; v++) reg0[v] = s0 ? u32x4_t{0u, 0u, 0u, 0u} : reg0[v];
-  lstore(reg0, 0);
-  __syncthreads();
-  // issue order pinned (reg0 before reg1, as in the loop): the wait counter then needs only the older set
-  gload(reg0, s0 + 1);
-  __builtin_amdgcn_sched_barrier(0);
-  gload(reg1, min(s0 + 2, nst - 1));
-  __builtin_amdgcn_sched_barrier(0);
-  for (int st = s0; st < nst; st += 2) {
-    compute(0);       // stage st
-    lstore(reg0, 1);  // stage st + 1
-    __syncthreads();
-    gload(reg0, min(st + 3, nst - 1));
-    __builtin_amdgcn_sched_barrier(0);
-    compute(1);       // stage st + 1
-    lstore(reg1, 0);  // stage st + 2
-    __syncthreads();
-    gload(reg1, min(st + 4, nst - 1));
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  half_t* oc = o + c * N * ld;
-#pragma unroll
-  for (int ib = 0; ib < 2; ib++) {
-    const int64_t i = i0 + 64 * wi + 32 * ib + r;
-    if (i >= N) continue;
-#pragma unroll
-    for (int jb = 0; jb < 2; jb++)
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const int64_t j = j0 + 64 * wj + 32 * jb + 8 * q + 4 * h;
-        if (j >= ld) continue;
-        const f16x& v = acc[jb][ib];
-        *reinterpret_cast<half4*>(oc + i * ld + j) =
-            half4{(half_t)v[4 * q], (half_t)v[4 * q + 1], (half_t)v[4 * q + 2], (half_t)v[4 * q + 3]};
+        for (int rr = 0; rr < 4; rr++) {
+          const int R = (l >> 3) + 8 * rr;
+          const u32x4_t val = *reinterpret_cast<const u32x4_t*>(ob + R * 128 + (((l & 7) ^ (R & 7)) * 16));
+          const int64_t i = tl.i0 + 64 * wi + 32 * ib + R;
+          const int64_t j = tl.j0 + 128 * wj + 64 * jp + 8 * (l & 7);
+          if (i < N && j < ld) *reinterpret_cast<u32x4_t*>(oc + i * ld + j) = val;
+        }
       }
+  };
+  zero();
+  const int sw = ct_swz<BK>(r);  // rows read by this lane: (block base, a multiple of 32) + r
+  // fragment sets: the reads of MFMA step g + 1 are issued before the MFMAs of step g (two register sets), across
+  // stage boundaries too, so each wave's own MFMAs cover its LDS latency and the barrier
+  half8 fa[2][4], fb[2][2];
+  auto read = [&](int set, int slot, int s) {
+    const char* base = lds + slot * STAGE;
+    const int chunk = (STEPS * h + s) ^ sw;
+#pragma unroll
+    for (int jb = 0; jb < 4; jb++)
+      fa[set][jb] = *reinterpret_cast<const half8*>(base + (BT + 128 * wj + 32 * jb + r) * ROWB + 16 * chunk);
+#pragma unroll
+    for (int ib = 0; ib < 2; ib++)
+      fb[set][ib] = *reinterpret_cast<const half8*>(base + (64 * wi + 32 * ib + r) * ROWB + 16 * chunk);
+  };
+  auto mfma = [&](int set) {
+#pragma unroll
+    for (int jb = 0; jb < 4; jb++)
+#pragma unroll
+      for (int ib = 0; ib < 2; ib++)
+        acc[jb][ib] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[set][jb], fb[set][ib], acc[jb][ib], 0, 0, 0);
+  };
+  // stages gs + 1 .. gs + NS - 1 are in flight while stage gs computes, so every wave always has (NS - 2) * LPW
+  // loads younger than the stage it waits for
+  constexpr int YOUNGER = (NS - 2) * LPW;
+  constexpr int WAIT = (YOUNGER & 15) | ((YOUNGER >> 4) << 14) | (0x7 << 4) | (0xF << 8);  // vmcnt only
+#pragma unroll
+  for (int p = 0; p < NS - 1; p++) issue(p, p);
+  __builtin_amdgcn_s_waitcnt(WAIT);  // stage 0 has landed (this wave's part)
+  __builtin_amdgcn_s_barrier();      // (everyone's)
+  __builtin_amdgcn_sched_barrier(0);
+  issue(NS - 1, NS - 1);
+  read(0, 0, 0);
+  int stage = 0, k = 0;
+  for (int gs = 0; gs < total; gs++) {
+    const int slot = gs % NS;
+#pragma unroll
+    for (int s = 0; s < STEPS; s++) {
+      const int cur = s & 1;  // STEPS is even: step 0 of every stage uses set 0
+      if (s + 1 < STEPS) {
+        read(cur ^ 1, slot, s + 1);
+      } else if (gs + 1 < total) {
+        // every read of this slot by this wave is done (the last set is in registers) and stage gs + 1 has landed;
+        // after the barrier the slot takes stage gs + NS
+        __builtin_amdgcn_s_waitcnt(WAIT & ~(0xF << 8));  // vmcnt as above, lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        issue(gs + NS, slot);
+        read(cur ^ 1, (gs + 1) % NS, 0);
+      }
+      mfma(cur);
+      // interleave: the next set's LDS reads between this set's MFMAs
+#pragma unroll
+      for (int q = 0; q < 6; q++) {
+        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+        __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(0x008, 2, 0);
+    }
+    if (++stage == nst) {  // tile k done: its stores drain while the next tile computes
+      store(k);
+      zero();
+      stage = 0;
+      k++;
+    }
   }
+  __builtin_amdgcn_s_waitcnt(0);  // no LDS write of a trailing (unused) stage load outlives the workgroup
 }
 
 template <typename T>
 static hipError_t contract_t(const void* ab, void* o, int64_t N, int64_t ld, int D, hipStream_t st) {
-  const int BT = sizeof(T) == 2 ? CT_BT : 128;
+  const int BT = sizeof(T) == 2 ? 256 : 128;
   const int64_t tiles1 = (N + BT - 1) / BT;
   const int64_t units = (int64_t)D * tiles1 * tiles1;
   const int64_t per_xcd = (units + 7) / 8;
   const dim3 grid((unsigned)(per_xcd * 8));
-  if constexpr (sizeof(T) == 2)
-    trimul_contract_f16_k<<<grid, 64 * CT_WAVES, 0, st>>>(static_cast<const half_t*>(ab), static_cast<half_t*>(o), N,
-                                                          ld, D, tiles1, units, per_xcd);
-  else
+  if constexpr (sizeof(T) == 2) {
+    static int cache[kMaxDevices] = {};
+    const int resident = resident_grid(trimul_contract_f16_k<64, 2>, 512, cache);
+    if (resident < 8) return hipErrorInvalidConfiguration;
+    const int wpx = (int)(resident / 8 < per_xcd ? resident / 8 : per_xcd);
+    trimul_contract_f16_k<64, 2><<<dim3(8 * wpx), 512, 0, st>>>(static_cast<const half_t*>(ab), static_cast<half_t*>(o),
+                                                               N, ld, D, tiles1, units, per_xcd, wpx);
+  } else {
     trimul_contract_kernel<T><<<grid, 256, 0, st>>>(static_cast<const T*>(ab), static_cast<T*>(o), N, ld, D, tiles1,
                                                     units, per_xcd);
+  }
   return hipGetLastError();
 }
 

@@ -106,12 +106,27 @@ def row_pitch(N: int) -> int:
 
 # ------------------------------------------------------------------------------------------------ weight caches
 
+WCACHE_TRACE = None  # set by mixed.trace_groups: called as (owner, name, params, dtype) on every wcache call
+
+
+def _wkey(dtype, params) -> tuple:
+    return (dtype,) + tuple((p.data_ptr(), p._version, p.device) for p in params)
+
+
+def wcache_seed(owner: torch.nn.Module, name: str, params, w: torch.Tensor) -> None:
+    """Install `w` (already concatenate(params, 0) in w's dtype, e.g. the buffer the parameters are views of) as the
+    cache entry wcache(owner, name, *params, dtype=w.dtype) returns."""
+    owner.__dict__.setdefault("_bzpf_cache", {})[name] = (_wkey(w.dtype, params), w)
+
+
 def wcache(owner: torch.nn.Module, name: str, *params: torch.Tensor, dtype=None) -> torch.Tensor:
     """concatenate(params, 0) in `dtype` (default: the storage dtype), cached on `owner` and rebuilt when a source
     parameter changes (data pointer or in-place version). Mirrors the reference's w16 cache
     (boltz_mlx/kernels.py:1330-1357)."""
     dtype = dtype or storage_dtype()
-    key = (dtype,) + tuple((p.data_ptr(), p._version, p.device) for p in params)
+    if WCACHE_TRACE is not None:
+        WCACHE_TRACE(owner, name, params, dtype)
+    key = _wkey(dtype, params)
     hit = owner.__dict__.get("_bzpf_cache", {}).get(name)
     if hit is not None and hit[0] == key:
         return hit[1]

@@ -33,9 +33,10 @@ pytestmark = pytest.mark.gpu
 F16_MODULE = (2e-2, 5e-3)
 F16_LAYER = (3e-2, 1e-2)
 # f16 against fp32 after many blocks / layers: the per-block fp16 storage rounding compounds through the residual
-# streams (bounds set with about 3x margin over the values measured on MI355X, printed by the tests)
-TRUNK_REL_FRO = 3e-2
-DIFF_STACK_REL_FRO = 2e-2
+# streams. Measured on MI355X (printed by the tests): 64-block trunk at N = 1000, rel_fro of the z update 1.1e-3 and of
+# the s update 6.7e-4; 24-layer diffusion stack 7.0e-4. The bounds leave about 4x margin.
+TRUNK_REL_FRO = 5e-3
+DIFF_STACK_REL_FRO = 3e-3
 
 
 @pytest.fixture(scope="module", autouse=True)

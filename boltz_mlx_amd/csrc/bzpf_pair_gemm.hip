@@ -205,7 +205,12 @@ __global__ __launch_bounds__(256) void trimul_tail_k(const T* __restrict__ o, co
 // row fragments back, with no barrier (a wave's LDS accesses complete in order). The next tile's o block and gate
 // inputs are loaded while the current tile computes; its residual rows are issued at the start of the tile. The
 // gates are computed first and held as fp16 (sigmoid values in (0, 1)), which keeps the tile within 168 VGPRs.
+// One 128-byte line of an o channel row holds 64 positions, i.e. four tiles. Tiles per row are a multiple of four
+// (tiles past N store nothing), so the workgroup's 12 consecutive tiles hold whole lines, and one barrier per round
+// keeps its waves in step: the four loads of a line reach L2 together and it is read from HBM once. Without the
+// barrier the waves drift apart by more than the L2 residency of a line and o is read about 2.3 times.
 constexpr int TAIL_WAVES = 12;
+__host__ __device__ constexpr int64_t tail_tiles_per_row(int64_t N) { return (N + 63) / 64 * 4; }
 
 __global__ __launch_bounds__(64 * TAIL_WAVES) void trimul_tail_f16_k(
     const half_t* __restrict__ o, const float* __restrict__ now, const float* __restrict__ nob, float eps_out,
@@ -250,9 +255,12 @@ __global__ __launch_bounds__(64 * TAIL_WAVES) void trimul_tail_f16_k(
   const int l = threadIdx.x & 63, g = l >> 4, r = l & 15;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   T* ts = Ts[wave];
-  const int tpr = (int)((N + 15) / 16), ntiles = (int)N * tpr, stride = gridDim.x * TAIL_WAVES;
-  int t = grid_wave(TAIL_WAVES);
-  if (t >= ntiles) return;
+  const int tpr = (int)tail_tiles_per_row(N), ntiles = (int)N * tpr, stride = gridDim.x * TAIL_WAVES;
+  // rounds are workgroup-uniform (the barrier below needs every wave in every round); a wave whose tile is past the
+  // end of a round recomputes the last tile and stores nothing
+  int tb = blockIdx.x * TAIL_WAVES;
+  if (tb >= ntiles) return;  // whole workgroup
+  int t = min(tb + wave, ntiles - 1);
   const int ocg = l >> 1, opc = l & 1;
   // o element offsets are 32-bit (the launcher checks D * N * ld < 2^31): channel rows of this lane, one apart
   const uint32_t ochan = (uint32_t)(4 * ocg) * (uint32_t)N * (uint32_t)ld, orow = (uint32_t)N * (uint32_t)ld;
@@ -267,9 +275,12 @@ __global__ __launch_bounds__(64 * TAIL_WAVES) void trimul_tail_f16_k(
   half8 ob[4];
   typename RG<T>::frag xf[1][STEPS];
   load(t, ob, xf);
-  for (; t < ntiles; t += stride) {
+  for (; tb < ntiles; tb += stride) {
+    const bool live = tb + wave < ntiles;
+    t = live ? tb + wave : ntiles - 1;
+    __syncthreads();
     const int i = t / tpr, j0 = (t - i * tpr) * 16;
-    const int64_t zr = j0 + r < N ? (int64_t)i * N + j0 + r : -1;
+    const int64_t zr = live && j0 + r < N ? (int64_t)i * N + j0 + r : -1;
     const auto zrow = [&](int) { return zr; };
     float* zt = opaque_ptr(z);
     half_t* xnt = opaque_ptr(xn_next);
@@ -785,7 +796,7 @@ static hipError_t tm_tail_f16(const void* o, const float* now, const float* nob,
   static int cache[kMaxDevices];
   const int resident = resident_grid(trimul_tail_f16_k, 64 * TAIL_WAVES, cache);
   if (resident <= 0) return hipErrorInvalidDevice;
-  const int64_t ntiles = N * ((N + 15) / 16);
+  const int64_t ntiles = N * tail_tiles_per_row(N);  // the last tile of a row ends at ld (ld = N rounded up to 64)
   if (ntiles >= (1LL << 30)) return hipErrorInvalidValue;  // tile indices are 32-bit in the kernel
   const dim3 grid((unsigned)std::min<int64_t>(resident, (ntiles + TAIL_WAVES - 1) / TAIL_WAVES));
   trimul_tail_f16_k<<<grid, 64 * TAIL_WAVES, 0, st>>>(static_cast<const half_t*>(o), now, nob, eps_out,

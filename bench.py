@@ -7,9 +7,10 @@ one Pairformer block (layer i % 64 of the trunk, applied in place to the residen
 full trunk pass. Inputs and weights are resident in HBM before the timed region.
 
 Prints one JSON line. `roofline` is for the kernel with the largest share of the timed region, from HIP events
-recorded around every launch on the launch stream; `cpu_baseline` times the numpy oracle (reference-equivalent
-fp32 CPU path) on the N=128 block, N=400 triangle attention and N=800 triangle multiplication configurations and
-estimates one N=1000 block from row samples and FLOP ratios (see cpu_baseline).
+recorded around every launch on the launch stream, against the published peaks (`frac`) and against the GEMM and
+copy rates measured in the same run (`frac_measured`, `measured_ceilings`); `cpu_baseline` times the numpy oracle
+(reference-equivalent fp32 CPU path) on the N=128 block, N=400 triangle attention, N=800 triangle multiplication and
+one diffusion-transformer layer, and estimates one N=1000 block from row samples and FLOP ratios (see cpu_baseline).
 """
 
 from __future__ import annotations
@@ -69,20 +70,64 @@ def profiled_traffic(name: str, N: int):
         return None
 
 
-def roofline_for(name: str, ms: float, N: int) -> dict:
+def roofline_for(name: str, ms: float, N: int, ceilings: dict | None = None) -> dict:
+    """Roofline of one launch against the published peaks; with `ceilings` (measured_ceilings) also the fraction of
+    the rate measured in the same run (frac_measured)."""
     fl, by = kernel_work(name, N)
     traffic = profiled_traffic(name, N)
     t_fl = fl / (MFMA_F16_PEAK_TFLOPS * 1e12)
     t_by = by / (HBM_PEAK_GBS * 1e9)
     if t_fl >= t_by:
         ach = fl / (ms * 1e-3) / 1e12
-        return {"kernel": name, "bound": "mfma", "achieved": round(ach, 2), "peak": MFMA_F16_PEAK_TFLOPS,
-                "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK_TFLOPS, 4), "traffic": traffic,
-                "avg_ms": round(ms, 4), "algorithmic_flop": fl, "algorithmic_bytes": by}
+        out = {"kernel": name, "bound": "mfma", "achieved": round(ach, 2), "peak": MFMA_F16_PEAK_TFLOPS,
+               "unit": "TFLOP/s", "frac": round(ach / MFMA_F16_PEAK_TFLOPS, 4), "traffic": traffic,
+               "avg_ms": round(ms, 4), "algorithmic_flop": fl, "algorithmic_bytes": by}
+        if ceilings:
+            out["frac_measured"] = round(ach / ceilings["gemm_f16_tflops"], 4)
+        return out
     ach = by / (ms * 1e-3) / 1e9
-    return {"kernel": name, "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-            "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic, "avg_ms": round(ms, 4),
-            "algorithmic_flop": fl, "algorithmic_bytes": by}
+    out = {"kernel": name, "bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+           "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": traffic, "avg_ms": round(ms, 4),
+           "algorithmic_flop": fl, "algorithmic_bytes": by}
+    if ceilings:
+        out["frac_measured"] = round(ach / ceilings["copy_gbs"], 4)
+    return out
+
+
+def measured_ceilings(device) -> dict:
+    """Attainable rates measured in the same run: a plain fp16 GEMM through torch (hipBLASLt / rocBLAS), 8192^3,
+    and a 1 GiB device-to-device copy (bytes read + written); best of 10 after 3 warm-ups each."""
+    import torch
+
+    def best_ms(fn, reps=10):
+        for _ in range(3):
+            fn()
+        best = float("inf")
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            fn()
+            b.record()
+            torch.cuda.synchronize()
+            best = min(best, a.elapsed_time(b))
+        return best
+
+    n = 8192
+    g = torch.Generator(device=device).manual_seed(3)
+    x = torch.randn((n, n), generator=g, device=device).half()
+    y = torch.randn((n, n), generator=g, device=device).half()
+    c = torch.empty((n, n), dtype=torch.float16, device=device)
+    t_gemm = best_ms(lambda: torch.matmul(x, y, out=c))
+    del x, y, c
+    src = torch.empty(256 << 20, dtype=torch.float32, device=device).fill_(1.0)
+    dst = torch.empty_like(src)
+    t_copy = best_ms(lambda: dst.copy_(src))
+    nbytes = 2.0 * src.numel() * 4
+    del src, dst
+    torch.cuda.empty_cache()
+    return {"gemm_f16_tflops": round(2.0 * n ** 3 / (t_gemm * 1e-3) / 1e12, 1),
+            "copy_gbs": round(nbytes / (t_copy * 1e-3) / 1e9, 1),
+            "how": "torch fp16 matmul 8192^3 (hipBLASLt/rocBLAS) and a 1 GiB device copy, best of 10"}
 
 
 def make_trunk(N: int, blocks: int, seed: int, device):
@@ -235,7 +280,8 @@ def cpu_baseline(budget_s: float = 25.0) -> dict:
     1 warm-up and the median of up to 5 timed runs (fewer if 5 would exceed budget_s), on the BLAS thread pool the
     environment gives (OMP_NUM_THREADS; numpy's elementwise work is single-threaded).
       C1: one PairformerLayer, N = 128;  C2: triangle attention N = 400 (last 40 padded), starting + ending node;
-      C3: triangle multiplication N = 800, outgoing + incoming.
+      C3: triangle multiplication N = 800, outgoing + incoming;  C5: one diffusion-transformer layer (D 768,
+      16 heads, N = 400, 5 samples), with a sampler-step ESTIMATE of 24 layers.
     value: blocks/s at N = 1000 (ESTIMATE): triangle attention from a row sample at N = 1000 (rows are independent:
     fixed + per-row cost from two sample sizes, times 1000 rows, both nodes), triangle multiplication from C3 scaled
     by its module FLOP ratio 800 -> 1000, the pair transition from a 10^5-row sample (row-wise, times 10), and the s
@@ -298,13 +344,28 @@ def cpu_baseline(budget_s: float = 25.0) -> dict:
 
     t_s = _time_once(s_track)
     t_block = t_att + t_mul + t_tr + t_s
+    del z, xr
+    # C5: one diffusion-transformer layer (D 768, 16 heads x 48) over 5 samples at N = 400; a sampler step is 24 layers
+    from boltz_mlx_amd.layers.transformersv2 import DiffusionTransformer
+    from oracle import diffusion as OD
+
+    pd = synthetic_state(DiffusionTransformer(depth=1, heads=16, dim=768), seed=2, std=0.02)
+    a5 = rng.standard_normal((5, 400, 768), dtype=f32)
+    s5 = rng.standard_normal((5, 400, 768), dtype=f32)
+    b5 = rng.standard_normal((1, 400, 400, 16), dtype=f32)
+    m5 = np.ones((5, 400), f32)
+    m5[:, 380:] = 0
+    t_c5, n = _median_time(lambda: OD.diffusion_transformer(a5, s5, b5, m5, pd, 1, 16, 5), 5, budget_s)
+    cfg["C5_diffusion_layer_N400_5samples"] = {"s": round(t_c5, 4), "runs": n,
+                                               "step_estimate_s": round(24 * t_c5, 3)}
     return {"value": round(1.0 / t_block, 6), "unit": "blocks/s", "cores": int(threads), "kind": "port",
             "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count(),
             "sample": (f"numpy float32 oracle, {threads} BLAS threads; configs (1 warm-up + median): "
                        + ", ".join(f"{k} {v['s']} s (median of {v['runs']})" for k, v in cfg.items())
                        + f"; value = ESTIMATE of one N=1000 block ({t_block:.1f} s): tri-att {t_att:.1f} s "
                          f"(rows {r1}/{r2} sampled), tri-mul {t_mul:.1f} s (C3 x FLOP ratio), transition "
-                         f"{t_tr:.1f} s (1e5-row sample), s track {t_s:.1f} s"),
+                         f"{t_tr:.1f} s (1e5-row sample), s track {t_s:.1f} s; C5 step ESTIMATE = 24 x one "
+                         f"layer ({24 * t_c5:.2f} s)"),
             "configs": cfg}
 
 
@@ -335,7 +396,7 @@ def main() -> int:
                     help="time only the diffusion-transformer leg (for profiling it) and print its JSON line")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="end with one 512 MiB device-to-device copy (the known-size kernel that scales the "
-                         "FETCH_SIZE / WRITE_SIZE counters of rocprofv3 --pmc)")
+                         "FETCH_SIZE / WRITE_SIZE counters of rocprofv3 --pmc); skips the measured ceilings")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -394,12 +455,16 @@ def main() -> int:
             b.copy_(a)
             torch.cuda.synchronize()
             del a, b
+    ceilings = None
+    if not args.calibrate_copy:  # a counter run keeps the calibration copy the only large device copy
+        with torch.no_grad():
+            ceilings = measured_ceilings(dev)
     total = {k: sum(v) for k, v in times.items()}
     dom = max(total, key=total.get)
-    roof = roofline_for(dom, total[dom] / len(times[dom]), args.n)
+    roof = roofline_for(dom, total[dom] / len(times[dom]), args.n, ceilings)
     breakdown = {k: {"ms_total": round(v, 3), "launches": len(times[k]), "share": round(v / sum(total.values()), 4)}
                  for k, v in sorted(total.items(), key=lambda kv: -kv[1])}
-    per_kernel_roof = {k: roofline_for(k, total[k] / len(times[k]), args.n) for k in total
+    per_kernel_roof = {k: roofline_for(k, total[k] / len(times[k]), args.n, ceilings) for k in total
                        if kernel_work(k, args.n)[0] > 0}
     value = args.steps / dt
     out = {
@@ -425,6 +490,7 @@ def main() -> int:
         "kernel_breakdown": breakdown,
         "kernel_roofline": per_kernel_roof,
         "timed_with_events_s": round(dt_ev, 4),
+        "measured_ceilings": ceilings,
     }
     if args.c5_steps:
         with torch.no_grad():

@@ -597,16 +597,19 @@ __global__ __launch_bounds__(256) void transition_k(const T* __restrict__ xn, co
                        lnb, eps, xn_next);
 }
 
-// fp16 transition, persistent: one 512-thread workgroup per CU walks 256-row tiles (8 waves x 32 rows). The hidden
-// dimension streams through LDS in chunks of 32 units (fc1 and fc2 rows, fc3 columns: 24 KB; 4% faster than 64). Chunk q + 1 is loaded
-// into registers while chunk q computes from LDS and is written to the other buffer afterwards, so a chunk costs one
-// barrier and no exposed L2 latency; the buffer written in step q was last read in step q - 1, which every wave
-// finished before the barrier of step q - 1. The chunk sequence runs on across tiles (the weights repeat), and the
-// next tile's rows are loaded during the current tile's last chunk.
-constexpr int TR_WAVES = 8, TR_HCH = 32;
+// fp16 transition, persistent: TRW-wave workgroups (32 rows per wave, 2 waves per SIMD) walk tiles of 32 TRW rows.
+// The hidden dimension streams through LDS in chunks of 32 units (fc1 and fc2 rows, fc3 columns: 24 KB; 4% faster
+// than 64). Chunk q + 1 is loaded into registers while chunk q computes from LDS and is written to the other buffer
+// afterwards, so a chunk costs one barrier and no exposed L2 latency; the buffer written in step q was last read in
+// step q - 1, which every wave finished before the barrier of step q - 1. The chunk sequence runs on across tiles
+// (the weights repeat), and the next tile's rows are loaded during the current tile's last chunk.
+// TRW = 8: one workgroup per CU (large grids). TRW = 4: two per CU, whose barriers are independent, so one can run
+// its row epilogue while the other computes; that wins at N = 400 (0.126 against 0.139 ms) and loses at N = 1000
+// (0.687 against 0.656 ms), where the 256-row tile's fewer weight passes per row count more.
+constexpr int TR_HCH = 32;
 
-template <bool PB>
-__global__ __launch_bounds__(64 * TR_WAVES) void transition_f16_k(const half_t* __restrict__ xn,
+template <bool PB, int TRW>
+__global__ __launch_bounds__(64 * TRW, 8 / TRW) void transition_f16_k(const half_t* __restrict__ xn,
                                                                   const half_t* __restrict__ w12,
                                                                   const half_t* __restrict__ w3,
                                                                   float* __restrict__ z, int accumulate,
@@ -619,7 +622,7 @@ __global__ __launch_bounds__(64 * TR_WAVES) void transition_f16_k(const half_t* 
                                                                   half_t* __restrict__ pb_out, int pb_heads) {
   using T = half_t;
   constexpr int RB = 2, STEPS = RG<T>::STEPS, LDW = ldw_of<T>(), LDH = TR_HCH + Pad<T>::v, HB = TR_HCH / 16;
-  constexpr int TROWS = 16 * RB * TR_WAVES;
+  constexpr int TR_WAVES = TRW, TROWS = 16 * RB * TR_WAVES;
   constexpr int VPM = TR_HCH * 16 / (64 * TR_WAVES), VPT = 3 * VPM;  // 16-byte vectors of a chunk per thread
   constexpr int V3 = TR_HCH / 8;                                       // 16-byte vectors per fc3 row of a chunk
   static_assert(HB % 2 == 0 && VPM >= 1, "chunk shape");
@@ -653,7 +656,7 @@ __global__ __launch_bounds__(64 * TR_WAVES) void transition_f16_k(const half_t* 
     }
   }
 
-  // chunk staging: vector v of thread t is element e = (v % VPM) * 512 + t of matrix v / VPM (fc1, fc2: TR_HCH rows x
+  // chunk staging: vector v of thread t is element e = (v % VPM) * 64 TRW + t of matrix v / VPM (fc1, fc2: TR_HCH rows x
   // 16 vectors; fc3: 128 rows x V3 vectors of the chunk's TR_HCH columns)
   u32x4 pre[VPT];
   // element offsets of the thread's vectors in chunk 0 (chunk c adds c * TR_HCH * D in fc1/fc2, c * TR_HCH in fc3)
@@ -880,21 +883,33 @@ static hipError_t trans_t(const void* xn, const void* w12, const void* w3, float
   return hipGetLastError();
 }
 
+template <bool PB, int TRW>
+static hipError_t trans_f16_w(const void* xn, const void* w12, const void* w3, float* z, int accumulate,
+                              const float* lnw, const float* lnb, float eps, void* xn_next, int64_t rows, int hidden,
+                              const void* pb_w, const float* pb_lnw, const float* pb_lnb, float pb_eps, void* pb_out,
+                              int pb_heads, hipStream_t st) {
+  static int cache[kMaxDevices];
+  const int resident = resident_grid(transition_f16_k<PB, TRW>, 64 * TRW, cache);
+  if (resident <= 0) return hipErrorInvalidDevice;
+  const int64_t ntiles = (rows + 32 * TRW - 1) / (32 * TRW);  // 32 TRW-row tiles
+  const dim3 grid((unsigned)std::min<int64_t>(resident, ntiles));
+  transition_f16_k<PB, TRW><<<grid, 64 * TRW, 0, st>>>(
+      static_cast<const half_t*>(xn), static_cast<const half_t*>(w12), static_cast<const half_t*>(w3), z, accumulate,
+      lnw, lnb, eps, static_cast<half_t*>(xn_next), rows, hidden, static_cast<const half_t*>(pb_w), pb_lnw, pb_lnb,
+      pb_eps, static_cast<half_t*>(pb_out), pb_heads);
+  return hipGetLastError();
+}
+
+// rows below 400,000 (N = 632 for a pair stack) take the two-workgroup form
 template <bool PB>
 static hipError_t trans_f16(const void* xn, const void* w12, const void* w3, float* z, int accumulate,
                             const float* lnw, const float* lnb, float eps, void* xn_next, int64_t rows, int hidden,
                             const void* pb_w, const float* pb_lnw, const float* pb_lnb, float pb_eps, void* pb_out,
                             int pb_heads, hipStream_t st) {
-  static int cache[kMaxDevices];
-  const int resident = resident_grid(transition_f16_k<PB>, 64 * TR_WAVES, cache);
-  if (resident <= 0) return hipErrorInvalidDevice;
-  const int64_t ntiles = (rows + 32 * TR_WAVES - 1) / (32 * TR_WAVES);  // 256-row tiles
-  const dim3 grid((unsigned)std::min<int64_t>(resident, ntiles));
-  transition_f16_k<PB><<<grid, 64 * TR_WAVES, 0, st>>>(
-      static_cast<const half_t*>(xn), static_cast<const half_t*>(w12), static_cast<const half_t*>(w3), z, accumulate,
-      lnw, lnb, eps, static_cast<half_t*>(xn_next), rows, hidden, static_cast<const half_t*>(pb_w), pb_lnw, pb_lnb,
-      pb_eps, static_cast<half_t*>(pb_out), pb_heads);
-  return hipGetLastError();
+  return rows < 400000 ? trans_f16_w<PB, 4>(xn, w12, w3, z, accumulate, lnw, lnb, eps, xn_next, rows, hidden, pb_w,
+                                            pb_lnw, pb_lnb, pb_eps, pb_out, pb_heads, st)
+                       : trans_f16_w<PB, 8>(xn, w12, w3, z, accumulate, lnw, lnb, eps, xn_next, rows, hidden, pb_w,
+                                            pb_lnw, pb_lnb, pb_eps, pb_out, pb_heads, st);
 }
 
 hipError_t launch_transition(const void* xn, const void* w12, const void* w3, float* z, int accumulate,

@@ -247,6 +247,79 @@ def msa_layer_leg(steps: int, device, N: int = 400, S: int = 1024) -> dict:
             "finite": bool(torch.isfinite(zo).all().item() and torch.isfinite(mo).all().item())}
 
 
+def config_legs(device) -> dict:
+    """The module-level configurations on the GPU, each through the reference's module API with random-init weights
+    and seeded inputs: C1 one PairformerLayer in fp32 at N = 128 (all-ones mask); C2 triangle attention, starting +
+    ending node, N = 400 with the last 40 tokens padded, fp16; C3 triangle multiplication, outgoing + incoming,
+    N = 800, fp16. Each: 3 warm-up calls, then the best of 5 timed batches of 5 calls (HIP events); TFLOP/s from the
+    algorithmic counts (C1: the block FLOP; C2: per node 512 N^3 + 164,864 N^2 (core, projection, linear_o);
+    C3: per direction 256 N^3 + 196,608 N^2)."""
+    import torch
+
+    from boltz_mlx_amd import kernels as K
+    from boltz_mlx_amd.layers.pairformer import PairformerLayer
+    from boltz_mlx_amd.layers.triangular_attention.attention import (TriangleAttentionEndingNode,
+                                                                     TriangleAttentionStartingNode)
+    from boltz_mlx_amd.layers.triangular_mult import TriangleMultiplicationIncoming, TriangleMultiplicationOutgoing
+    from boltz_mlx_amd.weights import load_module, synthetic_state
+
+    def best_ms(fn, calls=5, reps=5):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        best = float("inf")
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            for _ in range(calls):
+                fn()
+            b.record()
+            torch.cuda.synchronize()
+            best = min(best, a.elapsed_time(b) / calls)
+        return best
+
+    def module(m, seed):
+        load_module(m, synthetic_state(m, seed))
+        return m.to(device)
+
+    g = torch.Generator(device=device).manual_seed(11)
+    out = {}
+    old = K.PRECISION
+    try:
+        K.set_precision("fp32")
+        N = 128
+        layer = module(PairformerLayer(384, 128, 16), 21)
+        z = torch.randn((1, N, N, 128), generator=g, device=device)
+        s = torch.randn((1, N, 384), generator=g, device=device)
+        tok = torch.ones((1, N), device=device)
+        pm = tok[:, :, None] * tok[:, None, :]
+        ms = best_ms(lambda: layer(s, z, tok, pm))
+        out["C1_block_N128_fp32"] = {"ms": round(ms, 4), "blocks_per_s": round(1e3 / ms, 1),
+                                     "tflops": round(block_flops(N) / (ms * 1e-3) / 1e12, 2)}
+        K.set_precision("f16")
+        N = 400
+        ts, te = module(TriangleAttentionStartingNode(128, 32, 4), 22), module(TriangleAttentionEndingNode(128, 32, 4), 23)
+        z = torch.randn((1, N, N, 128), generator=g, device=device)
+        tok = torch.ones((1, N), device=device)
+        tok[:, N - 40:] = 0
+        pm = tok[:, :, None] * tok[:, None, :]
+        ms = best_ms(lambda: (ts(z, pm), te(z, pm)))
+        fl = 2 * (512.0 * N ** 3 + 164864.0 * N ** 2)
+        out["C2_tri_att_N400_start_end_f16"] = {"ms": round(ms, 4), "tflops": round(fl / (ms * 1e-3) / 1e12, 2)}
+        N = 800
+        mo, mi = module(TriangleMultiplicationOutgoing(128), 24), module(TriangleMultiplicationIncoming(128), 25)
+        z = torch.randn((1, N, N, 128), generator=g, device=device)
+        pm = torch.ones((1, N, N), device=device)
+        ms = best_ms(lambda: (mo(z, pm), mi(z, pm)))
+        fl = 2 * (256.0 * N ** 3 + 196608.0 * N ** 2)
+        out["C3_tri_mul_N800_out_in_f16"] = {"ms": round(ms, 4), "tflops": round(fl / (ms * 1e-3) / 1e12, 2)}
+        del z, pm
+        torch.cuda.empty_cache()
+    finally:
+        K.set_precision(old)
+    return out
+
+
 def _median_time(fn, reps: int, budget_s: float):
     """1 warm-up call, then up to `reps` timed calls (fewer when the warm-up shows they would exceed budget_s;
     at least 1); returns (median seconds, timed calls)."""
@@ -391,6 +464,7 @@ def main() -> int:
     ap.add_argument("--c5-steps", type=int, default=20,
                     help="diffusion-transformer sampler steps timed after the trunk (0: skip)")
     ap.add_argument("--msa-steps", type=int, default=5, help="MSA-block layer calls timed after the trunk (0: skip)")
+    ap.add_argument("--no-configs", action="store_true", help="skip the C1 / C2 / C3 module timings")
     ap.add_argument("--msa-only", action="store_true", help="time only the MSA-block leg and print its JSON line")
     ap.add_argument("--c5-only", action="store_true",
                     help="time only the diffusion-transformer leg (for profiling it) and print its JSON line")
@@ -498,6 +572,9 @@ def main() -> int:
     if args.msa_steps:
         with torch.no_grad():
             out["msa_layer"] = msa_layer_leg(args.msa_steps, dev)
+    if not args.no_configs and not args.calibrate_copy:
+        with torch.no_grad():
+            out["config_legs"] = config_legs(dev)
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(args.cpu_budget)
     print(json.dumps(out), flush=True)

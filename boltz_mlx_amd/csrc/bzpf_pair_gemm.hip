@@ -24,15 +24,17 @@ template <typename T> constexpr int ldw_of() { return D + Pad<T>::v; }
 // ---------------------------------------------------------------- triangle multiplication projection
 // Persistent, one 512-thread workgroup per CU (8 waves, up to 256 VGPRs each). The launch covers output channels
 // [c_lo, c_lo + PCH): the projection rows c_lo.. and gate rows 2D + c_lo.. of w (PCH = 256 in fp16: all of them;
-// 128 in fp32, two launches) are staged in LDS once; each wave then streams tiles of 2 TW positions
-// (i, k0 .. k0 + 2 TW) over the padded rows of length ld as two halves of TW, computing (ROWS orientation) two
-// 16-byte runs per channel: a whole 128-byte line of ab[c][i][k] (fp16) per channel row and tile, written by one
-// wave with two adjacent stores (incoming: xn read at (k, i)). The next tile's rows and mask values are loaded
-// while the current tile computes (8 waves with the prefetch measured 3-4% faster than 12 without).
+// 128 in fp32, two launches) are staged in LDS once; each wave then streams tiles of HV TW positions
+// (i, k0 .. k0 + HV TW) over the padded rows of length ld as HV halves of TW, computing (ROWS orientation) one
+// 16-byte run per channel and half: with HV = 2 a whole 128-byte line of ab[c][i][k] (fp16) per channel row and
+// tile, written by one wave with two adjacent stores (incoming: xn read at (k, i)). The next tile's rows and mask
+// values are loaded while the current tile computes (8 waves with the prefetch measured 3-4% faster than 12
+// without). HV = 1 (half tiles) is taken when it balances the last round of tiles better: at N = 400 (2,800 full
+// tiles on 2,048 waves) 0.041-0.045 against 0.050 ms; at N = 1000 full tiles are faster (0.23 against 0.26 ms).
 template <typename T> constexpr int proj_ch() { return sizeof(T) == 2 ? 256 : 128; }
 constexpr int PROJ_WAVES = 8;
 
-template <typename T>
+template <typename T, int HV>
 __global__ __launch_bounds__(64 * PROJ_WAVES) void trimul_proj_k(const T* __restrict__ xn, const T* __restrict__ w,
                                                                  const float* __restrict__ mask, float scale,
                                                                  int incoming, T* __restrict__ ab, int64_t N,
@@ -44,17 +46,17 @@ __global__ __launch_bounds__(64 * PROJ_WAVES) void trimul_proj_k(const T* __rest
               [&](int r) { return w + (int64_t)(r < PCH ? c_lo + r : 2 * D + c_lo + r - PCH) * D; });
   __syncthreads();
   const int l = threadIdx.x & 63, g = l >> 4, r = l & 15;
-  const int tpr = (int)(ld / (2 * TW)), ntiles = (int)N * tpr, stride = gridDim.x * PROJ_WAVES;
+  const int tpr = (int)(ld / (HV * TW)), ntiles = (int)N * tpr, stride = gridDim.x * PROJ_WAVES;
   int t = grid_wave(PROJ_WAVES);
   if (t >= ntiles) return;
 
   typedef typename RG<T>::frag Frag;
-  Frag x[2][RB][STEPS];
-  float mk[2][RB];  // mask * scale of the rows this lane loads (0 past N: padding columns are written as 0)
-  const auto load = [&](int tt, Frag (&xx)[2][RB][STEPS], float (&mm)[2][RB]) {
-    const int i = tt / tpr, k0 = (tt - i * tpr) * 2 * TW;
+  Frag x[HV][RB][STEPS];
+  float mk[HV][RB];  // mask * scale of the rows this lane loads (0 past N: padding columns are written as 0)
+  const auto load = [&](int tt, Frag (&xx)[HV][RB][STEPS], float (&mm)[HV][RB]) {
+    const int i = tt / tpr, k0 = (tt - i * tpr) * HV * TW;
 #pragma unroll
-    for (int hh = 0; hh < 2; hh++)
+    for (int hh = 0; hh < HV; hh++)
 #pragma unroll
       for (int rb = 0; rb < RB; rb++) {
         const int64_t k = k0 + hh * TW + RT::pos(rb, r), kc = k < N ? k : N - 1;
@@ -65,13 +67,13 @@ __global__ __launch_bounds__(64 * PROJ_WAVES) void trimul_proj_k(const T* __rest
   };
   load(t, x, mk);
   for (; t < ntiles; t += stride) {
-    Frag xnx[2][RB][STEPS];
-    float mkn[2][RB];
+    Frag xnx[HV][RB][STEPS];
+    float mkn[HV][RB];
     load(min(t + stride, ntiles - 1), xnx, mkn);
-    const int i = t / tpr, k0 = (t - i * tpr) * 2 * TW;
-    float mo[2][RB][4];  // mask of this lane's output positions RUN g + 4 rb + e of each half, from lane 4 g + e
+    const int i = t / tpr, k0 = (t - i * tpr) * HV * TW;
+    float mo[HV][RB][4];  // mask of this lane's output positions RUN g + 4 rb + e of each half, from lane 4 g + e
 #pragma unroll
-    for (int hh = 0; hh < 2; hh++)
+    for (int hh = 0; hh < HV; hh++)
 #pragma unroll
       for (int rb = 0; rb < RB; rb++)
 #pragma unroll
@@ -79,7 +81,7 @@ __global__ __launch_bounds__(64 * PROJ_WAVES) void trimul_proj_k(const T* __rest
     T* dst = ab + ((int64_t)(c_lo + r) * N + i) * ld + k0 + RT::RUN * g;
     for (int cb = 0; cb < PCH / 16; cb++) {
 #pragma unroll
-      for (int hh = 0; hh < 2; hh++) {
+      for (int hh = 0; hh < HV; hh++) {
         f4 pa[RB][1], ga[RB][1];
         zero_acc(pa);
         zero_acc(ga);
@@ -95,7 +97,7 @@ __global__ __launch_bounds__(64 * PROJ_WAVES) void trimul_proj_k(const T* __rest
       __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
-    for (int hh = 0; hh < 2; hh++)
+    for (int hh = 0; hh < HV; hh++)
 #pragma unroll
       for (int rb = 0; rb < RB; rb++) {
         mk[hh][rb] = mkn[hh][rb];
@@ -759,22 +761,34 @@ __global__ __launch_bounds__(64 * TRW, 8 / TRW) void transition_f16_k(const half
 
 // ---------------------------------------------------------------- launchers
 
-template <typename T>
-static hipError_t tm_proj(const void* xn, const void* w, const float* mask, float scale, int incoming, void* ab,
-                          int64_t N, int64_t ld, hipStream_t st) {
-  static int cache[kMaxDevices];
-  const int resident = resident_grid(trimul_proj_k<T>, 64 * PROJ_WAVES, cache);
-  if (resident <= 0) return hipErrorInvalidDevice;
-  const int64_t ntiles = N * (ld / (2 * RunTile<T>::TW));  // ld is a multiple of 64
+template <typename T, int HV>
+static hipError_t tm_proj_hv(const void* xn, const void* w, const float* mask, float scale, int incoming, void* ab,
+                             int64_t N, int64_t ld, int resident, hipStream_t st) {
+  const int64_t ntiles = N * (ld / (HV * RunTile<T>::TW));  // ld is a multiple of 64
   if (ntiles >= (1LL << 30)) return hipErrorInvalidValue;  // tile indices are 32-bit in the kernel
   const dim3 grid((unsigned)std::min<int64_t>(resident, (ntiles + PROJ_WAVES - 1) / PROJ_WAVES));
   for (int c_lo = 0; c_lo < 2 * D; c_lo += proj_ch<T>()) {
-    trimul_proj_k<T><<<grid, 64 * PROJ_WAVES, 0, st>>>(static_cast<const T*>(xn), static_cast<const T*>(w), mask, scale,
-                                            incoming, static_cast<T*>(ab), N, ld, c_lo);
+    trimul_proj_k<T, HV><<<grid, 64 * PROJ_WAVES, 0, st>>>(static_cast<const T*>(xn), static_cast<const T*>(w), mask,
+                                                          scale, incoming, static_cast<T*>(ab), N, ld, c_lo);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
+}
+
+template <typename T>
+static hipError_t tm_proj(const void* xn, const void* w, const float* mask, float scale, int incoming, void* ab,
+                          int64_t N, int64_t ld, hipStream_t st) {
+  static int cache[kMaxDevices];
+  // both tile forms have the same resources (the LDS weights and 8 waves set the occupancy)
+  const int resident = resident_grid(trimul_proj_k<T, 2>, 64 * PROJ_WAVES, cache);
+  if (resident <= 0) return hipErrorInvalidDevice;
+  // rounds of full tiles on the resident waves, against rounds of half tiles (counted in full tiles, with 10% for
+  // the half tile's own overhead)
+  const int64_t waves = (int64_t)resident * PROJ_WAVES, full = N * (ld / (2 * RunTile<T>::TW));
+  const int64_t r2 = (full + waves - 1) / waves, r1x2 = (2 * full + waves - 1) / waves;
+  return 10 * r1x2 < 18 * r2 ? tm_proj_hv<T, 1>(xn, w, mask, scale, incoming, ab, N, ld, resident, st)
+                             : tm_proj_hv<T, 2>(xn, w, mask, scale, incoming, ab, N, ld, resident, st);
 }
 
 hipError_t launch_trimul_proj(const void* xn, const void* w, const float* mask, float scale, int incoming, void* ab,

@@ -465,6 +465,7 @@ def main() -> int:
                     help="diffusion-transformer sampler steps timed after the trunk (0: skip)")
     ap.add_argument("--msa-steps", type=int, default=5, help="MSA-block layer calls timed after the trunk (0: skip)")
     ap.add_argument("--no-configs", action="store_true", help="skip the C1 / C2 / C3 module timings")
+    ap.add_argument("--no-ceilings", action="store_true", help="skip the measured GEMM / copy ceilings")
     ap.add_argument("--msa-only", action="store_true", help="time only the MSA-block leg and print its JSON line")
     ap.add_argument("--c5-only", action="store_true",
                     help="time only the diffusion-transformer leg (for profiling it) and print its JSON line")
@@ -530,7 +531,7 @@ def main() -> int:
             torch.cuda.synchronize()
             del a, b
     ceilings = None
-    if not args.calibrate_copy:  # a counter run keeps the calibration copy the only large device copy
+    if not (args.calibrate_copy or args.no_ceilings):  # a counter run keeps the calibration copy the only large copy
         with torch.no_grad():
             ceilings = measured_ceilings(dev)
     total = {k: sum(v) for k, v in times.items()}

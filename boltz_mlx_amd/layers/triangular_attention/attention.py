@@ -70,7 +70,8 @@ class TriangleAttention(torch.nn.Module):
         # the projection reads xn at the attention frame's position: transposed for the ending node unless the
         # caller already transposed it
         proj_trans = trans and not xn_transposed
-        if D != 128:  # the projection and output kernels are built for 128 channels: GEMMs plus layout kernels
+        if D != 128 or H * C != D:  # the fused projection / output kernels are built for 128 = H * C channels:
+            # otherwise GEMMs plus layout kernels (the core takes C = 16, 32 or 64)
             qkg, vt, tb = K.triattn_pack(K.linear(xn, w), proj_trans, N, H, C)
             if before_core is not None:
                 before_core()

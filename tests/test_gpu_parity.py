@@ -184,6 +184,25 @@ def test_tri_att(precision, starting, N):
 
 
 @pytest.mark.parametrize("precision", ["fp32", "f16"], indirect=True)
+@pytest.mark.parametrize("starting", [True, False])
+@pytest.mark.parametrize("N", [17, 117])
+def test_tri_att_other_head_shape(precision, starting, N):
+    """3 heads of 16 channels at c_in = 128 (H * C != c_in, as in the reference's layer test,
+    tests/test_triatt_mma.py:98): the GEMM + layout path and the VALU core (C = 16)."""
+    from boltz_mlx_amd.layers.triangular_attention.attention import (TriangleAttentionEndingNode,
+                                                                     TriangleAttentionStartingNode)
+
+    D, C, H = 128, 16, 3
+    p = rand_params(shapes_tri_att(D, C, H), seed=300 + N, std=0.1)
+    x, _, pm = pair_inputs(N, D, seed=N + 9, n_pad=N // 6)
+    pm[0, 3, 1] = 0
+    ref = O.tri_att(x.astype(np.float32), pm.astype(np.float32), cast(p, np.float32), starting, row_chunk=16)
+    mod = load(TriangleAttentionStartingNode(D, C, H) if starting else TriangleAttentionEndingNode(D, C, H), p)
+    got = mod(dev(x), dev(pm)).cpu().numpy()
+    check(f"tri_att_H3C16_{'start' if starting else 'end'} N={N}", got, ref, precision)
+
+
+@pytest.mark.parametrize("precision", ["fp32", "f16"], indirect=True)
 @pytest.mark.parametrize("dim,rows", [(128, 1), (128, 37), (128, 4111), (384, 5), (384, 300)])
 def test_transition(precision, dim, rows):
     from boltz_mlx_amd.layers.transition import Transition

@@ -674,13 +674,22 @@ __global__ __launch_bounds__(64 * TRW, 8 / TRW) void transition_f16_k(const half
     for (int v = 0; v < VPT; v++)
       pre[v] = *reinterpret_cast<const u32x4*>(v < 2 * VPM ? w12 + (goff[v] + h12) : w3 + (goff[v] + h3));
   };
+  // fc3 columns are stored permuted within each 32-column group: column 16 hi + 4 gg + e (gg < 4, e < 4) sits at
+  // 8 gg + 4 hi + e, so the 8 columns lane group g multiplies (4 g .. 4 g + 3 and 16 + 4 g .. 16 + 4 g + 3, in
+  // that k order) are one 16-byte read; a staged 16-byte vector (8 columns) splits into two 8-byte halves.
   const auto lstore = [&](int buf) {
 #pragma unroll
     for (int v = 0; v < VPT; v++) {
       const int m = v / VPM, e = (v % VPM) * (64 * TR_WAVES) + t;
-      T* dst = m == 0 ? W1s[buf] + (e >> 4) * LDW + (e & 15) * 8
-                      : (m == 1 ? W2s[buf] + (e >> 4) * LDW + (e & 15) * 8 : W3s[buf] + (e / V3) * LDH + (e % V3) * 8);
-      *reinterpret_cast<u32x4*>(dst) = pre[v];
+      if (m < 2) {
+        T* dst = (m == 0 ? W1s[buf] : W2s[buf]) + (e >> 4) * LDW + (e & 15) * 8;
+        *reinterpret_cast<u32x4*>(dst) = pre[v];
+      } else {
+        const int u = e % V3, ug = u & 3;  // vector u holds columns 8 u .. 8 u + 7
+        T* dst = W3s[buf] + (e / V3) * LDH + 32 * (u >> 2) + 16 * (ug & 1) + 4 * (ug >> 1);
+        *reinterpret_cast<uint2*>(dst) = uint2{pre[v][0], pre[v][1]};
+        *reinterpret_cast<uint2*>(dst + 8) = uint2{pre[v][2], pre[v][3]};
+      }
     }
   };
   const auto xload = [&](int64_t tl, typename RG<T>::frag (&xx)[RB][STEPS]) {
@@ -730,10 +739,7 @@ __global__ __launch_bounds__(64 * TRW, 8 / TRW) void transition_f16_k(const half
           }
 #pragma unroll
         for (int ob = 0; ob < 8; ob++) {
-          const T* wr = W3s[buf] + (16 * ob + (l & 15)) * LDH + 32 * m + 4 * g;
-          const half4 lo = *reinterpret_cast<const half4*>(wr);
-          const half4 hi = *reinterpret_cast<const half4*>(wr + 16);
-          const half8 af = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          const half8 af = *reinterpret_cast<const half8*>(W3s[buf] + (16 * ob + (l & 15)) * LDH + 32 * m + 8 * g);
 #pragma unroll
           for (int rb = 0; rb < RB; rb++)
             out[rb][ob] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[rb], out[rb][ob], 0, 0, 0);

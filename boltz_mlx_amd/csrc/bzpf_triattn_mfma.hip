@@ -215,7 +215,16 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
       for (int e = 0; e < 8; e++)
         if (k0 + vk8 + e >= N) vreg[e] = (half_t)0.0f;
     }
-    *reinterpret_cast<half8*>(Vb + vd * LDV + vk8) = vreg;
+    {
+      // keys 8 u .. 8 u + 7 (u = vk8 / 8) go to two 4-key runs: within each 16-key slab, key 8 a + 4 h + e sits at
+      // 8 h + 4 a + e, so the 8 keys a lane half multiplies (4 hl .. 4 hl + 3, 8 + 4 hl .. 8 + 4 hl + 3) are one
+      // 16-byte read
+      const int u = vk8 >> 3;
+      half_t* vd0 = Vb + vd * LDV + 16 * (u >> 1) + 4 * (u & 1);
+      const u32x4_t vw = __builtin_bit_cast(u32x4_t, vreg);
+      *reinterpret_cast<uint2*>(vd0) = uint2{vw[0], vw[1]};
+      *reinterpret_cast<uint2*>(vd0 + 8) = uint2{vw[2], vw[3]};
+    }
     // key-mask bias of key k0 + l (keys past N: -inf); uniform across waves, so each wave decides by itself
     const float mbias = k0 + l < N ? fmaf(mraw, infl, -infl) : -INFINITY;
     const bool masked = __any(mbias != 0.0f);
@@ -303,10 +312,7 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
 #pragma unroll
       for (int sl = 0; sl < 2; sl++) {
         // keys 32 kt + 16 sl + {4 hl .. 4 hl + 3, 8 + 4 hl .. 8 + 4 hl + 3}: accumulator elements 8 sl .. 8 sl + 7
-        const half_t* vr = Vb + qi * LDV + 32 * kt + 16 * sl + 4 * hl;
-        const half4 lo = *reinterpret_cast<const half4*>(vr);
-        const half4 hi4 = *reinterpret_cast<const half4*>(vr + 8);
-        const half8 vf = half8{lo[0], lo[1], lo[2], lo[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+        const half8 vf = *reinterpret_cast<const half8*>(Vb + qi * LDV + 32 * kt + 16 * sl + 8 * hl);
         oacc = __builtin_amdgcn_mfma_f32_32x32x16_f16(vf, pf[sl], oacc, 0, 0, 0);
       }
     }

@@ -214,6 +214,34 @@ int bzpf_transition_pb(const void* xn, const void* w12, const void* w3, float* z
               "bzpf_transition_pb");
 }
 
+int bzpf_attn_out_transition(const void* o, const void* w_o, int trans, const float* ln_w, const float* ln_b,
+                             float ln_eps, const void* w12, const void* w3, float* z, const float* next_w,
+                             const float* next_b, float next_eps, void* xn_next, const void* pb_w,
+                             const float* pb_lnw, const float* pb_lnb, float pb_eps, void* pb_out, int pb_heads, int dt,
+                             int64_t N, int D, int hidden, void* stream) {
+  REQUIRE_PTR(o);
+  REQUIRE_PTR(w_o);
+  REQUIRE(ln_w != nullptr && ln_b != nullptr, "bzpf_attn_out_transition: NULL LayerNorm pointer");
+  REQUIRE_PTR(w12);
+  REQUIRE_PTR(w3);
+  REQUIRE_PTR(z);
+  REQUIRE(next_w == nullptr || (next_b != nullptr && xn_next != nullptr),
+          "bzpf_attn_out_transition: next LN needs next_b and xn_next");
+  REQUIRE(pb_w == nullptr || (pb_lnw != nullptr && pb_lnb != nullptr && pb_out != nullptr),
+          "bzpf_attn_out_transition: pair bias needs pb_lnw, pb_lnb and pb_out");
+  REQUIRE(pb_w == nullptr || (pb_heads >= 1 && pb_heads <= 16), "bzpf_attn_out_transition: 1 <= heads <= 16 (got %d)",
+          pb_heads);
+  REQUIRE(dt == BZPF_F16, "bzpf_attn_out_transition: fp16 only (dt=%d)", dt);
+  REQUIRE(D == 128 && hidden >= 64 && hidden % 64 == 0,
+          "bzpf_attn_out_transition: need D=128, hidden %% 64 == 0 (D=%d H=%d)", D, hidden);
+  REQUIRE(N >= 0 && N <= 46340, "bzpf_attn_out_transition: bad N=%lld", (long long)N);
+  if (N == 0) return BZPF_OK;
+  return done(bzpf::launch_attn_out_transition(o, w_o, trans, ln_w, ln_b, ln_eps, w12, w3, z, next_w, next_b, next_eps,
+                                               xn_next, pb_w, pb_lnw, pb_lnb, pb_eps, pb_out, pb_heads, N, hidden,
+                                               S(stream)),
+              "bzpf_attn_out_transition");
+}
+
 int bzpf_linear(const void* x, const void* w, const float* bias, void* y, int dt, int y_dt, int64_t rows, int K,
                 int M, int accumulate, void* stream) {
   REQUIRE_PTR(x);

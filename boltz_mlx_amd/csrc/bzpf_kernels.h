@@ -43,6 +43,11 @@ hipError_t launch_transition_pb(const void* xn, const void* w12, const void* w3,
                                 const float* lnw, const float* lnb, float eps, void* xn_next, const void* pb_w,
                                 const float* pb_lnw, const float* pb_lnb, float pb_eps, void* pb_out, int pb_heads,
                                 int dt, int64_t rows, int hidden, hipStream_t st);
+hipError_t launch_attn_out_transition(const void* o, const void* w_o, int trans, const float* ln_w, const float* ln_b,
+                                      float ln_eps, const void* w12, const void* w3, float* z, const float* next_w,
+                                      const float* next_b, float next_eps, void* xn_next, const void* pb_w,
+                                      const float* pb_lnw, const float* pb_lnb, float pb_eps, void* pb_out,
+                                      int pb_heads, int64_t N, int hidden, hipStream_t st);
 
 hipError_t launch_linear(const void* x, const void* w, const float* bias, void* y, int dt, int y_dt, int64_t rows,
                          int K, int M, int epi, hipStream_t st);

@@ -610,7 +610,21 @@ __global__ __launch_bounds__(256) void transition_k(const T* __restrict__ xn, co
 // (0.687 against 0.656 ms), where the 256-row tile's fewer weight passes per row count more.
 constexpr int TR_HCH = 32;
 
-template <bool PB, int TRW>
+// AO: the ending-node attention's output stage runs in front (attn_out_rows): the kernel reads the attention core's
+// output o (row of position (i, j) at (j, i) when trans) instead of xn, adds o W_o^T to z, and feeds LN(z) with
+// the transition's own norm to the chunk loop from registers. z is written once in between and read back by the
+// epilogue; the separate kernel's xn round trip through memory is gone.
+struct AttnOutArgs {
+  const half_t* o;
+  const half_t* w_o;  // [128][128]
+  int trans;
+  int64_t n;  // tokens: rows_total = n * n
+  const float* lnw;
+  const float* lnb;
+  float eps;
+};
+
+template <bool PB, int TRW, bool AO = false>
 __global__ __launch_bounds__(64 * TRW, 8 / TRW) void transition_f16_k(const half_t* __restrict__ xn,
                                                                   const half_t* __restrict__ w12,
                                                                   const half_t* __restrict__ w3,
@@ -621,7 +635,8 @@ __global__ __launch_bounds__(64 * TRW, 8 / TRW) void transition_f16_k(const half
                                                                   int hidden, const half_t* __restrict__ pb_w,
                                                                   const float* __restrict__ pb_lnw,
                                                                   const float* __restrict__ pb_lnb, float pb_eps,
-                                                                  half_t* __restrict__ pb_out, int pb_heads) {
+                                                                  half_t* __restrict__ pb_out, int pb_heads,
+                                                                  AttnOutArgs ao) {
   using T = half_t;
   constexpr int RB = 2, STEPS = RG<T>::STEPS, LDW = ldw_of<T>(), LDH = TR_HCH + Pad<T>::v, HB = TR_HCH / 16;
   constexpr int TR_WAVES = TRW, TROWS = 16 * RB * TR_WAVES;
@@ -636,12 +651,15 @@ __global__ __launch_bounds__(64 * TRW, 8 / TRW) void transition_f16_k(const half
   constexpr int LDP = D + 8;
   __shared__ LDS_ALIGN T Wpb[PB ? 16 * LDP : 8];
   __shared__ float Bpb[16];
+  __shared__ LDS_ALIGN T Wo[AO ? D * LDW : 8];
+  __shared__ LDS_ALIGN T Scr[AO ? TRW * 16 * SCR_P : 8];  // per wave: 16 rows of the attention stage's LayerNorm
   const int t = threadIdx.x, l = t & 63, g = l >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int nch = hidden / TR_HCH;
   const int64_t ntiles = (rows_total + TROWS - 1) / TROWS;
   int64_t tile = blockIdx.x;
   if (tile >= ntiles) return;  // whole workgroup
+  if constexpr (AO) lds_rows<T>(Wo, LDW, D, D, [&](int r) { return ao.w_o + (int64_t)r * D; });
   if constexpr (PB) {
     for (int e = t; e < 16 * D; e += 64 * TR_WAVES) {
       const int h = e >> 7, c = e & (D - 1);
@@ -695,8 +713,13 @@ __global__ __launch_bounds__(64 * TRW, 8 / TRW) void transition_f16_k(const half
   const auto xload = [&](int64_t tl, typename RG<T>::frag (&xx)[RB][STEPS]) {
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) {
-      const int64_t row = tl * TROWS + wave * 16 * RB + 16 * rb + (l & 15);
-      RG<T>::load_row(xx[rb], xn + (row < rows_total ? row : rows_total - 1) * D, g);
+      const int64_t row = tl * TROWS + wave * 16 * RB + 16 * rb + (l & 15), rc = row < rows_total ? row : rows_total - 1;
+      if constexpr (AO) {
+        const int64_t orow = ao.trans ? (rc % ao.n) * ao.n + rc / ao.n : rc;
+        RG<T>::load_row(xx[rb], ao.o + orow * D, g);
+      } else {
+        RG<T>::load_row(xx[rb], xn + rc * D, g);
+      }
     }
   };
 
@@ -708,6 +731,11 @@ __global__ __launch_bounds__(64 * TRW, 8 / TRW) void transition_f16_k(const half
   gload(nch > 1 ? 1 : 0);
   int q = 0;  // chunks computed so far (LDS buffer parity)
   for (; tile < ntiles; tile += gridDim.x) {
+    if constexpr (AO) {
+      const int64_t r0 = tile * TROWS + wave * 16 * RB + (l & 15);
+      attn_out_rows<RB>(x, Wo, LDW, [&](int rb) -> int64_t { return r0 + 16 * rb < rows_total ? r0 + 16 * rb : -1; },
+                        z, ao.lnw, ao.lnb, ao.eps, Scr + wave * 16 * SCR_P);
+    }
     f4 out[RB][8];
     zero_acc(out);
     typename RG<T>::frag xnext[RB][STEPS];
@@ -903,20 +931,20 @@ static hipError_t trans_t(const void* xn, const void* w12, const void* w3, float
   return hipGetLastError();
 }
 
-template <bool PB, int TRW>
+template <bool PB, int TRW, bool AO = false>
 static hipError_t trans_f16_w(const void* xn, const void* w12, const void* w3, float* z, int accumulate,
                               const float* lnw, const float* lnb, float eps, void* xn_next, int64_t rows, int hidden,
                               const void* pb_w, const float* pb_lnw, const float* pb_lnb, float pb_eps, void* pb_out,
-                              int pb_heads, hipStream_t st) {
+                              int pb_heads, hipStream_t st, const AttnOutArgs& ao = AttnOutArgs{}) {
   static int cache[kMaxDevices];
-  const int resident = resident_grid(transition_f16_k<PB, TRW>, 64 * TRW, cache);
+  const int resident = resident_grid(transition_f16_k<PB, TRW, AO>, 64 * TRW, cache);
   if (resident <= 0) return hipErrorInvalidDevice;
   const int64_t ntiles = (rows + 32 * TRW - 1) / (32 * TRW);  // 32 TRW-row tiles
   const dim3 grid((unsigned)std::min<int64_t>(resident, ntiles));
-  transition_f16_k<PB, TRW><<<grid, 64 * TRW, 0, st>>>(
+  transition_f16_k<PB, TRW, AO><<<grid, 64 * TRW, 0, st>>>(
       static_cast<const half_t*>(xn), static_cast<const half_t*>(w12), static_cast<const half_t*>(w3), z, accumulate,
       lnw, lnb, eps, static_cast<half_t*>(xn_next), rows, hidden, static_cast<const half_t*>(pb_w), pb_lnw, pb_lnb,
-      pb_eps, static_cast<half_t*>(pb_out), pb_heads);
+      pb_eps, static_cast<half_t*>(pb_out), pb_heads, ao);
   return hipGetLastError();
 }
 
@@ -955,6 +983,26 @@ hipError_t launch_transition_pb(const void* xn, const void* w12, const void* w3,
   const hipError_t e = launch_transition(xn, w12, w3, z, accumulate, lnw, lnb, eps, xn_next, dt, rows, hidden, st);
   if (e != hipSuccess) return e;
   return launch_pair_bias(z, pb_lnw, pb_lnb, pb_eps, pb_w, pb_out, dt, rows, pb_heads, st);
+}
+
+// The ending-node attention's output stage fused in front of the transition (fp16): one 8-wave workgroup per CU
+// (its LDS holds W_o and the LayerNorm scratch next to the weight chunks).
+hipError_t launch_attn_out_transition(const void* o, const void* w_o, int trans, const float* ln_w, const float* ln_b,
+                                      float ln_eps, const void* w12, const void* w3, float* z, const float* next_w,
+                                      const float* next_b, float next_eps, void* xn_next, const void* pb_w,
+                                      const float* pb_lnw, const float* pb_lnb, float pb_eps, void* pb_out,
+                                      int pb_heads, int64_t N, int hidden, hipStream_t st) {
+  if (hidden % TR_HCH || hidden < 2 * TR_HCH || (int64_t)2 * hidden * D >= (1LL << 31) || N < 1)
+    return hipErrorInvalidValue;
+  const AttnOutArgs ao{static_cast<const half_t*>(o), static_cast<const half_t*>(w_o), trans, N, ln_w, ln_b, ln_eps};
+  const int64_t rows = N * N;
+  if (pb_w != nullptr) {
+    if (pb_heads < 1 || pb_heads > 16) return hipErrorInvalidValue;
+    return trans_f16_w<true, 8, true>(nullptr, w12, w3, z, 1, next_w, next_b, next_eps, xn_next, rows, hidden, pb_w,
+                                      pb_lnw, pb_lnb, pb_eps, pb_out, pb_heads, st, ao);
+  }
+  return trans_f16_w<false, 8, true>(nullptr, w12, w3, z, 1, next_w, next_b, next_eps, xn_next, rows, hidden, nullptr,
+                                     nullptr, nullptr, 0.f, nullptr, 0, st, ao);
 }
 
 }  // namespace bzpf

@@ -237,6 +237,57 @@ __device__ __forceinline__ void resid_ln_rows(const f4 (&y)[RB][8], ZRow zrow, f
   resid_ln_apply<TO, RB>(y, zv, zrow, z, lnw, lnb, eps, xn_next);
 }
 
+// The triangle attention's output stage run in front of a fused transition, on RB row blocks of 16 rows: y = W_o o^T
+// (x holds the o rows as B fragments, W_o [128][ldw] in LDS), z[zr] += y (stored), then x <- LN(z[zr]) in fp16 as
+// B fragments again (the transition's input). The LayerNorm output leaves the accumulator layout (lane: 4 channels
+// of each 16-channel block) through a wave-private LDS scratch of 16 rows (pitch SCR_P halves), written and read
+// back by the same wave in program order, so it needs no barrier; the arithmetic is resid_ln_apply's, so x equals
+// the fp16 rows that kernel would have written.
+constexpr int SCR_P = 144;
+template <int RB, typename ZRow>
+__device__ __forceinline__ void attn_out_rows(RG<half_t>::frag (&x)[RB][4], const half_t* Wo, int ldw, ZRow zrow,
+                                              float* __restrict__ z, const float* __restrict__ lnw,
+                                              const float* __restrict__ lnb, float eps, half_t* scr) {
+  constexpr int D = 128;
+  const int l = threadIdx.x & 63, g = l >> 4, r = l & 15;
+  f4 y[RB][8];
+  zero_acc(y);
+  mma_rows_grouped<half_t, RB, 8, 2>(y, x, Wo, ldw);
+  f4 zv[RB][8];
+  load_z_rows<RB>(zv, zrow, z, 1);
+#pragma unroll
+  for (int rb = 0; rb < RB; rb++) {
+    const int64_t zr = zrow(rb);
+    float* zp = z + (zr >= 0 ? zr : 0) * D + 4 * g;
+    f4 v[8];
+    float s = 0.f;
+#pragma unroll
+    for (int cb = 0; cb < 8; cb++) {
+      v[cb] = y[rb][cb] + zv[rb][cb];
+      s += v[cb][0] + v[cb][1] + v[cb][2] + v[cb][3];
+    }
+    if (zr >= 0) {
+#pragma unroll
+      for (int cb = 0; cb < 8; cb++) *reinterpret_cast<f4*>(zp + 16 * cb) = v[cb];  // read back by the epilogue
+    }
+    const float mean = xgroups_sum(s) * (1.0f / D);
+    float ss = 0.f;
+#pragma unroll
+    for (int cb = 0; cb < 8; cb++) {
+      const f4 d = v[cb] - mean;
+      ss += d[0] * d[0] + d[1] * d[1] + d[2] * d[2] + d[3] * d[3];
+    }
+    const float rstd = 1.0f / sqrtf(xgroups_sum(ss) * (1.0f / D) + eps);
+    half_t* sw = scr + r * SCR_P + 4 * g;
+#pragma unroll
+    for (int cb = 0; cb < 8; cb++) {
+      const int c = 16 * cb + 4 * g;
+      st4(sw + 16 * cb, (v[cb] - mean) * rstd * ld4(lnw + c) + ld4(lnb + c));
+    }
+    RG<half_t>::load_row(x[rb], scr + r * SCR_P, g);
+  }
+}
+
 // resid_ln_rows for fp16 rows, plus the pair bias Linear(LN_pb(z_new)) of the s track from the same row statistics:
 // with W' = W ⊙ gamma_pb (fp16, LDS [16][ldp]) and bp = W . beta_pb (LDS, fp32),
 //   pb_out[h][zr] = (x_hat . W'[h]) + bp[h],  x_hat = (z_new - mean) * rstd_pb,

@@ -374,6 +374,39 @@ def transition(xn, w12, w3, z, accumulate: bool, next_ln=None, pair_bias=None):
     return nxt, bias
 
 
+def attn_out_transition(o, w_o, trans: bool, z, ln, w12, w3, next_ln=None, pair_bias=None):
+    """fp16: z += o' w_o^T (o' = o at the transposed position when trans: the ending-node attention's output stage),
+    then z += transition(ln(z)) in the same kernel (the intermediate LayerNorm stays in registers); returns
+    next_ln(z_new) (or None), with pair_bias = (ln_pb, w) also the s track's pair bias: (next_ln(z_new), bias). Equals
+    linear_resid_ln(o, w_o, trans, z, True, ln) followed by transition(.., z, True, next_ln, pair_bias) bit for bit."""
+    _dev(o, w_o, w12, w3, z)
+    N, D = z.shape[0], z.shape[-1]
+    rows = z.numel() // D
+    hidden = w3.shape[1]
+    if z.dtype != torch.float32 or o.dtype != torch.float16 or o.numel() != rows * D or rows != N * N or \
+            w_o.shape != (D, D) or w12.shape != (2 * hidden, D) or w3.shape != (D, hidden):
+        raise ValueError("attn_out_transition: shape/dtype mismatch")
+    nxt = nw = nb = None
+    neps = 1e-5
+    if next_ln is not None:
+        nxt = torch.empty((rows, D), dtype=o.dtype, device=o.device)
+        nw, nb, neps = f32c(next_ln.weight), f32c(next_ln.bias), next_ln.eps
+    pw = plw = plb = bias = None
+    peps, H = 1e-5, 0
+    if pair_bias is not None:
+        ln_pb, pw = pair_bias
+        _dev(pw)
+        H = pw.shape[0]
+        if pw.shape != (H, D) or pw.dtype != o.dtype:
+            raise ValueError("attn_out_transition: pair-bias weight must be [H, D] in fp16")
+        plw, plb, peps = f32c(ln_pb.weight), f32c(ln_pb.bias), ln_pb.eps
+        bias = torch.empty((H, N, N), dtype=pw.dtype, device=z.device)
+    call("bzpf_attn_out_transition", _p(o), _p(w_o), int(trans), _p(f32c(ln.weight)), _p(f32c(ln.bias)),
+         float(ln.eps), _p(w12), _p(w3), _p(z), _p(nw), _p(nb), float(neps), _p(nxt), _p(pw), _p(plw), _p(plb),
+         float(peps), _p(bias), H, _dt(o), N, D, hidden, _stream())
+    return nxt if pair_bias is None else (nxt, bias)
+
+
 def linear(x, w, bias=None, out=None, out_dtype=None, accumulate: bool = False) -> torch.Tensor:
     """y = x w^T + bias over the rows of x (w [M, K] in x's dtype); accumulate adds into the fp32 `out`."""
     _dev(x, w)

@@ -40,8 +40,14 @@ def _pair_chain(layer, z: torch.Tensor, pm: torch.Tensor, xn_in: Optional[torch.
     xn = layer.tri_mul_out.fused(xn, pm, z, True, next_ln=layer.tri_mul_in.norm_in)
     xn = layer.tri_mul_in.fused(xn, pm, z, True, next_ln=layer.tri_att_start.layer_norm)
     xn = layer.tri_att_start.fused(xn, pm, z, True, next_ln=layer.tri_att_end.layer_norm, before_core=hooks[0])
-    xn = layer.tri_att_end.fused(xn, pm, z, True, next_ln=layer.transition_z.norm, before_core=hooks[1])
-    return layer.transition_z.fused(xn, z, True, next_ln=next_ln, pair_bias=pair_bias)
+    tr = layer.transition_z
+    if K.f16() and tr.fused_after_attention_ok(z):
+        # the ending node's output stage (linear_o + residual) runs inside the transition kernel
+        core = layer.tri_att_end.fused_core(xn, pm, before_core=hooks[1])
+        if core is not None:
+            return tr.fused_after_attention(core[0], core[1], True, z, next_ln=next_ln, pair_bias=pair_bias)
+    xn = layer.tri_att_end.fused(xn, pm, z, True, next_ln=tr.norm, before_core=hooks[1])
+    return tr.fused(xn, z, True, next_ln=next_ln, pair_bias=pair_bias)
 
 
 def _guarded(owner: torch.nn.Module, run, outs: tuple, ins: tuple) -> None:

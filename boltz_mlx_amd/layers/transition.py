@@ -79,6 +79,18 @@ class Transition(torch.nn.Module):
         w12, w3 = self.prepare()
         return K.transition(xn, w12, w3, z, accumulate, next_ln, pair_bias)
 
+    def fused_after_attention_ok(self, z: torch.Tensor) -> bool:
+        """Whether fused_after_attention applies: fp16 mode, the 128-channel pair kernel, z [N, N, 128]."""
+        return K.f16() and self._pair_kernel() and z.dim() == 3 and z.shape[0] == z.shape[1]
+
+    def fused_after_attention(self, o: torch.Tensor, w_o: torch.Tensor, trans: bool, z: torch.Tensor, next_ln=None,
+                              pair_bias=None):
+        """z += o' w_o^T (a triangle attention's output stage: o' = its core output o at the transposed position
+        when trans), then z += self(z) in one fp16 kernel (fused_after_attention_ok(z) must hold); returns what
+        fused() returns."""
+        w12, w3 = self.prepare()
+        return K.attn_out_transition(o, w_o, trans, z, self.norm, w12, w3, next_ln, pair_bias)
+
     def unfused(self, xn: torch.Tensor, out: Optional[torch.Tensor] = None, accumulate: bool = False):
         """fc3(SwiGLU(xn fc12^T)) as row GEMMs (in fp16 the up-projection carries the SwiGLU product in its
         epilogue); accumulate adds into the fp32 `out`."""

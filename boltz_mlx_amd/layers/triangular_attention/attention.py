@@ -82,12 +82,27 @@ class TriangleAttention(torch.nn.Module):
                 z.zero_()
             nxt = K.add_ln(z, y, ln=next_ln, trans_y=trans, out_dtype=K.storage_dtype())
             return None if nxt is None else nxt.view(N * N, D)
+        core = self._core_128(xn, mask, N, before_core, proj_trans)
+        return K.linear_resid_ln(core, w_o, trans, z, accumulate, next_ln, N)
+
+    def fused_core(self, xn: torch.Tensor, mask: torch.Tensor, before_core=None):
+        """The 128-channel path of fused() without its output stage, for a consumer that applies linear_o and the
+        residual itself (K.attn_out_transition): returns (core output [N*N, 128] in the storage dtype, in this node's
+        attention frame, linear_o's kernel weight), or None where fused() takes the generic path."""
+        N, D = mask.shape[0], xn.shape[-1]
+        if D != 128 or self.no_heads * self.mha.c_hidden != D:
+            return None
+        return self._core_128(xn, mask, N, before_core, not self.starting), self.prepare()[1]
+
+    def _core_128(self, xn, mask, N: int, before_core, proj_trans: bool):
+        H, C = self.no_heads, self.mha.c_hidden
+        w = self.prepare()[0]
         qkg, vt, tb = K.triattn_proj(xn, w, proj_trans, N, H, C)
         if before_core is not None:
             before_core()
-        core = K.triattn_core(qkg, vt, tb, mask, trans, self.inf, N, H, C)
+        core = K.triattn_core(qkg, vt, tb, mask, not self.starting, self.inf, N, H, C)
         del qkg, vt, tb
-        return K.linear_resid_ln(core, w_o, trans, z, accumulate, next_ln, N)
+        return core
 
     def prepare(self):
         """The kernel weights in the storage dtype ([q; k; v; g; triangle bias] and linear_o), cached on the

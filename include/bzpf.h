@@ -134,6 +134,22 @@ int bzpf_transition_pb(const void* xn, const void* w12, const void* w3, float* z
                        const float* pb_lnb, float pb_eps, void* pb_out, int pb_heads, int dt, int64_t rows, int D,
                        int hidden, void* stream);
 
+/* The ending-node attention's output stage and the pair transition in one pass (fp16 only, D = 128): for every pair
+ * row r = (i, j) of z [N*N][128] fp32,
+ *   z[r] += o[r'] . w_o^T,  r' = (j, i) when trans (the attention frame of the ending node), else r;
+ *   xn = LN(z[r]) with ln_w / ln_b / ln_eps (the transition's own norm, fp16);
+ *   z[r] += fc3(silu(xn . fc1^T) * (xn . fc2^T)),
+ * then next LN and (pb_w != NULL) the s track's pair bias as in bzpf_transition_pb. Equals bzpf_linear_resid_ln
+ * (accumulate = 1, next LN = the transition's norm) followed by bzpf_transition(_pb) bit for bit, without writing
+ * and reading back the intermediate xn. Replaces the triangle attention's linear_o + residual
+ * (f16_addln, boltz_mlx/layers/triangular_attention/attention.py:170-190) followed by the pair transition
+ * (boltz_mlx/layers/transition.py:50-54; kernels_nax3.transition_lnx, boltz_mlx/kernels_nax3.py:713-827). */
+int bzpf_attn_out_transition(const void* o, const void* w_o, int trans, const float* ln_w, const float* ln_b,
+                             float ln_eps, const void* w12, const void* w3, float* z, const float* next_w,
+                             const float* next_b, float next_eps, void* xn_next, const void* pb_w,
+                             const float* pb_lnw, const float* pb_lnb, float pb_eps, void* pb_out, int pb_heads, int dt,
+                             int64_t N, int D, int hidden, void* stream);
+
 /* Linear layer y[r] = x[r] . W^T + bias (K % 8 == 0; bias may be NULL); accumulate != 0 adds into an fp32 y.
  * Replaces the nn.Linear / kernels.lin16 calls of the s track (boltz_mlx/layers/attentionv2.py:50-52, 70, 84;
  * boltz_mlx/kernels.py:1360-1370). */

@@ -497,3 +497,44 @@ def test_transition_pair_bias(precision, N):
     lnz = (zn - mu) / np.sqrt(var + ln_pb.eps) * gam + bet
     ref = np.einsum("ijc,hc->hij", lnz, w_pb.double().cpu().numpy())
     assert np.abs(b1 - ref).max() <= (1e-5 if precision == "fp32" else 6e-3) * np.abs(ref).max()
+
+
+@pytest.mark.parametrize("precision", ["f16"], indirect=True)
+@pytest.mark.parametrize("N", [1, 5, 37, 130])
+@pytest.mark.parametrize("trans", [False, True])
+@pytest.mark.parametrize("with_pb", [False, True])
+def test_attn_out_transition_equals_two_stages(precision, N, trans, with_pb):
+    """bzpf_attn_out_transition (the ending node's linear_o + residual run in the transition kernel, the
+    intermediate LayerNorm kept in registers) against bzpf_linear_resid_ln followed by bzpf_transition(_pb) on the
+    same inputs: z, the next LayerNorm and the pair bias bit for bit."""
+    import torch
+
+    from boltz_mlx_amd import kernels as K
+    from boltz_mlx_amd.layers.norm import LayerNorm
+    from boltz_mlx_amd.layers.transition import Transition
+
+    D, H = 128, 16
+    rng = np.random.default_rng(1300 + N + 7 * trans + 3 * with_pb)
+    tr = load(Transition(D, 4 * D), rand_params(shapes_transition(D, 4 * D), seed=1310 + N, std=0.1))
+    ln_next, ln_pb = LayerNorm(D).cuda(), LayerNorm(D).cuda()
+    with torch.no_grad():
+        for ln in (ln_next, ln_pb):
+            ln.weight.copy_(torch.tensor(1 + 0.3 * rng.standard_normal(D)))
+            ln.bias.copy_(torch.tensor(0.3 * rng.standard_normal(D)))
+    w_o = dev(0.1 * rng.standard_normal((D, D)), torch.float16)
+    o = dev(rng.standard_normal((N * N, D)), torch.float16)
+    w_pb = dev(0.2 * rng.standard_normal((H, D)), torch.float16)
+    z0 = dev(3 * rng.standard_normal((N, N, D)))
+    pb = (ln_pb, w_pb) if with_pb else None
+    z1, z2 = z0.clone(), z0.clone()
+    r1 = tr.fused_after_attention(o, w_o, trans, z1, next_ln=ln_next, pair_bias=pb)
+    xn = K.linear_resid_ln(o, w_o, trans, z2, True, tr.norm, N)
+    r2 = tr.fused(xn, z2, True, next_ln=ln_next, pair_bias=pb)
+    torch.cuda.synchronize()
+    print(f"attn_out_transition N={N} trans={trans} pb={with_pb}: max|dz|="
+          f"{float((z1 - z2).abs().max()):.3e}", flush=True)
+    assert torch.equal(z1, z2)
+    if with_pb:
+        assert torch.equal(r1[0], r2[0]) and torch.equal(r1[1], r2[1])
+    else:
+        assert torch.equal(r1, r2)

@@ -46,6 +46,9 @@ def kernel_work(name: str, N: int, H: int = 4, C: int = 32, D: int = 128) -> tup
         return 393216.0 * R, R * D * (2 + 4 + 4 + 2.0)
     if name == "bzpf_transition_pb":     # the transition plus the s track's 128 -> 16 pair bias (16 fp16 out)
         return (393216.0 + 2.0 * 128 * 16) * R, R * (D * (2 + 4 + 4 + 2.0) + 32.0)
+    if name == "bzpf_attn_out_transition":  # linear_o + residual, then the transition with the pair bias: o in, z r/w,
+        # next LN and the 16-head pair bias out (the intermediate z, written and read back, is not algorithmic)
+        return (2.0 * 128 * 128 + 393216.0 + 2.0 * 128 * 16) * R, R * (256 + 1024 + 256 + 32.0)
     if name == "bzpf_trimul_proj":       # 128 -> 512 per row; xn in, a|b (256 ch) out
         return 131072.0 * R, R * (D * 2 + 256 * 2.0)
     if name == "bzpf_trimul_tail":       # two 128 x 128 GEMMs per row; o, xn in, z r/w, next LN out

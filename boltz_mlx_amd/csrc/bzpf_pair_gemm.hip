@@ -611,9 +611,9 @@ __global__ __launch_bounds__(256) void transition_k(const T* __restrict__ xn, co
 constexpr int TR_HCH = 32;
 
 // AO: the ending-node attention's output stage runs in front (attn_out_rows): the kernel reads the attention core's
-// output o (row of position (i, j) at (j, i) when trans) instead of xn, adds o W_o^T to z, and feeds LN(z) with
-// the transition's own norm to the chunk loop from registers. z is written once in between and read back by the
-// epilogue; the separate kernel's xn round trip through memory is gone.
+// output o (row of position (i, j) at (j, i) when trans) instead of xn and feeds LN(z + o W_o^T) with the
+// transition's own norm to the chunk loop from registers; the epilogue recomputes z + o W_o^T from the tile's o and
+// z rows (same bits) as its residual. Against the two kernels, the intermediate z and xn never go to memory.
 struct AttnOutArgs {
   const half_t* o;
   const half_t* w_o;  // [128][128]
@@ -779,11 +779,38 @@ __global__ __launch_bounds__(64 * TRW, 8 / TRW) void transition_f16_k(const half
     }
     const int64_t row0 = tile * TROWS + wave * 16 * RB + (l & 15);
     const auto zrow = [&](int rb) -> int64_t { return row0 + 16 * rb < rows_total ? row0 + 16 * rb : -1; };
-    if constexpr (PB)
+    if constexpr (AO) {
+      // the residual is z' = z + W_o o^T again, recomputed from the tile's o and z rows (x now holds the next
+      // tile's o rows)
+      const auto zvf = [&](int rb, f4(&zv)[8]) {
+        typename RG<T>::frag x1[1][STEPS];
+        {
+          const int64_t rc = row0 + 16 * rb < rows_total ? row0 + 16 * rb : rows_total - 1;
+          RG<T>::load_row(x1[0], ao.o + (ao.trans ? (rc % ao.n) * ao.n + rc / ao.n : rc) * D, g);
+        }
+        f4 zz[1][8];
+        load_z_rows<1>(zz, [&](int) { return zrow(rb); }, z, 1);
+        f4 y1[1][8];
+        zero_acc(y1);
+        mma_rows_grouped<T, 1, 8, 2>(y1, x1, Wo, LDW);
+#pragma unroll
+        for (int cb = 0; cb < 8; cb++) zv[cb] = y1[0][cb] + zz[0][cb];
+      };
+      if constexpr (PB) {
+        resid_ln_pb_apply<RB>(out, zvf, zrow, z, lnw, lnb, eps, xn_next, Wpb, LDP, Bpb, pb_eps, pb_out, rows_total,
+                              pb_heads);
+      } else {
+        f4 zv[RB][8];
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++) zvf(rb, zv[rb]);
+        resid_ln_apply<T, RB>(out, zv, zrow, z, lnw, lnb, eps, xn_next);
+      }
+    } else if constexpr (PB) {
       resid_ln_pb_rows<RB>(out, zrow, z, accumulate, lnw, lnb, eps, xn_next, Wpb, LDP, Bpb, pb_eps, pb_out,
                            rows_total, pb_heads);
-    else
+    } else {
       resid_ln_rows<T, RB>(out, zrow, z, accumulate, lnw, lnb, eps, xn_next);
+    }
 #pragma unroll
     for (int rb = 0; rb < RB; rb++)
 #pragma unroll

@@ -238,15 +238,16 @@ __device__ __forceinline__ void resid_ln_rows(const f4 (&y)[RB][8], ZRow zrow, f
 }
 
 // The triangle attention's output stage run in front of a fused transition, on RB row blocks of 16 rows: y = W_o o^T
-// (x holds the o rows as B fragments, W_o [128][ldw] in LDS), z[zr] += y (stored), then x <- LN(z[zr]) in fp16 as
-// B fragments again (the transition's input). The LayerNorm output leaves the accumulator layout (lane: 4 channels
-// of each 16-channel block) through a wave-private LDS scratch of 16 rows (pitch SCR_P halves), written and read
-// back by the same wave in program order, so it needs no barrier; the arithmetic is resid_ln_apply's, so x equals
-// the fp16 rows that kernel would have written.
+// (x holds the o rows as B fragments, W_o [128][ldw] in LDS), z' = z[zr] + y, then x <- LN(z') in fp16 as B
+// fragments again (the transition's input). z' is not stored: the epilogue recomputes it (the same MFMA order,
+// so the same bits) rather than reading back a copy. The LayerNorm output leaves the accumulator layout
+// (lane: 4 channels of each 16-channel block) through a wave-private LDS scratch of 16 rows (pitch SCR_P halves),
+// written and read back by the same wave in program order, so it needs no barrier; the arithmetic is
+// resid_ln_apply's, so x equals the fp16 rows that kernel would have written.
 constexpr int SCR_P = 144;
 template <int RB, typename ZRow>
 __device__ __forceinline__ void attn_out_rows(RG<half_t>::frag (&x)[RB][4], const half_t* Wo, int ldw, ZRow zrow,
-                                              float* __restrict__ z, const float* __restrict__ lnw,
+                                              const float* __restrict__ z, const float* __restrict__ lnw,
                                               const float* __restrict__ lnb, float eps, half_t* scr) {
   constexpr int D = 128;
   const int l = threadIdx.x & 63, g = l >> 4, r = l & 15;
@@ -257,18 +258,12 @@ __device__ __forceinline__ void attn_out_rows(RG<half_t>::frag (&x)[RB][4], cons
   load_z_rows<RB>(zv, zrow, z, 1);
 #pragma unroll
   for (int rb = 0; rb < RB; rb++) {
-    const int64_t zr = zrow(rb);
-    float* zp = z + (zr >= 0 ? zr : 0) * D + 4 * g;
     f4 v[8];
     float s = 0.f;
 #pragma unroll
     for (int cb = 0; cb < 8; cb++) {
       v[cb] = y[rb][cb] + zv[rb][cb];
       s += v[cb][0] + v[cb][1] + v[cb][2] + v[cb][3];
-    }
-    if (zr >= 0) {
-#pragma unroll
-      for (int cb = 0; cb < 8; cb++) *reinterpret_cast<f4*>(zp + 16 * cb) = v[cb];  // read back by the epilogue
     }
     const float mean = xgroups_sum(s) * (1.0f / D);
     float ss = 0.f;
@@ -295,18 +290,20 @@ __device__ __forceinline__ void attn_out_rows(RG<half_t>::frag (&x)[RB][4], cons
 // (k slot 8 g + t <-> channel 32 s + 16 (t / 4) + 4 g + t % 4 in step s), A the same channels of W' for head l % 16,
 // and the accumulator lane (row, g) receives heads 4 g .. 4 g + 3 of its row. The MFMAs run with every lane active;
 // lanes without a row compute on finite stand-in values and store nothing.
-template <int RB, typename ZRow>
-__device__ __forceinline__ void resid_ln_pb_rows(const f4 (&y)[RB][8], ZRow zrow, float* __restrict__ z, int accumulate,
-                                                 const float* __restrict__ lnw, const float* __restrict__ lnb,
-                                                 float eps, half_t* __restrict__ xn_next, const half_t* Wp, int ldp,
-                                                 const float* Bp, float eps_pb, half_t* __restrict__ pb_out,
-                                                 int64_t pb_stride, int pb_heads) {
+// resid_ln_pb_apply takes the residual rows from zvf(rb, zv) (zv: the row block's 8 column blocks, accumulator
+// layout); resid_ln_pb_rows loads them from z first.
+template <int RB, typename ZRow, typename ZvFn>
+__device__ __forceinline__ void resid_ln_pb_apply(const f4 (&y)[RB][8], ZvFn zvf, ZRow zrow, float* __restrict__ z,
+                                                  const float* __restrict__ lnw, const float* __restrict__ lnb,
+                                                  float eps, half_t* __restrict__ xn_next, const half_t* Wp, int ldp,
+                                                  const float* Bp, float eps_pb, half_t* __restrict__ pb_out,
+                                                  int64_t pb_stride, int pb_heads) {
   constexpr int D = 128;
   const int l = threadIdx.x & 63, g = l >> 4, r = l & 15;
-  f4 zv[RB][8];
-  load_z_rows<RB>(zv, zrow, z, accumulate);
 #pragma unroll
   for (int rb = 0; rb < RB; rb++) {
+    f4 zv[8];
+    zvf(rb, zv);
     const int64_t zr = zrow(rb);
     const int64_t rowoff = (zr >= 0 ? zr : 0) * D + 4 * g;
     float* zp = z + rowoff;
@@ -314,7 +311,7 @@ __device__ __forceinline__ void resid_ln_pb_rows(const f4 (&y)[RB][8], ZRow zrow
     float s = 0.f;
 #pragma unroll
     for (int cb = 0; cb < 8; cb++) {
-      v[cb] = y[rb][cb] + zv[rb][cb];
+      v[cb] = y[rb][cb] + zv[cb];
       s += v[cb][0] + v[cb][1] + v[cb][2] + v[cb][3];
     }
     if (zr >= 0) {
@@ -359,6 +356,23 @@ __device__ __forceinline__ void resid_ln_pb_rows(const f4 (&y)[RB][8], ZRow zrow
       }
     }
   }
+}
+
+template <int RB, typename ZRow>
+__device__ __forceinline__ void resid_ln_pb_rows(const f4 (&y)[RB][8], ZRow zrow, float* __restrict__ z, int accumulate,
+                                                 const float* __restrict__ lnw, const float* __restrict__ lnb,
+                                                 float eps, half_t* __restrict__ xn_next, const half_t* Wp, int ldp,
+                                                 const float* Bp, float eps_pb, half_t* __restrict__ pb_out,
+                                                 int64_t pb_stride, int pb_heads) {
+  f4 zv[RB][8];
+  load_z_rows<RB>(zv, zrow, z, accumulate);
+  resid_ln_pb_apply<RB>(
+      y,
+      [&](int rb, f4(&o)[8]) {
+#pragma unroll
+        for (int cb = 0; cb < 8; cb++) o[cb] = zv[rb][cb];
+      },
+      zrow, z, lnw, lnb, eps, xn_next, Wp, ldp, Bp, eps_pb, pb_out, pb_stride, pb_heads);
 }
 
 // Index of the calling wave in the grid as a wave-uniform (scalar) value: the compiler cannot prove threadIdx.x / 64

@@ -9,8 +9,9 @@
 // A 256-thread workgroup owns a BM x BR tile of y^T (BM, BR = 64 or 128; gemm_tile_choice picks), 4 waves of
 // BM / 2 x BR / 2 on v_mfma_f32_32x32x16_f16. The tile is computed transposed (y^T = W x^T: A = rows of W, B = rows
 // of x), so an accumulator lane holds 4 runs of 4 consecutive output columns of one row and stores 8- or 16-byte
-// vectors. K stages of 64 are double-buffered in LDS (36-72 KB) and two register sets carry the next two stages, as
-// in the triangle contraction.
+// vectors. K stages of 64 are double-buffered in LDS (36-72 KB) and two register sets carry the next two stages.
+// gemm_lds_k is the same computation with the stages loaded straight into LDS, three deep (the default below the
+// large-grid case).
 // Rows of x past R and rows of W past M read as zeros through the buffer range check; their outputs are not stored.
 #include "bzpf_common.h"
 #include "bzpf_kernels.h"
@@ -162,6 +163,136 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_k(const TX* __restrict__ x, co
   }
 }
 
+// fp16 operands with the K stages loaded straight into LDS (buffer_load ... lds), NS stages deep: the same tiles,
+// waves and lane-to-k assignment as gemm_nt_k (so the same sums in the same order), but NS - 1 stages in flight
+// without staging registers. A wave's load instruction fills 1 KB of LDS in lane order (8 rows of 128 bytes); each
+// lane picks the global 16-byte chunk that makes LDS chunk p of row R hold the row's chunk p ^ gl_swz(R), so the
+// fragment reads (16 lanes on 16 consecutive rows at one logical chunk) hit distinct banks.
+__device__ __forceinline__ int gl_swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
+
+template <int BM, int BR, int NS, typename TY>
+__global__ __launch_bounds__(256, 2) void gemm_lds_k(const half_t* __restrict__ x, const half_t* __restrict__ w,
+                                                     const float* __restrict__ bias, TY* __restrict__ y, int64_t R,
+                                                     int K, int M, int epi, const float* __restrict__ gate,
+                                                     int64_t ld_gate, int64_t gate_rows) {
+  static_assert((BM == 64 || BM == 128) && (BR == 64 || BR == 128) && NS >= 2, "tile / stages");
+  constexpr int BK = 64, ROWB = 128, ROWS = BM + BR, STAGE = ROWS * ROWB;
+  constexpr int LPW = ROWS / 32;             // load instructions per wave per stage (8 rows each, 4 waves)
+  constexpr int MB = BM / 64, RB = BR / 64;  // 32 x 32 MFMA blocks per wave along m and r
+  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE];
+  const int64_t r0 = (int64_t)blockIdx.x * BR;
+  const int m0 = blockIdx.y * BM;
+  const int t = threadIdx.x, l = t & 63, rr = l & 31, hh = l >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+  const int wm = wave >> 1, wr = wave & 1;  // wave tile: m = BM / 2 wm .., r = BR / 2 wr ..
+
+  constexpr int RSRC_CFG = 0x00020000;
+  const int64_t xrows = R - r0 < BR ? R - r0 : BR;
+  const int wrows = M - m0 < BM ? M - m0 : BM;
+  const __amdgpu_buffer_rsrc_t xrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(x + r0 * K), 0, (int)(xrows * K * 2), RSRC_CFG);
+  const __amdgpu_buffer_rsrc_t wrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)(w + (int64_t)m0 * K), 0, (int)((int64_t)wrows * K * 2), RSRC_CFG);
+  // instruction v of this wave fills stage rows 8 (4 v + wave) .. + 7: W rows [0, BM), then x rows [BM, ROWS)
+  const int nst = K / BK;
+  auto issue = [&](int st, int slot) {
+    st = min(st, nst - 1);  // issues past the last stage reload it into a slot that is never read
+#pragma unroll
+    for (int v = 0; v < LPW; v++) {
+      const int row = 8 * (4 * v + wave) + (l >> 3);
+      const bool isw = 8 * (4 * v + wave) < BM;  // wave-uniform
+      const int rloc = isw ? row : row - BM;
+      const int voff = (rloc * K + 8 * ((l & 7) ^ gl_swz(row))) * 2;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          isw ? wrs : xrs, (__attribute__((address_space(3))) void*)(lds + slot * STAGE + (4 * v + wave) * 1024), 16,
+          voff, st * BK * 2, 0, 0);
+    }
+  };
+  f16x acc[MB][RB];
+#pragma unroll
+  for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[mb][rb][e] = 0.0f;
+  // lane half hh takes k = 32 hh + 8 s .. + 7 of the stage in MFMA step s (gemm_nt_k's order)
+  half8 fa[2][MB], fb[2][RB];
+  auto read = [&](int set, int slot, int s) {
+    const char* base = lds + slot * STAGE;
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++) {
+      const int row = BM / 2 * wm + 32 * mb + rr;
+      fa[set][mb] = *reinterpret_cast<const half8*>(base + row * ROWB + 16 * ((4 * hh + s) ^ gl_swz(row)));
+    }
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) {
+      const int row = BM + BR / 2 * wr + 32 * rb + rr;
+      fb[set][rb] = *reinterpret_cast<const half8*>(base + row * ROWB + 16 * ((4 * hh + s) ^ gl_swz(row)));
+    }
+  };
+  constexpr int YOUNGER = (NS - 2) * LPW;  // loads of later stages in flight when a stage is waited for
+  constexpr int WAIT = (YOUNGER & 15) | ((YOUNGER >> 4) << 14) | (0x7 << 4) | (0xF << 8);  // vmcnt only
+#pragma unroll
+  for (int p = 0; p < NS - 1; p++) issue(p, p);
+  __builtin_amdgcn_s_waitcnt(WAIT);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  issue(NS - 1, NS - 1);
+  read(0, 0, 0);
+  for (int st = 0; st < nst; st++) {
+    const int slot = st % NS;
+#pragma unroll
+    for (int s = 0; s < 4; s++) {
+      const int cur = s & 1;
+      if (s < 3) {
+        read(cur ^ 1, slot, s + 1);
+      } else if (st + 1 < nst) {
+        // this wave's reads of the slot are done and stage st + 1 has landed; after the barrier the slot takes
+        // stage st + NS
+        __builtin_amdgcn_s_waitcnt(WAIT & ~(0xF << 8));  // vmcnt as above, lgkmcnt(0)
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        issue(st + NS, slot);
+        read(cur ^ 1, (st + 1) % NS, 0);
+      }
+#pragma unroll
+      for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++)
+          acc[mb][rb] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[cur][mb], fb[cur][rb], acc[mb][rb], 0, 0, 0);
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);  // the reloads past the last stage land before the workgroup's LDS is released
+  // epilogue: lane (rr, hh) of block (mb, rb) holds y[r][m .. m + 3] for r = BR / 2 wr + 32 rb + rr and
+  // m = BM / 2 wm + 32 mb + 8 q + 4 hh, q < 4
+#pragma unroll
+  for (int rb = 0; rb < RB; rb++) {
+    const int64_t r = r0 + BR / 2 * wr + 32 * rb + rr;
+    if (r >= R) continue;
+#pragma unroll
+    for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        const int m = m0 + BM / 2 * wm + 32 * mb + 8 * q + 4 * hh;
+        if (m >= M) continue;
+        f4 v4 = f4{acc[mb][rb][4 * q], acc[mb][rb][4 * q + 1], acc[mb][rb][4 * q + 2], acc[mb][rb][4 * q + 3]};
+        if (bias != nullptr) v4 += *reinterpret_cast<const f4*>(bias + m);
+        if (epi == 2) {
+          const f4 gv = *reinterpret_cast<const f4*>(gate + (r % gate_rows) * ld_gate + m);
+          v4 = f4{v4[0] * sigmoidf_(gv[0]), v4[1] * sigmoidf_(gv[1]), v4[2] * sigmoidf_(gv[2]),
+                  v4[3] * sigmoidf_(gv[3])};
+        }
+        TY* yp = y + r * M + m;
+        if constexpr (sizeof(TY) == 4) {
+          if (epi >= 1) v4 += *reinterpret_cast<const f4*>(yp);
+          *reinterpret_cast<f4*>(yp) = v4;
+        } else {
+          *reinterpret_cast<half4*>(yp) = half4{(half_t)v4[0], (half_t)v4[1], (half_t)v4[2], (half_t)v4[3]};
+        }
+      }
+  }
+}
+
 // Feed-forward GEMM with the gated product in its epilogue, NP = 3: u[r][c] = silu(x[r] . Wg[c]) * (x[r] . Wx[c]) *
 // (x[r] . Wab[c]) (the conditioned transition's silu(gates) * x * a_to_b, transformersv2.py:44-66); NP = 2:
 // u[r][c] = silu(x[r] . W1[c]) * (x[r] . W2[c]) (Transition's SwiGLU, transition.py:27-54), without the [R, NP H]
@@ -277,6 +408,21 @@ hipError_t gemm_t(const void* x, const void* w, const float* bias, void* y, int 
   return hipGetLastError();
 }
 
+template <int BM, int BR, int NS>
+hipError_t gemm_lds_t(const void* x, const void* w, const float* bias, void* y, int y_dt, int64_t R, int K, int M,
+                      int epi, const float* gate, int64_t ld_gate, int64_t gate_rows, hipStream_t st) {
+  const dim3 grid((unsigned)((R + BR - 1) / BR), (unsigned)((M + BM - 1) / BM));
+  if (y_dt == DT_F16)
+    gemm_lds_k<BM, BR, NS, half_t><<<grid, 256, 0, st>>>(static_cast<const half_t*>(x), static_cast<const half_t*>(w),
+                                                         bias, static_cast<half_t*>(y), R, K, M, epi, gate, ld_gate,
+                                                         gate_rows);
+  else
+    gemm_lds_k<BM, BR, NS, float><<<grid, 256, 0, st>>>(static_cast<const half_t*>(x), static_cast<const half_t*>(w),
+                                                        bias, static_cast<float*>(y), R, K, M, epi, gate, ld_gate,
+                                                        gate_rows);
+  return hipGetLastError();
+}
+
 // Tile choice (W rows x x rows per workgroup): 0 = 128 x 128, 1 = 128 x 64, 2 = 64 x 128, 3 = 64 x 64. The loop
 // is latency-bound at these sizes (each stage's loads have two stages of compute to land), so more, smaller
 // workgroups per CU win up to the 2000 x 768 x 4608 projections (64 x 64: 403-434 TF/s against 373-393 for
@@ -322,6 +468,12 @@ hipError_t launch_gemm_nt(const void* x, const void* w, const float* bias, void*
     return hipErrorInvalidValue;
   if (x_dt == DT_F32)  // fp32 operands: 64 x 64 tiles (the m track's 409,600-row projections)
     return gemm_t<64, 64, float>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st);
+  // below the large-grid case the LDS-direct form with 3 stages (2 in flight) takes the same tiles: the diffusion
+  // transformer's 2000 x 768 -> 3072 projection 24.4 -> 22.1 us (128 x 64), its 768-wide gated outputs 12.6 -> 11.7
+  // and 17.2 -> 16.1 us (64 x 64); the s track's small GEMMs are unchanged. Same sums in the same order.
+  if (gemm_tile_choice(R, M) != 0)
+    return M >= 2048 ? gemm_lds_t<128, 64, 3>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st)
+                     : gemm_lds_t<64, 64, 3>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st);
   switch (gemm_tile_choice(R, M)) {
     case 0: return gemm_t<128, 128, half_t>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st);
     case 1: return gemm_t<128, 64, half_t>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st);

@@ -538,3 +538,34 @@ def test_attn_out_transition_equals_two_stages(precision, N, trans, with_pb):
         assert torch.equal(r1[0], r2[0]) and torch.equal(r1[1], r2[1])
     else:
         assert torch.equal(r1, r2)
+
+
+@pytest.mark.parametrize("impl", [1, 2])
+@pytest.mark.parametrize("N", [7, 70, 200])
+def test_triattn_core_strided_mask(impl, N):
+    """bzpf_triattn_core reading the natural-orientation mask with strides (mask_si = 1, mask_sk = N), as a C caller
+    may pass it for the ending node, equals the call on the transposed copy (the path the module takes), bit for
+    bit, for both cores."""
+    import torch
+
+    from boltz_mlx_amd import _lib
+    from boltz_mlx_amd import kernels as K
+
+    H, C = 4, 32
+    rng = np.random.default_rng(1500 + N + impl)
+    ldk = K.row_pitch(N)
+    qkg = dev(rng.standard_normal((3 * H, N * N, C)), torch.float16)
+    vt = dev(rng.standard_normal((H, N, C, ldk)), torch.float16)
+    vt[..., N:] = 0
+    tb = dev(rng.standard_normal(K.tri_bias_numel(N, H)), torch.float16)
+    mask = (rng.random((N, N)) > 0.3).astype(np.float32)
+    mask[:, 0] = 1  # no fully masked row of the ending frame
+    mg = dev(mask)
+    ref = K.triattn_core(qkg, vt, tb, mg, True, 1e9, N, H, C, impl=impl)
+    out = torch.empty_like(ref)
+    rc = _lib.load().bzpf_triattn_core(qkg.data_ptr(), vt.data_ptr(), tb.data_ptr(), mg.data_ptr(), 1, N, 1e9,
+                                       out.data_ptr(), K._dt(qkg), N, ldk, H, C, impl,
+                                       torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, _lib.load().bzpf_last_error()
+    torch.cuda.synchronize()
+    assert torch.equal(out, ref)

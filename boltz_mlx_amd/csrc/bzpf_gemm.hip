@@ -468,10 +468,12 @@ hipError_t launch_gemm_nt(const void* x, const void* w, const float* bias, void*
     return hipErrorInvalidValue;
   if (x_dt == DT_F32)  // fp32 operands: 64 x 64 tiles (the m track's 409,600-row projections)
     return gemm_t<64, 64, float>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st);
-  // below the large-grid case the LDS-direct form with 3 stages (2 in flight) takes the same tiles: the diffusion
-  // transformer's 2000 x 768 -> 3072 projection 24.4 -> 22.1 us (128 x 64), its 768-wide gated outputs 12.6 -> 11.7
-  // and 17.2 -> 16.1 us (64 x 64); the s track's small GEMMs are unchanged. Same sums in the same order.
-  if (gemm_tile_choice(R, M) != 0)
+  // below the large-grid case, for 2048 rows and more, the LDS-direct form with 3 stages (2 in flight) takes the
+  // same tiles: the diffusion transformer's 2000 x 768 -> 3072 projection 24.4 -> 22.1 us (128 x 64), its 768-wide
+  // gated outputs 12.6 -> 11.7 and 17.2 -> 16.1 us (64 x 64). Same sums in the same order. The s track's GEMMs
+  // (N rows) keep the register-staged form: they run beside the attention core, and there the LDS-direct form's
+  // workgroups found compute units far later (0.85 ms against 0.04 ms per launch at N = 1000).
+  if (gemm_tile_choice(R, M) != 0 && R >= 1536)
     return M >= 2048 ? gemm_lds_t<128, 64, 3>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st)
                      : gemm_lds_t<64, 64, 3>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st);
   switch (gemm_tile_choice(R, M)) {

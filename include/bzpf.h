@@ -101,7 +101,9 @@ int bzpf_triattn_proj(const void* xn, const void* w, int trans, float q_scale, f
  * with softmax2 the base-2 softmax (2^x normalised; equal to the reference's softmax of the natural-log logits
  * (q/sqrt(C)).k + inf*(mask-1) + linear, summed in that order). fp32 softmax and accumulation; out [N*N, H*C] (dt).
  * impl selects the kernel like the reference's impl argument: 0 = auto (MFMA for fp16 with C = 32, else VALU),
- * 1 = the VALU kernel, 2 = the MFMA kernel (fp16, C = 32). Replaces kernels.tri_attention_fused
+ * 1 = the VALU kernel, 2 = the MFMA kernel (fp16, C = 32). With inf >= 1e6 the MFMA kernel skips the key blocks
+ * after a row's last unmasked key (found among the row's last 256 keys): their probabilities are exactly zero, so
+ * the output is the same bit for bit. Replaces kernels.tri_attention_fused
  * (boltz_mlx/kernels.py:531-945, impl "scalar" / "mma") and kernels_nax.tri_attention_nax
  * (boltz_mlx/kernels_nax.py:323-558). */
 int bzpf_triattn_core(const void* qkg, const void* vt, const void* tri_bias, const float* mask, int64_t mask_si,

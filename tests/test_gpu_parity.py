@@ -569,3 +569,38 @@ def test_triattn_core_strided_mask(impl, N):
     assert rc == 0, _lib.load().bzpf_last_error()
     torch.cuda.synchronize()
     assert torch.equal(out, ref)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("N", [200, 300, 700])
+def test_triattn_core_trailing_block_skip_exact(N):
+    """The MFMA core skips the key blocks after a row's last unmasked key (scanned over the row's last 256 keys) when
+    inf >= 1e6, since those keys' probabilities are exactly zero. Pinned bit for bit against the same call with
+    inf = 5e5 (no skip; the masked probabilities are zero there too): trailing padding that covers whole blocks,
+    rows whose last unmasked key lies before the scanned range, rows masked at the start, interior holes and fully
+    masked rows."""
+    import torch
+
+    from boltz_mlx_amd import kernels as K
+
+    H, C = 4, 32
+    rng = np.random.default_rng(2600 + N)
+    ldk = K.row_pitch(N)
+    qkg = dev(rng.standard_normal((3 * H, N * N, C)), torch.float16)
+    vt = dev(rng.standard_normal((H, N, C, ldk)), torch.float16)
+    vt[..., N:] = 0
+    tb = dev(rng.standard_normal(K.tri_bias_numel(N, H)), torch.float16)
+    tok = np.ones(N, np.float32)
+    tok[N - N // 6:] = 0  # trailing padding: whole 64-key blocks for N = 700, 300
+    mask = tok[:, None] * tok[None, :] * (rng.random((N, N)) > 0.2)
+    mask[:, 0] = np.where(tok > 0, 1.0, 0.0)  # rows of real tokens keep key 0
+    if N > 256:
+        mask[3, N // 4:] = 0  # last unmasked key before the scanned range
+    mask[5, : N // 2] = 0  # masked at the start (the maximum is set late)
+    mask[5, N // 2] = 1
+    mg = dev(mask.astype(np.float32))
+    for trans in (False, True):
+        skip = K.triattn_core(qkg, vt, tb, mg, trans, 1e9, N, H, C, impl=2)
+        full = K.triattn_core(qkg, vt, tb, mg, trans, 5e5, N, H, C, impl=2)
+        torch.cuda.synchronize()
+        assert torch.equal(skip, full), (N, trans)

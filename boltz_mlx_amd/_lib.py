@@ -27,7 +27,7 @@ SIGNATURES = {
     "bzpf_swiglu3": [vp, vp, i32, i64, i32, vp],
     "bzpf_adaln": [vp, vp, vp, i64, i64, f32, vp, i32, i64, i32, vp],
     "bzpf_trimul_proj": [vp, vp, vp, f32, i32, vp, i32, i64, i64, i32, vp],
-    "bzpf_trimul_contract": [vp, vp, i32, i64, i64, i32, vp],
+    "bzpf_trimul_contract": [vp, vp, i32, i64, i64, i32, i64, vp],
     "bzpf_trimul_tail": [vp, vp, vp, f32, vp, vp, vp, vp, i32, vp, vp, f32, vp, i32, i64, i64, i32, vp],
     "bzpf_triattn_proj": [vp, vp, i32, f32, f32, vp, vp, vp, i32, i64, i64, i32, i32, i32, vp],
     "bzpf_triattn_core": [vp, vp, vp, vp, i64, i64, f32, vp, i32, i64, i64, i32, i32, i32, vp],

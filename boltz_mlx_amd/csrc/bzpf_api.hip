@@ -93,13 +93,14 @@ int bzpf_trimul_proj(const void* xn, const void* w_pg, const float* pair_mask, f
               "bzpf_trimul_proj");
 }
 
-int bzpf_trimul_contract(const void* ab, void* o, int dt, int64_t N, int64_t ld, int D, void* stream) {
+int bzpf_trimul_contract(const void* ab, void* o, int dt, int64_t N, int64_t ld, int D, int64_t k_len,
+                         void* stream) {
   REQUIRE_PTR(ab);
   REQUIRE_PTR(o);
   REQUIRE(dt_ok(dt), "bzpf_trimul_contract: bad dtype %d", dt);
   REQUIRE(D >= 1 && D <= 65535, "bzpf_trimul_contract: bad D=%d", D);
   REQUIRE(N >= 1 && ld == bzpf_row_pitch(N), "bzpf_trimul_contract: N=%lld ld=%lld", (long long)N, (long long)ld);
-  return done(bzpf::launch_trimul_contract(ab, o, dt, N, ld, D, S(stream)), "bzpf_trimul_contract");
+  return done(bzpf::launch_trimul_contract(ab, o, dt, N, ld, k_len, D, S(stream)), "bzpf_trimul_contract");
 }
 
 int bzpf_trimul_tail(const void* o, const float* norm_out_w, const float* norm_out_b, float eps_out,

@@ -16,7 +16,8 @@ hipError_t launch_count_nonfinite(const void* x, int dt, int64_t n, int* count, 
 
 hipError_t launch_trimul_proj(const void* xn, const void* w, const float* mask, float scale, int incoming, void* ab,
                               int dt, int64_t N, int64_t ld, hipStream_t st);
-hipError_t launch_trimul_contract(const void* ab, void* o, int dt, int64_t N, int64_t ld, int D, hipStream_t st);
+hipError_t launch_trimul_contract(const void* ab, void* o, int dt, int64_t N, int64_t ld, int64_t k_len, int D,
+                                  hipStream_t st);
 hipError_t launch_trimul_tail(const void* o, const float* now, const float* nob, float eps_out, const void* w_po,
                               const void* xn, const void* w_go, float* z, int accumulate, const float* lnw,
                               const float* lnb, float eps_next, void* xn_next, int dt, int64_t N, int64_t ld,

@@ -23,7 +23,7 @@ namespace bzpf {
 template <typename T>
 __global__ __launch_bounds__(256, 2) void trimul_contract_kernel(const T* __restrict__ ab, T* __restrict__ o,
                                                                  int64_t N, int64_t ld, int D, int64_t tiles1,
-                                                                 int64_t units, int64_t per_xcd) {
+                                                                 int64_t units, int64_t per_xcd, int nst) {
   constexpr int BT = 128;
   constexpr int BK = sizeof(T) == 2 ? 64 : 32;      // k per stage: 128 bytes of a row
   constexpr int KG = BK / 4;                        // contiguous k per lane group
@@ -72,7 +72,6 @@ __global__ __launch_bounds__(256, 2) void trimul_contract_kernel(const T* __rest
   gload(0);
   lstore(0);
   __syncthreads();
-  const int nst = (int)(ld / BK);
   for (int st = 0; st < nst; st++) {
     const int buf = st & 1;
     if (st + 1 < nst) gload((int64_t)(st + 1) * BK);
@@ -137,7 +136,8 @@ __device__ __forceinline__ int ct_swz(int row) {
 template <int BK, int NS>
 __global__ __launch_bounds__(512, 1) void trimul_contract_f16_k(const half_t* __restrict__ ab, half_t* __restrict__ o,
                                                                 int64_t N, int64_t ld, int D, int64_t tiles1,
-                                                                int64_t units, int64_t per_xcd, int wg_per_xcd) {
+                                                                int64_t units, int64_t per_xcd, int wg_per_xcd,
+                                                                int nst) {
   constexpr int BT = 256, NW = 8;
   constexpr int ROWB = BK * 2;               // bytes of a row per stage
   constexpr int CPR = ROWB / 16;             // 16-byte chunks per row
@@ -155,7 +155,6 @@ __global__ __launch_bounds__(512, 1) void trimul_contract_f16_k(const half_t* __
   const int64_t end = min(units, (int64_t)(xcd + 1) * per_xcd);
   if (first >= end) return;
   const int cnt = (int)((end - first + wg_per_xcd - 1) / wg_per_xcd);
-  const int nst = (int)(ld / BK);
   const int total = cnt * nst;
 
   const int t = threadIdx.x, w = t >> 6, l = t & 63, r = l & 31, h = l >> 5;
@@ -303,8 +302,9 @@ __global__ __launch_bounds__(512, 1) void trimul_contract_f16_k(const half_t* __
   __builtin_amdgcn_s_waitcnt(0);  // no LDS write of a trailing (unused) stage load outlives the workgroup
 }
 
+// kl: the k range contracted (a multiple of the stage width, <= ld); columns past it are zero in a and b.
 template <typename T>
-static hipError_t contract_t(const void* ab, void* o, int64_t N, int64_t ld, int D, hipStream_t st) {
+static hipError_t contract_t(const void* ab, void* o, int64_t N, int64_t ld, int64_t kl, int D, hipStream_t st) {
   const int BT = sizeof(T) == 2 ? 256 : 128;
   const int64_t tiles1 = (N + BT - 1) / BT;
   const int64_t units = (int64_t)D * tiles1 * tiles1;
@@ -316,17 +316,20 @@ static hipError_t contract_t(const void* ab, void* o, int64_t N, int64_t ld, int
     if (resident < 8) return hipErrorInvalidConfiguration;
     const int wpx = (int)(resident / 8 < per_xcd ? resident / 8 : per_xcd);
     trimul_contract_f16_k<64, 2><<<dim3(8 * wpx), 512, 0, st>>>(static_cast<const half_t*>(ab), static_cast<half_t*>(o),
-                                                               N, ld, D, tiles1, units, per_xcd, wpx);
+                                                               N, ld, D, tiles1, units, per_xcd, wpx, (int)(kl / 64));
   } else {
     trimul_contract_kernel<T><<<grid, 256, 0, st>>>(static_cast<const T*>(ab), static_cast<T*>(o), N, ld, D, tiles1,
-                                                    units, per_xcd);
+                                                    units, per_xcd, (int)(kl / 32));
   }
   return hipGetLastError();
 }
 
-hipError_t launch_trimul_contract(const void* ab, void* o, int dt, int64_t N, int64_t ld, int D, hipStream_t st) {
+hipError_t launch_trimul_contract(const void* ab, void* o, int dt, int64_t N, int64_t ld, int64_t k_len, int D,
+                                  hipStream_t st) {
   if (dt == DT_F16 && 2 * N * ld >= (1LL << 31)) return hipErrorInvalidValue;  // 32-bit buffer offsets per channel
-  return dt == DT_F16 ? contract_t<half_t>(ab, o, N, ld, D, st) : contract_t<float>(ab, o, N, ld, D, st);
+  // contract over k < k_len rounded up to 64 (a whole number of stages of either kernel); 0 or >= N: every k
+  const int64_t kl = k_len <= 0 || k_len >= N ? ld : (k_len + 63) / 64 * 64;
+  return dt == DT_F16 ? contract_t<half_t>(ab, o, N, ld, kl, D, st) : contract_t<float>(ab, o, N, ld, kl, D, st);
 }
 
 }  // namespace bzpf

@@ -13,6 +13,7 @@ multiplication operands a, b are pre-scaled by 2^-TRIMULT_K and norm_out's eps b
 
 from __future__ import annotations
 
+import contextlib
 import os
 
 import torch
@@ -244,15 +245,67 @@ def triattn_pack(P: torch.Tensor, trans: bool, N: int, H: int, C: int):
     return qkg, vt, tb
 
 
-def trimul_contract(ab: torch.Tensor, N: int) -> torch.Tensor:
+def trimul_contract(ab: torch.Tensor, N: int, k_len: int = 0) -> torch.Tensor:
+    """o [D, N, ld] = per-channel a b^T; k_len > 0: columns k >= k_len of ab are zero and the sum stops there (the
+    trailing padded tokens; key_extent gives it for a pair mask)."""
     _dev(ab)
     D = ab.shape[0] // 2
     ld = row_pitch(N)
     if ab.shape != (2 * D, N, ld):
         raise ValueError("trimul_contract: ab must be [2D, N, ld]")
     o = torch.empty((D, N, ld), dtype=ab.dtype, device=ab.device)
-    call("bzpf_trimul_contract", _p(ab), _p(o), _dt(ab), N, ld, D, _stream())
+    call("bzpf_trimul_contract", _p(ab), _p(o), _dt(ab), N, ld, D, int(k_len), _stream())
     return o
+
+
+# Per-mask values derived once inside pair_mask_scope(): {key: {"t": transposed copy, ("ext", incoming): k_len}}
+_MASK_SCOPE: dict | None = None
+
+
+@contextlib.contextmanager
+def pair_mask_scope():
+    """Inside the block, the values derived from a pair mask (the ending-node core's transposed copy, the
+    contraction's key extent) are computed once per mask (keyed by its storage, shape, strides and version) and
+    reused by every later call with the same mask: a module run derives them once instead of once per layer.
+    Outside a scope each call transposes for itself and the contraction runs over every key."""
+    global _MASK_SCOPE
+    prev, _MASK_SCOPE = _MASK_SCOPE, {}
+    try:
+        yield
+    finally:
+        _MASK_SCOPE = prev
+
+
+def _mask_entry(mask: torch.Tensor):
+    if _MASK_SCOPE is None:
+        return None
+    key = (mask.data_ptr(), tuple(mask.shape), tuple(mask.stride()), mask._version)
+    return _MASK_SCOPE.setdefault(key, {})
+
+
+def mask_transposed(mask: torch.Tensor, N: int) -> torch.Tensor:
+    """The pair mask [N, N] transposed, contiguous (cached inside pair_mask_scope)."""
+    ent = _mask_entry(mask)
+    if ent is None:
+        return mask.reshape(N, N).t().contiguous()
+    if "t" not in ent:
+        ent["t"] = mask.reshape(N, N).t().contiguous()
+    return ent["t"]
+
+
+def key_extent(mask: torch.Tensor, N: int, incoming: bool) -> int:
+    """1 + the last token k whose pair-mask column (outgoing; row for incoming) is not all zero: bzpf_trimul_proj
+    writes zeros in ab for every k past it. Computed (one host sync) only inside pair_mask_scope, once per mask;
+    0 (every key) outside."""
+    ent = _mask_entry(mask)
+    if ent is None:
+        return 0
+    if ("ext", incoming) not in ent:
+        m = mask.reshape(N, N) != 0
+        live = m.any(dim=1 if incoming else 0)
+        idx = torch.nonzero(live)
+        ent[("ext", incoming)] = int(idx[-1, 0].item()) + 1 if idx.numel() else N
+    return ent[("ext", incoming)]
 
 
 def trimul_tail(o, norm_out, eps_out: float, w_po, xn, w_go, z, accumulate: bool, next_ln=None, N: int = 0):
@@ -331,7 +384,7 @@ def triattn_core(qkg, vt, tb, mask, trans: bool, inf: float, N: int, H: int, C: 
     if trans:
         # the ending node's row i reads column i of the mask: a transposed copy makes the kernel's per-block mask
         # loads contiguous (strided, every lane touched its own cache line: 13% of the core at N = 1000)
-        mask = mask.reshape(N, N).t().contiguous()
+        mask = mask_transposed(mask, N)
     call("bzpf_triattn_core", _p(qkg), _p(vt), _p(tb), _p(mask), N, 1, float(inf), _p(out), _dt(qkg), N, ldk, H, C,
          TRIATT_IMPL if impl is None else int(impl), _stream())
     return out

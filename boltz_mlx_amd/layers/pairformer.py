@@ -214,20 +214,21 @@ class PairformerModule(torch.nn.Module):
             return (lambda: release(lambda: [lay._s_attention(sb, bias, mb) for lay, sb, bias, mb in pending]),
                     lambda: release(lambda: [lay._s_transition(sb) for lay, sb, _, _ in pending]))
 
-        xn = xn if B == 1 else None
-        pending = []  # s-track work of the previous layer: (layer, s[b], pair bias, mask[b])
-        for k in range(count):
-            i = (start + k) % n
-            layer = self.layers[i]
-            nxt = self.layers[(i + 1) % n].tri_mul_out.norm_in if (i + 1 < n or cycle) else None
-            done = []
-            for b in range(B):
-                hooks = hooks_for(pending) if b == 0 else (None, None)
-                xn, bias = _pair_chain(layer, z[b], pair_mask[b], xn if B == 1 else None, nxt if B == 1 else None,
-                                       hooks, pair_bias=layer._pair_bias_args())
-                bias.record_stream(side)  # allocated on the main stream, read on the side stream
-                done.append((layer, s[b], bias, mask[b]))
-            pending = done
+        with K.pair_mask_scope():  # the mask-derived values are made once for all the layers
+            xn = xn if B == 1 else None
+            pending = []  # s-track work of the previous layer: (layer, s[b], pair bias, mask[b])
+            for k in range(count):
+                i = (start + k) % n
+                layer = self.layers[i]
+                nxt = self.layers[(i + 1) % n].tri_mul_out.norm_in if (i + 1 < n or cycle) else None
+                done = []
+                for b in range(B):
+                    hooks = hooks_for(pending) if b == 0 else (None, None)
+                    xn, bias = _pair_chain(layer, z[b], pair_mask[b], xn if B == 1 else None,
+                                           nxt if B == 1 else None, hooks, pair_bias=layer._pair_bias_args())
+                    bias.record_stream(side)  # allocated on the main stream, read on the side stream
+                    done.append((layer, s[b], bias, mask[b]))
+                pending = done
         hooks = hooks_for(pending)
         hooks[0]()
         hooks[1]()
@@ -285,9 +286,10 @@ class PairformerNoSeqModule(torch.nn.Module):
 
         def run():
             n, xn = len(self.layers), None
-            for i, layer in enumerate(self.layers):
-                nxt = self.layers[i + 1].tri_mul_out.norm_in if i + 1 < n else None
-                xn = layer.inplace(z, pm, xn_in=xn, next_ln=nxt)
+            with K.pair_mask_scope():
+                for i, layer in enumerate(self.layers):
+                    nxt = self.layers[i + 1].tri_mul_out.norm_in if i + 1 < n else None
+                    xn = layer.inplace(z, pm, xn_in=xn, next_ln=nxt)
 
         _guarded(self, run, (z,), (z_in,))
         return z

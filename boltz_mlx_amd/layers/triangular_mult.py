@@ -65,7 +65,7 @@ class _TriangleMultiplication(torch.nn.Module):
             K.linear_gated(on, w_po, K.linear(xn, w_go, out_dtype=torch.float32), z2)
             return None if next_ln is None else next_ln.to_storage(z).reshape(N * N, D)
         ab = K.trimul_proj(xn, w_pg, mask, 2.0 ** -kexp, not self.outgoing, N)
-        o = K.trimul_contract(ab, N)
+        o = K.trimul_contract(ab, N, K.key_extent(mask, N, not self.outgoing))
         del ab
         return K.trimul_tail(o, self.norm_out, self.norm_out.eps * 2.0 ** (-4 * kexp), w_po, xn, w_go, z,
                              accumulate, next_ln, N)

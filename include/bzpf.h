@@ -66,9 +66,13 @@ int bzpf_trimul_proj(const void* xn, const void* w_pg, const float* pair_mask, f
                      int dt, int64_t N, int64_t ld, int D, void* stream);
 
 /* Per-channel contraction o[c][i][j] = sum_k ab[c][i][k] * ab[D + c][j][k] for c < D, o [D][N][ld] (dt; columns
- * j >= N are not written). Replaces the mx.matmul contraction (boltz_mlx/layers/triangular_mult.py:90-93, 172-175)
- * and kernels_nax2.trimul_contract_nax (boltz_mlx/kernels_nax2.py:315-407). */
-int bzpf_trimul_contract(const void* ab, void* o, int dt, int64_t N, int64_t ld, int D, void* stream);
+ * j >= N are not written). k_len: when 0 < k_len < N, the caller guarantees that columns k >= k_len of ab are zero
+ * (bzpf_trimul_proj writes zeros where the pair mask is zero, so k_len = 1 + the last token whose mask column
+ * (outgoing) or row (incoming) is not all zero), and the sum stops at k_len rounded up to 64: the same result bit
+ * for bit, without the trailing padded tokens' work. 0 (or >= N): every k. Replaces the mx.matmul contraction
+ * (boltz_mlx/layers/triangular_mult.py:90-93, 172-175) and kernels_nax2.trimul_contract_nax
+ * (boltz_mlx/kernels_nax2.py:315-407). */
+int bzpf_trimul_contract(const void* ab, void* o, int dt, int64_t N, int64_t ld, int D, int64_t k_len, void* stream);
 
 /* Triangle-multiplication tail: at each position p = (i, j),
  *   y = (LN_out(o[:, i, j]; eps_out) . W_po^T) * sigmoid(xn[p] . W_go^T);  z[p] = (accumulate ? z[p] : 0) + y;

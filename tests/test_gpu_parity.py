@@ -141,6 +141,57 @@ def test_trimul_contract_raw(N, dt):
     assert np.array_equal(o, ref)
 
 
+@pytest.mark.parametrize("N", [130, 300])
+@pytest.mark.parametrize("dt", [torch.float32, torch.float16])
+def test_trimul_contract_key_extent_exact(N, dt):
+    """With columns k >= k_len of ab zero (trailing padded tokens), the contraction stopped at k_len (rounded up to
+    64) equals the full one bit for bit, for extents inside a stage, on a stage edge and of one key; 0 and N mean
+    every key. Random fp16/fp32 values (not exact integers), so any change in the summed terms would show."""
+    from boltz_mlx_amd import kernels as K
+
+    D = 8
+    ld = K.row_pitch(N)
+    rng = np.random.default_rng(4100 + N)
+    for k_len in (1, 64, N - 37, N - 1, 0, N):
+        ab = np.zeros((2 * D, N, ld))
+        kk = k_len if 0 < k_len < N else N
+        ab[:, :, :kk] = rng.standard_normal((2 * D, N, kk))
+        abd = dev(ab, dt)
+        full = K.trimul_contract(abd, N)
+        part = K.trimul_contract(abd, N, k_len)
+        torch.cuda.synchronize()
+        assert torch.equal(part[:, :, :N], full[:, :, :N]), (N, k_len)
+
+
+@pytest.mark.parametrize("precision", ["f16"], indirect=True)
+@pytest.mark.parametrize("outgoing", [True, False])
+def test_tri_mul_in_mask_scope_equals_plain(precision, outgoing):
+    """Inside pair_mask_scope the module contracts only up to the key extent of its (asymmetric, trailing-padded)
+    mask; the update equals the call outside a scope (every key) bit for bit, in f16."""
+    from boltz_mlx_amd import kernels as K
+    from boltz_mlx_amd.layers.triangular_mult import TriangleMultiplicationIncoming, TriangleMultiplicationOutgoing
+
+    N, D = 200, 128
+    torch.manual_seed(3)
+    m = (TriangleMultiplicationOutgoing if outgoing else TriangleMultiplicationIncoming)(D).cuda()
+    with torch.no_grad():
+        for prm in m.parameters():
+            prm.normal_(0.0, 0.05)
+    rng = np.random.default_rng(7)
+    z = dev(rng.standard_normal((N, N, D)))
+    tok = np.ones(N)
+    tok[N - 70:] = 0
+    mask = dev((tok[:, None] * tok[None, :] * (rng.random((N, N)) > 0.1)).astype(np.float32))
+    xn = m.norm_in.to_storage(z).reshape(N * N, D)
+    z1, z2 = z.clone(), z.clone()
+    m.fused(xn, mask, z1, True)
+    with K.pair_mask_scope():
+        assert K.key_extent(mask, N, not outgoing) <= N - 70
+        m.fused(xn, mask, z2, True)
+    torch.cuda.synchronize()
+    assert torch.equal(z1, z2)
+
+
 # ------------------------------------------------------------------------------------------------ modules
 
 TRI_N = [1, 2, 17, 33, 70, 130]

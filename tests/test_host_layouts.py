@@ -21,3 +21,34 @@ def test_group_swiglu_rows():
         assert torch.equal(g2[64 * q:64 * q + 32], ws[0][32 * q:32 * (q + 1)])
         assert torch.equal(g2[64 * q + 32:64 * (q + 1)], ws[1][32 * q:32 * (q + 1)])
     assert torch.equal(torch.sort(g3.flatten())[0], torch.sort(torch.cat(ws).flatten())[0])
+
+
+def test_pair_mask_scope_extent_and_transpose():
+    """key_extent / mask_transposed: nothing is derived outside a scope (extent 0 = every key, a fresh transposed
+    copy per call); inside, the extent is 1 + the last live token (columns for outgoing, rows for incoming, checked
+    by brute force on an asymmetric mask), each value is made once per mask, and an in-place change of the mask
+    (a new version) is seen."""
+    from boltz_mlx_amd import kernels as K
+
+    N = 70
+    g = torch.Generator().manual_seed(5)
+    m = (torch.rand((N, N), generator=g) > 0.4).float()
+    m[:, 61:] = 0  # columns past 60 dead (outgoing extent 61)
+    m[55:, :] = 0  # rows past 54 dead (incoming extent 55)
+    brute_out = 1 + max(k for k in range(N) if any(m[i, k] != 0 for i in range(N)))
+    brute_in = 1 + max(k for k in range(N) if any(m[k, i] != 0 for i in range(N)))
+    assert (brute_out, brute_in) == (61, 55)
+    assert K.key_extent(m, N, False) == 0 and K.key_extent(m, N, True) == 0
+    t0 = K.mask_transposed(m, N)
+    assert torch.equal(t0, m.t()) and t0.is_contiguous() and K.mask_transposed(m, N) is not t0
+    with K.pair_mask_scope():
+        assert K.key_extent(m, N, False) == brute_out and K.key_extent(m, N, True) == brute_in
+        t1 = K.mask_transposed(m, N)
+        assert torch.equal(t1, m.t()) and K.mask_transposed(m.view(N, N), N) is t1  # a view of the same storage
+        m[:, 69] = 1  # in place: a new version
+        assert K.key_extent(m, N, False) == N and K.key_extent(m, N, True) == N
+        assert torch.equal(K.mask_transposed(m, N), m.t())
+        with K.pair_mask_scope():  # nested scopes start empty and restore the outer one
+            assert K.key_extent(torch.zeros(N, N), N, False) == N
+        assert K.mask_transposed(m, N) is K.mask_transposed(m, N)
+    assert K.key_extent(m, N, False) == 0

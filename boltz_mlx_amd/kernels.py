@@ -296,9 +296,9 @@ def mask_transposed(mask: torch.Tensor, N: int) -> torch.Tensor:
 def key_extent(mask: torch.Tensor, N: int, incoming: bool) -> int:
     """1 + the last token k whose pair-mask column (outgoing; row for incoming) is not all zero: bzpf_trimul_proj
     writes zeros in ab for every k past it. Computed (one host sync) only inside pair_mask_scope, once per mask;
-    0 (every key) outside."""
+    0 (every key) outside, and during stream capture (no sync there)."""
     ent = _mask_entry(mask)
-    if ent is None:
+    if ent is None or torch.cuda.is_current_stream_capturing():
         return 0
     if ("ext", incoming) not in ent:
         m = mask.reshape(N, N) != 0

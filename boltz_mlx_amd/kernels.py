@@ -298,7 +298,7 @@ def key_extent(mask: torch.Tensor, N: int, incoming: bool) -> int:
     writes zeros in ab for every k past it. Computed (one host sync) only inside pair_mask_scope, once per mask;
     0 (every key) outside, and during stream capture (no sync there)."""
     ent = _mask_entry(mask)
-    if ent is None or torch.cuda.is_current_stream_capturing():
+    if ent is None or (mask.is_cuda and torch.cuda.is_current_stream_capturing()):
         return 0
     if ("ext", incoming) not in ent:
         m = mask.reshape(N, N) != 0

@@ -476,8 +476,11 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 3 : 2) void linear_resid_ln_k
                                                                                 int64_t N) {
   constexpr int STEPS = RG<T>::STEPS, LDW = ldw_of<T>();
   __shared__ LDS_ALIGN T Ws[D * LDW];
+  __shared__ LnLds lns;
   lds_rows<T>(Ws, LDW, D, D, [&](int r) { return w + (int64_t)r * D; });
+  stage_ln(lns, lnw, lnb);
   __syncthreads();
+  const float* lw = lnw != nullptr ? lns.w : nullptr;
   const int64_t NN = N * N;
   const int ntiles = (int)((NN + 15) / 16), stride = gridDim.x * 4;
   const int l = threadIdx.x & 63, g = l >> 4;
@@ -505,7 +508,7 @@ __global__ __launch_bounds__(256, sizeof(T) == 2 ? 3 : 2) void linear_resid_ln_k
     zero_acc(y);
     mma_rows_grouped<T, 1, 8, 2>(y, x, Ws, LDW);
     const int64_t zr = zrow_of(t);
-    resid_ln_apply<T, 1>(y, zv, [&](int) { return zr; }, z, lnw, lnb, eps, xn_next);
+    resid_ln_apply<T, 1>(y, zv, [&](int) { return zr; }, z, lw, lns.b, eps, xn_next);
 #pragma unroll
     for (int s = 0; s < STEPS; s++) x[0][s] = xnext[0][s];
 #pragma unroll
@@ -653,6 +656,7 @@ __global__ __launch_bounds__(64 * TRW, 8 / TRW) void transition_f16_k(const half
   __shared__ float Bpb[16];
   __shared__ LDS_ALIGN T Wo[AO ? D * LDW : 8];
   __shared__ LDS_ALIGN T Scr[AO ? TRW * 16 * SCR_P : 8];  // per wave: 16 rows of the attention stage's LayerNorm
+  __shared__ LnLds lns[AO ? 2 : 1];                         // the next LayerNorm; [1]: the attention stage's
   const int t = threadIdx.x, l = t & 63, g = l >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int nch = hidden / TR_HCH;
@@ -660,6 +664,10 @@ __global__ __launch_bounds__(64 * TRW, 8 / TRW) void transition_f16_k(const half
   int64_t tile = blockIdx.x;
   if (tile >= ntiles) return;  // whole workgroup
   if constexpr (AO) lds_rows<T>(Wo, LDW, D, D, [&](int r) { return ao.w_o + (int64_t)r * D; });
+  stage_ln(lns[0], lnw, lnb);
+  if constexpr (AO) stage_ln(lns[AO ? 1 : 0], ao.lnw, ao.lnb);
+  const float* lw = lnw != nullptr ? lns[0].w : nullptr;
+  const float* lb = lns[0].b;
   if constexpr (PB) {
     for (int e = t; e < 16 * D; e += 64 * TR_WAVES) {
       const int h = e >> 7, c = e & (D - 1);
@@ -734,7 +742,7 @@ __global__ __launch_bounds__(64 * TRW, 8 / TRW) void transition_f16_k(const half
     if constexpr (AO) {
       const int64_t r0 = tile * TROWS + wave * 16 * RB + (l & 15);
       attn_out_rows<RB>(x, Wo, LDW, [&](int rb) -> int64_t { return r0 + 16 * rb < rows_total ? r0 + 16 * rb : -1; },
-                        z, ao.lnw, ao.lnb, ao.eps, Scr + wave * 16 * SCR_P);
+                        z, lns[AO ? 1 : 0].w, lns[AO ? 1 : 0].b, ao.eps, Scr + wave * 16 * SCR_P);
     }
     f4 out[RB][8];
     zero_acc(out);
@@ -797,19 +805,19 @@ __global__ __launch_bounds__(64 * TRW, 8 / TRW) void transition_f16_k(const half
         for (int cb = 0; cb < 8; cb++) zv[cb] = y1[0][cb] + zz[0][cb];
       };
       if constexpr (PB) {
-        resid_ln_pb_apply<RB>(out, zvf, zrow, z, lnw, lnb, eps, xn_next, Wpb, LDP, Bpb, pb_eps, pb_out, rows_total,
+        resid_ln_pb_apply<RB>(out, zvf, zrow, z, lw, lb, eps, xn_next, Wpb, LDP, Bpb, pb_eps, pb_out, rows_total,
                               pb_heads);
       } else {
         f4 zv[RB][8];
 #pragma unroll
         for (int rb = 0; rb < RB; rb++) zvf(rb, zv[rb]);
-        resid_ln_apply<T, RB>(out, zv, zrow, z, lnw, lnb, eps, xn_next);
+        resid_ln_apply<T, RB>(out, zv, zrow, z, lw, lb, eps, xn_next);
       }
     } else if constexpr (PB) {
-      resid_ln_pb_rows<RB>(out, zrow, z, accumulate, lnw, lnb, eps, xn_next, Wpb, LDP, Bpb, pb_eps, pb_out,
+      resid_ln_pb_rows<RB>(out, zrow, z, accumulate, lw, lb, eps, xn_next, Wpb, LDP, Bpb, pb_eps, pb_out,
                            rows_total, pb_heads);
     } else {
-      resid_ln_rows<T, RB>(out, zrow, z, accumulate, lnw, lnb, eps, xn_next);
+      resid_ln_rows<T, RB>(out, zrow, z, accumulate, lw, lb, eps, xn_next);
     }
 #pragma unroll
     for (int rb = 0; rb < RB; rb++)

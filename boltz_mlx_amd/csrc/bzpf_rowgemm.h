@@ -153,6 +153,22 @@ __device__ __forceinline__ void lds_rows(T* dst, int ld, int rows, int k, RowFn 
   }
 }
 
+// LayerNorm weight and bias (128 channels each) staged in LDS for the epilogues below, which read them per 16-channel
+// block. From global memory each of those reads is a separate round trip whose s_waitcnt vmcnt(0) also waits for
+// every tile prefetch and store issued before it (the counter is in order), once per column block; from LDS they
+// are lgkmcnt waits only. stage_ln runs before the kernel's first barrier; w == nullptr leaves the arrays unset.
+struct LnLds {
+  float w[128];
+  float b[128];
+};
+__device__ __forceinline__ void stage_ln(LnLds& s, const float* __restrict__ w, const float* __restrict__ b) {
+  if (w == nullptr) return;
+  for (int c = threadIdx.x; c < 128; c += blockDim.x) {
+    s.w[c] = w[c];
+    s.b[c] = b[c];
+  }
+}
+
 // 4 consecutive elements of T from / to memory as fp32.
 __device__ __forceinline__ f4 ld4(const float* p) { return *reinterpret_cast<const f4*>(p); }
 __device__ __forceinline__ f4 ld4(const half_t* p) {

@@ -52,7 +52,9 @@ __global__ __launch_bounds__(64 * PROJ_WAVES) void trimul_proj_k(const T* __rest
 
   typedef typename RG<T>::frag Frag;
   Frag x[HV][RB][STEPS];
-  float mk[HV][RB];  // mask * scale of the rows this lane loads (0 past N: padding columns are written as 0)
+  // mask values of the rows this lane loads, raw (at the clamped position): scaled, and zeroed past N (padding columns
+  // are written as 0), where they are used. Any arithmetic on them at the load would wait for the prefetch there.
+  float mk[HV][RB];
   const auto load = [&](int tt, Frag (&xx)[HV][RB][STEPS], float (&mm)[HV][RB]) {
     const int i = tt / tpr, k0 = (tt - i * tpr) * HV * TW;
 #pragma unroll
@@ -62,7 +64,7 @@ __global__ __launch_bounds__(64 * PROJ_WAVES) void trimul_proj_k(const T* __rest
         const int64_t k = k0 + hh * TW + RT::pos(rb, r), kc = k < N ? k : N - 1;
         const int64_t src = incoming ? kc * N + i : (int64_t)i * N + kc;
         RG<T>::load_row(xx[hh][rb], xn + src * D, g);
-        mm[hh][rb] = k < N ? mask[src] * scale : 0.0f;
+        mm[hh][rb] = mask[src];
       }
   };
   load(t, x, mk);
@@ -75,9 +77,11 @@ __global__ __launch_bounds__(64 * PROJ_WAVES) void trimul_proj_k(const T* __rest
 #pragma unroll
     for (int hh = 0; hh < HV; hh++)
 #pragma unroll
-      for (int rb = 0; rb < RB; rb++)
+      for (int rb = 0; rb < RB; rb++) {
+        const float mv = k0 + hh * TW + RT::pos(rb, r) < N ? mk[hh][rb] * scale : 0.0f;
 #pragma unroll
-        for (int e = 0; e < 4; e++) mo[hh][rb][e] = __shfl(mk[hh][rb], 4 * g + e);
+        for (int e = 0; e < 4; e++) mo[hh][rb][e] = __shfl(mv, 4 * g + e);
+      }
     T* dst = ab + ((int64_t)(c_lo + r) * N + i) * ld + k0 + RT::RUN * g;
     for (int cb = 0; cb < PCH / 16; cb++) {
 #pragma unroll

@@ -455,11 +455,14 @@ def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=64, help="timed Pairformer blocks at N")
-    ap.add_argument("--warmup", type=int, default=4)
+    ap.add_argument("--warmup", type=int, default=32)
     ap.add_argument("--n", type=int, default=1000)
     ap.add_argument("--n-small", type=int, default=400)
-    ap.add_argument("--small-warmup", type=int, default=16, help="untimed blocks before the N=400 figure")
-    ap.add_argument("--small-steps", type=int, default=128, help="timed blocks for the N=400 figure")
+    ap.add_argument("--small-warmup", type=int, default=64,
+                    help="untimed blocks before the N=400 figure (at least, and at least 0.5 s of them)")
+    ap.add_argument("--small-steps", type=int, default=128, help="timed blocks per window for the N=400 figure")
+    ap.add_argument("--small-windows", type=int, default=3,
+                    help="timed windows at N=400; the figure is the median window")
     ap.add_argument("--cpu-budget", type=float, default=25.0,
                     help="seconds per CPU-baseline configuration (bounds the timed runs after the warm-up)")
     ap.add_argument("--blocks", type=int, default=64)
@@ -498,17 +501,28 @@ def main() -> int:
         with torch.no_grad():
             print(json.dumps({"msa_layer": msa_layer_leg(args.msa_steps, dev)}), flush=True)
         return 0
-    result_small = None
+    result_small, small_windows = None, None
     with torch.no_grad():
         # N = 400 blocks/s (secondary figure)
         if args.n_small:
             m, s, z, tok, pm = make_trunk(args.n_small, args.blocks, 0, dev)
-            xn = run_blocks(m, s, z, tok, pm, 0, args.small_warmup)
-            torch.cuda.synchronize()
-            t0 = time.perf_counter()
-            run_blocks(m, s, z, tok, pm, args.small_warmup, args.small_steps, xn)
-            torch.cuda.synchronize()
-            result_small = args.small_steps / (time.perf_counter() - t0)
+            # warm-up: at least small_warmup blocks and 0.5 s of them (clocks settle), then the median of the
+            # timed windows
+            done, t0 = 0, time.perf_counter()
+            xn = None
+            while done < args.small_warmup or time.perf_counter() - t0 < 0.5:
+                xn = run_blocks(m, s, z, tok, pm, done, 16, xn)
+                done += 16
+                torch.cuda.synchronize()
+            windows = []
+            for _ in range(max(1, args.small_windows)):
+                t0 = time.perf_counter()
+                xn = run_blocks(m, s, z, tok, pm, done, args.small_steps, xn)
+                torch.cuda.synchronize()
+                windows.append(args.small_steps / (time.perf_counter() - t0))
+                done += args.small_steps
+            result_small = sorted(windows)[len(windows) // 2]
+            small_windows = [round(w, 1) for w in windows]
             del m, s, z, tok, pm
             torch.cuda.empty_cache()
         m, s, z, tok, pm = make_trunk(args.n, args.blocks, 0, dev)
@@ -566,6 +580,7 @@ def main() -> int:
                    "blocks": args.blocks, "token_s": 384, "token_z": 128, "s_heads": 16,
                    "tri_heads": 4, "tri_head_dim": 32, "pad_frac": 0.05, "parallelism": "none (1 GPU)"},
         "blocks_per_s_n400": None if result_small is None else round(result_small, 4),
+        "n400_windows": small_windows,
         "tflops_effective": round(value * block_flops(args.n) / 1e12, 2),
         "finite": finite,
         "roofline": roof,

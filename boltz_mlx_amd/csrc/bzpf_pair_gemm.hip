@@ -643,7 +643,8 @@ __global__ __launch_bounds__(64 * TRW, 8 / TRW) void transition_f16_k(const half
                                                                   const float* __restrict__ pb_lnw,
                                                                   const float* __restrict__ pb_lnb, float pb_eps,
                                                                   half_t* __restrict__ pb_out, int pb_heads,
-                                                                  AttnOutArgs ao) {
+                                                                  AttnOutArgs ao, int64_t full_items,
+                                                                  int part_rows) {
   using T = half_t;
   constexpr int RB = 2, STEPS = RG<T>::STEPS, LDW = ldw_of<T>(), LDH = TR_HCH + Pad<T>::v, HB = TR_HCH / 16;
   constexpr int TR_WAVES = TRW, TROWS = 16 * RB * TR_WAVES;
@@ -664,7 +665,18 @@ __global__ __launch_bounds__(64 * TRW, 8 / TRW) void transition_f16_k(const half
   const int t = threadIdx.x, l = t & 63, g = l >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int nch = hidden / TR_HCH;
-  const int64_t ntiles = (rows_total + TROWS - 1) / TROWS;
+  // Work items: full_items tiles of TROWS rows, then the remaining rows in items of part_rows (a multiple of 32: whole
+  // waves), so that the last round spreads over the grid instead of leaving most workgroups idle; in such an item
+  // the waves past its rows stage chunks and meet the barriers but compute nothing.
+  const int64_t part_base = full_items * TROWS;
+  const int64_t ntiles =
+      full_items + (rows_total > part_base ? (rows_total - part_base + part_rows - 1) / part_rows : 0);
+  const auto item_base = [&](int64_t it) -> int64_t {
+    return it < full_items ? it * TROWS : part_base + (it - full_items) * part_rows;
+  };
+  const auto item_rows = [&](int64_t it) -> int {
+    return it < full_items ? TROWS : (int)min((int64_t)part_rows, rows_total - item_base(it));
+  };
   int64_t tile = blockIdx.x;
   if (tile >= ntiles) return;  // whole workgroup
   if constexpr (AO) lds_rows<T>(Wo, LDW, D, D, [&](int r) { return ao.w_o + (int64_t)r * D; });
@@ -725,7 +737,7 @@ __global__ __launch_bounds__(64 * TRW, 8 / TRW) void transition_f16_k(const half
   const auto xload = [&](int64_t tl, typename RG<T>::frag (&xx)[RB][STEPS]) {
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) {
-      const int64_t row = tl * TROWS + wave * 16 * RB + 16 * rb + (l & 15), rc = row < rows_total ? row : rows_total - 1;
+      const int64_t row = item_base(tl) + wave * 16 * RB + 16 * rb + (l & 15), rc = row < rows_total ? row : rows_total - 1;
       if constexpr (AO) {
         const int64_t orow = ao.trans ? (rc % ao.n) * ao.n + rc / ao.n : rc;
         RG<T>::load_row(xx[rb], ao.o + orow * D, g);
@@ -743,10 +755,14 @@ __global__ __launch_bounds__(64 * TRW, 8 / TRW) void transition_f16_k(const half
   gload(nch > 1 ? 1 : 0);
   int q = 0;  // chunks computed so far (LDS buffer parity)
   for (; tile < ntiles; tile += gridDim.x) {
+    const int64_t base = item_base(tile);
+    const int cnt = item_rows(tile), lrow0 = wave * 16 * RB + (l & 15);
+    const bool wact = wave * 16 * RB < cnt;  // wave-uniform: the wave has rows in this item
+    const int64_t row0 = base + lrow0;
+    const auto zrow = [&](int rb) -> int64_t { return lrow0 + 16 * rb < cnt ? row0 + 16 * rb : -1; };
     if constexpr (AO) {
-      const int64_t r0 = tile * TROWS + wave * 16 * RB + (l & 15);
-      attn_out_rows<RB>(x, Wo, LDW, [&](int rb) -> int64_t { return r0 + 16 * rb < rows_total ? r0 + 16 * rb : -1; },
-                        z, lns[AO ? 1 : 0].w, lns[AO ? 1 : 0].b, ao.eps, Scr + wave * 16 * SCR_P);
+      if (wact)
+        attn_out_rows<RB>(x, Wo, LDW, zrow, z, lns[AO ? 1 : 0].w, lns[AO ? 1 : 0].b, ao.eps, Scr + wave * 16 * SCR_P);
     }
     f4 out[RB][8];
     zero_acc(out);
@@ -754,6 +770,7 @@ __global__ __launch_bounds__(64 * TRW, 8 / TRW) void transition_f16_k(const half
     for (int c = 0; c < nch; c++, q++) {
       const int buf = q & 1;
       if (c == nch - 1) xload(min(tile + (int64_t)gridDim.x, ntiles - 1), xnext);
+      if (wact) {
       f4 a[RB][HB];
 #pragma unroll
       for (int hb = 0; hb < HB; hb++) {
@@ -785,13 +802,14 @@ __global__ __launch_bounds__(64 * TRW, 8 / TRW) void transition_f16_k(const half
             out[rb][ob] = __builtin_amdgcn_mfma_f32_16x16x32_f16(af, bf[rb], out[rb][ob], 0, 0, 0);
         }
       }
+      }
       lstore(buf ^ 1);
       __syncthreads();
       gload(c + 2 < nch ? c + 2 : c + 2 - nch >= nch ? 0 : c + 2 - nch);
     }
-    const int64_t row0 = tile * TROWS + wave * 16 * RB + (l & 15);
-    const auto zrow = [&](int rb) -> int64_t { return row0 + 16 * rb < rows_total ? row0 + 16 * rb : -1; };
-    if constexpr (AO) {
+    if (!wact) {
+      // no rows here: the next item's rows (loaded during the last chunk) become current
+    } else if constexpr (AO) {
       // the residual is z' = z + W_o o^T again, recomputed from the tile's o and z rows (x now holds the next
       // tile's o rows)
       const auto zvf = [&](int rb, f4(&zv)[8]) {
@@ -978,12 +996,17 @@ static hipError_t trans_f16_w(const void* xn, const void* w12, const void* w3, f
   static int cache[kMaxDevices];
   const int resident = resident_grid(transition_f16_k<PB, TRW, AO>, 64 * TRW, cache);
   if (resident <= 0) return hipErrorInvalidDevice;
-  const int64_t ntiles = (rows + 32 * TRW - 1) / (32 * TRW);  // 32 TRW-row tiles
-  const dim3 grid((unsigned)std::min<int64_t>(resident, ntiles));
+  if (rows <= 0) return hipSuccess;
+  // whole rounds of 32 TRW-row tiles over the resident grid, then the remaining rows split evenly over it in items
+  // of whole waves (32 rows each)
+  const int64_t trows = 32 * TRW, full_items = rows / (trows * resident) * resident, rem = rows - full_items * trows;
+  const int64_t part = rem > 0 ? ((rem + resident - 1) / resident + 31) / 32 * 32 : trows;
+  const int64_t nitems = full_items + (rem + part - 1) / part;
+  const dim3 grid((unsigned)std::min<int64_t>(resident, nitems));
   transition_f16_k<PB, TRW, AO><<<grid, 64 * TRW, 0, st>>>(
       static_cast<const half_t*>(xn), static_cast<const half_t*>(w12), static_cast<const half_t*>(w3), z, accumulate,
       lnw, lnb, eps, static_cast<half_t*>(xn_next), rows, hidden, static_cast<const half_t*>(pb_w), pb_lnw, pb_lnb,
-      pb_eps, static_cast<half_t*>(pb_out), pb_heads, ao);
+      pb_eps, static_cast<half_t*>(pb_out), pb_heads, ao, full_items, (int)part);
   return hipGetLastError();
 }
 

@@ -38,7 +38,7 @@ SIGNATURES = {
                                  i64, i32, i32, vp],
     "bzpf_linear": [vp, vp, vp, vp, i32, i32, i64, i32, i32, i32, vp],
     "bzpf_swiglu": [vp, vp, i32, i64, i32, vp],
-    "bzpf_seq_attention": [vp, vp, vp, vp, i64, vp, vp, f32, vp, i64, i32, i64, i32, i32, vp],
+    "bzpf_seq_attention": [vp, vp, vp, vp, i64, vp, vp, f32, vp, i64, i32, i32, i64, i32, i32, vp],
     "bzpf_linear_swiglu3": [vp, vp, vp, i64, i32, i32, vp],
     "bzpf_linear_swiglu": [vp, vp, vp, i64, i32, i32, vp],
     "bzpf_trimul_pack": [vp, vp, f32, i32, vp, i32, i64, i64, i32, vp],
@@ -47,8 +47,8 @@ SIGNATURES = {
     "bzpf_opm_outer": [vp, i64, vp, vp, vp, i32, i32, i32, i32, i32, vp],
     "bzpf_pwa_softmax": [vp, vp, f32, vp, i32, i64, i32, vp],
     "bzpf_pwa_avg": [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32, vp],
-    "bzpf_seq_attention_batched": [vp, vp, vp, vp, i64, i64, vp, i64, i32, vp, i64, f32, vp, i64, i64, i32, i32, i64,
-                                   i32, i32, vp],
+    "bzpf_seq_attention_batched": [vp, vp, vp, vp, i64, i64, vp, i64, i32, vp, i64, f32, vp, i64, i64, i32, i32, i32,
+                                   i64, i32, i32, vp],
     "bzpf_pair_bias": [vp, vp, vp, f32, vp, vp, i32, i64, i32, i32, vp],
 }
 _RESTYPES = {"bzpf_version": C.c_char_p, "bzpf_last_error": C.c_char_p, "bzpf_row_pitch": i64}

@@ -300,25 +300,25 @@ int bzpf_adaln(const float* a, const float* scale, const float* shift, int64_t l
 
 int bzpf_seq_attention_batched(const void* q, const void* k, const void* v, const void* g, int64_t ld_in,
                                int64_t s_in, const void* bias, int64_t s_bias, int mult, const float* mask,
-                               int64_t s_mask, float inf, void* out, int64_t ld_out, int64_t s_out, int dt, int n_samples,
-                               int64_t N, int H, int hd, void* stream) {
+                               int64_t s_mask, float inf, void* out, int64_t ld_out, int64_t s_out, int dt, int bias_dt,
+                               int n_samples, int64_t N, int H, int hd, void* stream) {
   REQUIRE(q && k && v && g && bias && mask && out, "bzpf_seq_attention: NULL pointer");
-  REQUIRE(dt_ok(dt), "bzpf_seq_attention: bad dtype");
+  REQUIRE(dt_ok(dt) && dt_ok(bias_dt), "bzpf_seq_attention: bad dtype");
   REQUIRE(hd == 16 || hd == 24 || hd == 32 || hd == 48 || hd == 64, "bzpf_seq_attention: hd=%d unsupported", hd);
   REQUIRE(H >= 1 && H <= 65535 && N >= 1 && ld_in >= (int64_t)H * hd && ld_out >= (int64_t)H * hd,
           "bzpf_seq_attention: bad sizes");
   REQUIRE(n_samples >= 1 && n_samples <= 65535 && mult >= 1 && s_in >= 0 && s_bias >= 0 && s_mask >= 0 && s_out >= 0,
           "bzpf_seq_attention: bad sample count or strides (S=%d mult=%d)", n_samples, mult);
   return done(bzpf::launch_seq_attention(q, k, v, g, ld_in, s_in, bias, s_bias, mult, mask, s_mask, inf, out, ld_out,
-                                         s_out, dt, n_samples, N, H, hd, S(stream)),
+                                         s_out, dt, bias_dt, n_samples, N, H, hd, S(stream)),
               "bzpf_seq_attention");
 }
 
 int bzpf_seq_attention(const void* q, const void* k, const void* v, const void* g, int64_t ld_in, const void* bias,
-                       const float* mask, float inf, void* out, int64_t ld_out, int dt, int64_t N, int H, int hd,
-                       void* stream) {
-  return bzpf_seq_attention_batched(q, k, v, g, ld_in, 0, bias, 0, 1, mask, 0, inf, out, ld_out, 0, dt, 1, N, H, hd,
-                                    stream);
+                       const float* mask, float inf, void* out, int64_t ld_out, int dt, int bias_dt, int64_t N, int H,
+                       int hd, void* stream) {
+  return bzpf_seq_attention_batched(q, k, v, g, ld_in, 0, bias, 0, 1, mask, 0, inf, out, ld_out, 0, dt, bias_dt, 1, N,
+                                    H, hd, stream);
 }
 
 int bzpf_linear_swiglu3(const void* x, const void* w, void* u, int64_t rows, int K, int H, void* stream) {

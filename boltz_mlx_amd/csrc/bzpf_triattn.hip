@@ -83,11 +83,12 @@ __global__ __launch_bounds__(64) void triattn_core_valu(const T* __restrict__ qk
 //   out[j][h*hd + d] = sigmoid(g[j][h*hd + d]) * sum_k softmax_k(q.k * scale + bias[h][j][k] + (1 - mask[k]) * -inf) v
 // A 256-thread workgroup owns (head h, 16 queries); the 16 threads of a query split the keys (key = 16 * t + lane)
 // with an online softmax each, and merge their (max, sum, accumulator) states with shuffles at the end. K, V and
-// the [16 x 64] bias tile are staged 64 keys at a time in LDS.
-template <typename T, int HD>
+// the [16 x 64] bias tile are staged 64 keys at a time in LDS. The bias type TB may differ from T (fp32 logits with
+// an fp16 pair bias, the reference's f16-mode s track).
+template <typename T, typename TB, int HD>
 __global__ __launch_bounds__(256) void seq_attn_kernel(const T* __restrict__ q, const T* __restrict__ k,
                                                        const T* __restrict__ v, const T* __restrict__ g,
-                                                       int64_t ld_in, const T* __restrict__ bias,
+                                                       int64_t ld_in, const TB* __restrict__ bias,
                                                        const float* __restrict__ mask, float inf,
                                                        T* __restrict__ out, int64_t ld_out, int64_t N, float scale) {
   constexpr int TK = 64;
@@ -107,7 +108,7 @@ __global__ __launch_bounds__(256) void seq_attn_kernel(const T* __restrict__ q, 
     acc[d] = 0.f;
   }
   float m = -INFINITY, lsum = 0.f;
-  const T* bh = bias + (int64_t)h * N * N;
+  const TB* bh = bias + (int64_t)h * N * N;
   for (int64_t k0 = 0; k0 < N; k0 += TK) {
     __syncthreads();
     for (int e = t; e < TK * HD; e += 256) {
@@ -162,17 +163,17 @@ __global__ __launch_bounds__(256) void seq_attn_kernel(const T* __restrict__ q, 
     out[j * ld_out + h * HD + d] = from_f<T>(acc[d] * inv * sigmoidf_(to_f(g[j * ld_in + h * HD + d])));
 }
 
-template <typename T>
+template <typename T, typename TB>
 static hipError_t seq_attn_t(const void* q, const void* k, const void* v, const void* g, int64_t ld_in,
                              const void* bias, const float* mask, float inf, void* out, int64_t ld_out, int64_t N,
                              int H, int hd, hipStream_t st) {
   const dim3 grid((unsigned)((N + 15) / 16), (unsigned)H);
   const float scale = 1.0f / sqrtf((float)hd);
 #define BZ_SEQ(HDV)                                                                                              \
-  seq_attn_kernel<T, HDV><<<grid, 256, 0, st>>>(static_cast<const T*>(q), static_cast<const T*>(k),            \
-                                                static_cast<const T*>(v), static_cast<const T*>(g), ld_in,      \
-                                                static_cast<const T*>(bias), mask, inf, static_cast<T*>(out),   \
-                                                ld_out, N, scale)
+  seq_attn_kernel<T, TB, HDV><<<grid, 256, 0, st>>>(static_cast<const T*>(q), static_cast<const T*>(k),        \
+                                                    static_cast<const T*>(v), static_cast<const T*>(g), ld_in,  \
+                                                    static_cast<const TB*>(bias), mask, inf,                    \
+                                                    static_cast<T*>(out), ld_out, N, scale)
   switch (hd) {
     case 16: BZ_SEQ(16); break;
     case 24: BZ_SEQ(24); break;
@@ -210,30 +211,33 @@ hipError_t launch_triattn_core_simple(const void* qkg, const void* vt, const voi
                       : core_valu_t<float>(qkg, vt, tb, mask, mask_si, mask_sk, inf, out, N, ldk, H, C, st);
 }
 
-// fp16 with head width 16, 24, 32, 48 or 64 (and the alignment its vector loads need) runs on the MFMA kernel
-// (bzpf_seqattn_mfma.hip), all S samples in one launch; fp32 and other widths on the VALU kernel
-// above, one launch per sample.
+// Head widths 16, 24, 32, 48 and 64 (with the alignment their vector loads need) run on the matrix cores, all S
+// samples in one launch: fp16 with an fp16 bias on bzpf_seqattn_mfma.hip, fp32 (with an fp32 or fp16 bias) on
+// bzpf_seqattn_f32.hip. fp16 with an fp32 bias and other widths run on the VALU kernel above, one launch per
+// sample.
 hipError_t launch_seq_attention(const void* q, const void* k, const void* v, const void* g, int64_t ld_in,
                                 int64_t s_in, const void* bias, int64_t s_bias, int mult, const float* mask,
-                                int64_t s_mask, float inf, void* out, int64_t ld_out, int64_t s_out, int dt, int S,
-                                int64_t N, int H, int hd, hipStream_t st) {
+                                int64_t s_mask, float inf, void* out, int64_t ld_out, int64_t s_out, int dt,
+                                int bias_dt, int S, int64_t N, int H, int hd, hipStream_t st) {
   const auto al = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; };
   if (S < 1 || mult < 1) return hipErrorInvalidValue;
-  if (dt == DT_F16 && (hd == 16 || hd == 24 || hd == 32 || hd == 48 || hd == 64) && N % 4 == 0 && ld_in % 8 == 0 &&
+  if (dt == DT_F16 && bias_dt == DT_F16 && (hd == 16 || hd == 24 || hd == 32 || hd == 48 || hd == 64) && N % 4 == 0 && ld_in % 8 == 0 &&
       ld_out % 4 == 0 && s_in % 8 == 0 && s_bias % 4 == 0 && s_out % 4 == 0 && al(q, 16) && al(k, 16) &&
       al(v, 16) && al(g, 16) && al(bias, 8) && al(out, 8) && N <= 32767 && S <= 65535 &&
       (N + 64) * ld_in * 2 <= 0x7fffffffLL && N * N * 2 <= 0x7fffffffLL)
     return launch_seq_attention_f16_mfma(q, k, v, g, ld_in, s_in, bias, s_bias, mult, mask, s_mask, inf, out, ld_out,
                                          s_out, S, N, H, hd, st);
-  const int64_t es = dt == DT_F16 ? 2 : 4;
+  if (dt == DT_F32 && (hd == 16 || hd == 24 || hd == 32 || hd == 48 || hd == 64) && ld_in % 4 == 0 &&
+      s_in % 4 == 0 && al(q, 16) && al(k, 16) && al(v, 16) && al(g, 16) && N <= 46340 && S <= 65535)
+    return launch_seq_attention_f32_mfma(q, k, v, g, ld_in, s_in, bias, s_bias, mult, mask, s_mask, inf, out, ld_out,
+                                         s_out, bias_dt, S, N, H, hd, st);
+  const int64_t es = dt == DT_F16 ? 2 : 4, esb = bias_dt == DT_F16 ? 2 : 4;
+  const auto launch = dt == DT_F16 ? (bias_dt == DT_F16 ? seq_attn_t<half_t, half_t> : seq_attn_t<half_t, float>)
+                                   : (bias_dt == DT_F16 ? seq_attn_t<float, half_t> : seq_attn_t<float, float>);
   for (int smp = 0; smp < S; smp++) {
-    const int64_t oi = smp * s_in * es, ob = (int64_t)(smp / mult) * s_bias * es, oo = smp * s_out * es;
+    const int64_t oi = smp * s_in * es, ob = (int64_t)(smp / mult) * s_bias * esb, oo = smp * s_out * es;
     const auto at = [](const void* p, int64_t off) { return static_cast<const void*>(static_cast<const char*>(p) + off); };
-    const hipError_t e =
-        dt == DT_F16
-            ? seq_attn_t<half_t>(at(q, oi), at(k, oi), at(v, oi), at(g, oi), ld_in, at(bias, ob), mask + smp * s_mask,
-                                 inf, static_cast<char*>(out) + oo, ld_out, N, H, hd, st)
-            : seq_attn_t<float>(at(q, oi), at(k, oi), at(v, oi), at(g, oi), ld_in, at(bias, ob), mask + smp * s_mask,
+    const hipError_t e = launch(at(q, oi), at(k, oi), at(v, oi), at(g, oi), ld_in, at(bias, ob), mask + smp * s_mask,
                                 inf, static_cast<char*>(out) + oo, ld_out, N, H, hd, st);
     if (e != hipSuccess) return e;
   }

@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import contextlib
 import os
+from typing import NamedTuple
 
 import torch
 
@@ -113,7 +114,30 @@ def row_pitch(N: int) -> int:
 
 # ------------------------------------------------------------------------------------------------ weight caches
 
-WCACHE_TRACE = None  # set by mixed.trace_groups: called as (owner, name, params, dtype) on every wcache call
+class KernelWeight(NamedTuple):
+    """A weight matrix a kernel reads, as its module declares it (``kernel_weights()``): the row concatenation of the
+    module's parameters at the paths ``srcs`` (relative to the module), kept in the storage dtype when ``half`` (fp16
+    in f16 mode), else always in fp32. The declarations are the one place that says which parameters f16 mode reads
+    only as fp16: the mixed-checkpoint manifest (boltz_mlx_amd/mixed.py) is read off them."""
+
+    name: str
+    srcs: tuple
+    half: bool = True
+
+
+def declared_weights(owner: torch.nn.Module) -> dict:
+    """{name: KernelWeight} of a module that declares kernel weights (else empty)."""
+    fn = getattr(owner, "kernel_weights", None)
+    return {} if fn is None else {kw.name: kw for kw in fn()}
+
+
+def kernel_weight(owner: torch.nn.Module, name: str) -> torch.Tensor:
+    """The declared kernel weight `name` of `owner` in its dtype, cached on the module (wcache)."""
+    kw = declared_weights(owner).get(name)
+    if kw is None:
+        raise KeyError(f"{type(owner).__name__} declares no kernel weight {name!r}")
+    params = [owner.get_parameter(p) for p in kw.srcs]
+    return wcache(owner, name, *params, dtype=storage_dtype() if kw.half else torch.float32)
 
 
 def _wkey(dtype, params) -> tuple:
@@ -131,8 +155,6 @@ def wcache(owner: torch.nn.Module, name: str, *params: torch.Tensor, dtype=None)
     parameter changes (data pointer or in-place version). Mirrors the reference's w16 cache
     (boltz_mlx/kernels.py:1330-1357)."""
     dtype = dtype or storage_dtype()
-    if WCACHE_TRACE is not None:
-        WCACHE_TRACE(owner, name, params, dtype)
     key = _wkey(dtype, params)
     hit = owner.__dict__.get("_bzpf_cache", {}).get(name)
     if hit is not None and hit[0] == key:
@@ -579,7 +601,7 @@ def swiglu(h: torch.Tensor) -> torch.Tensor:
 
 
 def seq_attention(q, k, v, g, bias, mask, inf: float, H: int) -> torch.Tensor:
-    """q/k/v/g [N, H*hd], bias [H, N, N], mask [N] fp32 -> [N, H*hd]."""
+    """q/k/v/g [N, H*hd], bias [H, N, N] (fp32 or fp16, independently of q's dtype), mask [N] fp32 -> [N, H*hd]."""
     _dev(q, k, v, g, bias, mask)
     N, HD = q.shape
     hd = HD // H
@@ -587,14 +609,15 @@ def seq_attention(q, k, v, g, bias, mask, inf: float, H: int) -> torch.Tensor:
         raise ValueError("seq_attention: bias must be [H, N, N] and mask fp32 [N]")
     out = torch.empty_like(q)
     call("bzpf_seq_attention", _p(q), _p(k), _p(v), _p(g), HD, _p(bias), _p(mask), float(inf), _p(out), HD,
-         _dt(q), N, H, hd, _stream())
+         _dt(q), _dt(bias), N, H, hd, _stream())
     return out
 
 
 def seq_attention_packed(qkvg, bias, mask, inf: float, H: int, out=None, multiplicity: int = 1) -> torch.Tensor:
     """seq_attention over [N, 4*H*hd] or [S, N, 4*H*hd] buffers holding q | k | v | g per row (the fused
     projection's output), one launch for all S samples; bias [H, N, N] or [S / multiplicity, H, N, N] (consecutive
-    groups of `multiplicity` samples share one), mask [N] or [S, N] fp32. Writes `out` [(S,) N, H*hd] when given."""
+    groups of `multiplicity` samples share one; fp32 or fp16, independently of qkvg's dtype), mask [N] or [S, N] fp32.
+    Writes `out` [(S,) N, H*hd] when given."""
     _dev(qkvg, bias, mask)
     batched = qkvg.dim() == 3
     q3 = qkvg if batched else qkvg[None]
@@ -614,8 +637,8 @@ def seq_attention_packed(qkvg, bias, mask, inf: float, H: int, out=None, multipl
         raise ValueError("seq_attention: out must be a contiguous [(S,) N, H*hd] tensor of qkvg's dtype")
     base, es = q3.data_ptr(), q3.element_size()
     call("bzpf_seq_attention_batched", base, base + HD * es, base + 2 * HD * es, base + 3 * HD * es, HD4, N * HD4,
-         _p(b4), H * N * N, int(multiplicity), _p(m2), N, float(inf), _p(out), HD, N * HD, _dt(qkvg), S, N, H, hd,
-         _stream())
+         _p(b4), H * N * N, int(multiplicity), _p(m2), N, float(inf), _p(out), HD, N * HD, _dt(qkvg), _dt(b4), S, N,
+         H, hd, _stream())
     return out
 
 

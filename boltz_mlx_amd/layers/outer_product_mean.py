@@ -31,6 +31,12 @@ class OuterProductMean(torch.nn.Module):
         self.proj_b = torch.nn.Linear(c_in, c_hidden, bias=False)
         self.proj_o = torch.nn.Linear(c_hidden * c_hidden, c_out)
 
+    def kernel_weights(self):
+        """[proj_a; proj_b] in fp32 (the MSA-side projection keeps fp32 in both modes) and proj_o in the storage
+        dtype."""
+        return (K.KernelWeight("w_ab", ("proj_a.weight", "proj_b.weight"), half=False),
+                K.KernelWeight("w_o", ("proj_o.weight",)))
+
     def forward(self, m: torch.Tensor, mask: torch.Tensor, chunk_size=None) -> torch.Tensor:
         """m [B, S, N, c_in], mask [B, S, N] -> [B, N, N, c_out] fp32. chunk_size is accepted and ignored."""
         B, S, N, _ = m.shape
@@ -43,8 +49,7 @@ class OuterProductMean(torch.nn.Module):
         """z [N, N, c_out] fp32 contiguous (+)= the layer's output for one MSA m [S, N, c_in], mask [S, N]."""
         S, N, c_in = m.shape
         co = self.proj_o.out_features
-        w_ab = K.wcache(self, "w_ab", self.proj_a.weight, self.proj_b.weight, dtype=torch.float32)
-        w_o = K.wcache(self, "w_o", self.proj_o.weight)
+        w_ab, w_o = K.kernel_weight(self, "w_ab"), K.kernel_weight(self, "w_o")
         mn = K.layer_norm(m.reshape(S * N, c_in).to(torch.float32), self.norm.weight, self.norm.bias, self.norm.eps)
         ab = K.linear(mn, w_ab).view(S, N, 2 * self.c_hidden)
         mk = mask.to(torch.float32).reshape(S, N).contiguous()

@@ -31,6 +31,12 @@ class PairWeightedAveraging(torch.nn.Module):
         self.proj_z = torch.nn.Linear(c_z, num_heads, bias=False)
         self.proj_o = torch.nn.Linear(c_h * num_heads, c_m, bias=False)
 
+    def kernel_weights(self):
+        """[proj_m; proj_g] and proj_o in fp32 (both modes); proj_z in the storage dtype (its fp16 copy is upcast for
+        the fp32 logits, as the reference's fused path does)."""
+        return (K.KernelWeight("w_mg", ("proj_m.weight", "proj_g.weight"), half=False),
+                K.KernelWeight("w_o", ("proj_o.weight",), half=False), K.KernelWeight("w_z", ("proj_z.weight",)))
+
     def forward(self, m: torch.Tensor, z: torch.Tensor, mask: torch.Tensor, chunk_heads: bool = False) -> torch.Tensor:
         """m [B, S, N, c_m], z [B, N, N, c_z], mask [B, N, N] -> [B, S, N, c_m] fp32 (chunk_heads is ignored)."""
         out = torch.empty(m.shape, dtype=torch.float32, device=m.device)
@@ -43,9 +49,8 @@ class PairWeightedAveraging(torch.nn.Module):
         """out [S, N, c_m] fp32 contiguous (+)= the layer's output for one MSA m [S, N, c_m] and z [N, N, c_z]."""
         S, N, _ = m.shape
         HC = self.c_h * self.num_heads
-        w_mg = K.wcache(self, "w_mg", self.proj_m.weight, self.proj_g.weight, dtype=torch.float32)
-        w_o = K.wcache(self, "w_o", self.proj_o.weight, dtype=torch.float32)
-        w_z = K.wcache(self, "w_z", self.proj_z.weight).float()
+        w_mg, w_o = K.kernel_weight(self, "w_mg"), K.kernel_weight(self, "w_o")
+        w_z = K.kernel_weight(self, "w_z").float()
         mn = K.layer_norm(m.reshape(S * N, self.c_m).to(torch.float32), self.norm_m.weight, self.norm_m.bias,
                           self.norm_m.eps)
         vg = K.linear(mn, w_mg)

@@ -134,8 +134,10 @@ class PairformerLayer(torch.nn.Module):
         self._s_transition(s)
 
     def _s_attention(self, s: torch.Tensor, bias: torch.Tensor, mask: torch.Tensor) -> None:
-        dt = K.storage_dtype()
-        s_n = K.layer_norm(s, self.pre_norm_s.weight, self.pre_norm_s.bias, self.pre_norm_s.eps, out_dtype=dt)
+        # fp32 in both modes (the reference's f16 mode keeps the s attention's projections and softmax in fp32; the
+        # pair bias is fp16 there)
+        s_n = K.layer_norm(s, self.pre_norm_s.weight, self.pre_norm_s.bias, self.pre_norm_s.eps,
+                           out_dtype=torch.float32)
         self.attention.fused(s_n, s_n, bias, mask, s, accumulate=True)
 
     def _s_transition(self, s: torch.Tensor) -> None:

@@ -77,25 +77,38 @@ class DiffusionTransformerLayer(torch.nn.Module):
         if post_layer_norm:
             self.post_lnorm = LayerNorm(dim)
 
-    def prepare(self):
-        """The layer's kernel weights in the storage dtype, cached: q|k|v|g (with proj_q's bias, fp32), proj_o, the
-        transition's [gates; x; a_to_b] rows (so the gated product reads silu's input first) and b_to_a."""
-        at, tr = self.pair_bias_attn, self.transition
-        w_qkvg, b_qkvg, w_o, _ = at.prepare()
-        inner = tr.a_to_b.weight.shape[0]
-        wg = tr.swish_gate[0].weight
-        w_ff = K.wcache(self, "w_ff", wg[inner:], wg[:inner], tr.a_to_b.weight)
-        w_ba = K.wcache(self, "w_ba", tr.b_to_a.weight)
-        return w_qkvg, b_qkvg, w_o, w_ff, w_ba
+    def kernel_weights(self):
+        """In the storage dtype: the attention's [proj_q; proj_k; proj_v; proj_g] and proj_o (fp16 GEMMs in f16 mode,
+        unlike the Pairformer's s track), the transition's [swish_gate; a_to_b] rows (x, then the SiLU gates, then
+        a_to_b: swish_gate's two halves in checkpoint order) and b_to_a."""
+        return (K.KernelWeight("w_qkvg", ("pair_bias_attn.proj_q.weight", "pair_bias_attn.proj_k.weight",
+                                          "pair_bias_attn.proj_v.weight", "pair_bias_attn.proj_g.weight")),
+                K.KernelWeight("w_o", ("pair_bias_attn.proj_o.weight",)),
+                K.KernelWeight("w_ff", ("transition.swish_gate.0.weight", "transition.a_to_b.weight")),
+                K.KernelWeight("w_ba", ("transition.b_to_a.weight",)))
 
-    def ff_grouped(self, w_ff):
-        """w_ff regrouped for the fused fp16 feed-forward kernel (K.linear_swiglu3), cached with its source."""
-        hit = self.__dict__.get("_bzpf_ffg")
+    def prepare(self):
+        """The layer's kernel weights, cached: q|k|v|g with proj_q's bias (fp32), proj_o, the transition's
+        [x; gates; a_to_b] rows and b_to_a."""
+        w_qkvg, w_o, w_ff, w_ba = (K.kernel_weight(self, n) for n in ("w_qkvg", "w_o", "w_ff", "w_ba"))
+        return w_qkvg, self.pair_bias_attn.qkvg_bias(), w_o, w_ff, w_ba
+
+    def _ff_derived(self, w_ff, grouped: bool):
+        """w_ff's rows for the feed-forward kernels, cached with its source: the SiLU gates first, then x, then a_to_b
+        (the unfused GEMM + K.swiglu3), or those three regrouped per 32 output columns (K.linear_swiglu3)."""
+        key = "_bzpf_ffg" if grouped else "_bzpf_ffr"
+        hit = self.__dict__.get(key)
         if hit is None or hit[0] is not w_ff:
             H = w_ff.shape[0] // 3
-            hit = (w_ff, K.group_swiglu3_rows(w_ff[:H], w_ff[H:2 * H], w_ff[2 * H:]))
-            self.__dict__["_bzpf_ffg"] = hit
+            x, gates, ab = w_ff[:H], w_ff[H:2 * H], w_ff[2 * H:]
+            w = K.group_swiglu3_rows(gates, x, ab) if grouped else torch.cat([gates, x, ab], 0).contiguous()
+            hit = (w_ff, w)
+            self.__dict__[key] = hit
         return hit[1]
+
+    def ff_grouped(self, w_ff):
+        """w_ff regrouped for the fused fp16 feed-forward kernel (K.linear_swiglu3)."""
+        return self._ff_derived(w_ff, True)
 
     def forward(self, a, s, bias=None, mask=None, to_keys=None, multiplicity: int = 1, cond=None, attn_bias=None):
         """One layer on its own (a [B*mult, N, D], s [B*mult, N, Dc], bias [B, N, N, H], mask [B*mult, N])."""
@@ -108,10 +121,10 @@ class DiffusionTransformerLayer(torch.nn.Module):
         return out
 
 
-def _cond_weights(layers, dtype):
+def _cond_weights(layers, dtype, w_gates=None):
     """[s_scale g; s_bias g; s_scale' g'; s_bias' g'] per layer with g the s_norm weight folded into the columns (the
     product in fp32, then the storage dtype), their biases, and [output_projection; transition output_projection]
-    with biases (transformersv2.py:376-420)."""
+    with biases (transformersv2.py:376-420). w_gates: the latter rows already built (the stack's kernel weight)."""
     w1, b1, w2, b2 = [], [], [], []
     for layer in layers:
         for ad in (layer.adaln, layer.transition.adaln):
@@ -121,8 +134,8 @@ def _cond_weights(layers, dtype):
         op = layer.transition.output_projection[0]
         w2 += [layer.output_projection_linear.weight.detach(), op.weight.detach()]
         b2 += [layer.output_projection_linear.bias.detach().float(), op.bias.detach().float()]
-    return (torch.cat(w1, 0).to(dtype).contiguous(), torch.cat(b1, 0).contiguous(),
-            torch.cat(w2, 0).to(dtype).contiguous(), torch.cat(b2, 0).contiguous())
+    w2 = torch.cat(w2, 0).to(dtype).contiguous() if w_gates is None else w_gates
+    return torch.cat(w1, 0).to(dtype).contiguous(), torch.cat(b1, 0).contiguous(), w2, torch.cat(b2, 0).contiguous()
 
 
 def _precompute_cond(layers, s, weights=None):
@@ -167,7 +180,7 @@ def _layer_fast(layer, a, h1, h2, i: int, L: int, bias_l, mask, multiplicity: in
     if dt == torch.float16 and D % 64 == 0 and (H3 // 3) % 32 == 0:
         u = K.linear_swiglu3(t, layer.ff_grouped(w_ff))
     else:
-        u = K.swiglu3(K.linear(t, w_ff))
+        u = K.swiglu3(K.linear(t, layer._ff_derived(w_ff, False)))
     K.linear_gated(u, w_ba, c2[:, 1], a2)
     if layer.post_layer_norm:
         a2.copy_(layer.post_lnorm(a2))
@@ -186,13 +199,22 @@ class DiffusionTransformer(torch.nn.Module):
             DiffusionTransformerLayer(heads, dim, dim_single_cond, post_layer_norm) for _ in range(depth)
         ])
 
+    def kernel_weights(self):
+        """The output gates of every layer in the storage dtype: [output_projection; transition output_projection]
+        per layer (one GEMM per call over the conditioning s)."""
+        srcs = []
+        for i in range(len(self.layers)):
+            srcs += [f"layers.{i}.output_projection_linear.weight", f"layers.{i}.transition.output_projection.0.weight"]
+        return (K.KernelWeight("w_gates", tuple(srcs)),)
+
     def precompute_cond(self, s):
         """(h1, h2): every layer's s-side projections for s [..., Dc] (cached weights per storage dtype)."""
         dt = K.storage_dtype()
-        key = (dt,) + tuple((p.data_ptr(), p._version) for p in self.parameters())
+        w_gates = K.kernel_weight(self, "w_gates")
+        key = (dt, w_gates.data_ptr()) + tuple((p.data_ptr(), p._version) for p in self.parameters())
         hit = self.__dict__.get("_bzpf_cond_w")
         if hit is None or hit[0] != key:
-            hit = (key, _cond_weights(self.layers, dt))
+            hit = (key, _cond_weights(self.layers, dt, w_gates))
             self.__dict__["_bzpf_cond_w"] = hit
         return _precompute_cond(self.layers, s, hit[1])
 

@@ -50,12 +50,16 @@ class Transition(torch.nn.Module):
             return out
         return self.unfused(xn)
 
+    def kernel_weights(self):
+        """[fc1; fc2] (the up-projection, SiLU branch first) and fc3, in the storage dtype."""
+        return K.KernelWeight("w12", ("fc1.weight", "fc2.weight")), K.KernelWeight("w3", ("fc3.weight",))
+
     def prepare(self):
         """The kernel weights in the storage dtype ([fc1; fc2] and fc3), cached on the module. In f16 mode at 64
         channels the hidden activations are scaled by 2^-TRANS64_K before their fp16 store and the output by
         2^TRANS64_K (the reference's fp16 overflow margin, boltz_mlx/kernels.py:1327, layers/transition.py:60-92):
         folded exactly into the weights as fc2 * 2^-k and fc3 * 2^k."""
-        w12, w3 = K.wcache(self, "w12", self.fc1.weight, self.fc2.weight), K.wcache(self, "w3", self.fc3.weight)
+        w12, w3 = K.kernel_weight(self, "w12"), K.kernel_weight(self, "w3")
         k = K.TRANS64_K if (K.f16() and self.fc1.in_features == 64) else 0
         if not k:
             return w12, w3

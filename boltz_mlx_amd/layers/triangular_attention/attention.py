@@ -53,7 +53,9 @@ class TriangleAttention(torch.nn.Module):
         for b in range(B):
             xb = xn[b].contiguous() if use_xn else self.layer_norm.to_storage(x[b])
             self.fused(xb.reshape(N * N, D), mask[b], out[b], accumulate=False, xn_transposed=use_xn)
-        if keep_t and not self.starting:
+        # keep_t (the ending node's update left in its attention frame, [B, J, I, C]) is an f16-path option of the
+        # reference (attention.py:130-131); its fp32 path always returns the natural layout (attention.py:45-46, 91-92)
+        if keep_t and not self.starting and K.f16():
             out = out.transpose(1, 2).contiguous()
         return out
 
@@ -104,13 +106,15 @@ class TriangleAttention(torch.nn.Module):
         del qkg, vt, tb
         return core
 
+    def kernel_weights(self):
+        """[q; k; v; g; triangle bias] (the projection's 4·H·C + H rows) and linear_o, in the storage dtype."""
+        return (K.KernelWeight("w_qkvgb", ("mha.linear_q.weight", "mha.linear_k.weight", "mha.linear_v.weight",
+                                           "mha.linear_g.weight", "linear.weight")),
+                K.KernelWeight("w_o", ("mha.linear_o.weight",)))
+
     def prepare(self):
-        """The kernel weights in the storage dtype ([q; k; v; g; triangle bias] and linear_o), cached on the
-        module."""
-        mha = self.mha
-        return (K.wcache(self, "w_qkvgb", mha.linear_q.weight, mha.linear_k.weight, mha.linear_v.weight,
-                         mha.linear_g.weight, self.linear.weight),
-                K.wcache(self, "w_o", mha.linear_o.weight))
+        """The kernel weights ([q; k; v; g; triangle bias] and linear_o), cached on the module."""
+        return K.kernel_weight(self, "w_qkvgb"), K.kernel_weight(self, "w_o")
 
 
 TriangleAttentionStartingNode = TriangleAttention

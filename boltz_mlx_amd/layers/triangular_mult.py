@@ -70,10 +70,14 @@ class _TriangleMultiplication(torch.nn.Module):
         return K.trimul_tail(o, self.norm_out, self.norm_out.eps * 2.0 ** (-4 * kexp), w_po, xn, w_go, z,
                              accumulate, next_ln, N)
 
+    def kernel_weights(self):
+        """[p_in; g_in] (the projection kernel's 4·128 rows), p_out and g_out (the tail), all in the storage dtype."""
+        return (K.KernelWeight("w_pg", ("p_in.weight", "g_in.weight")), K.KernelWeight("w_po", ("p_out.weight",)),
+                K.KernelWeight("w_go", ("g_out.weight",)))
+
     def prepare(self):
-        """The kernel weights in the storage dtype ([p_in; g_in], p_out, g_out), cached on the module."""
-        return (K.wcache(self, "w_pg", self.p_in.weight, self.g_in.weight), K.wcache(self, "w_po", self.p_out.weight),
-                K.wcache(self, "w_go", self.g_out.weight))
+        """The kernel weights ([p_in; g_in], p_out, g_out), cached on the module."""
+        return tuple(K.kernel_weight(self, n) for n in ("w_pg", "w_po", "w_go"))
 
 
 class TriangleMultiplicationOutgoing(_TriangleMultiplication):

@@ -1,19 +1,23 @@
-"""Mixed fp16 / fp32 checkpoints for f16 mode: fp16 GEMM weights stored once, checked against a manifest.
+"""Mixed fp16 / fp32 checkpoints for f16 mode.
 
-A mixed checkpoint holds, under the PyTorch names of the fp32 checkpoint, fp16 copies of exactly the parameters that
-f16 mode consumes only through fp16 kernel weights, and the fp32 values of everything else; its safetensors metadata
-carries ``format`` and ``manifest_sha``. Loading checks both (a stale or partially converted file raises), keeps the
-fp16 tensors in fp16, builds each multi-parameter kernel weight once and makes its source parameters views into it,
-so no fp32 copy of a GEMM weight exists and no second fp16 copy is made at first use.
+A mixed checkpoint holds every parameter of the model under its checkpoint name. The parameters that f16 mode reads
+only as fp16 kernel weights are stored in fp16 (the round-to-nearest-even value of the fp32 one); all others stay
+fp32. Loading one keeps those parameters in fp16 on the device and lays each multi-parameter kernel weight out once,
+with its source parameters as views into it, so the model never holds an fp32 copy of an fp16 GEMM weight and the
+first f16 call builds no second copy.
 
-Which parameters are fp16 is derived from the code: every kernel weight is built by ``kernels.wcache(owner, name,
-*params)``; with ``kernels.WCACHE_TRACE`` set, each module's ``prepare()`` reports (owner, cache name, sources) and
-sources that are parameters (by identity) map to their qualified names. A group whose sources are all parameters is
-"storable". The manifest entry is {"groups": [...], "params": [...]}, hashed by ``entry_sha``.
+Which parameters are fp16 is read off the modules' declarations: a module that feeds a kernel lists its weight
+matrices in ``kernel_weights()`` (``kernels.KernelWeight``: cache name, source parameter paths, ``half``), and its
+``prepare()`` reads exactly those through ``kernels.kernel_weight``. The ``half`` declarations of a model, with their
+owners, make the manifest entry:
+    {"groups": [{"owner", "cache", "srcs", "shape", "storable"}, ...], "params": [every name of every source]}.
 
-Kept alike with the reference on purpose (boltz_mlx/mixed.py:49-60, 216-287), so that files its converter wrote for
-the same parameter set validate here: the format string, the entry hash (sha256 of the sorted-key JSON, 16 hex
-digits), the metadata keys, the overflow check of the conversion and the prefuse of multi-parameter groups.
+The file contract is shared with the reference's converter on purpose (boltz_mlx/mixed.py:49-60, 143-153, 216-287),
+so that files converted on either side load on the other: the format tag, the safetensors metadata keys ``format``
+and ``manifest_sha``, the entry hash (sha256 of the entry's sorted-key JSON, first 16 hex digits) and the fields of a
+group record. A file the reference converted is loaded with the reference's manifest entry (``load_mixed(...,
+entry=its entry, prefix=...)`` for a sub-model of the whole Boltz-2 checkpoint); its groups are matched to this
+library's kernel weights by their source parameters, since the two libraries name their caches differently.
 """
 
 from __future__ import annotations
@@ -21,201 +25,228 @@ from __future__ import annotations
 import hashlib
 import json
 
-import numpy as np
 import torch
 
 from boltz_mlx_amd import kernels as K
 
 FORMAT = "boltz-mlx-mixed-v1"
-FP16_MAX = 65504.0
+META_FORMAT, META_SHA = "format", "manifest_sha"
+# fp16's largest finite value is 65504; under round to nearest even everything from 65520 up becomes inf
+HALF_OVERFLOW = 65520.0
 
 
 def entry_sha(entry: dict) -> str:
-    """Hash of a manifest entry (stored in the mixed file; a mismatch at load means a stale file)."""
-    return hashlib.sha256(json.dumps(entry, sort_keys=True).encode()).hexdigest()[:16]
+    """The manifest hash written into a mixed file (a different hash at load time means a stale file)."""
+    blob = json.dumps(entry, sort_keys=True).encode()
+    return hashlib.sha256(blob).hexdigest()[:16]
 
 
-def _param_names(model: torch.nn.Module) -> dict:
-    """id(parameter) -> its qualified names (a module registered twice gives two names for one tensor)."""
-    out: dict = {}
-    for n, p in model.named_parameters(remove_duplicate=False):
-        out.setdefault(id(p), []).append(n)
-    return out
+def _join(path: str, name: str) -> str:
+    return f"{path}.{name}" if path else name
 
 
-def trace_groups(model: torch.nn.Module) -> list:
-    """The fp16 kernel-weight groups of `model`, from every submodule's argument-free prepare() run in f16 mode (on
-    any device: the weight caches are torch casts and concatenations)."""
-    paths = {id(m): p for p, m in model.named_modules()}
-    names = _param_names(model)
-    groups: dict = {}
-
-    def hook(owner, name, params, dtype):
-        if dtype != torch.float16:
-            return
-        op = paths.get(id(owner))
-        if op is None:
-            raise RuntimeError(f"kernel weight {name!r}: owner {type(owner).__name__} is not a submodule")
-        pre = op + "." if op else ""
-        srcs = []
-        for t in params:
-            ns = [n for n in names.get(id(t), []) if n.startswith(pre)]
-            srcs.append(ns[0][len(pre):] if ns else None)
-        groups[(op, name)] = {"owner": op, "cache": name, "srcs": srcs, "storable": all(s is not None for s in srcs),
-                              "shape": [int(sum(t.shape[0] for t in params)), *map(int, params[0].shape[1:])]}
-
-    old_trace, old_prec = K.WCACHE_TRACE, K.PRECISION
-    K.WCACHE_TRACE = hook
-    K.set_precision("f16")
-    try:
-        with torch.no_grad():
-            for m in model.modules():
-                prep = getattr(type(m), "prepare", None)
-                if prep is None:
-                    continue
-                try:
-                    m.prepare()
-                except TypeError:  # prepare(...) that needs arguments (per-call inputs): no weight group
-                    continue
-    finally:
-        K.WCACHE_TRACE = old_trace
-        K.set_precision(old_prec)
-    return sorted(groups.values(), key=lambda g: (g["owner"], g["cache"]))
+def _names_by_tensor(model: torch.nn.Module) -> dict:
+    """id(parameter) -> all of its qualified names (a module registered under two names gives a tensor two)."""
+    names: dict = {}
+    for name, p in model.named_parameters(remove_duplicate=False):
+        names.setdefault(id(p), []).append(name)
+    return names
 
 
-def manifest_entry(model: torch.nn.Module, groups: list | None = None) -> dict:
-    """{"groups": [...], "params": [every qualified name of a storable group's sources, aliases included]}."""
-    groups = trace_groups(model) if groups is None else groups
-    names = _param_names(model)
-    by_name = {n: ns for ns in names.values() for n in ns}
+def half_groups(model: torch.nn.Module) -> list:
+    """Group records of every kernel weight the model's modules declare as fp16-in-f16-mode, sorted by (owner,
+    cache). Each source is a parameter of its owner, so every record is storable."""
+    records = []
+    for path, mod in model.named_modules():
+        for kw in K.declared_weights(mod).values():
+            if not kw.half:
+                continue
+            params = [mod.get_parameter(src) for src in kw.srcs]
+            rows = sum(int(p.shape[0]) for p in params)
+            records.append({"owner": path, "cache": kw.name, "srcs": list(kw.srcs),
+                            "shape": [rows, *(int(d) for d in params[0].shape[1:])], "storable": True})
+    records.sort(key=lambda r: (r["owner"], r["cache"]))
+    return records
+
+
+def manifest_entry(model: torch.nn.Module) -> dict:
+    """This library's manifest entry for `model`: its fp16 groups and the sorted names (aliases included) of their
+    source parameters."""
+    groups = half_groups(model)
+    aliases = _names_by_tensor(model)
     params = set()
     for g in groups:
-        if g["storable"]:
-            for s in g["srcs"]:
-                params.update(by_name[f"{g['owner']}.{s}" if g["owner"] else s])
+        owner = model.get_submodule(g["owner"])
+        for src in g["srcs"]:
+            params.update(aliases[id(owner.get_parameter(src))])
     return {"groups": groups, "params": sorted(params)}
 
 
-def to_mixed(state: dict, entry: dict) -> tuple:
-    """fp32 state dict -> (mixed state dict, per-tensor fp16 range stats). Raises on a missing manifest parameter, a
-    non-fp32 source or any fp16 overflow."""
-    params = set(entry["params"])
-    missing = params - set(state)
-    if missing:
-        raise KeyError(f"manifest parameters missing from the checkpoint: {sorted(missing)[:5]}")
-    out, stats, bad = {}, {}, {}
-    for k, v in state.items():
-        t = torch.as_tensor(np.asarray(v)) if not isinstance(v, torch.Tensor) else v.detach().cpu()
-        if k in params:
-            if t.dtype != torch.float32:
-                raise TypeError(f"{k}: expected an fp32 source, got {t.dtype}")
-            a = t.abs()
-            h = t.to(torch.float16)
-            stats[k] = {"n": t.numel(), "max_abs": float(a.max()) if t.numel() else 0.0,
-                        "overflow": int((~torch.isfinite(h) & torch.isfinite(t)).sum()),
-                        "flushed": int(((t != 0) & (h == 0)).sum())}
-            if stats[k]["overflow"]:
-                bad[k] = stats[k]["overflow"]
-            out[k] = h
-        else:
-            out[k] = t
-    if bad:
-        raise OverflowError(f"fp16 overflow (|w| > {FP16_MAX}) in {len(bad)} tensors: {bad}")
-    return out, stats
+def restrict(entry: dict, prefix: str) -> dict:
+    """The part of a manifest entry that lies under `prefix` (a sub-model's checkpoint prefix such as
+    "pairformer_module."), with the prefix removed from owners and parameter names."""
+    if not prefix:
+        return entry
+    root = prefix[:-1] if prefix.endswith(".") else prefix
+    groups = []
+    for g in entry["groups"]:
+        owner = g["owner"]
+        if owner == root:
+            groups.append({**g, "owner": ""})
+        elif owner.startswith(prefix):
+            groups.append({**g, "owner": owner[len(prefix):]})
+    params = [p[len(prefix):] for p in entry["params"] if p.startswith(prefix)]
+    return {"groups": groups, "params": params}
 
 
-def save_mixed(path: str, state: dict, entry: dict) -> None:
-    """Write a mixed checkpoint (to_mixed of an fp32 state) with its format and manifest hash."""
+def convert(state: dict, entry: dict) -> tuple:
+    """fp32 state dict -> (mixed state dict, {name: range report} for the fp16 tensors).
+
+    Raises KeyError when the state lacks a parameter the entry lists, TypeError when such a parameter is not fp32,
+    and OverflowError when any of them holds a finite value that fp16 cannot represent."""
+    half = set(entry["params"])
+    absent = sorted(half.difference(state))
+    if absent:
+        raise KeyError(f"{len(absent)} fp16 parameters of the manifest are not in the state dict, e.g. {absent[:3]}")
+    mixed, report, too_large = {}, {}, []
+    for name, value in state.items():
+        t = value.detach().cpu() if isinstance(value, torch.Tensor) else torch.as_tensor(value)
+        if name not in half:
+            mixed[name] = t
+            continue
+        if t.dtype != torch.float32:
+            raise TypeError(f"{name}: the fp16 conversion takes fp32 values, got {t.dtype}")
+        h = t.to(torch.float16)
+        mag = t.abs()
+        rep = {"n": t.numel(), "max_abs": float(mag.max()) if t.numel() else 0.0,
+               "overflow": int((torch.isfinite(t) & (mag >= HALF_OVERFLOW)).sum()),
+               "flushed": int(((t != 0) & (h == 0)).sum())}
+        report[name] = rep
+        if rep["overflow"]:
+            too_large.append(f"{name} ({rep['overflow']} values)")
+        mixed[name] = h
+    if too_large:
+        raise OverflowError(f"values beyond the fp16 range (|w| >= {HALF_OVERFLOW:g}) in {len(too_large)} tensors: "
+                            + ", ".join(too_large[:5]))
+    return mixed, report
+
+
+def save_mixed(path: str, state: dict, entry: dict) -> dict:
+    """Convert an fp32 state dict and write it as a mixed safetensors file; returns the range report."""
     from safetensors.torch import save_file
 
-    mixed, _ = to_mixed(state, entry)
+    mixed, report = convert(state, entry)
     save_file({k: v.contiguous() for k, v in mixed.items()}, path,
-              metadata={"format": FORMAT, "manifest_sha": entry_sha(entry)})
+              metadata={META_FORMAT: FORMAT, META_SHA: entry_sha(entry)})
+    return report
 
 
-def _resolve(model: torch.nn.Module, path: str):
-    m = model
-    for part in path.split(".") if path else []:
-        m = getattr(m, part, None)
-        if m is None:
-            return None
-    return m
+def _places(model: torch.nn.Module) -> dict:
+    """id(parameter) -> every (module, attribute) it is registered at."""
+    places: dict = {}
+    for path, mod in model.named_modules(remove_duplicate=False):
+        for leaf, p in mod.named_parameters(recurse=False):
+            places.setdefault(id(p), []).append((mod, leaf))
+    return places
 
 
-def prefuse(model: torch.nn.Module, entry: dict) -> int:
-    """After a mixed load: build each storable multi-parameter group's fp16 kernel weight once, put it in the
-    module's weight cache, and make the source parameters views into it (their own buffers are freed), so the
-    concatenated fp16 weight exists once. A parameter shared by two groups keeps its own buffer. Returns the number of
-    groups seeded. Owners missing from the model are skipped."""
-    groups = [g for g in entry["groups"] if g["storable"]]
-    count: dict = {}
-    for g in groups:
-        for s in g["srcs"]:
-            key = f"{g['owner']}.{s}"
-            count[key] = count.get(key, 0) + 1
-    n = 0
+def _rebind(places: dict, old: torch.Tensor, new: torch.nn.Parameter) -> None:
+    for mod, leaf in places.get(id(old), []):
+        setattr(mod, leaf, new)
+
+
+def bind_groups(model: torch.nn.Module, entry: dict) -> int:
+    """Lay out every multi-parameter fp16 kernel weight of `model` that `entry` also groups (same source parameters,
+    whatever the entry calls the cache) as one buffer: the buffer becomes the owner's cached kernel weight and the
+    source parameters become views into it. A source that two such groups share keeps its own buffer (the cache then
+    concatenates at first use). Returns the number of buffers laid out."""
+    declared = {}  # tuple(id of each source) -> (owner module, kernel weight)
+    for path, mod in model.named_modules():
+        for kw in K.declared_weights(mod).values():
+            if kw.half and len(kw.srcs) > 1:
+                declared[tuple(id(mod.get_parameter(s)) for s in kw.srcs)] = (mod, kw)
+    matched = []
+    for g in entry["groups"]:
+        if not g.get("storable") or len(g["srcs"]) < 2:
+            continue
+        try:
+            ids = tuple(id(model.get_parameter(_join(g["owner"], s))) for s in g["srcs"])
+        except AttributeError:  # a module of another model (e.g. outside this sub-model)
+            continue
+        if ids in declared and declared[ids] not in [m for m, _ in matched]:
+            matched.append((declared[ids], ids))
+    uses: dict = {}
+    for _, ids in matched:
+        for i in ids:
+            uses[i] = uses.get(i, 0) + 1
+    places = _places(model)
+    laid = 0
     with torch.no_grad():
-        for g in groups:
-            owner = _resolve(model, g["owner"])
-            if owner is None:
+        for (mod, kw), ids in matched:
+            params = [mod.get_parameter(s) for s in kw.srcs]
+            if any(uses[i] > 1 for i in ids) or any(p.dtype != torch.float16 for p in params):
                 continue
-            leaves = []
-            for s in g["srcs"]:
-                *pp, leaf = s.split(".")
-                parent = _resolve(owner, ".".join(pp))
-                leaves.append((parent, leaf, getattr(parent, leaf)))
-            if any(t.dtype != torch.float16 for _, _, t in leaves):
-                continue  # not stored in fp16 in this file: the cache casts at first use
-            if len(leaves) > 1 and all(count[f"{g['owner']}.{s}"] == 1 for s in g["srcs"]):
-                w = torch.cat([t.detach() for _, _, t in leaves], 0).contiguous()
-                r = 0
-                for parent, leaf, t in leaves:
-                    setattr(parent, leaf, torch.nn.Parameter(w[r:r + t.shape[0]], requires_grad=False))
-                    r += t.shape[0]
-                K.wcache_seed(owner, g["cache"], [getattr(parent, leaf) for parent, leaf, _ in leaves], w)
-            else:  # one source (the cache is the parameter itself) or a shared source (the cache concatenates)
-                K.wcache(owner, g["cache"], *[getattr(parent, leaf) for parent, leaf, _ in leaves],
-                         dtype=torch.float16)
-            n += 1
-    return n
+            buf = torch.empty((sum(p.shape[0] for p in params), *params[0].shape[1:]), dtype=torch.float16,
+                              device=params[0].device)
+            row, views = 0, []
+            for p in params:
+                n = p.shape[0]
+                buf[row:row + n].copy_(p)
+                view = torch.nn.Parameter(buf[row:row + n], requires_grad=False)
+                _rebind(places, p, view)
+                views.append(view)
+                row += n
+            K.wcache_seed(mod, kw.name, views, buf)
+            laid += 1
+    return laid
 
 
-def load_mixed(model: torch.nn.Module, path: str, entry: dict, device=None) -> torch.nn.Module:
-    """Load a mixed checkpoint into `model` (strict names and shapes) after checking its format and manifest hash
-    against `entry` (this build's manifest_entry(model), or the manifest entry the file was converted with). fp16
-    tensors stay fp16 (the parameter changes dtype); the model is placed on `device`, then prefused."""
+def load_mixed(model: torch.nn.Module, path: str, entry: dict | None = None, prefix: str = "",
+               device=None) -> torch.nn.Module:
+    """Load a mixed checkpoint into `model` and lay out its fp16 kernel weights (bind_groups).
+
+    entry: the manifest entry the file was converted with: this library's manifest_entry(model) (the default), or
+    another converter's entry for the whole checkpoint. prefix: the checkpoint prefix of `model` inside the file
+    ("" when the file holds this model alone); tensors outside it are not read. The file's format tag and manifest
+    hash must match, and its tensors under the prefix must be exactly the model's parameters and buffers, with the
+    same shapes; the entry's fp16 parameters must be fp16 in the file."""
     from safetensors import safe_open
 
+    entry = manifest_entry(model) if entry is None else entry
+    want = entry_sha(entry)
     with safe_open(path, framework="pt") as f:
         meta = f.metadata() or {}
-        if meta.get("format") != FORMAT or meta.get("manifest_sha") != entry_sha(entry):
-            raise ValueError(f"{path}: format {meta.get('format')!r} / manifest {meta.get('manifest_sha')!r} do not "
-                             f"match this manifest ({FORMAT} / {entry_sha(entry)}); convert the checkpoint again")
-        state = {k: f.get_tensor(k) for k in f.keys()}
-    ours = dict(model.named_parameters(remove_duplicate=False))
-    ours.update(dict(model.named_buffers()))
-    missing, extra = set(ours) - set(state), set(state) - set(ours)
-    if missing or extra:
-        raise ValueError(f"{path}: missing={sorted(missing)[:10]} unexpected={sorted(extra)[:10]}")
+        if meta.get(META_FORMAT) != FORMAT:
+            raise ValueError(f"{path}: not a mixed checkpoint (format tag {meta.get(META_FORMAT)!r}, expected "
+                             f"{FORMAT!r})")
+        if meta.get(META_SHA) != want:
+            raise ValueError(f"{path}: converted with manifest {meta.get(META_SHA)!r}, but the given entry hashes to "
+                             f"{want!r}; convert the checkpoint again")
+        state = {k[len(prefix):]: f.get_tensor(k) for k in f.keys() if k.startswith(prefix)}
     if device is not None:
         model.to(device)
-    fp16 = set(entry["params"])
-    replaced: dict = {}  # id(old parameter) -> its fp16 replacement (a tensor registered under two names stays one)
+    own = dict(model.named_parameters(remove_duplicate=False))
+    own.update(model.named_buffers(remove_duplicate=False))
+    lacking, extra = sorted(set(own) - set(state)), sorted(set(state) - set(own))
+    if lacking or extra:
+        raise ValueError(f"{path}: tensors do not match the model (absent from the file: {lacking[:8]}; not in the "
+                         f"model: {extra[:8]})")
+    half = set(restrict(entry, prefix)["params"])
+    places = _places(model)
+    done: dict = {}  # id(old parameter) -> its replacement (a tensor with two names is replaced once)
     with torch.no_grad():
-        for k, v in state.items():
-            *pp, leaf = k.split(".")
-            parent = _resolve(model, ".".join(pp))
-            cur = getattr(parent, leaf)
-            if tuple(v.shape) != tuple(cur.shape):
-                raise ValueError(f"{k}: shape {tuple(v.shape)} != {tuple(cur.shape)}")
-            if k in fp16:
-                if v.dtype != torch.float16:
-                    raise ValueError(f"{k}: the manifest lists it as fp16, the file holds {v.dtype}")
-                new = replaced.get(id(cur))
-                if new is None:
-                    new = replaced[id(cur)] = torch.nn.Parameter(v.to(cur.device), requires_grad=False)
-                setattr(parent, leaf, new)
-            elif id(cur) not in replaced:
-                cur.copy_(v.to(cur.dtype))
-    prefuse(model, entry)
+        for name, value in state.items():
+            cur = own[name]
+            if tuple(value.shape) != tuple(cur.shape):
+                raise ValueError(f"{path}: {name} has shape {tuple(value.shape)}, the model {tuple(cur.shape)}")
+            if name in half:
+                if value.dtype != torch.float16:
+                    raise ValueError(f"{path}: {name} is an fp16 parameter of the manifest but the file holds "
+                                     f"{value.dtype}")
+                if id(cur) not in done:
+                    done[id(cur)] = torch.nn.Parameter(value.to(cur.device), requires_grad=False)
+                    _rebind(places, cur, done[id(cur)])
+            elif id(cur) not in done:
+                cur.copy_(value.to(device=cur.device, dtype=cur.dtype))
+    bind_groups(model, restrict(entry, prefix))
     return model

@@ -186,11 +186,12 @@ int bzpf_adaln(const float* a, const float* scale, const float* shift, int64_t l
 /* Sequence attention with pair bias: for head h and query j,
  *   out[j][h*hd + c] = sigmoid(g[j][h*hd + c]) * sum_k softmax_k(q.k/sqrt(hd) + bias[h][j][k]
  *                                                                 + (1 - mask[k]) * (-inf)) v[k][h*hd + c]
- * q/k/v/g rows of pitch ld_in, out rows of pitch ld_out. Replaces the attention core of AttentionPairBias
- * (boltz_mlx/layers/attentionv2.py:70-83). */
+ * q/k/v/g rows of pitch ld_in, out rows of pitch ld_out; q/k/v/g/out are of type dt, the bias of type bias_dt (the
+ * reference's f16 mode adds an fp16 pair bias to fp32 logits: dt = fp32, bias_dt = fp16). Replaces the attention
+ * core of AttentionPairBias (boltz_mlx/layers/attentionv2.py:70-83). */
 int bzpf_seq_attention(const void* q, const void* k, const void* v, const void* g, int64_t ld_in, const void* bias,
-                       const float* mask, float inf, void* out, int64_t ld_out, int dt, int64_t N, int H, int hd,
-                       void* stream);
+                       const float* mask, float inf, void* out, int64_t ld_out, int dt, int bias_dt, int64_t N, int H,
+                       int hd, void* stream);
 
 /* bzpf_seq_attention over n_samples samples in one call: sample i reads q/k/v/g rows from q + i*s_in (elements),
  * the mask row mask + i*s_mask, the bias bias + (i / mult)*s_bias (mult consecutive samples share one [H, N, N]
@@ -199,7 +200,7 @@ int bzpf_seq_attention(const void* q, const void* k, const void* v, const void* 
 int bzpf_seq_attention_batched(const void* q, const void* k, const void* v, const void* g, int64_t ld_in,
                                int64_t s_in, const void* bias, int64_t s_bias, int mult, const float* mask,
                                int64_t s_mask, float inf, void* out, int64_t ld_out, int64_t s_out, int dt,
-                               int n_samples, int64_t N, int H, int hd, void* stream);
+                               int bias_dt, int n_samples, int64_t N, int H, int hd, void* stream);
 
 /* Pair updates at channel counts other than 128 (the template stack's c_z = 64): the projections run as bzpf_linear
  * GEMMs over xn [N*N, D] and these three calls move their outputs into the layouts bzpf_trimul_contract and

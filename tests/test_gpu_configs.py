@@ -413,6 +413,37 @@ def test_tri_att_xn_reference_layout(starting):
         K.set_precision(old)
 
 
+@pytest.mark.parametrize("starting", [True, False])
+def test_tri_att_keep_t(starting):
+    """keep_t is an f16-path option of the reference (attention.py:130-131): in f16 the ending node returns its
+    update in the attention frame (the transpose of keep_t=False's); the fp32 path ignores it and always returns the
+    natural layout (attention.py:45-46, 91-92), as does the starting node in both modes."""
+    from boltz_mlx_amd import kernels as K
+    from boltz_mlx_amd.layers.triangular_attention.attention import (TriangleAttentionEndingNode,
+                                                                     TriangleAttentionStartingNode)
+
+    N, D, C, H = 45, 128, 32, 4
+    p = rand_params(shapes_tri_att(D, C, H), seed=1710, std=0.1)
+    x, _, pm = pair_inputs(N, D, seed=1711, n_pad=4)
+    pm[0, 3, 11] = 0
+    mod = load(TriangleAttentionStartingNode(D, C, H) if starting else TriangleAttentionEndingNode(D, C, H), p)
+    old = K.PRECISION
+    try:
+        xg, mg = dev(x), dev(pm)
+        K.set_precision("fp32")
+        a32, b32 = mod(xg, mg), mod(xg, mg, keep_t=True)
+        K.set_precision("f16")
+        a16, b16 = mod(xg, mg), mod(xg, mg, keep_t=True)
+        torch.cuda.synchronize()
+        assert torch.equal(a32, b32)
+        if starting:
+            assert torch.equal(a16, b16)
+        else:
+            assert torch.equal(b16, a16.transpose(1, 2)) and not torch.equal(b16, a16)
+    finally:
+        K.set_precision(old)
+
+
 def test_tri_mul_and_transition_xn():
     """f16 with B = 1: a given xn is used as the norm_in / norm output (equal to the call without it); fp32 ignores
     it (triangular_mult.py:23-29, transition.py:27-31)."""

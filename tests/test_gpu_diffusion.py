@@ -230,7 +230,7 @@ def test_seq_attention_mfma_vs_valu(hd, N, all_masked):
     base, es = wide.data_ptr(), wide.element_size()
     slow = torch.empty((N, HD), dtype=torch.float16, device="cuda")
     K.call("bzpf_seq_attention", base, base + HD * es, base + 2 * HD * es, base + 3 * HD * es, 4 * HD + 4,
-           bg.data_ptr(), mg.data_ptr(), 1e6, slow.data_ptr(), HD, K.F16, N, H, hd,
+           bg.data_ptr(), mg.data_ptr(), 1e6, slow.data_ptr(), HD, K.F16, K.F16, N, H, hd,
            K._stream())
     torch.cuda.synchronize()
     f, sl = fast.float().cpu().numpy(), slow.float().cpu().numpy()
@@ -247,11 +247,74 @@ def test_seq_attention_mfma_vs_valu(hd, N, all_masked):
     assert m2["max_rel"] <= 1e-2, m2
 
 
+@pytest.mark.parametrize("hd", [16, 24, 32, 48, 64])
+@pytest.mark.parametrize("N", [1, 37, 64, 130])
+@pytest.mark.parametrize("bias16", [False, True])
+def test_seq_attention_f32_mfma(hd, N, bias16):
+    """fp32 sequence attention on the fp32 matrix cores (fp32 q / k / v / g, an fp32 or fp16 bias: the s track's
+    arithmetic in both precision modes) against the float64 definition at the fp32 gate (1e-5 of the largest
+    output) and against the VALU kernel on the same values (forced by a row pitch that is not a multiple of 4).
+    Every seventh key and, for N > 4, the last two are masked."""
+    from boltz_mlx_amd import kernels as K
+
+    H = 3
+    HD = H * hd
+    rng = np.random.default_rng(hd * 7 + N)
+    qkvg = rng.standard_normal((N, 4 * HD)).astype(np.float32)
+    bias = (2 * rng.standard_normal((H, N, N))).astype(np.float16 if bias16 else np.float32)
+    mask = np.ones(N, np.float32)
+    mask[3::7] = 0
+    if N > 4:
+        mask[-2:] = 0
+    a, bg, mg = dev(qkvg), dev(bias, torch.float16 if bias16 else torch.float32), dev(mask)
+    fast = K.seq_attention_packed(a, bg, mg, 1e6, H)
+    wide = torch.zeros((N, 4 * HD + 1), dtype=torch.float32, device="cuda")
+    wide[:, :4 * HD] = a
+    base, es = wide.data_ptr(), wide.element_size()
+    slow = torch.empty((N, HD), dtype=torch.float32, device="cuda")
+    K.call("bzpf_seq_attention", base, base + HD * es, base + 2 * HD * es, base + 3 * HD * es, 4 * HD + 1,
+           bg.data_ptr(), mg.data_ptr(), 1e6, slow.data_ptr(), HD, K.F32, K.F16 if bias16 else K.F32, N, H, hd,
+           K._stream())
+    torch.cuda.synchronize()
+    f, sl = fast.cpu().numpy(), slow.cpu().numpy()
+    x = qkvg.astype(np.float64)
+    ref = np.empty((N, HD))
+    for h in range(H):
+        q, k, v, g = (x[:, c * HD + h * hd: c * HD + (h + 1) * hd] for c in range(4))
+        lg = q @ k.T / np.sqrt(hd) + bias[h].astype(np.float64) + (1 - mask.astype(np.float64))[None, :] * -1e6
+        ref[:, h * hd:(h + 1) * hd] = OD.sigmoid(g) * (O.softmax(lg, -1) @ v)
+    m, mv = O.metrics(f, ref), O.metrics(f, sl)
+    print(f"seq_attention f32 hd={hd} N={N} bias16={bias16}: vs float64 {m['max_rel']:.2e}, vs VALU "
+          f"{mv['max_rel']:.2e}", flush=True)
+    assert m["finite"] and m["max_rel"] <= 1e-5, m
+    assert mv["max_rel"] <= 1e-5, mv
+
+
+def test_seq_attention_f32_mfma_all_keys_masked():
+    """A sequence whose keys are all masked: the mask term is one shift of every logit, which the softmax cancels;
+    the fp32 kernel leaves it out (as the fp16 one does), so the output is the unmasked softmax."""
+    from boltz_mlx_amd import kernels as K
+
+    N, H, hd = 70, 2, 24
+    HD = H * hd
+    rng = np.random.default_rng(5)
+    qkvg = rng.standard_normal((N, 4 * HD)).astype(np.float32)
+    bias = rng.standard_normal((H, N, N)).astype(np.float32)
+    out = K.seq_attention_packed(dev(qkvg), dev(bias), dev(np.zeros(N, np.float32)), 1e6, H)
+    x = qkvg.astype(np.float64)
+    ref = np.empty((N, HD))
+    for h in range(H):
+        q, k, v, g = (x[:, c * HD + h * hd: c * HD + (h + 1) * hd] for c in range(4))
+        ref[:, h * hd:(h + 1) * hd] = OD.sigmoid(g) * (O.softmax(q @ k.T / np.sqrt(hd) + bias[h], -1) @ v)
+    m = O.metrics(out.cpu().numpy(), ref)
+    assert m["finite"] and m["max_rel"] <= 1e-5, m
+
+
 @pytest.mark.parametrize("dt,N", [(torch.float16, 68), (torch.float32, 68), (torch.float16, 67)])
 def test_seq_attention_batched_samples(dt, N):
     """All samples in one launch (sample groups of `multiplicity` sharing a bias, a mask row each) equal one call per
-    sample: the MFMA kernel in fp16 (one grid over the samples), the VALU kernel in fp32 and for N % 4 != 0 (one
-    launch per sample)."""
+    sample: the MFMA kernels in fp16 and fp32 (one grid over the samples), the VALU kernel for N % 4 != 0 in fp16
+    (one launch per sample)."""
     from boltz_mlx_amd import kernels as K
 
     S, mult, H, hd = 6, 3, 4, 48

@@ -284,6 +284,42 @@ def test_attention_pair_bias(precision, N):
     check(f"attention_pair_bias N={N}", got, ref, precision)
 
 
+@pytest.mark.parametrize("N", [7, 64, 200])
+def test_attention_pair_bias_f16_keeps_fp32_projections(N):
+    """The reference's f16 mode keeps AttentionPairBias's projections, logits and softmax in fp32 and only computes
+    the pair bias in fp16 (attentionv2.py:50-84; proj_z.1 is its one fp16 weight of the module). So f16 mode with a
+    given pair bias computes exactly what fp32 mode computes with it, and without one it differs from the fp32
+    oracle only by the fp16 bias: bounds 4e-3 max_rel and 1e-3 rel_fro, against the module gate's 2e-2 / 5e-3."""
+    from boltz_mlx_amd import kernels as K
+    from boltz_mlx_amd.layers.attentionv2 import AttentionPairBias
+
+    cs, cz, H = 384, 128, 16
+    p = rand_params(shapes_attention(cs, cz, H), seed=470 + N, std=0.1)
+    rng = np.random.default_rng(471 + N)
+    s, z = rng.standard_normal((1, N, cs)), rng.standard_normal((1, N, N, cz))
+    mask = np.ones((1, N))
+    mask[:, -(N // 6):] = 0 if N >= 6 else 1
+    mod = load(AttentionPairBias(cs, cz, H), p)
+    bias16 = dev(rng.standard_normal((1, H, N, N)), torch.float16)
+    old = K.PRECISION
+    try:
+        out = {}
+        for prec in ("fp32", "f16"):
+            K.set_precision(prec)
+            out[prec] = (mod(dev(s), dev(z), dev(mask), dev(s), pair_bias=bias16),
+                         mod(dev(s), dev(z), dev(mask), dev(s), pair_bias=bias16.float()),
+                         mod(dev(s), dev(z), dev(mask), dev(s)))
+        torch.cuda.synchronize()
+    finally:
+        K.set_precision(old)
+    assert torch.equal(out["fp32"][0], out["f16"][0]) and torch.equal(out["fp32"][1], out["f16"][1])
+    assert torch.equal(out["f16"][0], out["f16"][1])  # the fp16 bias is added as it is
+    ref = O.attention_pair_bias(s, z, mask, s, cast(p, np.float64), H)
+    m = O.metrics(out["f16"][2].cpu().numpy(), ref)
+    print(f"attention_pair_bias f16 N={N}: max_rel={m['max_rel']:.3e} rel_fro={m['rel_fro']:.3e}", flush=True)
+    assert m["finite"] and m["max_rel"] <= 4e-3 and m["rel_fro"] <= 1e-3, m
+
+
 @pytest.mark.parametrize("precision", ["fp32", "f16"], indirect=True)
 @pytest.mark.parametrize("N,n_pad", [(24, 3), (50, 0)])
 def test_pairformer_layer(precision, N, n_pad):

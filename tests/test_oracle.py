@@ -281,23 +281,19 @@ def test_layer_zero_weights_identity():
     assert np.array_equal(z2, z) and np.array_equal(s2, s)
 
 
-def test_layer_order():
-    """Only tri_mul_out non-zero -> z + tri_mul_out(z); only transition_z non-zero -> z + transition(z)."""
-    base = rand_params(shapes_layer(48, 32, heads=4, pw=8, pheads=2), seed=43)
-    z, tok, pm = pair_inputs(5, 32, seed=44)
-    s = np.random.default_rng(45).standard_normal((1, 5, 48))
-    for keep in ("tri_mul_out", "tri_att_end", "transition_z"):
-        p = {k: (v if (k.startswith(keep) or v.ndim == 1 and not k.endswith("proj_q.bias")) else np.zeros_like(v))
-             for k, v in base.items()}
-        _, z2 = O.pairformer_layer(s, z, tok, pm, p, num_heads=4)
-        q = O.sub(p, keep)
-        if keep == "tri_mul_out":
-            ref = z + O.tri_mul(z, pm, q, True)
-        elif keep == "tri_att_end":
-            ref = z + O.tri_att(z, pm, q, False)
-        else:
-            ref = z + O.transition(z, q)
-        assert np.abs(z2 - ref).max() < 1e-12
+PAIR_MODULES = ("tri_mul_out", "tri_mul_in", "tri_att_start", "tri_att_end", "transition_z")
+
+
+def _tri_mul_torch(x, mask, p, outgoing):
+    """torch einsum form of a triangle multiplication (float64)."""
+    D = p["p_out.weight"].shape[0]
+    xt = T(x[0])
+    xn = F.layer_norm(xt, (D,), T(p["norm_in.weight"]), T(p["norm_in.bias"]), 1e-5)
+    ab = (xn @ T(p["p_in.weight"]).T) * torch.sigmoid(xn @ T(p["g_in.weight"]).T) * T(mask[0])[..., None]
+    a, b = ab[..., :D], ab[..., D:]
+    o = torch.einsum("ikd,jkd->ijd", a, b) if outgoing else torch.einsum("kid,kjd->ijd", a, b)
+    on = F.layer_norm(o, (D,), T(p["norm_out.weight"]), T(p["norm_out.bias"]), 1e-5)
+    return ((on @ T(p["p_out.weight"]).T) * torch.sigmoid(xn @ T(p["g_out.weight"]).T)).numpy()[None]
 
 
 def _torch_transition(x, p):
@@ -317,6 +313,60 @@ def _torch_apb(s_n, z, mask, p, H, inf=1e6):
     bias = zb.permute(0, 3, 1, 2) + (1 - mask)[:, None, None, :] * -inf
     o = F.scaled_dot_product_attention(q, k, v, attn_mask=bias).transpose(1, 2).reshape(B, N, Cs)
     return F.linear(torch.sigmoid(F.linear(s_n, T(p["proj_g.weight"]))) * o, T(p["proj_o.weight"]))
+
+
+def _pair_module_torch(name, z, pm, q):
+    """The torch formulation of one pair module of the layer (the wiring pairformer.py:84-88 gives it)."""
+    if name.startswith("tri_mul"):
+        return _tri_mul_torch(z, pm, q, name == "tri_mul_out")
+    if name.startswith("tri_att"):
+        return _tri_att_sdpa(z, pm, q, name == "tri_att_start")
+    return _torch_transition(T(z), q).numpy()
+
+
+def _only(base, keep):
+    """The layer's parameters with every matrix outside the modules `keep` zeroed (their updates vanish)."""
+    return {k: (v if (k.startswith(keep) or v.ndim == 1 and not k.endswith("proj_q.bias")) else np.zeros_like(v))
+            for k, v in base.items()}
+
+
+def _layer_case():
+    base = rand_params(shapes_layer(48, 32, heads=4, pw=8, pheads=2), seed=43, std=0.3)
+    z, tok, pm = pair_inputs(6, 32, seed=44, n_pad=1)
+    pm[0, 1, 3] = 0  # an asymmetric hole: a transposed mask or a swapped node would show
+    s = np.random.default_rng(45).standard_normal((1, 6, 48))
+    return base, z, tok, pm, s
+
+
+@pytest.mark.parametrize("keep", PAIR_MODULES)
+def test_layer_order(keep):
+    """With one pair module live the layer's z update is that module alone, in its own wiring (direction, node)."""
+    base, z, tok, pm, s = _layer_case()
+    p = _only(base, (keep,))
+    _, z2 = O.pairformer_layer(s, z, tok, pm, p, num_heads=4)
+    ref = z + _pair_module_torch(keep, z, pm, O.sub(p, keep))
+    assert np.abs(z2 - ref).max() < 1e-12
+    # the other wiring of the same weights (incoming for outgoing, ending for starting) gives another result
+    other = {"tri_mul_out": "tri_mul_in", "tri_mul_in": "tri_mul_out", "tri_att_start": "tri_att_end",
+             "tri_att_end": "tri_att_start"}.get(keep)
+    if other is not None:
+        assert np.abs(z + _pair_module_torch(other, z, pm, O.sub(p, keep)) - z2).max() > 1e-4
+
+
+@pytest.mark.parametrize("first,second", [(a, b) for i, a in enumerate(PAIR_MODULES) for b in PAIR_MODULES[i + 1:]])
+def test_layer_two_live_modules_in_reference_order(first, second):
+    """Two live pair modules compose in the reference order (pairformer.py:84-88): the later one reads the z the
+    earlier one updated; the reversed order gives another result."""
+    base, z, tok, pm, s = _layer_case()
+    p = _only(base, (first, second))
+    _, z2 = O.pairformer_layer(s, z, tok, pm, p, num_heads=4)
+    qa, qb = O.sub(p, first), O.sub(p, second)
+    z1 = z + _pair_module_torch(first, z, pm, qa)
+    ref = z1 + _pair_module_torch(second, z1, pm, qb)
+    assert np.abs(z2 - ref).max() < 1e-12
+    zr = z + _pair_module_torch(second, z, pm, qb)
+    rev = zr + _pair_module_torch(first, zr, pm, qa)
+    assert np.abs(rev - ref).max() > 1e-6
 
 
 def test_layer_s_track_composition():

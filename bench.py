@@ -18,6 +18,7 @@ from __future__ import annotations
 import argparse
 import json
 import os
+import statistics
 import sys
 import time
 
@@ -462,7 +463,8 @@ def main() -> int:
                     help="untimed blocks before the N=400 figure (at least, and at least 0.5 s of them)")
     ap.add_argument("--small-steps", type=int, default=128, help="timed blocks per window for the N=400 figure")
     ap.add_argument("--small-windows", type=int, default=3,
-                    help="timed windows at N=400; the figure is the median window")
+                    help="timed windows at N=400 (at least; more, up to 3x as many, until three of them agree "
+                         "within 3%%); the figure is the median window")
     ap.add_argument("--cpu-budget", type=float, default=25.0,
                     help="seconds per CPU-baseline configuration (bounds the timed runs after the warm-up)")
     ap.add_argument("--blocks", type=int, default=64)
@@ -501,7 +503,7 @@ def main() -> int:
         with torch.no_grad():
             print(json.dumps({"msa_layer": msa_layer_leg(args.msa_steps, dev)}), flush=True)
         return 0
-    result_small, small_windows = None, None
+    result_small, small_windows, times_small = None, None, None
     with torch.no_grad():
         # N = 400 blocks/s (secondary figure)
         if args.n_small:
@@ -515,14 +517,25 @@ def main() -> int:
                 done += 16
                 torch.cuda.synchronize()
             windows = []
-            for _ in range(max(1, args.small_windows)):
+            nmin = max(1, args.small_windows)
+
+            def settled(ws):  # three windows within 3% of each other
+                w = sorted(ws)
+                return any(w[i + 2] <= 1.03 * w[i] for i in range(len(w) - 2))
+
+            while len(windows) < nmin or (len(windows) < 3 * nmin and not settled(windows)):
                 t0 = time.perf_counter()
                 xn = run_blocks(m, s, z, tok, pm, done, args.small_steps, xn)
                 torch.cuda.synchronize()
                 windows.append(args.small_steps / (time.perf_counter() - t0))
                 done += args.small_steps
-            result_small = sorted(windows)[len(windows) // 2]
+            result_small = float(statistics.median(windows))
             small_windows = [round(w, 1) for w in windows]
+            # per-kernel event times at N = 400 over one more window
+            K.start_timing()
+            run_blocks(m, s, z, tok, pm, done, args.small_steps, xn)
+            torch.cuda.synchronize()
+            times_small = K.stop_timing()
             del m, s, z, tok, pm
             torch.cuda.empty_cache()
         m, s, z, tok, pm = make_trunk(args.n, args.blocks, 0, dev)
@@ -562,6 +575,10 @@ def main() -> int:
                  for k, v in sorted(total.items(), key=lambda kv: (kv[0].endswith(K.SIDE), -kv[1]))}
     per_kernel_roof = {k: roofline_for(k, total[k] / len(times[k]), args.n, ceilings) for k in total
                        if kernel_work(k, args.n)[0] > 0}
+    roof_small = None
+    if times_small:
+        roof_small = {k: roofline_for(k, sum(v) / len(v), args.n_small, ceilings) for k, v in times_small.items()
+                      if not k.endswith(K.SIDE) and kernel_work(k, args.n_small)[0] > 0}
     value = args.steps / dt
     out = {
         "metric": "Pairformer blocks/sec at N=1000 fp16",
@@ -586,6 +603,7 @@ def main() -> int:
         "roofline": roof,
         "kernel_breakdown": breakdown,
         "kernel_roofline": per_kernel_roof,
+        "kernel_roofline_n400": roof_small,
         "timed_with_events_s": round(dt_ev, 4),
         "measured_ceilings": ceilings,
     }

@@ -23,7 +23,7 @@
 // inf*(m-1)*log2(e). A row whose keys are all masked gets uniform weights over its N keys, which is what the
 // reference's rounding gives (every logit rounds to -inf*log2(e); boltz_mlx/kernels.py:579-581). Softmax and
 // accumulation are fp32, P is rounded to fp16 for the PV product. Key blocks after the row's last unmasked key
-// (trailing padded tokens) are not visited: their probabilities are exactly zero.
+// (trailing padded tokens, however many) are not visited: their probabilities are exactly zero.
 // Work units are ordered (h, i, query block) and dealt to the 8 XCDs in contiguous ranges, so the blocks of one
 // row share K / V^T in their XCD's L2 and each XCD keeps one head's bias resident.
 // Reference behaviour: boltz_mlx/kernels_nax.py:323-558 (f16 flash core), kernels.py:531-600.
@@ -104,26 +104,26 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
   // channels of the lane's accumulator (O^T rows) and of its gate / output vectors: 8 q + 4 hl + e, q < 4
   half_t* oq = out + ((int64_t)i * N + jq) * (int64_t)(H * C) + h * C;
 
-  // A row whose keys are all masked gets uniform weights over its N keys (every logit rounds to the same value in
-  // the reference): out = sigmoid(g) * mean_k v[k], no key loop. The first 64 keys settle it for almost every row;
-  // only rows that mask all of them are scanned further. The decision is the workgroup-wide reduction, never a
-  // thread's own flag: the branch holds barriers, and the key loop's MFMAs must run with every lane active.
-  // The row's key extent: key blocks after its last unmasked key are skipped. Once an unmasked key has been seen, a
-  // masked key's probability is exactly zero (its bias, about -inf*log2(e), puts it more than 25 below the maximum
-  // in base 2 for any logit spread under ~inf, and P is fp16), so skipping changes no bit of the result. Only the
-  // last 256 keys are scanned; an extent before them keeps every block, as does a small inf.
+  // The row's key extent kend (1 + its last unmasked key; 0 when every key is masked), scanned backwards from the
+  // end of the row 256 keys at a time: one step for almost every row. Key blocks after kend are skipped. Once an
+  // unmasked key has been seen, a masked key's probability is exactly zero (its bias, about -inf*log2(e), puts it
+  // more than 25 below the maximum in base 2 for any logit spread under ~inf, and P is fp16), so skipping changes no
+  // bit of the result. A row whose keys are all masked gets uniform weights over its N keys (every logit rounds to
+  // the same value in the reference): out = sigmoid(g) * mean_k v[k], no key loop. Both decisions come from the
+  // workgroup-wide reduction, never a thread's own flag: the branches hold barriers, and the key loop's MFMAs must
+  // run with every lane active.
   __shared__ int kend_w[4];
-  {
-    const int kq = N - 256 + t;
+  int kend = 0;
+  for (int base = N - 256;; base -= 256) {  // workgroup-uniform
+    const int kq = base + t;  // < N
     const uint64_t b = __ballot(kq >= 0 && mrow[(int64_t)kq * mask_sk] != 0.0f);
-    if (l == 0) kend_w[wave] = b ? N - 256 + 64 * wave + 64 - __clzll(b) : 0;
+    if (l == 0) kend_w[wave] = b ? base + 64 * wave + 64 - __clzll(b) : 0;
+    __syncthreads();
+    kend = max(max(kend_w[0], kend_w[1]), max(kend_w[2], kend_w[3]));
+    __syncthreads();  // kend_w is written again by the next step
+    if (kend > 0 || base <= 0) break;
   }
-  bool any_key = __syncthreads_or(l < N && mrow[(int64_t)l * mask_sk] != 0.0f) != 0;
-  if (!any_key) {
-    int found = 0;
-    for (int k = 64 + t; k < N; k += 256) found |= (mrow[(int64_t)k * mask_sk] != 0.0f);
-    any_key = __syncthreads_or(found) != 0;
-  }
+  const bool any_key = kend > 0;
   if (!any_key) {
     {
       const int d = t >> 3, part = t & 7;  // 8 lanes per channel
@@ -173,8 +173,7 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
   // every wave loads the raw mask values of the block's 64 keys (lane l: key k0 + l)
   const int skey = t >> 2, sd8 = (t & 3) * 8;
   const int vd = t >> 3, vk8 = (t & 7) * 8;
-  int kend = max(max(kend_w[0], kend_w[1]), max(kend_w[2], kend_w[3]));
-  if (kend == 0 || inf < 1e6f) kend = N;
+  if (inf < 1e6f) kend = N;
   const int nblk = (kend + BK - 1) / BK;
   half8 kreg, vreg;
   float mraw;

@@ -659,13 +659,13 @@ def test_triattn_core_strided_mask(impl, N):
 
 
 @pytest.mark.gpu
-@pytest.mark.parametrize("N", [200, 300, 700])
-def test_triattn_core_trailing_block_skip_exact(N):
-    """The MFMA core skips the key blocks after a row's last unmasked key (scanned over the row's last 256 keys) when
-    inf >= 1e6, since those keys' probabilities are exactly zero. Pinned bit for bit against the same call with
+@pytest.mark.parametrize("N,n_pad", [(200, 33), (300, 50), (700, 116), (700, 330)])
+def test_triattn_core_trailing_block_skip_exact(N, n_pad):
+    """The MFMA core skips the key blocks after a row's last unmasked key (found by a backward scan in 256-key steps)
+    when inf >= 1e6, since those keys' probabilities are exactly zero. Pinned bit for bit against the same call with
     inf = 5e5 (no skip; the masked probabilities are zero there too): trailing padding that covers whole blocks,
-    rows whose last unmasked key lies before the scanned range, rows masked at the start, interior holes and fully
-    masked rows."""
+    more than 256 padded tokens, rows whose last unmasked key lies far before the end, rows masked at the start,
+    interior holes and fully masked rows."""
     import torch
 
     from boltz_mlx_amd import kernels as K
@@ -678,7 +678,7 @@ def test_triattn_core_trailing_block_skip_exact(N):
     vt[..., N:] = 0
     tb = dev(rng.standard_normal(K.tri_bias_numel(N, H)), torch.float16)
     tok = np.ones(N, np.float32)
-    tok[N - N // 6:] = 0  # trailing padding: whole 64-key blocks for N = 700, 300
+    tok[N - n_pad:] = 0  # trailing padding: whole 64-key blocks for N = 700, 300
     mask = tok[:, None] * tok[None, :] * (rng.random((N, N)) > 0.2)
     mask[:, 0] = np.where(tok > 0, 1.0, 0.0)  # rows of real tokens keep key 0
     if N > 256:

@@ -43,7 +43,7 @@ const char* bzpf_version(void) { return "bzpf 0.1.0 (gfx950)"; }
 
 const char* bzpf_last_error(void) { return g_err; }
 
-int64_t bzpf_row_pitch(int64_t N) { return (N + 63) / 64 * 64; }
+int64_t bzpf_row_pitch(int64_t N) { return bzpf::row_pitch(N); }
 
 int bzpf_layernorm(const void* x, int x_dt, const float* w, const float* b, float eps, void* y, int y_dt,
                    int64_t rows, int D, void* stream) {

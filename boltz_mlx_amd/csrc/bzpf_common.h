@@ -5,6 +5,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include "bzpf_layout.h"
+
 typedef _Float16 half_t;
 typedef _Float16 half8 __attribute__((ext_vector_type(8)));
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
@@ -96,19 +98,6 @@ __device__ __forceinline__ void zero_acc(f4 (&acc)[MB][NB]) {
 // 16-byte vector of T.
 template <typename T> struct Vec16 { static constexpr int n = 16 / sizeof(T); };
 
-// Triangle-bias layout: element (head h, query j, key k) of the [H][N][N] bias, stored in the order the MFMA
-// attention core consumes it (the accumulator layout of v_mfma_f32_32x32x16_f16). For a 32-query tile jt and a
-// 64-key block kb, lane l = 32*hl + q of a wave owns the 32 values of query 32*jt + q at keys
-// 64*kb + 32*kt + 8*p + 4*hl + e (kt < 2, p < 4, e < 4); element x = 16*kt + 4*p + e of lane l sits at
-// 512*(x/8) + 8*l + x%8 of the block's 2048, so each of the lane's four 16-byte loads is one contiguous 1 KB across
-// the wave (8 whole cache lines). ldk = N rounded up to 64; 4 consecutive keys 4m .. 4m + 3 are contiguous.
-__host__ __device__ inline int64_t tb_offset(int64_t h, int64_t j, int64_t k, int64_t N, int64_t ldk) {
-  const int64_t njt = (N + 31) / 32, nkb = ldk / 64;
-  const int64_t jt = j >> 5, q = j & 31, kb = k >> 6, kk = k & 63;
-  const int64_t kt = kk >> 5, p = (kk >> 3) & 3, hl = (kk >> 2) & 1, e = kk & 3;
-  const int64_t x = kt * 16 + p * 4 + e;
-  return ((h * njt + jt) * nkb + kb) * 2048 + (x >> 3) * 512 + (hl * 32 + q) * 8 + (x & 7);
-}
 struct alignas(16) U128 { uint32_t w[4]; };
 typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
 

@@ -141,12 +141,13 @@ __global__ __launch_bounds__(64 * NW, 2) void seq_attn_mfma(const half_t* __rest
   const int nblk = (N + BK - 1) / BK;
   constexpr int RSRC_CFG = 0x00020000;  // raw buffer, 32-bit data format
   // K / V rows (keys past N read as zeros), the bias plane of head h, the mask row
+  // (extents as in bzpf_layout.h, which the host-side layout check evaluates at the launcher's limits)
   const __amdgpu_buffer_rsrc_t krs =
-      __builtin_amdgcn_make_buffer_rsrc((void*)kh, 0, (int)(((int64_t)(N - 1) * ld_in + HD) * 2), RSRC_CFG);
+      __builtin_amdgcn_make_buffer_rsrc((void*)kh, 0, (int)seqattn_kv_extent(N, ld_in, HD), RSRC_CFG);
   const __amdgpu_buffer_rsrc_t vrs =
-      __builtin_amdgcn_make_buffer_rsrc((void*)vh, 0, (int)(((int64_t)(N - 1) * ld_in + HD) * 2), RSRC_CFG);
-  const __amdgpu_buffer_rsrc_t brs = __builtin_amdgcn_make_buffer_rsrc((void*)bh, 0, (int)((int64_t)N * N * 2),
-                                                                       RSRC_CFG);
+      __builtin_amdgcn_make_buffer_rsrc((void*)vh, 0, (int)seqattn_kv_extent(N, ld_in, HD), RSRC_CFG);
+  const __amdgpu_buffer_rsrc_t brs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)bh, 0, (int)seqattn_bias_extent(N), RSRC_CFG);
   const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc((void*)mask, 0, N * 4, RSRC_CFG);
   const int boff = (jc * N + 4 * hl) * 2, mvo = l * 4;
   // PF register sets: block kb is loaded PF blocks ahead into set kb % PF (two for 4-wave workgroups, whose VGPR
@@ -339,8 +340,7 @@ hipError_t launch_seq_attention_f16_mfma(const void* q, const void* k, const voi
                                          int S, int64_t N, int H, int hd, hipStream_t st) {
   // 32-bit buffer offsets over a head's K / V rows (block offsets included) and bias plane; 8-byte bias loads need
   // N % 4 == 0, 16-byte row loads ld_in % 8 == 0
-  if (N < 1 || N > 32767 || N % 4 || ld_in % 8 || ld_out % 4 || (N + 64) * ld_in * 2 > 0x7fffffffLL ||
-      N * N * 2 > 0x7fffffffLL || S < 1 || S > 65535 || mult < 1)
+  if (!seqattn_shape_ok(N, ld_in) || ld_out % 4 || S < 1 || S > 65535 || mult < 1)
     return hipErrorInvalidValue;
   // 64-query workgroups (2 waves) when 128-query ones would not give two per CU: more of them per CU hide each
   // key block's load latency, and the last query block of a sequence wastes fewer lanes

@@ -223,8 +223,7 @@ hipError_t launch_seq_attention(const void* q, const void* k, const void* v, con
   if (S < 1 || mult < 1) return hipErrorInvalidValue;
   if (dt == DT_F16 && bias_dt == DT_F16 && (hd == 16 || hd == 24 || hd == 32 || hd == 48 || hd == 64) && N % 4 == 0 && ld_in % 8 == 0 &&
       ld_out % 4 == 0 && s_in % 8 == 0 && s_bias % 4 == 0 && s_out % 4 == 0 && al(q, 16) && al(k, 16) &&
-      al(v, 16) && al(g, 16) && al(bias, 8) && al(out, 8) && N <= 32767 && S <= 65535 &&
-      (N + 64) * ld_in * 2 <= 0x7fffffffLL && N * N * 2 <= 0x7fffffffLL)
+      al(v, 16) && al(g, 16) && al(bias, 8) && al(out, 8) && S <= 65535 && seqattn_shape_ok(N, ld_in))
     return launch_seq_attention_f16_mfma(q, k, v, g, ld_in, s_in, bias, s_bias, mult, mask, s_mask, inf, out, ld_out,
                                          s_out, S, N, H, hd, st);
   if (dt == DT_F32 && (hd == 16 || hd == 24 || hd == 32 || hd == 48 || hd == 64) && ld_in % 4 == 0 &&

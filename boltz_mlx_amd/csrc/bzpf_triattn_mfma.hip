@@ -180,34 +180,38 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
   // Row-local sources as buffer resources: each lane's offset is fixed and the block offset rides in the scalar
   // offset, so the loads need no address arithmetic; keys past N read as zeros (range-checked).
   constexpr int RSRC_CFG = 0x00020000;  // raw buffer, 32-bit data format
-  const __amdgpu_buffer_rsrc_t krs = __builtin_amdgcn_make_buffer_rsrc((void*)kp, 0, N * C * 2, RSRC_CFG);
-  const __amdgpu_buffer_rsrc_t vrs = __builtin_amdgcn_make_buffer_rsrc((void*)vp, 0, C * ldk * 2, RSRC_CFG);
-  const int koff = (skey * C + sd8) * 2, voff = (vd * ldk + vk8) * 2;
+  // (offsets and extents as in bzpf_layout.h, which the host-side layout check evaluates at the launcher's limits)
+  const __amdgpu_buffer_rsrc_t krs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)kp, 0, (int)core_k_extent(N, C), RSRC_CFG);
+  const __amdgpu_buffer_rsrc_t vrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)vp, 0, (int)core_v_extent(ldk, C), RSRC_CFG);
+  const int koff = core_k_lane(t, C), voff = core_v_lane(t, ldk);
   // bias fragments (fragment-ordered layout): 32 contiguous values per lane per 32-query tile and 64-key block
   const int njt = (N + 31) / 32, nkb = ldk / 64;
   __amdgpu_buffer_rsrc_t brs;
   {
     int jt = qb * (WQ / 32) + wave;
     if (jt >= njt) jt = njt - 1;
-    brs = __builtin_amdgcn_make_buffer_rsrc((void*)(tb + (((int64_t)h * njt + jt) * nkb) * 2048), 0, nkb * 4096,
-                                            RSRC_CFG);
+    brs = __builtin_amdgcn_make_buffer_rsrc((void*)(tb + (((int64_t)h * njt + jt) * nkb) * 2048), 0,
+                                            (int)core_b_extent(ldk), RSRC_CFG);
   }
   half8 bcur[4];  // bias of keys 32 kt + 8 (e / 4) + 4 hl + e % 4: elements 16 kt + e of the lane's 32
   // mask: lane l reads key kb * 64 + l; only the partial last block clamps (to key N - 1)
   // (as a buffer resource over keys 0 .. N - 1 of the row: keys past N read as 0 and are set to -inf below)
-  const __amdgpu_buffer_rsrc_t mrs = __builtin_amdgcn_make_buffer_rsrc(
-      (void*)mrow, 0, (int)(uint32_t)((N - 1) * mask_sk * 4 + 4), RSRC_CFG);
-  const int mvo = (int)(l * mask_sk * 4);
+  const __amdgpu_buffer_rsrc_t mrs =
+      __builtin_amdgcn_make_buffer_rsrc((void*)mrow, 0, (int)core_m_extent(N, mask_sk), RSRC_CFG);
+  const int mvo = core_m_lane(l, mask_sk);
   // loads of block kb (kb < nblk; the loop clamps, so it issues them unconditionally)
   auto prefetch = [&](int kb) {
-    kreg = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(krs, koff, kb * BK * C * 2, 0));
-    vreg = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff, kb * BK * 2, 0));
-    mraw = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(mrs, mvo, (int)(kb * BK * mask_sk * 4), 0));
+    kreg = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(krs, koff, core_k_block(kb, C), 0));
+    vreg = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(vrs, voff, core_v_block(kb), 0));
+    mraw = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(mrs, mvo, core_m_block(kb, mask_sk), 0));
   };
   auto prefetch_bias = [&](int kb) {
 #pragma unroll
     for (int v = 0; v < 4; v++)
-      bcur[v] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(brs, 1024 * v + 16 * l, kb * 4096, 0));
+      bcur[v] = __builtin_bit_cast(half8, __builtin_amdgcn_raw_buffer_load_b128(brs, core_b_lane(v, l),
+                                                                                core_b_block(kb), 0));
   };
   // Issue order pinned to the loop's (K, V^T, mask, then bias): the wait counter merges the prologue and the loop
   // back edge at the loop header, and any other order there turns the first wait of every iteration into a wait
@@ -350,8 +354,7 @@ hipError_t launch_triattn_core_f16_mfma(const void* qkg, const void* vt, const v
                                         int64_t mask_si, int64_t mask_sk, float inf, void* out, int64_t N,
                                         int64_t ldk, int H, int C, hipStream_t st) {
   // 32-bit buffer offsets: the mask row (keys 0 .. N - 1 at stride mask_sk floats) and the K / V^T / bias rows
-  if (C != 32 || ldk % 64 != 0 || ldk < N || N > 32767 || mask_sk < 1 || (N - 1) * mask_sk * 4 + 4 > 0x7fffffffLL)
-    return hipErrorInvalidValue;
+  if (!core_shape_ok(N, ldk, C, mask_sk)) return hipErrorInvalidValue;
   const int64_t units = (int64_t)H * N * ((N + 127) / 128);
   const int64_t per_xcd = (units + NXCD - 1) / NXCD;
   const dim3 grid((unsigned)(per_xcd * NXCD));

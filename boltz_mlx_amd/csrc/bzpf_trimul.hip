@@ -127,11 +127,7 @@ __global__ __launch_bounds__(256, 2) void trimul_contract_kernel(const T* __rest
 // that each store instruction writes whole 128-byte row segments (scattered 8-byte stores took a third of the time).
 // The lane-to-k assignment (lane half h takes k = 32 h + 8 s .. + 7 of a 64-element stage in step s) is the one the
 // earlier register-staged kernel used, so the accumulation order, and the result, are unchanged.
-template <int BK>
-__device__ __forceinline__ int ct_swz(int row) {
-  if constexpr (BK == 64) return (row & 7) ^ ((row >> 3) & 1);       // 8 chunks of a 128-byte row
-  else return ((row >> 1) & 3) ^ ((row >> 3) & 1);                     // 4 chunks of a 64-byte row
-}
+// (ct_swz, in bzpf_layout.h: the swizzle of a row, checked on the host for bijectivity and bank conflicts)
 
 template <int BK, int NS>
 __global__ __launch_bounds__(512, 1) void trimul_contract_f16_k(const half_t* __restrict__ ab, half_t* __restrict__ o,
@@ -168,7 +164,7 @@ __global__ __launch_bounds__(512, 1) void trimul_contract_f16_k(const half_t* __
   };
 
   constexpr int RSRC_CFG = 0x00020000;
-  const int chan_bytes = (int)(N * ld * 2);
+  const int chan_bytes = (int)contract_extent(N, ld);
   // lane part of every load: row w * RPI + l / CPR of its 8-wave group, logical chunk (l % CPR) ^ swz(row)
   const int lrow = w * RPI + l / CPR;
   const int voff = (int)(((int64_t)lrow * ld + 8 * ((l % CPR) ^ ct_swz<BK>(lrow))) * 2);
@@ -326,7 +322,7 @@ static hipError_t contract_t(const void* ab, void* o, int64_t N, int64_t ld, int
 
 hipError_t launch_trimul_contract(const void* ab, void* o, int dt, int64_t N, int64_t ld, int64_t k_len, int D,
                                   hipStream_t st) {
-  if (dt == DT_F16 && 2 * N * ld >= (1LL << 31)) return hipErrorInvalidValue;  // 32-bit buffer offsets per channel
+  if (dt == DT_F16 && !contract_shape_ok(N, ld)) return hipErrorInvalidValue;  // 32-bit buffer offsets per channel
   // contract over k < k_len rounded up to 64 (a whole number of stages of either kernel); 0 or >= N: every k
   const int64_t kl = k_len <= 0 || k_len >= N ? ld : (k_len + 63) / 64 * 64;
   return dt == DT_F16 ? contract_t<half_t>(ab, o, N, ld, kl, D, st) : contract_t<float>(ab, o, N, ld, kl, D, st);

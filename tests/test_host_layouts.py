@@ -1,7 +1,9 @@
-"""Host-side layout helpers of the fused kernels (CPU): the weight-row regrouping of the SwiGLU GEMMs."""
+"""Host-side layout helpers of the fused kernels (CPU): the weight-row regrouping of the SwiGLU GEMMs, the pair-mask
+scope, and the kernels' own index maps and 32-bit buffer ranges built on the host."""
 
 from __future__ import annotations
 
+import pytest
 import torch
 
 
@@ -52,3 +54,51 @@ def test_pair_mask_scope_extent_and_transpose():
             assert K.key_extent(torch.zeros(N, N), N, False) == N
         assert K.mask_transposed(m, N) is K.mask_transposed(m, N)
     assert K.key_extent(m, N, False) == 0
+
+
+# ---------------------------------------------------------------- kernel index maps and buffer ranges (host build)
+
+@pytest.fixture(scope="module")
+def layout_lib(tmp_path_factory):
+    """tests/layout_check.cpp built with g++ against boltz_mlx_amd/csrc/bzpf_layout.h (the header the kernels and
+    their launchers use; it needs no HIP)."""
+    import ctypes
+    import os
+    import subprocess
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    out = str(tmp_path_factory.mktemp("layout") / "layout_check.so")
+    subprocess.run(["g++", "-O2", "-std=c++17", "-shared", "-fPIC", "-I", os.path.join(root, "boltz_mlx_amd", "csrc"),
+                    os.path.join(root, "tests", "layout_check.cpp"), "-o", out], check=True)
+    lib = ctypes.CDLL(out)
+    lib.lc_check.argtypes = [ctypes.c_char_p, ctypes.c_int]
+    lib.lc_tb_offsets.argtypes = [ctypes.c_int64, ctypes.c_int, ctypes.c_void_p]
+    return lib
+
+
+def test_kernel_layouts_and_buffer_ranges(layout_lib):
+    """The fragment-ordered triangle bias is a bijection onto its buffer with the core's 1 KB load runs; the
+    contraction's LDS swizzle permutes each row and makes the fragment reads conflict-free; every buffer resource of
+    the attention core, the contraction and the fp16 sequence attention keeps its extent and largest offset below
+    2^31 at the launchers' size limits, which refuse the first size past them."""
+    import ctypes
+
+    buf = ctypes.create_string_buffer(1 << 17)
+    failures = layout_lib.lc_check(buf, len(buf))
+    report = buf.value.decode()
+    print(report)
+    assert failures == 0, [line for line in report.splitlines() if line.startswith("FAIL")]
+    assert report.count("ok") > 100
+
+
+@pytest.mark.parametrize("N,H", [(1, 1), (37, 4), (130, 3), (257, 4)])
+def test_tb_offset_matches_the_host_wrapper(layout_lib, N, H):
+    """The kernels' tb_offset (bzpf_layout.h) and kernels.tri_bias_offsets (the host's map of a dense bias into the
+    layout, used by the tests and the layout kernels' callers) agree element for element."""
+    import numpy as np
+
+    from boltz_mlx_amd import kernels as K
+
+    got = np.empty((H, N, N), dtype=np.int64)
+    layout_lib.lc_tb_offsets(N, H, got.ctypes.data)
+    assert np.array_equal(got, K.tri_bias_offsets(N, H))

@@ -4,6 +4,7 @@
 
 #include "bzpf.h"
 #include "bzpf_kernels.h"
+#include "bzpf_layout.h"
 
 namespace {
 

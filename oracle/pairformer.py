@@ -52,11 +52,15 @@ def sub(params: dict, prefix: str) -> dict:
 def layer_norm(x, w=None, b=None, eps=1e-5):
     """Row LayerNorm over the last axis: two-pass mean/variance, (x - mean) * rsqrt(var + eps) * w + b
     (kernels.py:438-462; norm.py:8-17)."""
+    # computed in the promoted type of the arguments (float32 x with float64 parameters gives float64, as
+    # (x - mean) * w would)
+    dt = np.result_type(x, *(a for a in (w, b) if a is not None))
+    x = np.asarray(x, dtype=dt)
     mean = x.mean(axis=-1, keepdims=True)
     d = x - mean
     var = (d * d).mean(axis=-1, keepdims=True)
     # in place from here (the values equal d / sqrt(var + eps) * w + b; fewer large temporaries at N^2 rows)
-    d /= np.sqrt(var + x.dtype.type(eps))
+    d /= np.sqrt(var + dt.type(eps))
     if w is not None:
         d *= w
     if b is not None:

@@ -446,3 +446,16 @@ def test_module_runs_layers_in_order():
 def test_metrics_definition():
     m = O.metrics(np.array([1.0, 2.0, 3.5]), np.array([1.0, 2.0, 4.0]))
     assert m["max_abs"] == 0.5 and m["max_rel"] == 0.125
+
+
+def test_layer_norm_promotes_like_its_formula():
+    """A float32 input with float64 parameters is normalised in float64 (as (x - mean) * w + b promotes), not in
+    the input's float32."""
+    rng = np.random.default_rng(60)
+    x = rng.standard_normal((3, 128)).astype(np.float32)
+    w, b = 1 + 0.1 * rng.standard_normal(128), 0.1 * rng.standard_normal(128)
+    got = O.layer_norm(x, w, b)
+    assert got.dtype == np.float64
+    ref = F.layer_norm(T(x), (128,), T(w), T(b), 1e-5).numpy()
+    assert np.abs(got - ref).max() < 1e-12
+    assert O.layer_norm(x, w.astype(np.float32), b.astype(np.float32)).dtype == np.float32

@@ -230,6 +230,29 @@ __global__ __launch_bounds__(256, 2) void gemm_lds_k(const half_t* __restrict__ 
       fb[set][rb] = *reinterpret_cast<const half8*>(base + row * ROWB + 16 * ((4 * hh + s) ^ gl_swz(row)));
     }
   };
+  // The epilogue's fp32 inputs (the y it accumulates into and the gate) are loaded before the K loop, so their
+  // latency overlaps the loop instead of following the last stage (for the 768-wide gated outputs the epilogue is a
+  // 12 MB read-modify-write). They are issued ahead of the stage loads: the loop's vmcnt waits count loads in issue
+  // order, so these complete by the first stage's wait and never hold back a later one.
+  f4 ypre[RB][MB][4], gpre[RB][MB][4];
+  if constexpr (sizeof(TY) == 4) {
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) {
+      const int64_t r = r0 + BR / 2 * wr + 32 * rb + rr;
+      const bool rin = r < R;
+      const float* grow = epi == 2 && rin ? gate + (r % gate_rows) * ld_gate : nullptr;
+#pragma unroll
+      for (int mb = 0; mb < MB; mb++)
+#pragma unroll
+        for (int q = 0; q < 4; q++) {
+          const int m = m0 + BM / 2 * wm + 32 * mb + 8 * q + 4 * hh;
+          const bool in = rin && m < M;
+          ypre[rb][mb][q] = in && epi >= 1 ? *reinterpret_cast<const f4*>(y + r * M + m) : f4{0.f, 0.f, 0.f, 0.f};
+          gpre[rb][mb][q] = in && grow != nullptr ? *reinterpret_cast<const f4*>(grow + m) : f4{0.f, 0.f, 0.f, 0.f};
+        }
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
   constexpr int YOUNGER = (NS - 2) * LPW;  // loads of later stages in flight when a stage is waited for
   constexpr int WAIT = (YOUNGER & 15) | ((YOUNGER >> 4) << 14) | (0x7 << 4) | (0xF << 8);  // vmcnt only
 #pragma unroll
@@ -277,14 +300,14 @@ __global__ __launch_bounds__(256, 2) void gemm_lds_k(const half_t* __restrict__ 
         if (m >= M) continue;
         f4 v4 = f4{acc[mb][rb][4 * q], acc[mb][rb][4 * q + 1], acc[mb][rb][4 * q + 2], acc[mb][rb][4 * q + 3]};
         if (bias != nullptr) v4 += *reinterpret_cast<const f4*>(bias + m);
-        if (epi == 2) {
-          const f4 gv = *reinterpret_cast<const f4*>(gate + (r % gate_rows) * ld_gate + m);
-          v4 = f4{v4[0] * sigmoidf_(gv[0]), v4[1] * sigmoidf_(gv[1]), v4[2] * sigmoidf_(gv[2]),
-                  v4[3] * sigmoidf_(gv[3])};
-        }
         TY* yp = y + r * M + m;
-        if constexpr (sizeof(TY) == 4) {
-          if (epi >= 1) v4 += *reinterpret_cast<const f4*>(yp);
+        if constexpr (sizeof(TY) == 4) {  // epi 1 and 2 (fp32 y only)
+          if (epi == 2) {
+            const f4 gv = gpre[rb][mb][q];
+            v4 = f4{v4[0] * sigmoidf_(gv[0]), v4[1] * sigmoidf_(gv[1]), v4[2] * sigmoidf_(gv[2]),
+                    v4[3] * sigmoidf_(gv[3])};
+          }
+          if (epi >= 1) v4 += ypre[rb][mb][q];
           *reinterpret_cast<f4*>(yp) = v4;
         } else {
           *reinterpret_cast<half4*>(yp) = half4{(half_t)v4[0], (half_t)v4[1], (half_t)v4[2], (half_t)v4[3]};

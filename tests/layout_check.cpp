@@ -1,5 +1,5 @@
 // Host-side check of the kernels' index maps and 32-bit buffer ranges (boltz_mlx_amd/csrc/bzpf_layout.h), built
-// with g++ by tests/test_layouts_host.py: no GPU, no HIP. Exports:
+// with g++ by tests/test_host_layouts.py: no GPU, no HIP. Exports:
 //   lc_tb_offsets(N, H, out): tb_offset(h, j, k) for h < H, j < N, k < N in [H][N][N] order;
 //   lc_check(report, cap):    every check below; returns the number of failures and writes one line per check.
 #include <stdint.h>

@@ -59,8 +59,8 @@ __global__ __launch_bounds__(64 * NW, 2) void seq_attn_mfma(const half_t* __rest
                                                         int64_t ld_in, const half_t* __restrict__ bias,
                                                         const float* __restrict__ mask, float inf,
                                                         half_t* __restrict__ out, int64_t ld_out, int N, int H,
-                                                        int64_t s_in, int64_t s_bias, int mult, int64_t s_mask,
-                                                        int64_t s_out) {
+                                                        int S, int64_t s_in, int64_t s_bias, int mult,
+                                                        int64_t s_mask, int64_t s_out, int per_xcd) {
   static_assert((HD % 16 == 0 || HD == 24) && HD >= 16 && HD <= 64, "head width 16, 24, 32, 48 or 64");
   constexpr int BK = 64;                   // keys per LDS stage
   constexpr int NTH = 64 * NW;             // threads: NW waves of 32 queries
@@ -80,20 +80,23 @@ __global__ __launch_bounds__(64 * NW, 2) void seq_attn_mfma(const half_t* __rest
   __shared__ LDS_ALIGN half_t Vs[2][32 * NT * LDV];
   __shared__ LDS_ALIGN float Mb[4][BK];
 
-  // sample blockIdx.y: its own q / k / v / g rows, mask row and output rows; the bias of sample group smp / mult
-  {
-    const int smp = (int)blockIdx.y;
-    q += smp * s_in;
-    k += smp * s_in;
-    v += smp * s_in;
-    g += smp * s_in;
-    bias += (int64_t)(smp / mult) * s_bias;
-    mask += smp * s_mask;
-    out += smp * s_out;
-  }
+  // Work units (head, sample, query block), query block fastest, are dealt to the 8 XCDs in contiguous ranges (the
+  // dispatcher sends workgroup b to XCD b % 8), so an XCD's units share a few heads' bias planes and their samples'
+  // K / V rows in its L2. Sample smp: its own q / k / v / g rows, mask row and output rows; the bias of sample group
+  // smp / mult.
   const int nqb = (N + WQ - 1) / WQ;
-  const int qb = (int)(blockIdx.x % nqb);
-  const int h = (int)(blockIdx.x / nqb);
+  const int u = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+  if (u >= nqb * S * H) return;  // whole workgroup
+  const int qb = u % nqb;
+  const int smp = (u / nqb) % S;
+  const int h = u / (nqb * S);
+  q += smp * s_in;
+  k += smp * s_in;
+  v += smp * s_in;
+  g += smp * s_in;
+  bias += (int64_t)(smp / mult) * s_bias;
+  mask += smp * s_mask;
+  out += smp * s_out;
   const int t = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6), l = t & 63;
   const int hl = l >> 5, qi = l & 31;
@@ -346,20 +349,22 @@ hipError_t launch_seq_attention_f16_mfma(const void* q, const void* k, const voi
   // key block's load latency, and the last query block of a sequence wastes fewer lanes
   const bool small = ((N + 127) / 128) * H * (int64_t)S < 512;
   const int wq = small ? 64 : 128;
-  const dim3 grid((unsigned)(((N + wq - 1) / wq) * H), (unsigned)S);
+  const int64_t units = (N + wq - 1) / wq * (int64_t)S * H, per_xcd = (units + 7) / 8;
+  if (units >= (1LL << 31) - 8) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)(8 * per_xcd));
 #define BZ_SEQ_MFMA(HDV)                                                                                          \
   if (small)                                                                                                     \
     seq_attn_mfma<HDV, 2><<<grid, 128, 0, st>>>(static_cast<const half_t*>(q), static_cast<const half_t*>(k),    \
                                                 static_cast<const half_t*>(v), static_cast<const half_t*>(g), ld_in, \
                                                 static_cast<const half_t*>(bias), mask, inf,                     \
-                                                static_cast<half_t*>(out), ld_out, (int)N, H, s_in, s_bias, mult, \
-                                                s_mask, s_out);                                                  \
+                                                static_cast<half_t*>(out), ld_out, (int)N, H, S, s_in, s_bias, \
+                                                mult, s_mask, s_out, (int)per_xcd);                                                  \
   else                                                                                                           \
     seq_attn_mfma<HDV, 4><<<grid, 256, 0, st>>>(static_cast<const half_t*>(q), static_cast<const half_t*>(k),    \
                                                 static_cast<const half_t*>(v), static_cast<const half_t*>(g), ld_in, \
                                                 static_cast<const half_t*>(bias), mask, inf,                     \
-                                                static_cast<half_t*>(out), ld_out, (int)N, H, s_in, s_bias, mult, \
-                                                s_mask, s_out)
+                                                static_cast<half_t*>(out), ld_out, (int)N, H, S, s_in, s_bias, \
+                                                mult, s_mask, s_out, (int)per_xcd)
   switch (hd) {
     case 16: BZ_SEQ_MFMA(16); break;
     case 24: BZ_SEQ_MFMA(24); break;

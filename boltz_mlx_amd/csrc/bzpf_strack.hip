@@ -146,6 +146,17 @@ __global__ __launch_bounds__(256) void adaln_kernel(const float* __restrict__ a,
   const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
   if (r >= R) return;  // whole wave
   const float* ar = a + r * D;
+  // the conditioning row's scale and shift are loaded first: they do not depend on the statistics, so the row costs
+  // one round trip to memory instead of two
+  const int64_t q = r % cond_rows;
+  const float* sc = scale + q * ldc;
+  const float* sh = shift + q * ldc;
+  float gs[NV], hs[NV];
+#pragma unroll
+  for (int j = 0; j < NV; j++) {
+    gs[j] = sc[l + 64 * j];
+    hs[j] = sh[l + 64 * j];
+  }
   float v[NV];
   float s = 0.f;
 #pragma unroll
@@ -165,15 +176,9 @@ __global__ __launch_bounds__(256) void adaln_kernel(const float* __restrict__ a,
 #pragma unroll
   for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o, 64);
   const float rstd = 1.0f / sqrtf(ss * (1.0f / D) + eps);
-  const int64_t q = r % cond_rows;
-  const float* sc = scale + q * ldc;
-  const float* sh = shift + q * ldc;
   TO* orow = out + r * D;
 #pragma unroll
-  for (int j = 0; j < NV; j++) {
-    const int c = l + 64 * j;
-    orow[c] = from_f<TO>(sigmoidf_(sc[c]) * ((v[j] - mean) * rstd) + sh[c]);
-  }
+  for (int j = 0; j < NV; j++) orow[l + 64 * j] = from_f<TO>(sigmoidf_(gs[j]) * ((v[j] - mean) * rstd) + hs[j]);
 }
 
 template <typename TO>

@@ -174,14 +174,22 @@ template <int BM, int BR, int NS, typename TY>
 __global__ __launch_bounds__(256, 2) void gemm_lds_k(const half_t* __restrict__ x, const half_t* __restrict__ w,
                                                      const float* __restrict__ bias, TY* __restrict__ y, int64_t R,
                                                      int K, int M, int epi, const float* __restrict__ gate,
-                                                     int64_t ld_gate, int64_t gate_rows) {
+                                                     int64_t ld_gate, int64_t gate_rows, int nr, int nm, int per_xcd,
+                                                     int mfast) {
   static_assert((BM == 64 || BM == 128) && (BR == 64 || BR == 128) && NS >= 2, "tile / stages");
   constexpr int BK = 64, ROWB = 128, ROWS = BM + BR, STAGE = ROWS * ROWB;
   constexpr int LPW = ROWS / 32;             // load instructions per wave per stage (8 rows each, 4 waves)
   constexpr int MB = BM / 64, RB = BR / 64;  // 32 x 32 MFMA blocks per wave along m and r
   __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE];
-  const int64_t r0 = (int64_t)blockIdx.x * BR;
-  const int m0 = blockIdx.y * BM;
+  // The nr x nm tiles are dealt to the 8 XCDs in contiguous ranges (the dispatcher sends workgroup b to XCD b % 8),
+  // enumerated with the W tile fastest (mfast: an XCD's range holds a few x row tiles against all of W) or the x
+  // tile fastest (a slice of W against all of x); the launcher picks the order whose per-XCD operand bytes are
+  // fewer, so that they stay in the XCD's L2.
+  const int u = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+  if (u >= nr * nm) return;  // whole workgroup
+  const int rt = mfast ? u / nm : u % nr, mt = mfast ? u % nm : u / nr;
+  const int64_t r0 = (int64_t)rt * BR;
+  const int m0 = mt * BM;
   const int t = threadIdx.x, l = t & 63, rr = l & 31, hh = l >> 5;
   const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int wm = wave >> 1, wr = wave & 1;  // wave tile: m = BM / 2 wm .., r = BR / 2 wr ..
@@ -324,12 +332,16 @@ __global__ __launch_bounds__(256, 2) void gemm_lds_k(const half_t* __restrict__ 
 // (NP MFMA blocks of 32 x 32), and each lane ends with the NP values of 4 x 4 outputs of one row.
 template <int NP>
 __global__ __launch_bounds__(256, 2) void gemm_swiglu_f16_k(const half_t* __restrict__ x, const half_t* __restrict__ w,
-                                                           half_t* __restrict__ u, int64_t R, int K, int H) {
+                                                           half_t* __restrict__ u, int64_t R, int K, int H, int nr,
+                                                           int nq, int per_xcd, int qfast) {
   constexpr int BM = 32 * NP, BR = 128, BK = 64, LDT = BK + 8, LA = BM / 32, LB = BR / 32;
   __shared__ LDS_ALIGN half_t As[2][BM * LDT];
   __shared__ LDS_ALIGN half_t Bs[2][BR * LDT];
-  const int64_t r0 = (int64_t)blockIdx.x * BR;
-  const int q = blockIdx.y;  // output columns 32 q .. 32 q + 31
+  // tiles dealt to the XCDs in contiguous ranges, in the order the launcher picks (as gemm_lds_k)
+  const int un = (int)(blockIdx.x % 8) * per_xcd + (int)(blockIdx.x / 8);
+  if (un >= nr * nq) return;  // whole workgroup
+  const int64_t r0 = (int64_t)(qfast ? un / nq : un % nr) * BR;
+  const int q = qfast ? un % nq : un / nr;  // output columns 32 q .. 32 q + 31
   const int t = threadIdx.x, wave = t >> 6, l = t & 63, rr = l & 31, hh = l >> 5;
   constexpr int RSRC_CFG = 0x00020000;
   const int64_t xrows = R - r0 < BR ? R - r0 : BR;
@@ -434,15 +446,22 @@ hipError_t gemm_t(const void* x, const void* w, const float* bias, void* y, int 
 template <int BM, int BR, int NS>
 hipError_t gemm_lds_t(const void* x, const void* w, const float* bias, void* y, int y_dt, int64_t R, int K, int M,
                       int epi, const float* gate, int64_t ld_gate, int64_t gate_rows, hipStream_t st) {
-  const dim3 grid((unsigned)((R + BR - 1) / BR), (unsigned)((M + BM - 1) / BM));
+  const int64_t nr = (R + BR - 1) / BR, nm = (M + BM - 1) / BM;
+  if (nr * nm >= (1LL << 31) - 8) return hipErrorInvalidValue;
+  const int per_xcd = (int)((nr * nm + 7) / 8);
+  // operand bytes one XCD reads: W tile fastest, R / 8 rows of x and all of W; x tile fastest, all of x and M / 8
+  // rows of W
+  const int64_t xb = R * K * 2, wb = (int64_t)M * K * 2;
+  const int mfast = xb / 8 + wb <= xb + wb / 8;
+  const dim3 grid((unsigned)(8 * per_xcd));
   if (y_dt == DT_F16)
     gemm_lds_k<BM, BR, NS, half_t><<<grid, 256, 0, st>>>(static_cast<const half_t*>(x), static_cast<const half_t*>(w),
                                                          bias, static_cast<half_t*>(y), R, K, M, epi, gate, ld_gate,
-                                                         gate_rows);
+                                                         gate_rows, (int)nr, (int)nm, per_xcd, mfast);
   else
     gemm_lds_k<BM, BR, NS, float><<<grid, 256, 0, st>>>(static_cast<const half_t*>(x), static_cast<const half_t*>(w),
                                                         bias, static_cast<float*>(y), R, K, M, epi, gate, ld_gate,
-                                                        gate_rows);
+                                                        gate_rows, (int)nr, (int)nm, per_xcd, mfast);
   return hipGetLastError();
 }
 
@@ -464,13 +483,18 @@ hipError_t launch_gemm_swiglu_f16(const void* x, const void* w, void* u, int64_t
   if (R < 1 || K % 64 || K < 64 || H % 32 || H < 32 || (int64_t)128 * K * 2 > 0x7fffffffLL || !al(x, 16) ||
       !al(w, 16) || !al(u, 8) || (R + 127) / 128 > 0x7fffffffLL || (np != 2 && np != 3))
     return hipErrorInvalidValue;
-  const dim3 grid((unsigned)((R + 127) / 128), (unsigned)(H / 32));
+  const int64_t nr = (R + 127) / 128, nq = H / 32;
+  if (nr * nq >= (1LL << 31) - 8) return hipErrorInvalidValue;
+  const int per_xcd = (int)((nr * nq + 7) / 8);
+  const int64_t xb = R * K * 2, wb = (int64_t)np * H * K * 2;
+  const int qfast = xb / 8 + wb <= xb + wb / 8;
+  const dim3 grid((unsigned)(8 * per_xcd));
   if (np == 3)
     gemm_swiglu_f16_k<3><<<grid, 256, 0, st>>>(static_cast<const half_t*>(x), static_cast<const half_t*>(w),
-                                               static_cast<half_t*>(u), R, K, H);
+                                               static_cast<half_t*>(u), R, K, H, (int)nr, (int)nq, per_xcd, qfast);
   else
     gemm_swiglu_f16_k<2><<<grid, 256, 0, st>>>(static_cast<const half_t*>(x), static_cast<const half_t*>(w),
-                                               static_cast<half_t*>(u), R, K, H);
+                                               static_cast<half_t*>(u), R, K, H, (int)nr, (int)nq, per_xcd, qfast);
   return hipGetLastError();
 }
 

@@ -170,13 +170,16 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_k(const TX* __restrict__ x, co
 // fragment reads (16 lanes on 16 consecutive rows at one logical chunk) hit distinct banks.
 __device__ __forceinline__ int gl_swz(int row) { return (row & 7) ^ ((row >> 3) & 1); }
 
-template <int BM, int BR, int NS, typename TY>
-__global__ __launch_bounds__(256, 2) void gemm_lds_k(const half_t* __restrict__ x, const half_t* __restrict__ w,
+// SW = 2 or 3: the gated-product epilogue of gemm_swiglu_f16_k on the same tiles (BM = 64 SW, so each wave's BM / 2
+// W rows are one group [W_0; W_1 (; W_2)] of 32 output columns); y is then the fp16 u [R][M / SW].
+template <int BM, int BR, int NS, typename TY, int SW = 0>
+__global__ __launch_bounds__(256, BM * BR > 128 * 64 ? 1 : 2) void gemm_lds_k(const half_t* __restrict__ x, const half_t* __restrict__ w,
                                                      const float* __restrict__ bias, TY* __restrict__ y, int64_t R,
                                                      int K, int M, int epi, const float* __restrict__ gate,
                                                      int64_t ld_gate, int64_t gate_rows, int nr, int nm, int per_xcd,
                                                      int mfast) {
-  static_assert((BM == 64 || BM == 128) && (BR == 64 || BR == 128) && NS >= 2, "tile / stages");
+  static_assert((BM == 64 || BM == 128 || BM == 192) && (BR == 64 || BR == 128) && NS >= 2, "tile / stages");
+  static_assert(SW == 0 || (BM == 64 * SW && sizeof(TY) == 2), "gated product: one 32-column group per wave");
   constexpr int BK = 64, ROWB = 128, ROWS = BM + BR, STAGE = ROWS * ROWB;
   constexpr int LPW = ROWS / 32;             // load instructions per wave per stage (8 rows each, 4 waves)
   constexpr int MB = BM / 64, RB = BR / 64;  // 32 x 32 MFMA blocks per wave along m and r
@@ -242,8 +245,10 @@ __global__ __launch_bounds__(256, 2) void gemm_lds_k(const half_t* __restrict__ 
   // latency overlaps the loop instead of following the last stage (for the 768-wide gated outputs the epilogue is a
   // 12 MB read-modify-write). They are issued ahead of the stage loads: the loop's vmcnt waits count loads in issue
   // order, so these complete by the first stage's wait and never hold back a later one.
+  // (tiles of up to two MFMA blocks per wave: larger ones would hold too many registers through the loop)
+  constexpr bool PRE = sizeof(TY) == 4 && MB * RB <= 2;
   f4 ypre[RB][MB][4], gpre[RB][MB][4];
-  if constexpr (sizeof(TY) == 4) {
+  if constexpr (PRE) {
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) {
       const int64_t r = r0 + BR / 2 * wr + 32 * rb + rr;
@@ -294,6 +299,29 @@ __global__ __launch_bounds__(256, 2) void gemm_lds_k(const half_t* __restrict__ 
     }
   }
   __builtin_amdgcn_s_waitcnt(0);  // the reloads past the last stage land before the workgroup's LDS is released
+  if constexpr (SW != 0) {
+    // gated product: the wave's blocks mb hold product mb of columns 32 grp .. + 31, grp = (m0 + BM / 2 wm) / 32 SW;
+    // lane (rr, hh) holds columns 32 grp + 8 q + 4 hh .. + 3 in elements 4 q .. 4 q + 3 (gemm_swiglu_f16_k's order)
+    const int H = M / SW, grp = (m0 + BM / 2 * wm) / (32 * SW);
+    if (32 * grp >= H) return;
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) {
+      const int64_t r = r0 + BR / 2 * wr + 32 * rb + rr;
+      if (r >= R) continue;
+#pragma unroll
+      for (int q = 0; q < 4; q++) {
+        half4 o;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+          float val = siluf_(acc[0][rb][4 * q + e]) * acc[1][rb][4 * q + e];
+          if constexpr (SW == 3) val *= acc[2][rb][4 * q + e];
+          o[e] = (half_t)val;
+        }
+        *reinterpret_cast<half4*>(y + r * H + 32 * grp + 8 * q + 4 * hh) = o;
+      }
+    }
+    return;
+  }
   // epilogue: lane (rr, hh) of block (mb, rb) holds y[r][m .. m + 3] for r = BR / 2 wr + 32 rb + rr and
   // m = BM / 2 wm + 32 mb + 8 q + 4 hh, q < 4
 #pragma unroll
@@ -311,11 +339,11 @@ __global__ __launch_bounds__(256, 2) void gemm_lds_k(const half_t* __restrict__ 
         TY* yp = y + r * M + m;
         if constexpr (sizeof(TY) == 4) {  // epi 1 and 2 (fp32 y only)
           if (epi == 2) {
-            const f4 gv = gpre[rb][mb][q];
+            const f4 gv = PRE ? gpre[rb][mb][q] : *reinterpret_cast<const f4*>(gate + (r % gate_rows) * ld_gate + m);
             v4 = f4{v4[0] * sigmoidf_(gv[0]), v4[1] * sigmoidf_(gv[1]), v4[2] * sigmoidf_(gv[2]),
                     v4[3] * sigmoidf_(gv[3])};
           }
-          if (epi >= 1) v4 += ypre[rb][mb][q];
+          if (epi >= 1) v4 += PRE ? ypre[rb][mb][q] : *reinterpret_cast<const f4*>(yp);
           *reinterpret_cast<f4*>(yp) = v4;
         } else {
           *reinterpret_cast<half4*>(yp) = half4{(half_t)v4[0], (half_t)v4[1], (half_t)v4[2], (half_t)v4[3]};
@@ -447,7 +475,7 @@ template <int BM, int BR, int NS>
 hipError_t gemm_lds_t(const void* x, const void* w, const float* bias, void* y, int y_dt, int64_t R, int K, int M,
                       int epi, const float* gate, int64_t ld_gate, int64_t gate_rows, hipStream_t st) {
   const int64_t nr = (R + BR - 1) / BR, nm = (M + BM - 1) / BM;
-  if (nr * nm >= (1LL << 31) - 8) return hipErrorInvalidValue;
+  if (nr * nm >= (1LL << 31) - 8 || (int64_t)(BM > BR ? BM : BR) * K * 2 > 0x7fffffffLL) return hipErrorInvalidValue;
   const int per_xcd = (int)((nr * nm + 7) / 8);
   // operand bytes one XCD reads: W tile fastest, R / 8 rows of x and all of W; x tile fastest, all of x and M / 8
   // rows of W
@@ -483,10 +511,27 @@ hipError_t launch_gemm_swiglu_f16(const void* x, const void* w, void* u, int64_t
   if (R < 1 || K % 64 || K < 64 || H % 32 || H < 32 || (int64_t)128 * K * 2 > 0x7fffffffLL || !al(x, 16) ||
       !al(w, 16) || !al(u, 8) || (R + 127) / 128 > 0x7fffffffLL || (np != 2 && np != 3))
     return hipErrorInvalidValue;
+  const int64_t xb = R * K * 2, wb = (int64_t)np * H * K * 2;
+  // 2048 rows and more, H a multiple of 64: the LDS-direct tiles (64 np W rows = two column groups x 128 rows, two
+  // stages, two workgroups per CU; the diffusion transformer's 2000 x 768 -> 3 x 1536 in one round of 384 tiles)
+  if (R >= 1536 && H % 64 == 0) {
+    const int64_t nr = (R + 127) / 128, nm = H / 64;
+    if (nr * nm >= (1LL << 31) - 8 || (int64_t)64 * np * K * 2 > 0x7fffffffLL) return hipErrorInvalidValue;
+    const int per_xcd = (int)((nr * nm + 7) / 8), mfast = xb / 8 + wb <= xb + wb / 8;
+    const dim3 grid((unsigned)(8 * per_xcd));
+    if (np == 3)
+      gemm_lds_k<192, 128, 2, half_t, 3><<<grid, 256, 0, st>>>(
+          static_cast<const half_t*>(x), static_cast<const half_t*>(w), nullptr, static_cast<half_t*>(u), R, K, 3 * H,
+          0, nullptr, 0, 1, (int)nr, (int)nm, per_xcd, mfast);
+    else
+      gemm_lds_k<128, 128, 2, half_t, 2><<<grid, 256, 0, st>>>(
+          static_cast<const half_t*>(x), static_cast<const half_t*>(w), nullptr, static_cast<half_t*>(u), R, K, 2 * H,
+          0, nullptr, 0, 1, (int)nr, (int)nm, per_xcd, mfast);
+    return hipGetLastError();
+  }
   const int64_t nr = (R + 127) / 128, nq = H / 32;
   if (nr * nq >= (1LL << 31) - 8) return hipErrorInvalidValue;
   const int per_xcd = (int)((nr * nq + 7) / 8);
-  const int64_t xb = R * K * 2, wb = (int64_t)np * H * K * 2;
   const int qfast = xb / 8 + wb <= xb + wb / 8;
   const dim3 grid((unsigned)(8 * per_xcd));
   if (np == 3)
@@ -521,7 +566,7 @@ hipError_t launch_gemm_nt(const void* x, const void* w, const float* bias, void*
   // (N rows) keep the register-staged form: they run beside the attention core, and there the LDS-direct form's
   // workgroups found compute units far later (0.85 ms against 0.04 ms per launch at N = 1000).
   if (gemm_tile_choice(R, M) != 0 && R >= 1536)
-    return M >= 2048 ? gemm_lds_t<128, 64, 3>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st)
+    return M >= 2048 ? gemm_lds_t<192, 128, 3>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st)
                      : gemm_lds_t<64, 64, 3>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st);
   switch (gemm_tile_choice(R, M)) {
     case 0: return gemm_t<128, 128, half_t>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st);

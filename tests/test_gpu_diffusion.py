@@ -361,6 +361,68 @@ def test_step_graph_replays_equal_eager(precision):
         _ = (torch.randn(1000, device="cuda") * 2).sum().item()  # unrelated eager work between replays
 
 
+@pytest.mark.parametrize("R,Kd,M", [(1537, 64, 132), (1600, 192, 2052), (2000, 768, 3072), (2100, 768, 772)])
+def test_gemm_lds_direct_paths(R, Kd, M):
+    """The LDS-direct GEMM (1536+ rows: 64 x 64 tiles, 192 x 128 for 2048+ output columns; tiles dealt to the XCDs
+    in contiguous ranges, ragged tile counts) in all four epilogues against float64, and bit for bit against the
+    register-staged kernel on the first 100 rows (same k order per element)."""
+    from boltz_mlx_amd import kernels as K
+
+    rng = np.random.default_rng(R + Kd + M)
+    x = dev(rng.standard_normal((R, Kd)), torch.float16)
+    w = dev(rng.standard_normal((M, Kd)) / np.sqrt(Kd), torch.float16)
+    b = dev(rng.standard_normal(M))
+    gate = rng.standard_normal((400, M))
+    y0 = rng.standard_normal((R, M))
+    y16 = K.linear(x, w, bias=b, out_dtype=torch.float16)
+    y32 = K.linear(x, w, bias=b, out_dtype=torch.float32)
+    yacc = dev(y0)
+    K.linear(x, w, bias=b, out=yacc, accumulate=True)
+    ygat = dev(y0)
+    K.linear_gated(x, w, dev(gate), ygat, bias=b)
+    small16 = K.linear(x[:100].contiguous(), w, bias=b, out_dtype=torch.float16)
+    small32 = K.linear(x[:100].contiguous(), w, bias=b, out_dtype=torch.float32)
+    sgat = dev(y0[:100])
+    K.linear_gated(x[:100].contiguous(), w, dev(gate), sgat, bias=b)
+    torch.cuda.synchronize()
+    assert torch.equal(y16[:100], small16) and torch.equal(y32[:100], small32) and torch.equal(ygat[:100], sgat)
+    rows = np.r_[0:64, R - 70:R]  # the first tile and the ragged last ones
+    ref = x[rows].double().cpu().numpy() @ w.double().cpu().numpy().T + b.double().cpu().numpy()
+    assert O.metrics(y16[rows].double().cpu().numpy(), ref)["max_rel"] <= 2e-3
+    assert O.metrics(y32[rows].cpu().numpy(), ref)["max_rel"] <= 1e-5
+    assert O.metrics(yacc[rows].cpu().numpy(), y0[rows] + ref)["max_rel"] <= 1e-5
+    sig = OD.sigmoid(gate[rows % 400])
+    assert O.metrics(ygat[rows].cpu().numpy(), y0[rows] + sig * ref)["max_rel"] <= 1e-5
+
+
+@pytest.mark.parametrize("np_,R,Kd,H", [(3, 1600, 768, 1536), (3, 1537, 64, 64), (2, 2000, 192, 256),
+                                        (2, 1600, 128, 96)])
+def test_linear_swiglu_lds_direct(np_, R, Kd, H):
+    """The gated product as the LDS-direct GEMM's epilogue (1536+ rows, H a multiple of 64; H = 96 keeps the
+    register-staged kernel) against float64, and bit for bit against the register-staged kernel on 100 rows."""
+    from boltz_mlx_amd import kernels as K
+
+    rng = np.random.default_rng(np_ * R + H)
+    x = dev(rng.standard_normal((R, Kd)), torch.float16)
+    w = dev(rng.standard_normal((np_ * H, Kd)) / np.sqrt(Kd), torch.float16)
+    if np_ == 3:
+        wg = K.group_swiglu3_rows(w[:H], w[H:2 * H], w[2 * H:])
+        run = K.linear_swiglu3
+    else:
+        wg = K.group_swiglu_rows(w[:H], w[H:])
+        run = K.linear_swiglu
+    fused = run(x, wg)
+    small = run(x[:100].contiguous(), wg)
+    torch.cuda.synchronize()
+    assert torch.equal(fused[:100], small)
+    rows = np.r_[0:40, R - 40:R]
+    h = x[rows].double().cpu().numpy() @ w.double().cpu().numpy().T
+    ref = OD.silu(h[:, :H]) * h[:, H:2 * H]
+    if np_ == 3:
+        ref = ref * h[:, 2 * H:]
+    assert O.metrics(fused[rows].double().cpu().numpy(), ref)["max_rel"] <= 2e-3
+
+
 @pytest.mark.parametrize("R,Kd,H", [(70, 64, 32), (300, 768, 1536), (129, 192, 96)])
 def test_linear_swiglu3_fused(R, Kd, H):
     """The fused feed-forward GEMM (gated product in the epilogue, grouped weight rows) against float64 on the same

@@ -185,10 +185,12 @@ class PairformerModule(torch.nn.Module):
         layer's norm_in(z) for B = 1 (the carry; None after the last layer unless cycle).
 
         The z updates of layer i + 1 read only z, so the s track of layer i (attention with the pair bias of layer
-        i's z, then transition_s) runs on a second stream, overlapped with the pair kernels of layer i + 1: its
-        attention half is released when layer i + 1's starting-node attention core starts and its transition half
-        when the ending-node core starts, so it shares the GPU with those two (non-persistent) kernels rather than
-        with the persistent row kernels, whose grids assume the whole GPU. The pair bias is computed on the main
+        i's z, then transition_s) runs on a second stream beside the pair kernels of layer i + 1: its attention half
+        is released when layer i + 1's starting-node attention core starts and its transition half when the
+        ending-node core starts, so it shares the GPU with those two (non-persistent) kernels rather than with the
+        persistent row kernels, whose grids assume the whole GPU. (Measured at N = 400 and 1000, this takes the same
+        block time as running the same kernels in series at those points: the s track's cost is its chain of small
+        kernels, not the lack of overlap.) The pair bias is computed on the main
         stream (by the transition's epilogue) before z moves on; the main stream waits for the side stream once at
         the end. (The reference
         pipelines the same way by submitting layer i + 1 while layer i's tail runs, pairformer.py:145-148.)"""

@@ -62,7 +62,7 @@ __device__ __forceinline__ float halves_sum(float v) {
   return __uint_as_float(a[0]) + __uint_as_float(a[1]);
 }
 
-template <int C>
+template <int C, bool GPRE>
 __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __restrict__ qkg,
                                                             const half_t* __restrict__ vt,
                                                             const half_t* __restrict__ tb,
@@ -221,8 +221,14 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
   prefetch_bias(0);
   __builtin_amdgcn_sched_barrier(0);
 
+  half4 gpre[4];  // GPRE: the output gates, loaded during the last key block
   for (int kb = 0; kb < nblk; kb++) {
     const int k0 = kb * BK, buf = kb & 1;
+    if (GPRE && kb == nblk - 1) {
+      const int jc = jq < N ? jq : N - 1;
+#pragma unroll
+      for (int q = 0; q < 4; q++) gpre[q] = *reinterpret_cast<const half4*>(gp + (int64_t)jc * C + 8 * q + 4 * hl);
+    }
     half_t* Kb = Ks[buf];
     half_t* Vb = Vs[buf];
     *reinterpret_cast<half8*>(Kb + skey * LDK + sd8) = kreg;
@@ -340,7 +346,7 @@ __global__ __launch_bounds__(256, 3) void triattn_core_mfma(const half_t* __rest
 #pragma unroll
   for (int q = 0; q < 4; q++) {
     const int d0 = 8 * q + 4 * hl;
-    const half4 gv = *reinterpret_cast<const half4*>(gp + (int64_t)jq * C + d0);
+    const half4 gv = GPRE ? gpre[q] : *reinterpret_cast<const half4*>(gp + (int64_t)jq * C + d0);
     half4 ov;
 #pragma unroll
     for (int e = 0; e < 4; e++) ov[e] = (half_t)(oacc[4 * q + e] * inv * sigmoidf_((float)gv[e]));
@@ -358,9 +364,14 @@ hipError_t launch_triattn_core_f16_mfma(const void* qkg, const void* vt, const v
   const int64_t units = (int64_t)H * N * ((N + 127) / 128);
   const int64_t per_xcd = (units + NXCD - 1) / NXCD;
   const dim3 grid((unsigned)(per_xcd * NXCD));
-  triattn_core_mfma<32><<<grid, 256, 0, st>>>(static_cast<const half_t*>(qkg), static_cast<const half_t*>(vt),
-                                              static_cast<const half_t*>(tb), mask, mask_si, mask_sk, inf,
-                                              static_cast<half_t*>(out), (int)N, (int)ldk, H, units, per_xcd);
+  if (N <= 512)
+    triattn_core_mfma<32, true><<<grid, 256, 0, st>>>(static_cast<const half_t*>(qkg), static_cast<const half_t*>(vt),
+                                                      static_cast<const half_t*>(tb), mask, mask_si, mask_sk, inf,
+                                                      static_cast<half_t*>(out), (int)N, (int)ldk, H, units, per_xcd);
+  else
+    triattn_core_mfma<32, false><<<grid, 256, 0, st>>>(static_cast<const half_t*>(qkg), static_cast<const half_t*>(vt),
+                                                       static_cast<const half_t*>(tb), mask, mask_si, mask_sk, inf,
+                                                       static_cast<half_t*>(out), (int)N, (int)ldk, H, units, per_xcd);
   return hipGetLastError();
 }
 

@@ -1,5 +1,5 @@
-// MSA-block pair kernels (fp32 operands and MFMA accumulation, the reference's numerics policy for the reductions
-// over MSA rows and tokens):
+// MSA-block pair kernels (fp32 operands and fp32-accurate reductions, the reference's numerics policy for the
+// reductions over MSA rows and tokens):
 //   opm_outer   : z[(i - i_base) N + j][c 32 + d] = sum_s mask[s][i] mask[s][j] a[s][i][c] b[s][j][d] / max(num, 1)
 //                 with num[i][j] = sum_s mask[s][i] mask[s][j] given (mask^T mask, one small GEMM) and
 //                 a | b = ab[s][i][0:32] | ab[s][j][32:64]
@@ -9,9 +9,6 @@
 //                 to ldw (boltz_mlx/layers/pair_averaging.py:43-49, kernels_msa.py:461-500);
 //   pwa_avg     : out[s][i][h 32 + d] = sigmoid(g[s][i][h 32 + d]) * sum_j w[h][i][j] v[s][j][h 32 + d]
 //                 (pair_averaging.py:50-57, kernels_msa.py:620-653).
-// The outer sum runs on v_mfma_f32_16x16x4f32 (lane l holds A[l % 16][k0 + l / 16] and B[l % 16][k0 + l / 16];
-// the accumulator holds D[4 (l / 16) + e][l % 16]) with a 128 x 128 tile per 256-thread workgroup, 4 waves of
-// 64 x 64, K stages of 16 double-buffered in LDS and the next stage's loads in flight during the current one.
 #include "bzpf_common.h"
 #include "bzpf_kernels.h"
 
@@ -19,91 +16,164 @@ namespace bzpf {
 
 namespace {
 
-constexpr int MBK = 16;  // K (MSA rows s for the outer sum, tokens j for the average) per stage
+// Both reductions run on the bf16 matrix cores at fp32 accuracy. Each fp32 operand value is split exactly into three
+// bf16 parts, x = x1 + x2 + x3 (x1 the round-to-nearest-even of x, x2 of x - x1, x3 = x - x1 - x2: 8 significant
+// bits each, 24 together), and a product is taken as the six part products x_a y_b with a + b <= 4, accumulated in
+// fp32 by v_mfma_f32_32x32x16_bf16 (exact bf16 products, fp32 sums); the three left out (x2 y3, x3 y2, x3 y3) are
+// below 2^-23 of |x y| together. That is the fp32 matrix cores' accuracy at 6 / 16 of their time (the bf16 rate is
+// 16 times the fp32 one). A 256-thread workgroup computes a 128 x 128 tile, 4 waves of 64 x 64 (2 x 2 blocks of
+// 32 x 32), over K stages of 16 (one MFMA K-step): the loads of stages st + 1 and st + 2 are in registers while stage
+// st computes; each stage is then split into its parts and stored as three K-contiguous planes per operand (LDS
+// double-buffered, one barrier per stage, two workgroups per CU).
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+
+struct Parts3 {
+  __bf16 p[3];
+};
+__device__ __forceinline__ Parts3 split3(float x) {
+  Parts3 o;
+  o.p[0] = (__bf16)x;
+  const float r1 = x - (float)o.p[0];  // exact
+  o.p[1] = (__bf16)r1;
+  o.p[2] = (__bf16)(r1 - (float)o.p[1]);  // exact: at most 8 significant bits are left
+  return o;
+}
+
+// LDS plane layout shared by the two kernels: 128 rows (A rows or B columns) of KS = 16 bf16 at a pitch of 24.
+constexpr int KS = 16, LDP = KS + 8, PLANE = 128 * LDP;
+
+// The six part products of one 32 x 32 block for one K-step (smaller ones first).
+__device__ __forceinline__ f16x mfma_parts6(const bf16x8 (&a)[3], const bf16x8 (&b)[3], f16x c) {
+  c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], c, 0, 0, 0);
+  c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], c, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], c, 0, 0, 0);
+}
+
+// One stage of a wave's 2 x 2 blocks: fragments of the three planes of A rows 64 wm + 32 bm + r32 and B rows
+// 64 wn + 32 bn + r32, k = 8 hl .. 8 hl + 7 (lane (r32, hl)).
+__device__ __forceinline__ void parts_stage(const __bf16* Ab, const __bf16* Bb, int wm, int wn, int r32, int hl,
+                                            f16x (&acc)[2][2]) {
+  bf16x8 fa[2][3], fb[2][3];
+#pragma unroll
+  for (int bm = 0; bm < 2; bm++)
+#pragma unroll
+    for (int p = 0; p < 3; p++)
+      fa[bm][p] = *reinterpret_cast<const bf16x8*>(Ab + p * PLANE + (64 * wm + 32 * bm + r32) * LDP + 8 * hl);
+#pragma unroll
+  for (int bn = 0; bn < 2; bn++)
+#pragma unroll
+    for (int p = 0; p < 3; p++)
+      fb[bn][p] = *reinterpret_cast<const bf16x8*>(Bb + p * PLANE + (64 * wn + 32 * bn + r32) * LDP + 8 * hl);
+#pragma unroll
+  for (int bm = 0; bm < 2; bm++)
+#pragma unroll
+    for (int bn = 0; bn < 2; bn++) acc[bm][bn] = mfma_parts6(fa[bm], fb[bn], acc[bm][bn]);
+}
 
 // ---------------------------------------------------------------- outer product mean
-// Workgroup tile: tokens i0 .. i0 + 3 (A rows (i, c)) x j0 .. j0 + 3 (B columns (j, d)). LDS holds each stage
-// K-major (As[s][i 32 + c]), the layout the loads arrive in.
+// Workgroup tile: tokens i0 .. i0 + 3 (A rows (i, c) = 32 (i - i0) + c) x j0 .. j0 + 3 (B columns (j, d)), K = MSA
+// rows s. Both operands arrive channel-contiguous per (s, token); a thread takes MSA rows 2 p and 2 p + 1 of the
+// stage, one token (the wave's) and 4 channels, multiplies by the mask, splits, and stores each channel's pair of
+// parts as one dword of the K-contiguous planes (a store's 64 lanes: 8 MSA-row pairs x 8 channel quads).
 template <typename TO>
 __global__ __launch_bounds__(256, 2) void opm_outer_k(const float* __restrict__ ab, int64_t ld_ab,
                                                       const float* __restrict__ mask, const float* __restrict__ num,
                                                       TO* __restrict__ out, int S, int N, int i_base, int n_i) {
-  constexpr int LD = 128 + 16;
-  __shared__ LDS_ALIGN float As[2][MBK * LD];
-  __shared__ LDS_ALIGN float Bs[2][MBK * LD];
-  const int t = threadIdx.x, wave = t >> 6, l = t & 63;
+  __shared__ LDS_ALIGN __bf16 As[2][3 * PLANE];
+  __shared__ LDS_ALIGN __bf16 Bs[2][3 * PLANE];
+  const int t = threadIdx.x, wave = t >> 6, l = t & 63, r32 = l & 31, hl = l >> 5;
   const int wm = wave >> 1, wn = wave & 1;
   const int i0 = i_base + 4 * (int)blockIdx.y, j0 = 4 * (int)blockIdx.x;
   const int i_end = min(i_base + n_i, N);
-  // vector v of thread t: e = t + 256 v, MSA row s = e / 32, token e / 8 % 4, columns 4 (e % 8) .. + 3
-  f4 ra[2], rb[2];
-  float ma[2], mb_[2];
-  auto gload = [&](int stage) {
+  // staging item: MSA rows 2 sp, 2 sp + 1 of the stage, token tk (= the wave), channels 4 sq .. + 3. Tokens past the
+  // range read the last one (their outputs are not stored); MSA rows past S read row S - 1 with mask 0.
+  const int sp = t & 7, sq = (t >> 3) & 7, tk = wave;
+  const int ia = min(i0 + tk, i_end - 1), jb = min(j0 + tk, N - 1);
+  f4 ra0[2], rb0[2], ra1[2], rb1[2];
+  float ma0[2], mb0[2], ma1[2], mb1[2];
+  auto gload = [&](f4 (&ra)[2], f4 (&rb)[2], float (&ma)[2], float (&mb)[2], int stage) {
 #pragma unroll
-    for (int v = 0; v < 2; v++) {
-      const int e = t + 256 * v, s = stage * MBK + (e >> 5), tk = (e >> 3) & 3, q = e & 7;
-      const bool va = s < S && i0 + tk < i_end, vb = s < S && j0 + tk < N;
-      ma[v] = va ? mask[(int64_t)s * N + i0 + tk] : 0.0f;
-      mb_[v] = vb ? mask[(int64_t)s * N + j0 + tk] : 0.0f;
-      ra[v] = va ? *reinterpret_cast<const f4*>(ab + ((int64_t)s * N + i0 + tk) * ld_ab + 4 * q) : f4{0, 0, 0, 0};
-      rb[v] = vb ? *reinterpret_cast<const f4*>(ab + ((int64_t)s * N + j0 + tk) * ld_ab + 32 + 4 * q)
-                 : f4{0, 0, 0, 0};
+    for (int b = 0; b < 2; b++) {
+      const int s = stage * KS + 2 * sp + b, sc = min(s, S - 1);
+      ra[b] = *reinterpret_cast<const f4*>(ab + ((int64_t)sc * N + ia) * ld_ab + 4 * sq);
+      rb[b] = *reinterpret_cast<const f4*>(ab + ((int64_t)sc * N + jb) * ld_ab + 32 + 4 * sq);
+      ma[b] = s < S ? mask[(int64_t)sc * N + ia] : 0.0f;
+      mb[b] = s < S ? mask[(int64_t)sc * N + jb] : 0.0f;
     }
   };
-  auto lstore = [&](int buf) {
+  auto lstore = [&](const f4 (&ra)[2], const f4 (&rb)[2], const float (&ma)[2], const float (&mb)[2], int buf) {
 #pragma unroll
-    for (int v = 0; v < 2; v++) {
-      const int e = t + 256 * v, s = e >> 5, tk = (e >> 3) & 3, q = e & 7;
-      *reinterpret_cast<f4*>(As[buf] + s * LD + 32 * tk + 4 * q) = ra[v] * ma[v];
-      *reinterpret_cast<f4*>(Bs[buf] + s * LD + 32 * tk + 4 * q) = rb[v] * mb_[v];
+    for (int e = 0; e < 4; e++) {
+      const int row = 32 * tk + 4 * sq + e;
+      {
+        const Parts3 x0 = split3(ra[0][e] * ma[0]), x1 = split3(ra[1][e] * ma[1]);
+        __bf16* dst = As[buf] + row * LDP + 2 * sp;
+        *reinterpret_cast<bf16x2*>(dst) = bf16x2{x0.p[0], x1.p[0]};
+        *reinterpret_cast<bf16x2*>(dst + PLANE) = bf16x2{x0.p[1], x1.p[1]};
+        *reinterpret_cast<bf16x2*>(dst + 2 * PLANE) = bf16x2{x0.p[2], x1.p[2]};
+      }
+      {
+        const Parts3 x0 = split3(rb[0][e] * mb[0]), x1 = split3(rb[1][e] * mb[1]);
+        __bf16* dst = Bs[buf] + row * LDP + 2 * sp;
+        *reinterpret_cast<bf16x2*>(dst) = bf16x2{x0.p[0], x1.p[0]};
+        *reinterpret_cast<bf16x2*>(dst + PLANE) = bf16x2{x0.p[1], x1.p[1]};
+        *reinterpret_cast<bf16x2*>(dst + 2 * PLANE) = bf16x2{x0.p[2], x1.p[2]};
+      }
     }
   };
-  f4 acc[4][4];
+  f16x acc[2][2];
 #pragma unroll
-  for (int a = 0; a < 4; a++)
+  for (int a = 0; a < 2; a++)
 #pragma unroll
-    for (int b = 0; b < 4; b++) acc[a][b] = f4{0.f, 0.f, 0.f, 0.f};
-  auto compute = [&](int buf) {
-    const float* Ab = As[buf] + (l >> 4) * LD + 64 * wm + (l & 15);
-    const float* Bb = Bs[buf] + (l >> 4) * LD + 64 * wn + (l & 15);
+    for (int b = 0; b < 2; b++)
 #pragma unroll
-    for (int kk = 0; kk < MBK / 4; kk++) {
-      float fa[4], fb[4];
-#pragma unroll
-      for (int q = 0; q < 4; q++) fa[q] = Ab[4 * kk * LD + 16 * q];
-#pragma unroll
-      for (int q = 0; q < 4; q++) fb[q] = Bb[4 * kk * LD + 16 * q];
-#pragma unroll
-      for (int a = 0; a < 4; a++)
-#pragma unroll
-        for (int b = 0; b < 4; b++) acc[a][b] = __builtin_amdgcn_mfma_f32_16x16x4f32(fa[a], fb[b], acc[a][b], 0, 0, 0);
-    }
-  };
-  const int nst = (S + MBK - 1) / MBK;
-  gload(0);
-  lstore(0);
+      for (int e = 0; e < 16; e++) acc[a][b][e] = 0.0f;
+  const int nst = (S + KS - 1) / KS;
+  gload(ra0, rb0, ma0, mb0, 0);
+  lstore(ra0, rb0, ma0, mb0, 0);
   __syncthreads();
-  for (int st = 0; st < nst; st++) {
-    if (st + 1 < nst) gload(st + 1);
-    compute(st & 1);
-    if (st + 1 < nst) lstore((st + 1) & 1);
+  if (nst > 1) gload(ra0, rb0, ma0, mb0, 1);
+  if (nst > 2) gload(ra1, rb1, ma1, mb1, 2);
+  // stage st computes from buffer st & 1; the stores of stage st + 1 go to the other buffer, whose last reader (stage
+  // st - 1) every wave finished before the previous barrier
+  for (int st = 0; st < nst; st += 2) {
+    parts_stage(As[0], Bs[0], wm, wn, r32, hl, acc);
+    if (st + 1 < nst) lstore(ra0, rb0, ma0, mb0, 1);
     __syncthreads();
+    if (st + 3 < nst) gload(ra0, rb0, ma0, mb0, st + 3);
+    if (st + 1 < nst) {
+      parts_stage(As[1], Bs[1], wm, wn, r32, hl, acc);
+      if (st + 2 < nst) lstore(ra1, rb1, ma1, mb1, 0);
+      __syncthreads();
+      if (st + 4 < nst) gload(ra1, rb1, ma1, mb1, st + 4);
+    }
   }
-  // block (a, b) of wave (wm, wn): rows 64 wm + 16 a + 4 (l / 16) + e = (token, c), columns 64 wn + 16 b + l % 16
+  // block (bm, bn): tokens i0 + 2 wm + bm and j0 + 2 wn + bn (wave-uniform); register r holds channel
+  // c = 8 (r / 4) + 4 hl + r % 4 of a, lane r32 channel d = r32 of b
+  float cnt[2][2];
 #pragma unroll
-  for (int a = 0; a < 4; a++)
+  for (int bm = 0; bm < 2; bm++)
 #pragma unroll
-    for (int b = 0; b < 4; b++) {
-      const int ti = 2 * wm + (a >> 1), tj = 2 * wn + (b >> 1);
-      const int i = i0 + ti, j = j0 + tj;
-      if (i >= i_end || j >= N) continue;
-      const float cnt = fmaxf(num[(int64_t)i * N + j], 1.0f);
-      const int d = 16 * (b & 1) + (l & 15);
-      TO* op = out + ((int64_t)(i - i_base) * N + j) * 1024 + d;
+    for (int bn = 0; bn < 2; bn++) {
+      const int i = min(i0 + 2 * wm + bm, N - 1), j = min(j0 + 2 * wn + bn, N - 1);
+      cnt[bm][bn] = fmaxf(num[(int64_t)i * N + j], 1.0f);
+    }
 #pragma unroll
-      for (int e = 0; e < 4; e++) {
-        const int c = 16 * (a & 1) + 4 * (l >> 4) + e;
-        op[c * 32] = (TO)(acc[a][b][e] / cnt);
+  for (int bm = 0; bm < 2; bm++)
+#pragma unroll
+    for (int bn = 0; bn < 2; bn++) {
+      const int i = i0 + 2 * wm + bm, j = j0 + 2 * wn + bn;
+      if (i >= i_end || j >= N) continue;  // wave-uniform
+      TO* op = out + ((int64_t)(i - i_base) * N + j) * 1024 + r32;
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int c = 8 * (r >> 2) + 4 * hl + (r & 3);
+        op[c * 32] = (TO)(acc[bm][bn][r] / cnt[bm][bn]);
       }
     }
 }
@@ -132,41 +202,14 @@ __global__ __launch_bounds__(256) void pwa_softmax_k(const float* __restrict__ l
   for (int j = l; j < ldw; j += 64) wr[j] = j < N ? expf(x[j] + (1.0f - mr[j]) * -inf - mx) * inv : 0.0f;
 }
 
-// The average on the bf16 matrix cores at fp32 accuracy. Each fp32 operand value is split exactly into three bf16
-// parts, x = x1 + x2 + x3 (x1 the round-to-nearest-even of x, x2 of x - x1, x3 = x - x1 - x2: 8 significant bits
-// each, 24 together), and a product is taken as the six part products x_a y_b with a + b <= 4, accumulated in fp32
-// by v_mfma_f32_32x32x16_bf16 (exact bf16 products, fp32 sums); the three left out (x2 y3, x3 y2, x3 y3) are below
-// 2^-23 of |x y| together. That is the fp32 kernel's accuracy at 6 / 16 of its matrix-core time (the bf16 rate is 16
-// times the fp32 one).
-// Workgroup tile: rows i0 .. i0 + 127 of head h (A = w[h], k = j) x four MSA rows s0 .. s0 + 3 times the head's 32
-// channels (B columns (s, d)); 4 waves of 64 x 64 (2 x 2 blocks of 32 x 32). A stage is 16 tokens j: the loads of
-// stage st + 1 are in registers while stage st computes, then split into the parts and stored (LDS double-buffered,
-// one barrier per stage). LDS holds each part as its own plane, K-contiguous rows: A[i][j] and B^T[(s, d)][j] (the
-// v rows arrive d-contiguous; a thread takes two consecutive tokens of 4 channels and stores each channel's pair
-// of parts as one dword).
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-
-struct Parts3 {
-  __bf16 p[3];
-};
-__device__ __forceinline__ Parts3 split3(float x) {
-  Parts3 o;
-  o.p[0] = (__bf16)x;
-  const float r1 = x - (float)o.p[0];  // exact
-  o.p[1] = (__bf16)r1;
-  o.p[2] = (__bf16)(r1 - (float)o.p[1]);  // exact: at most 8 significant bits are left
-  return o;
-}
-
+// The average, on the three-part bf16 scheme above. Workgroup tile: rows i0 .. i0 + 127 of head h (A = w[h], k = j)
+// x four MSA rows s0 .. s0 + 3 times the head's 32 channels (B columns (s, d)); a stage is 16 tokens j. The w rows
+// arrive K-contiguous; the v rows arrive d-contiguous, so a thread takes two consecutive tokens of 4 channels and
+// stores each channel's pair of parts as one dword.
 __global__ __launch_bounds__(256, 2) void pwa_avg_k(const float* __restrict__ w, int64_t ldw,
                                                     const float* __restrict__ v, int64_t ldv,
                                                     const float* __restrict__ g, int64_t ldg, float* __restrict__ out,
                                                     int64_t ldo, int S, int N) {
-  constexpr int KS = 16;            // tokens j per stage (one MFMA K-step)
-  constexpr int LDP = KS + 8;       // row pitch of a part plane (bf16)
-  constexpr int PLANE = 128 * LDP;  // bf16 per plane
   __shared__ LDS_ALIGN __bf16 As[2][3 * PLANE];
   __shared__ LDS_ALIGN __bf16 Bs[2][3 * PLANE];
   const int t = threadIdx.x, wave = t >> 6, l = t & 63, r32 = l & 31, hl = l >> 5;
@@ -228,32 +271,6 @@ __global__ __launch_bounds__(256, 2) void pwa_avg_k(const float* __restrict__ w,
     for (int b = 0; b < 2; b++)
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[a][b][e] = 0.0f;
-  auto compute = [&](int buf) {
-    bf16x8 fa[2][3], fb[2][3];
-#pragma unroll
-    for (int bm = 0; bm < 2; bm++)
-#pragma unroll
-      for (int p = 0; p < 3; p++)
-        fa[bm][p] = *reinterpret_cast<const bf16x8*>(As[buf] + p * PLANE + (64 * wm + 32 * bm + r32) * LDP + 8 * hl);
-#pragma unroll
-    for (int bn = 0; bn < 2; bn++)
-#pragma unroll
-      for (int p = 0; p < 3; p++)
-        fb[bn][p] = *reinterpret_cast<const bf16x8*>(Bs[buf] + p * PLANE + (64 * wn + 32 * bn + r32) * LDP + 8 * hl);
-#pragma unroll
-    for (int bm = 0; bm < 2; bm++)
-#pragma unroll
-      for (int bn = 0; bn < 2; bn++) {
-        // smaller part products first
-        f16x c = acc[bm][bn];
-        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[bm][2], fb[bn][0], c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[bm][1], fb[bn][1], c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[bm][0], fb[bn][2], c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[bm][1], fb[bn][0], c, 0, 0, 0);
-        c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[bm][0], fb[bn][1], c, 0, 0, 0);
-        acc[bm][bn] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[bm][0], fb[bn][0], c, 0, 0, 0);
-      }
-  };
   const int nst = (int)(ldw / KS);
   gload(ra0, rb0, 0);
   lstore(ra0, rb0, 0);
@@ -263,12 +280,12 @@ __global__ __launch_bounds__(256, 2) void pwa_avg_k(const float* __restrict__ w,
   // stage st computes from buffer st & 1; the stores of stage st + 1 go to the other buffer, whose last reader (stage
   // st - 1) every wave finished before the previous barrier
   for (int st = 0; st < nst; st += 2) {
-    compute(0);
+    parts_stage(As[0], Bs[0], wm, wn, r32, hl, acc);
     if (st + 1 < nst) lstore(ra0, rb0, 1);
     __syncthreads();
     if (st + 3 < nst) gload(ra0, rb0, st + 3);
     if (st + 1 < nst) {
-      compute(1);
+      parts_stage(As[1], Bs[1], wm, wn, r32, hl, acc);
       if (st + 2 < nst) lstore(ra1, rb1, 0);
       __syncthreads();
       if (st + 4 < nst) gload(ra1, rb1, st + 4);
@@ -319,7 +336,7 @@ hipError_t launch_opm_outer(const float* ab, int64_t ld_ab, const float* mask, c
 
 hipError_t launch_pwa_softmax(const float* logits, const float* pm, float inf, float* w, int N, int64_t ldw, int H,
                               hipStream_t st) {
-  if (N < 1 || H < 1 || ldw < N || ldw % MBK) return hipErrorInvalidValue;
+  if (N < 1 || H < 1 || ldw < N || ldw % KS) return hipErrorInvalidValue;
   const int64_t rows = (int64_t)H * N;
   pwa_softmax_k<<<(unsigned)((rows + 3) / 4), 256, 0, st>>>(logits, pm, inf, w, N, ldw, rows);
   return hipGetLastError();
@@ -328,7 +345,7 @@ hipError_t launch_pwa_softmax(const float* logits, const float* pm, float inf, f
 hipError_t launch_pwa_avg(const float* w, int64_t ldw, const float* v, int64_t ldv, const float* g, int64_t ldg,
                           float* out, int64_t ldo, int S, int N, int H, hipStream_t st) {
   const auto al = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; };
-  if (S < 1 || N < 1 || H < 1 || ldw < N || ldw % MBK || ldv % 4 || ldv < 32 * H || ldg < 32 * H ||
+  if (S < 1 || N < 1 || H < 1 || ldw < N || ldw % KS || ldv % 4 || ldv < 32 * H || ldg < 32 * H ||
       ldo < 32 * H || !al(w, 16) || !al(v, 16) || S > 4 * 65535 || H > 65535)
     return hipErrorInvalidValue;
   const dim3 grid((unsigned)((N + 127) / 128), (unsigned)((S + 3) / 4), (unsigned)H);

@@ -26,18 +26,23 @@ namespace {
 // st computes; each stage is then split into its parts and stored as three K-contiguous planes per operand (LDS
 // double-buffered, one barrier per stage, two workgroups per CU).
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
-struct Parts3 {
-  __bf16 p[3];
+// Two values split at once: part p of both, packed (value 0 in the low half), one v_cvt_pk_bf16_f32 per part.
+struct Pair3 {
+  uint32_t p[3];
 };
-__device__ __forceinline__ Parts3 split3(float x) {
-  Parts3 o;
-  o.p[0] = (__bf16)x;
-  const float r1 = x - (float)o.p[0];  // exact
-  o.p[1] = (__bf16)r1;
-  o.p[2] = (__bf16)(r1 - (float)o.p[1]);  // exact: at most 8 significant bits are left
+__device__ __forceinline__ uint32_t cvt_pair(float a, float b) {
+  return __builtin_bit_cast(uint32_t, bf16x2{(__bf16)a, (__bf16)b});
+}
+__device__ __forceinline__ Pair3 split3_pair(float x0, float x1) {
+#pragma clang fp contract(off)  // the parts are of the rounded x0, x1 (no product of the caller fused in)
+  Pair3 o;
+  o.p[0] = cvt_pair(x0, x1);
+  const float r0 = x0 - __uint_as_float(o.p[0] << 16), r1 = x1 - __uint_as_float(o.p[0] & 0xffff0000u);  // exact
+  o.p[1] = cvt_pair(r0, r1);
+  // exact: at most 8 significant bits are left
+  o.p[2] = cvt_pair(r0 - __uint_as_float(o.p[1] << 16), r1 - __uint_as_float(o.p[1] & 0xffff0000u));
   return o;
 }
 
@@ -109,20 +114,13 @@ __global__ __launch_bounds__(256, 2) void opm_outer_k(const float* __restrict__ 
   auto lstore = [&](const f4 (&ra)[2], const f4 (&rb)[2], const float (&ma)[2], const float (&mb)[2], int buf) {
 #pragma unroll
     for (int e = 0; e < 4; e++) {
-      const int row = 32 * tk + 4 * sq + e;
-      {
-        const Parts3 x0 = split3(ra[0][e] * ma[0]), x1 = split3(ra[1][e] * ma[1]);
-        __bf16* dst = As[buf] + row * LDP + 2 * sp;
-        *reinterpret_cast<bf16x2*>(dst) = bf16x2{x0.p[0], x1.p[0]};
-        *reinterpret_cast<bf16x2*>(dst + PLANE) = bf16x2{x0.p[1], x1.p[1]};
-        *reinterpret_cast<bf16x2*>(dst + 2 * PLANE) = bf16x2{x0.p[2], x1.p[2]};
-      }
-      {
-        const Parts3 x0 = split3(rb[0][e] * mb[0]), x1 = split3(rb[1][e] * mb[1]);
-        __bf16* dst = Bs[buf] + row * LDP + 2 * sp;
-        *reinterpret_cast<bf16x2*>(dst) = bf16x2{x0.p[0], x1.p[0]};
-        *reinterpret_cast<bf16x2*>(dst + PLANE) = bf16x2{x0.p[1], x1.p[1]};
-        *reinterpret_cast<bf16x2*>(dst + 2 * PLANE) = bf16x2{x0.p[2], x1.p[2]};
+      const int off = (32 * tk + 4 * sq + e) * LDP + 2 * sp;
+      const Pair3 xa = split3_pair(ra[0][e] * ma[0], ra[1][e] * ma[1]);
+      const Pair3 xb = split3_pair(rb[0][e] * mb[0], rb[1][e] * mb[1]);
+#pragma unroll
+      for (int p = 0; p < 3; p++) {
+        *reinterpret_cast<uint32_t*>(As[buf] + p * PLANE + off) = xa.p[p];
+        *reinterpret_cast<uint32_t*>(Bs[buf] + p * PLANE + off) = xb.p[p];
       }
     }
   };
@@ -241,27 +239,17 @@ __global__ __launch_bounds__(256, 2) void pwa_avg_k(const float* __restrict__ w,
 #pragma unroll
     for (int vv = 0; vv < 2; vv++) {
       const int e = t + 256 * vv, row = e >> 2, jq = e & 3;
-      bf16x4 p1, p2, p3;
-#pragma unroll
-      for (int q = 0; q < 4; q++) {
-        const Parts3 x = split3(ra[vv][q]);
-        p1[q] = x.p[0];
-        p2[q] = x.p[1];
-        p3[q] = x.p[2];
-      }
+      const Pair3 x01 = split3_pair(ra[vv][0], ra[vv][1]), x23 = split3_pair(ra[vv][2], ra[vv][3]);
       __bf16* dst = As[buf] + row * LDP + 4 * jq;
-      *reinterpret_cast<bf16x4*>(dst) = p1;
-      *reinterpret_cast<bf16x4*>(dst + PLANE) = p2;
-      *reinterpret_cast<bf16x4*>(dst + 2 * PLANE) = p3;
+#pragma unroll
+      for (int p = 0; p < 3; p++) *reinterpret_cast<uint2*>(dst + p * PLANE) = uint2{x01.p[p], x23.p[p]};
     }
 #pragma unroll
     for (int q = 0; q < 4; q++) {
-      const Parts3 x0 = split3(rb[0][q]), x1 = split3(rb[1][q]);
-      const bf16x2 p1 = {x0.p[0], x1.p[0]}, p2 = {x0.p[1], x1.p[1]}, p3 = {x0.p[2], x1.p[2]};
+      const Pair3 x = split3_pair(rb[0][q], rb[1][q]);
       __bf16* dst = Bs[buf] + (32 * bs + 4 * bq + q) * LDP + 2 * bp;
-      *reinterpret_cast<bf16x2*>(dst) = p1;
-      *reinterpret_cast<bf16x2*>(dst + PLANE) = p2;
-      *reinterpret_cast<bf16x2*>(dst + 2 * PLANE) = p3;
+#pragma unroll
+      for (int p = 0; p < 3; p++) *reinterpret_cast<uint32_t*>(dst + p * PLANE) = x.p[p];
     }
   };
   f16x acc[2][2];

@@ -44,7 +44,8 @@ SIGNATURES = {
     "bzpf_trimul_pack": [vp, vp, f32, i32, vp, i32, i64, i64, i32, vp],
     "bzpf_channels_to_rows": [vp, i32, vp, i32, i64, i64, i32, vp],
     "bzpf_triattn_pack": [vp, i32, f32, f32, vp, vp, vp, i32, i64, i64, i32, i32, vp],
-    "bzpf_opm_outer": [vp, i64, vp, vp, vp, i32, i32, i32, i32, i32, vp],
+    "bzpf_opm_split": [vp, i64, vp, vp, i32, i32, vp],
+    "bzpf_opm_outer": [vp, vp, vp, i32, i32, i32, i32, i32, vp],
     "bzpf_pwa_softmax": [vp, vp, f32, vp, i32, i64, i32, vp],
     "bzpf_pwa_avg": [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32, vp],
     "bzpf_seq_attention_batched": [vp, vp, vp, vp, i64, i64, vp, i64, i32, vp, i64, f32, vp, i64, i64, i32, i32, i32,

@@ -372,17 +372,25 @@ int bzpf_triattn_pack(const void* P, int trans, float q_scale, float bias_scale,
               "bzpf_triattn_pack");
 }
 
-int bzpf_opm_outer(const float* ab, int64_t ld_ab, const float* mask, const float* num, void* out, int out_dt,
-                   int n_seq, int N, int i_base, int n_i, void* stream) {
-  REQUIRE(ab && mask && num && out, "bzpf_opm_outer: NULL pointer");
+int bzpf_opm_split(const float* ab, int64_t ld_ab, const float* mask, void* planes, int n_seq, int N,
+                   void* stream) {
+  REQUIRE(ab && mask && planes, "bzpf_opm_split: NULL pointer");
+  REQUIRE(reinterpret_cast<uintptr_t>(planes) % 16 == 0 && ld_ab >= 64,
+          "bzpf_opm_split: planes must be 16-byte aligned and ab's row pitch >= 64 (ld_ab=%lld)", (long long)ld_ab);
+  REQUIRE(n_seq >= 1 && n_seq <= 16 * 65535 && N >= 1 && (int64_t)N * 6144 <= INT32_MAX,
+          "bzpf_opm_split: bad sizes (n_seq=%d N=%d)", n_seq, N);
+  return done(bzpf::launch_opm_split(ab, ld_ab, mask, planes, n_seq, N, S(stream)), "bzpf_opm_split");
+}
+
+int bzpf_opm_outer(const void* planes, const float* num, void* out, int out_dt, int n_seq, int N, int i_base,
+                   int n_i, void* stream) {
+  REQUIRE(planes && num && out, "bzpf_opm_outer: NULL pointer");
   REQUIRE(dt_ok(out_dt), "bzpf_opm_outer: bad dtype");
-  REQUIRE(reinterpret_cast<uintptr_t>(ab) % 16 == 0 && ld_ab >= 64 && ld_ab % 4 == 0,
-          "bzpf_opm_outer: ab must be 16-byte aligned with a row pitch >= 64 and a multiple of 4 (ld_ab=%lld)",
-          (long long)ld_ab);
-  REQUIRE(n_seq >= 1 && N >= 1 && i_base >= 0 && n_i >= 1 && i_base + n_i <= N,
+  REQUIRE(reinterpret_cast<uintptr_t>(planes) % 16 == 0, "bzpf_opm_outer: planes must be 16-byte aligned");
+  REQUIRE(n_seq >= 1 && n_seq <= 16 * 65535 && N >= 1 && (int64_t)N * 6144 <= INT32_MAX && i_base >= 0 &&
+              n_i >= 1 && i_base + n_i <= N,
           "bzpf_opm_outer: bad sizes (n_seq=%d N=%d i_base=%d n_i=%d)", n_seq, N, i_base, n_i);
-  return done(bzpf::launch_opm_outer(ab, ld_ab, mask, num, out, out_dt, n_seq, N, i_base, n_i, S(stream)),
-              "bzpf_opm_outer");
+  return done(bzpf::launch_opm_outer(planes, num, out, out_dt, n_seq, N, i_base, n_i, S(stream)), "bzpf_opm_outer");
 }
 
 int bzpf_pwa_softmax(const float* logits, const float* pair_mask, float inf, float* w, int N, int64_t ldw, int H,

@@ -79,8 +79,10 @@ hipError_t launch_seq_attention(const void* q, const void* k, const void* v, con
                                 int64_t s_in, const void* bias, int64_t s_bias, int mult, const float* mask,
                                 int64_t s_mask, float inf, void* out, int64_t ld_out, int64_t s_out, int dt,
                                 int bias_dt, int S, int64_t N, int H, int hd, hipStream_t st);
-hipError_t launch_opm_outer(const float* ab, int64_t ld_ab, const float* mask, const float* num, void* out,
-                            int out_dt, int S, int N, int i_base, int n_i, hipStream_t st);
+hipError_t launch_opm_split(const float* ab, int64_t ld_ab, const float* mask, void* planes, int S, int N,
+                            hipStream_t st);
+hipError_t launch_opm_outer(const void* planes, const float* num, void* out, int out_dt, int S, int N, int i_base,
+                            int n_i, hipStream_t st);
 hipError_t launch_pwa_softmax(const float* logits, const float* pm, float inf, float* w, int N, int64_t ldw, int H,
                               hipStream_t st);
 hipError_t launch_pwa_avg(const float* w, int64_t ldw, const float* v, int64_t ldv, const float* g, int64_t ldg,

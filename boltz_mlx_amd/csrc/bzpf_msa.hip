@@ -1,5 +1,6 @@
 // MSA-block pair kernels (fp32 operands and fp32-accurate reductions, the reference's numerics policy for the
 // reductions over MSA rows and tokens):
+//   opm_split   : the masked operands mask[s][n] ab[s][n][ch] as bf16 part planes for opm_outer;
 //   opm_outer   : z[(i - i_base) N + j][c 32 + d] = sum_s mask[s][i] mask[s][j] a[s][i][c] b[s][j][d] / max(num, 1)
 //                 with num[i][j] = sum_s mask[s][i] mask[s][j] given (mask^T mask, one small GEMM) and
 //                 a | b = ab[s][i][0:32] | ab[s][j][32:64]
@@ -22,9 +23,10 @@ namespace {
 // fp32 by v_mfma_f32_32x32x16_bf16 (exact bf16 products, fp32 sums); the three left out (x2 y3, x3 y2, x3 y3) are
 // below 2^-23 of |x y| together. That is the fp32 matrix cores' accuracy at 6 / 16 of their time (the bf16 rate is
 // 16 times the fp32 one). A 256-thread workgroup computes a 128 x 128 tile, 4 waves of 64 x 64 (2 x 2 blocks of
-// 32 x 32), over K stages of 16 (one MFMA K-step): the loads of stages st + 1 and st + 2 are in registers while stage
-// st computes; each stage is then split into its parts and stored as three K-contiguous planes per operand (LDS
-// double-buffered, one barrier per stage, two workgroups per CU).
+// 32 x 32), over K stages of 16 (one MFMA K-step), two workgroups per CU. The outer sum takes its operands split
+// beforehand (one pass over the MSA) and copies them straight into LDS; the weighted average splits in the loop:
+// the loads of stages st + 1 and st + 2 are in registers while stage st computes, and each stage is then split into
+// its parts and stored as three K-contiguous planes per operand (LDS double-buffered, one barrier per stage).
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 
@@ -81,48 +83,90 @@ __device__ __forceinline__ void parts_stage(const __bf16* Ab, const __bf16* Bb, 
 }
 
 // ---------------------------------------------------------------- outer product mean
+// The outer sum takes its operands already split: a pass over the MSA writes the masked values
+// x = mask[s][n] ab[s][n][ch] (the fp32 products) as their three bf16 parts, in 1 KB chunks that the outer sum
+// copies straight into LDS (buffer_load ... lds), so its loop holds no staging registers and no split work.
+// Chunk (g, n, p, h) at byte ((g N + n) 6 + 2 p + h) 1024 holds part p of channels 32 h .. 32 h + 31 of token n
+// (h = 0: a, h = 1: b) over MSA rows 16 g .. 16 g + 15: 32 rows (channel c) of 16 bf16 (k = s - 16 g), zeros for
+// s >= S.
+constexpr int OPM_CHUNK = 1024, OPM_TOKB = 6 * OPM_CHUNK;
+
+// A workgroup takes stage g of tokens 2 x .. 2 x + 1: thread (token t / 128, channel ch = (t / 2) % 64,
+// kh = t % 2) takes MSA rows 16 g + 8 kh .. + 7 of channel ch and stores each part's 8 values as 16 bytes, so a
+// wave's store of one part fills a 1 KB chunk.
+__global__ __launch_bounds__(256) void opm_split_k(const float* __restrict__ ab, int64_t ld_ab,
+                                                   const float* __restrict__ mask, __bf16* __restrict__ planes, int S,
+                                                   int N) {
+  const int t = threadIdx.x, n = 2 * (int)blockIdx.x + (t >> 7), g = (int)blockIdx.y;
+  const int ch = (t >> 1) & 63, kh = t & 1;
+  if (n >= N) return;  // the second half of the last workgroup for odd N (no barriers here)
+  float x[8];
+#pragma unroll
+  for (int e = 0; e < 8; e++) {
+    const int s = 16 * g + 8 * kh + e;
+    const int sc = min(s, S - 1);
+    const float v = ab[((int64_t)sc * N + n) * ld_ab + ch], m = mask[(int64_t)sc * N + n];
+    x[e] = s < S ? v * m : 0.0f;
+  }
+  Pair3 q[4];
+#pragma unroll
+  for (int e = 0; e < 4; e++) q[e] = split3_pair(x[2 * e], x[2 * e + 1]);
+  char* base = reinterpret_cast<char*>(planes) + ((int64_t)g * N + n) * OPM_TOKB + (ch >> 5) * OPM_CHUNK +
+               (ch & 31) * 32 + 16 * kh;
+#pragma unroll
+  for (int p = 0; p < 3; p++)
+    *reinterpret_cast<uint4*>(base + 2 * p * OPM_CHUNK) = uint4{q[0].p[p], q[1].p[p], q[2].p[p], q[3].p[p]};
+}
+
 // Workgroup tile: tokens i0 .. i0 + 3 (A rows (i, c) = 32 (i - i0) + c) x j0 .. j0 + 3 (B columns (j, d)), K = MSA
-// rows s. Both operands arrive channel-contiguous per (s, token); a thread takes MSA rows 2 p and 2 p + 1 of the
-// stage, one token (the wave's) and 4 channels, multiplies by the mask, splits, and stores each channel's pair of
-// parts as one dword of the K-contiguous planes (a store's 64 lanes: 8 MSA-row pairs x 8 channel quads).
+// rows s in stages of 16; a stage is 24 chunks (A: parts 0..2 of the a halves of tokens i0 .., B: of the b halves of
+// tokens j0 ..), 24 KB of LDS, three stages in flight (two workgroups per CU). In LDS, row c of a chunk keeps its two
+// 16-byte halves swapped when (c / 4) is odd, so the fragment reads (8 lanes on 8 consecutive rows per pass) hit
+// distinct banks; each lane of a load picks the global half that lands there.
 template <typename TO>
-__global__ __launch_bounds__(256, 2) void opm_outer_k(const float* __restrict__ ab, int64_t ld_ab,
-                                                      const float* __restrict__ mask, const float* __restrict__ num,
-                                                      TO* __restrict__ out, int S, int N, int i_base, int n_i) {
-  __shared__ LDS_ALIGN __bf16 As[2][3 * PLANE];
-  __shared__ LDS_ALIGN __bf16 Bs[2][3 * PLANE];
-  const int t = threadIdx.x, wave = t >> 6, l = t & 63, r32 = l & 31, hl = l >> 5;
+__global__ __launch_bounds__(256, 2) void opm_outer_k(const __bf16* __restrict__ planes, const float* __restrict__ num,
+                                                      TO* __restrict__ out, int G, int N, int i_base, int n_i) {
+  constexpr int NS = 3, STAGE = 24 * OPM_CHUNK, LPW = 6;  // load instructions per wave per stage
+  __shared__ __attribute__((aligned(1024))) char lds[NS * STAGE];
+  const int t = threadIdx.x, l = t & 63, r32 = l & 31, hl = l >> 5;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
   const int wm = wave >> 1, wn = wave & 1;
   const int i0 = i_base + 4 * (int)blockIdx.y, j0 = 4 * (int)blockIdx.x;
   const int i_end = min(i_base + n_i, N);
-  // staging item: MSA rows 2 sp, 2 sp + 1 of the stage, token tk (= the wave), channels 4 sq .. + 3. Tokens past the
-  // range read the last one (their outputs are not stored); MSA rows past S read row S - 1 with mask 0.
-  const int sp = t & 7, sq = (t >> 3) & 7, tk = wave;
-  const int ia = min(i0 + tk, i_end - 1), jb = min(j0 + tk, N - 1);
-  f4 ra0[2], rb0[2], ra1[2], rb1[2];
-  float ma0[2], mb0[2], ma1[2], mb1[2];
-  auto gload = [&](f4 (&ra)[2], f4 (&rb)[2], float (&ma)[2], float (&mb)[2], int stage) {
+  // load v of this wave fills chunk q = wave + 4 v of the stage: q < 12 is A part q / 4 of token i0 + q % 4, else
+  // B part (q - 12) / 4 of token j0 + q % 4 (tokens past the range load the last one; their outputs are not stored)
+  int voff[LPW];
 #pragma unroll
-    for (int b = 0; b < 2; b++) {
-      const int s = stage * KS + 2 * sp + b, sc = min(s, S - 1);
-      ra[b] = *reinterpret_cast<const f4*>(ab + ((int64_t)sc * N + ia) * ld_ab + 4 * sq);
-      rb[b] = *reinterpret_cast<const f4*>(ab + ((int64_t)sc * N + jb) * ld_ab + 32 + 4 * sq);
-      ma[b] = s < S ? mask[(int64_t)sc * N + ia] : 0.0f;
-      mb[b] = s < S ? mask[(int64_t)sc * N + jb] : 0.0f;
-    }
+  for (int v = 0; v < LPW; v++) {
+    const int q = wave + 4 * v, isb = q >= 12, p = (q % 12) / 4, tt = q % 4;
+    const int n = isb ? min(j0 + tt, N - 1) : min(i0 + tt, i_end - 1);
+    voff[v] = (n * 6 + 2 * p + isb) * OPM_CHUNK + (l >> 1) * 32 + 16 * ((l & 1) ^ ((l >> 3) & 1));
+  }
+  constexpr int RSRC_CFG = 0x00020000;
+  auto issue = [&](int st, int slot) {
+    st = min(st, G - 1);  // issues past the last stage reload it into a slot that is never read
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        (void*)(reinterpret_cast<const char*>(planes) + (int64_t)st * N * OPM_TOKB), 0, N * OPM_TOKB, RSRC_CFG);
+#pragma unroll
+    for (int v = 0; v < LPW; v++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          rs, (__attribute__((address_space(3))) void*)(lds + slot * STAGE + (wave + 4 * v) * OPM_CHUNK), 16,
+          voff[v], 0, 0, 0);
   };
-  auto lstore = [&](const f4 (&ra)[2], const f4 (&rb)[2], const float (&ma)[2], const float (&mb)[2], int buf) {
+  // fragments: part p of A rows 64 wm + 32 bm + r32 (chunk p * 4 + 2 wm + bm, row r32) and of B columns
+  // 64 wn + 32 bn + r32 (chunk 12 + p * 4 + 2 wn + bn), k = 8 hl .. 8 hl + 7
+  const int fro = r32 * 32 + 16 * (hl ^ ((r32 >> 2) & 1));
+  typedef bf16x8 Frag[2][3];
+  Frag fa0, fb0, fa1, fb1;  // two sets, named (an array indexed by the stage parity would live in scratch)
+  auto read = [&](Frag& fa, Frag& fb, int slot) {
+    const char* base = lds + slot * STAGE + fro;
 #pragma unroll
-    for (int e = 0; e < 4; e++) {
-      const int off = (32 * tk + 4 * sq + e) * LDP + 2 * sp;
-      const Pair3 xa = split3_pair(ra[0][e] * ma[0], ra[1][e] * ma[1]);
-      const Pair3 xb = split3_pair(rb[0][e] * mb[0], rb[1][e] * mb[1]);
+    for (int x = 0; x < 2; x++)
 #pragma unroll
       for (int p = 0; p < 3; p++) {
-        *reinterpret_cast<uint32_t*>(As[buf] + p * PLANE + off) = xa.p[p];
-        *reinterpret_cast<uint32_t*>(Bs[buf] + p * PLANE + off) = xb.p[p];
+        fa[x][p] = *reinterpret_cast<const bf16x8*>(base + (p * 4 + 2 * wm + x) * OPM_CHUNK);
+        fb[x][p] = *reinterpret_cast<const bf16x8*>(base + (12 + p * 4 + 2 * wn + x) * OPM_CHUNK);
       }
-    }
   };
   f16x acc[2][2];
 #pragma unroll
@@ -131,25 +175,33 @@ __global__ __launch_bounds__(256, 2) void opm_outer_k(const float* __restrict__ 
     for (int b = 0; b < 2; b++)
 #pragma unroll
       for (int e = 0; e < 16; e++) acc[a][b][e] = 0.0f;
-  const int nst = (S + KS - 1) / KS;
-  gload(ra0, rb0, ma0, mb0, 0);
-  lstore(ra0, rb0, ma0, mb0, 0);
-  __syncthreads();
-  if (nst > 1) gload(ra0, rb0, ma0, mb0, 1);
-  if (nst > 2) gload(ra1, rb1, ma1, mb1, 2);
-  // stage st computes from buffer st & 1; the stores of stage st + 1 go to the other buffer, whose last reader (stage
-  // st - 1) every wave finished before the previous barrier
-  for (int st = 0; st < nst; st += 2) {
-    parts_stage(As[0], Bs[0], wm, wn, r32, hl, acc);
-    if (st + 1 < nst) lstore(ra0, rb0, ma0, mb0, 1);
-    __syncthreads();
-    if (st + 3 < nst) gload(ra0, rb0, ma0, mb0, st + 3);
-    if (st + 1 < nst) {
-      parts_stage(As[1], Bs[1], wm, wn, r32, hl, acc);
-      if (st + 2 < nst) lstore(ra1, rb1, ma1, mb1, 0);
-      __syncthreads();
-      if (st + 4 < nst) gload(ra1, rb1, ma1, mb1, st + 4);
+  constexpr int YOUNGER = (NS - 2) * LPW;  // loads of later stages in flight when a stage is waited for
+  constexpr int WAIT = (YOUNGER & 15) | ((YOUNGER >> 4) << 14) | (0x7 << 4) | (0xF << 8);  // vmcnt only
+#pragma unroll
+  for (int p = 0; p < NS - 1; p++) issue(p, p);
+  __builtin_amdgcn_s_waitcnt(WAIT);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+  issue(NS - 1, NS - 1);
+  read(fa0, fb0, 0);
+  auto step = [&](int st, const Frag& ca, const Frag& cb, Frag& na, Frag& nb) {
+    if (st + 1 < G) {
+      // this wave's reads of slot st % NS are done and stage st + 1 has landed; after the barrier the slot takes
+      // stage st + NS, and the fragments of stage st + 1 are read while stage st computes
+      __builtin_amdgcn_s_waitcnt(WAIT & ~(0xF << 8));  // vmcnt as above, lgkmcnt(0)
+      __builtin_amdgcn_s_barrier();
+      __builtin_amdgcn_sched_barrier(0);
+      issue(st + NS, st % NS);
+      read(na, nb, (st + 1) % NS);
     }
+#pragma unroll
+    for (int bm = 0; bm < 2; bm++)
+#pragma unroll
+      for (int bn = 0; bn < 2; bn++) acc[bm][bn] = mfma_parts6(ca[bm], cb[bn], acc[bm][bn]);
+  };
+  for (int st = 0; st < G; st += 2) {
+    step(st, fa0, fb0, fa1, fb1);
+    if (st + 1 < G) step(st + 1, fa1, fb1, fa0, fb0);
   }
   // block (bm, bn): tokens i0 + 2 wm + bm and j0 + 2 wn + bn (wave-uniform); register r holds channel
   // c = 8 (r / 4) + 4 hl + r % 4 of a, lane r32 channel d = r32 of b
@@ -309,16 +361,30 @@ __global__ __launch_bounds__(256, 2) void pwa_avg_k(const float* __restrict__ w,
 
 }  // namespace
 
-hipError_t launch_opm_outer(const float* ab, int64_t ld_ab, const float* mask, const float* num, void* out,
-                            int out_dt, int S, int N, int i_base, int n_i, hipStream_t st) {
+hipError_t launch_opm_split(const float* ab, int64_t ld_ab, const float* mask, void* planes, int S, int N,
+                            hipStream_t st) {
   const auto al = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; };
-  if (S < 1 || N < 1 || i_base < 0 || n_i < 1 || i_base + n_i > N || ld_ab < 64 || ld_ab % 4 || !al(ab, 16))
+  const int G = (S + 15) / 16;
+  if (S < 1 || N < 1 || G > 65535 || ld_ab < 64 || (int64_t)N * OPM_TOKB > INT32_MAX || !al(planes, 16))
     return hipErrorInvalidValue;
+  opm_split_k<<<dim3((unsigned)((N + 1) / 2), (unsigned)G), 256, 0, st>>>(ab, ld_ab, mask,
+                                                                           static_cast<__bf16*>(planes), S, N);
+  return hipGetLastError();
+}
+
+hipError_t launch_opm_outer(const void* planes, const float* num, void* out, int out_dt, int S, int N, int i_base,
+                            int n_i, hipStream_t st) {
+  const auto al = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; };
+  if (S < 1 || N < 1 || i_base < 0 || n_i < 1 || i_base + n_i > N || (int64_t)N * OPM_TOKB > INT32_MAX ||
+      !al(planes, 16))
+    return hipErrorInvalidValue;
+  const int G = (S + 15) / 16;
+  const __bf16* pl = static_cast<const __bf16*>(planes);
   const dim3 grid((unsigned)((N + 3) / 4), (unsigned)((n_i + 3) / 4));
   if (out_dt == DT_F16)
-    opm_outer_k<half_t><<<grid, 256, 0, st>>>(ab, ld_ab, mask, num, static_cast<half_t*>(out), S, N, i_base, n_i);
+    opm_outer_k<half_t><<<grid, 256, 0, st>>>(pl, num, static_cast<half_t*>(out), G, N, i_base, n_i);
   else
-    opm_outer_k<float><<<grid, 256, 0, st>>>(ab, ld_ab, mask, num, static_cast<float*>(out), S, N, i_base, n_i);
+    opm_outer_k<float><<<grid, 256, 0, st>>>(pl, num, static_cast<float*>(out), G, N, i_base, n_i);
   return hipGetLastError();
 }
 

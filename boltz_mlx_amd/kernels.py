@@ -651,22 +651,39 @@ def opm_counts(mask: torch.Tensor) -> torch.Tensor:
     return linear(mt, mt)
 
 
+def opm_split(ab: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+    """The masked outer-product-mean operands x = mask[s, n] * ab[s, n, ch] as three exact bf16 parts, in the chunk
+    layout bzpf_opm_outer loads ([ceil(S / 16), N, 3, 2, 32, 16] bf16: stage, token, part, a | b, channel, MSA row
+    within the stage; zeros past S) for ab fp32 [S, N, 64], mask fp32 [S, N] (outer_product_mean.py:37-45)."""
+    _dev(ab, mask)
+    S, N, C2 = ab.shape
+    if ab.dtype != torch.float32 or C2 < 64 or not ab.is_contiguous() or mask.shape != (S, N) \
+            or mask.dtype != torch.float32 or not mask.is_contiguous():
+        raise ValueError("opm_split: need contiguous fp32 ab [S, N, 64] and mask [S, N]")
+    planes = torch.empty(((S + 15) // 16, N, 3, 2, 32, 16), dtype=torch.bfloat16, device=ab.device)
+    call("bzpf_opm_split", _p(ab), C2, _p(mask), _p(planes), S, N, _stream())
+    return planes
+
+
 def opm_outer(ab: torch.Tensor, mask: torch.Tensor, i_base: int = 0, n_i: int | None = None,
-              out_dtype=torch.float16, num: torch.Tensor | None = None) -> torch.Tensor:
+              out_dtype=torch.float16, num: torch.Tensor | None = None,
+              planes: torch.Tensor | None = None) -> torch.Tensor:
     """OuterProductMean's outer sum for one MSA: ab fp32 [S, N, 64] (LN(m) [W_a; W_b]^T, unmasked), mask fp32
     [S, N] -> [n_i * N, 1024] with row (i - i_base) * N + j and column c * 32 + d holding
-    sum_s mask_si mask_sj a[s, i, c] b[s, j, d] / max(sum_s mask_si mask_sj, 1) (outer_product_mean.py:37-45)."""
+    sum_s mask_si mask_sj a[s, i, c] b[s, j, d] / max(sum_s mask_si mask_sj, 1) (outer_product_mean.py:37-45).
+    planes: opm_split(ab, mask), when the caller already holds it (one split serves every i chunk)."""
     _dev(ab, mask)
     S, N, C2 = ab.shape
     n_i = N - i_base if n_i is None else n_i
-    if ab.dtype != torch.float32 or C2 < 64 or not ab.is_contiguous() or mask.shape != (S, N) \
-            or mask.dtype != torch.float32 or not mask.is_contiguous():
-        raise ValueError("opm_outer: need contiguous fp32 ab [S, N, 64] and mask [S, N]")
+    planes = opm_split(ab, mask) if planes is None else planes
+    if planes.shape != ((S + 15) // 16, N, 3, 2, 32, 16) or planes.dtype != torch.bfloat16 \
+            or not planes.is_contiguous():
+        raise ValueError("opm_outer: planes must be the contiguous output of opm_split for this ab")
     num = opm_counts(mask) if num is None else num
     if num.shape != (N, N) or num.dtype != torch.float32 or not num.is_contiguous():
         raise ValueError("opm_outer: num must be the contiguous fp32 [N, N] pair counts")
     out = torch.empty((n_i * N, 1024), dtype=out_dtype, device=ab.device)
-    call("bzpf_opm_outer", _p(ab), C2, _p(mask), _p(num), _p(out), _dt(out), S, N, int(i_base), int(n_i), _stream())
+    call("bzpf_opm_outer", _p(planes), _p(num), _p(out), _dt(out), S, N, int(i_base), int(n_i), _stream())
     return out
 
 

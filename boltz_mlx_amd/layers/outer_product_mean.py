@@ -3,7 +3,9 @@ boltz_mlx/layers/outer_product_mean.py:12-50 (inference).
 
   ab = LN(m) [W_a; W_b]^T                                  bzpf_layernorm + bzpf_linear (fp32)
   num = mask^T mask                                        bzpf_linear (fp32, the pair counts)
-  z16 = (sum_s mask_si mask_sj a_si (x) b_sj) / max(num, 1)  bzpf_opm_outer (fp32 MFMA; fp16 out in f16 mode)
+  x = mask * ab as three bf16 parts                        bzpf_opm_split (once per MSA)
+  z16 = (sum_s mask_si mask_sj a_si (x) b_sj) / max(num, 1)  bzpf_opm_outer (fp32-accurate: six bf16 part products
+                                                           per product, fp32 sums; fp16 out in f16 mode)
   out (+)= z16 W_o^T + bias                                bzpf_linear (fp16 GEMM in f16 mode, fp32 accumulate)
 The outer sum runs over all MSA rows in one kernel per block of token rows i (at most OPM_PAIRS_PER_CHUNK pairs),
 as the reference's fused f16 path does (outer_product_mean.py:52-84); the reference's re-associated form for very
@@ -55,8 +57,9 @@ class OuterProductMean(torch.nn.Module):
         mk = mask.to(torch.float32).reshape(S, N).contiguous()
         z2 = z.view(N * N, co)
         num = K.opm_counts(mk)
+        planes = K.opm_split(ab, mk)
         step = max(1, min(N, OPM_PAIRS_PER_CHUNK // N))
         for i0 in range(0, N, step):
             n = min(step, N - i0)
-            zz = K.opm_outer(ab, mk, i0, n, out_dtype=w_o.dtype, num=num)
+            zz = K.opm_outer(ab, mk, i0, n, out_dtype=w_o.dtype, num=num, planes=planes)
             K.linear(zz, w_o, bias=self.proj_o.bias, out=z2[i0 * N:(i0 + n) * N], accumulate=accumulate)

@@ -241,15 +241,24 @@ int bzpf_linear_swiglu3(const void* x, const void* w, void* u, int64_t rows, int
  * intermediate. */
 int bzpf_linear_swiglu(const void* x, const void* w, void* u, int64_t rows, int K, int H, void* stream);
 
-/* Outer-product-mean outer sum for MSA rows s < n_seq over tokens (fp32 ab [n_seq, N, ld_ab]: a = ab[.., 0:32],
- * b = ab[.., 32:64], unmasked; mask fp32 [n_seq, N]): for i_base <= i < i_base + n_i and j < N,
+/* Outer-product-mean operands, masked and split for bzpf_opm_outer: for MSA rows s < n_seq and tokens n < N
+ * (fp32 ab [n_seq, N, ld_ab]: a = ab[.., 0:32], b = ab[.., 32:64], unmasked; mask fp32 [n_seq, N]) the products
+ * x = mask[s][n] * ab[s][n][ch] as three bf16 parts x = x1 + x2 + x3 (exact; x1 = bf16(x), x2 = bf16(x - x1)).
+ * planes: 16-byte aligned, ceil(n_seq / 16) * N * 6144 bytes; 1 KB chunk (g, n, p, h) at byte
+ * ((g * N + n) * 6 + 2 * p + h) * 1024 holds part p + 1 of channels 32 h .. 32 h + 31 of token n over MSA rows
+ * 16 g .. 16 g + 15, as 32 rows (channel) of 16 bf16 (MSA row), zeros past n_seq. The masking of a and b in
+ * kernels_msa.opm_outer's operand staging (boltz_mlx/kernels_msa.py:292-343,
+ * boltz_mlx/layers/outer_product_mean.py:37-45). */
+int bzpf_opm_split(const float* ab, int64_t ld_ab, const float* mask, void* planes, int n_seq, int N, void* stream);
+
+/* Outer-product-mean outer sum over the planes of bzpf_opm_split: for i_base <= i < i_base + n_i and j < N,
  *   out[(i - i_base) * N + j][c * 32 + d] = sum_s mask[s][i] mask[s][j] a[s][i][c] b[s][j][d] / max(num[i][j], 1),
  * num fp32 [N, N] = mask^T mask (the pair counts; one bzpf_linear of the transposed mask with itself, as the
- * reference's num input); out fp16 or fp32 [n_i * N, 1024] (fp32 MFMA accumulation). Replaces
- * kernels_msa.opm_outer and the module path's outer sum (boltz_mlx/kernels_msa.py:292-343,
- * boltz_mlx/layers/outer_product_mean.py:37-45). */
-int bzpf_opm_outer(const float* ab, int64_t ld_ab, const float* mask, const float* num, void* out, int out_dt,
-                   int n_seq, int N, int i_base, int n_i, void* stream);
+ * reference's num input); out fp16 or fp32 [n_i * N, 1024]. Each product is the six bf16 part products x_a y_b with
+ * a + b <= 4, accumulated in fp32 (fp32 accuracy). Replaces kernels_msa.opm_outer and the module path's outer sum
+ * (boltz_mlx/kernels_msa.py:292-343, boltz_mlx/layers/outer_product_mean.py:37-45). */
+int bzpf_opm_outer(const void* planes, const float* num, void* out, int out_dt, int n_seq, int N, int i_base, int n_i,
+                   void* stream);
 
 /* Pair-weighted-averaging weights: w[h][i][j] = softmax_j(logits[h][i][j] + (1 - pair_mask[i][j]) * -inf) for
  * logits fp32 [H, N, N], pair_mask fp32 [N, N]; w fp32 [H, N, ldw] with zeros for N <= j < ldw (ldw a multiple of

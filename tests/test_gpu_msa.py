@@ -65,6 +65,29 @@ def test_opm_outer(S, N, i_base, n_i, out_dtype):
         assert np.abs(got - ref).max() <= np.abs(ref).max() * 2.0 ** -10, m
 
 
+@pytest.mark.parametrize("S,N", [(37, 5), (16, 3), (1, 2)])
+def test_opm_split_parts_and_layout(S, N):
+    """The split planes hold x = fp32(mask * ab) as x1 = bf16(x), x2 = bf16(x - x1), x3 = x - x1 - x2 (exact),
+    chunk (g, n, p, h) = part p of channels 32 h .. + 31 of token n over MSA rows 16 g .. + 15, zeros past S."""
+    from boltz_mlx_amd import kernels as K
+
+    ab, mask = _opm_inputs(S, N, 7 * S + N)
+    ab[0, 0, :4] = [1e-30, -3e38, 1.0 + 2.0 ** -20, 0.0]  # tiny, huge, a value needing all three parts, zero
+    got = K.opm_split(dev(ab), dev(mask)).cpu()
+    G = (S + 15) // 16
+    assert got.shape == (G, N, 3, 2, 32, 16) and got.dtype == torch.bfloat16
+    x = np.zeros((G * 16, N, 64), np.float32)
+    x[:S] = ab * mask[:, :, None]  # the fp32 products
+    xt = torch.from_numpy(x)
+    p1 = xt.to(torch.bfloat16)  # round to nearest even
+    p2 = (xt - p1.float()).to(torch.bfloat16)
+    p3 = (xt - p1.float() - p2.float()).to(torch.bfloat16)
+    assert torch.equal(p3.float(), xt - p1.float() - p2.float())  # the third part is exact
+    # [G * 16, N, 2 * 32] -> [G, N, part, h, c, k]
+    want = torch.stack([p1, p2, p3]).view(3, G, 16, N, 2, 32).permute(1, 3, 0, 4, 5, 2)
+    assert torch.equal(got.view(torch.int16), want.contiguous().view(torch.int16))
+
+
 def test_opm_outer_zero_count_pair():
     """Two tokens that never share an unmasked MSA row: their pair's count is 0, clamped to 1, and z is 0."""
     from boltz_mlx_amd import kernels as K

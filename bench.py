@@ -219,8 +219,8 @@ def diffusion_transformer_leg(steps: int, device) -> dict:
 def msa_layer_leg(steps: int, device, N: int = 400, S: int = 1024) -> dict:
     """One MSA block (MSALayer: pair-weighted averaging, transition on m, outer-product mean, NoSeq pair layer) at
     N tokens and S MSA rows (5 % padded tokens, 10 % masked MSA entries), random-init weights, timed over `steps`
-    layer calls. The outer sum and the weighted average are fp32 MFMA reductions (the reference's numerics policy);
-    their FLOPs are reported with the fraction of the fp32 MFMA peak they reach together."""
+    layer calls. The outer sum and the weighted average are fp32-accurate reductions (the reference's numerics
+    policy) on the bf16 matrix cores (three exact bf16 parts per fp32 operand); their fp32 FLOPs are reported."""
     import torch
 
     from boltz_mlx_amd.layers.msa import MSALayer

@@ -47,12 +47,15 @@ SIGNATURES = {
     "bzpf_opm_split": [vp, i64, vp, vp, i32, i32, vp],
     "bzpf_opm_outer": [vp, vp, vp, i32, i32, i32, i32, i32, vp],
     "bzpf_pwa_softmax": [vp, vp, f32, vp, i32, i64, i32, vp],
+    "bzpf_pwa_wsplit_bytes": [i32, i64, i32],
+    "bzpf_pwa_wsplit": [vp, i64, vp, i32, i32, vp],
     "bzpf_pwa_avg": [vp, i64, vp, i64, vp, i64, vp, i64, i32, i32, i32, vp],
     "bzpf_seq_attention_batched": [vp, vp, vp, vp, i64, i64, vp, i64, i32, vp, i64, f32, vp, i64, i64, i32, i32, i32,
                                    i64, i32, i32, vp],
     "bzpf_pair_bias": [vp, vp, vp, f32, vp, vp, i32, i64, i32, i32, vp],
 }
-_RESTYPES = {"bzpf_version": C.c_char_p, "bzpf_last_error": C.c_char_p, "bzpf_row_pitch": i64}
+_RESTYPES = {"bzpf_version": C.c_char_p, "bzpf_last_error": C.c_char_p, "bzpf_row_pitch": i64,
+             "bzpf_pwa_wsplit_bytes": i64}
 
 _lib = None
 

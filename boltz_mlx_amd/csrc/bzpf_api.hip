@@ -401,15 +401,29 @@ int bzpf_pwa_softmax(const float* logits, const float* pair_mask, float inf, flo
   return done(bzpf::launch_pwa_softmax(logits, pair_mask, inf, w, N, ldw, H, S(stream)), "bzpf_pwa_softmax");
 }
 
-int bzpf_pwa_avg(const float* w, int64_t ldw, const float* v, int64_t ldv, const float* g, int64_t ldg, float* out,
+int64_t bzpf_pwa_wsplit_bytes(int N, int64_t ldw, int H) {
+  if (N < 1 || H < 1 || ldw < N || ldw % 16) return -1;
+  return bzpf::pwa_wsplit_bytes(N, ldw, H);
+}
+
+int bzpf_pwa_wsplit(const float* w, int64_t ldw, void* wp, int N, int H, void* stream) {
+  REQUIRE(w && wp, "bzpf_pwa_wsplit: NULL pointer");
+  REQUIRE(reinterpret_cast<uintptr_t>(w) % 8 == 0 && reinterpret_cast<uintptr_t>(wp) % 16 == 0,
+          "bzpf_pwa_wsplit: w must be 8-byte and wp 16-byte aligned");
+  REQUIRE(N >= 1 && H >= 1 && H <= 65535 && ldw >= N && ldw % 16 == 0, "bzpf_pwa_wsplit: bad sizes (N=%d H=%d)", N,
+          H);
+  return done(bzpf::launch_pwa_wsplit(w, ldw, wp, N, H, S(stream)), "bzpf_pwa_wsplit");
+}
+
+int bzpf_pwa_avg(const void* wp, int64_t ldw, const float* v, int64_t ldv, const float* g, int64_t ldg, float* out,
                  int64_t ldo, int n_seq, int N, int H, void* stream) {
-  REQUIRE(w && v && g && out, "bzpf_pwa_avg: NULL pointer");
-  REQUIRE(reinterpret_cast<uintptr_t>(w) % 16 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0 && ldv % 4 == 0,
-          "bzpf_pwa_avg: w and v must be 16-byte aligned and ldv a multiple of 4");
+  REQUIRE(wp && v && g && out, "bzpf_pwa_avg: NULL pointer");
+  REQUIRE(reinterpret_cast<uintptr_t>(wp) % 16 == 0 && reinterpret_cast<uintptr_t>(v) % 16 == 0 && ldv % 4 == 0,
+          "bzpf_pwa_avg: wp and v must be 16-byte aligned and ldv a multiple of 4");
   REQUIRE(n_seq >= 1 && n_seq <= 4 * 65535 && N >= 1 && H >= 1 && H <= 65535 && ldw >= N && ldw % 16 == 0 &&
               ldv >= 32 * H && ldg >= 32 * H && ldo >= 32 * H,
           "bzpf_pwa_avg: bad sizes (n_seq=%d N=%d H=%d)", n_seq, N, H);
-  return done(bzpf::launch_pwa_avg(w, ldw, v, ldv, g, ldg, out, ldo, n_seq, N, H, S(stream)), "bzpf_pwa_avg");
+  return done(bzpf::launch_pwa_avg(wp, ldw, v, ldv, g, ldg, out, ldo, n_seq, N, H, S(stream)), "bzpf_pwa_avg");
 }
 
 int bzpf_pair_bias(const float* z, const float* ln_w, const float* ln_b, float eps, const void* w, void* out, int dt,

@@ -85,7 +85,9 @@ hipError_t launch_opm_outer(const void* planes, const float* num, void* out, int
                             int n_i, hipStream_t st);
 hipError_t launch_pwa_softmax(const float* logits, const float* pm, float inf, float* w, int N, int64_t ldw, int H,
                               hipStream_t st);
-hipError_t launch_pwa_avg(const float* w, int64_t ldw, const float* v, int64_t ldv, const float* g, int64_t ldg,
+int64_t pwa_wsplit_bytes(int N, int64_t ldw, int H);
+hipError_t launch_pwa_wsplit(const float* w, int64_t ldw, void* wp, int N, int H, hipStream_t st);
+hipError_t launch_pwa_avg(const void* wp, int64_t ldw, const float* v, int64_t ldv, const float* g, int64_t ldg,
                           float* out, int64_t ldo, int S, int N, int H, hipStream_t st);
 hipError_t launch_trimul_pack(const void* P, const float* mask, float scale, int incoming, void* ab, int dt,
                               int64_t N, int64_t ld, int D, hipStream_t st);

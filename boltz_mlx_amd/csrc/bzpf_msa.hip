@@ -8,79 +8,22 @@
 //                 boltz_mlx/kernels_msa.py:292-343), stored fp16 (the proj_o GEMM's operand) or fp32;
 //   pwa_softmax : w[h][i][j] = softmax_j(logit[h][i][j] + (1 - pair_mask[i][j]) * -inf), rows padded with zeros
 //                 to ldw (boltz_mlx/layers/pair_averaging.py:43-49, kernels_msa.py:461-500);
+//   pwa_wsplit  : the weights w as bf16 part chunks for pwa_avg;
 //   pwa_avg     : out[s][i][h 32 + d] = sigmoid(g[s][i][h 32 + d]) * sum_j w[h][i][j] v[s][j][h 32 + d]
 //                 (pair_averaging.py:50-57, kernels_msa.py:620-653).
 #include "bzpf_common.h"
 #include "bzpf_kernels.h"
+#include "bzpf_x3.h"
 
 namespace bzpf {
 
 namespace {
 
-// Both reductions run on the bf16 matrix cores at fp32 accuracy. Each fp32 operand value is split exactly into three
-// bf16 parts, x = x1 + x2 + x3 (x1 the round-to-nearest-even of x, x2 of x - x1, x3 = x - x1 - x2: 8 significant
-// bits each, 24 together), and a product is taken as the six part products x_a y_b with a + b <= 4, accumulated in
-// fp32 by v_mfma_f32_32x32x16_bf16 (exact bf16 products, fp32 sums); the three left out (x2 y3, x3 y2, x3 y3) are
-// below 2^-23 of |x y| together. That is the fp32 matrix cores' accuracy at 6 / 16 of their time (the bf16 rate is
-// 16 times the fp32 one). A 256-thread workgroup computes a 128 x 128 tile, 4 waves of 64 x 64 (2 x 2 blocks of
-// 32 x 32), over K stages of 16 (one MFMA K-step), two workgroups per CU. The outer sum takes its operands split
-// beforehand (one pass over the MSA) and copies them straight into LDS; the weighted average splits in the loop:
-// the loads of stages st + 1 and st + 2 are in registers while stage st computes, and each stage is then split into
-// its parts and stored as three K-contiguous planes per operand (LDS double-buffered, one barrier per stage).
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
-typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
-
-// Two values split at once: part p of both, packed (value 0 in the low half), one v_cvt_pk_bf16_f32 per part.
-struct Pair3 {
-  uint32_t p[3];
-};
-__device__ __forceinline__ uint32_t cvt_pair(float a, float b) {
-  return __builtin_bit_cast(uint32_t, bf16x2{(__bf16)a, (__bf16)b});
-}
-__device__ __forceinline__ Pair3 split3_pair(float x0, float x1) {
-#pragma clang fp contract(off)  // the parts are of the rounded x0, x1 (no product of the caller fused in)
-  Pair3 o;
-  o.p[0] = cvt_pair(x0, x1);
-  const float r0 = x0 - __uint_as_float(o.p[0] << 16), r1 = x1 - __uint_as_float(o.p[0] & 0xffff0000u);  // exact
-  o.p[1] = cvt_pair(r0, r1);
-  // exact: at most 8 significant bits are left
-  o.p[2] = cvt_pair(r0 - __uint_as_float(o.p[1] << 16), r1 - __uint_as_float(o.p[1] & 0xffff0000u));
-  return o;
-}
-
-// LDS plane layout shared by the two kernels: 128 rows (A rows or B columns) of KS = 16 bf16 at a pitch of 24.
-constexpr int KS = 16, LDP = KS + 8, PLANE = 128 * LDP;
-
-// The six part products of one 32 x 32 block for one K-step (smaller ones first).
-__device__ __forceinline__ f16x mfma_parts6(const bf16x8 (&a)[3], const bf16x8 (&b)[3], f16x c) {
-  c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], c, 0, 0, 0);
-  c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], c, 0, 0, 0);
-  c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], c, 0, 0, 0);
-  c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], c, 0, 0, 0);
-  c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], c, 0, 0, 0);
-  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], c, 0, 0, 0);
-}
-
-// One stage of a wave's 2 x 2 blocks: fragments of the three planes of A rows 64 wm + 32 bm + r32 and B rows
-// 64 wn + 32 bn + r32, k = 8 hl .. 8 hl + 7 (lane (r32, hl)).
-__device__ __forceinline__ void parts_stage(const __bf16* Ab, const __bf16* Bb, int wm, int wn, int r32, int hl,
-                                            f16x (&acc)[2][2]) {
-  bf16x8 fa[2][3], fb[2][3];
-#pragma unroll
-  for (int bm = 0; bm < 2; bm++)
-#pragma unroll
-    for (int p = 0; p < 3; p++)
-      fa[bm][p] = *reinterpret_cast<const bf16x8*>(Ab + p * PLANE + (64 * wm + 32 * bm + r32) * LDP + 8 * hl);
-#pragma unroll
-  for (int bn = 0; bn < 2; bn++)
-#pragma unroll
-    for (int p = 0; p < 3; p++)
-      fb[bn][p] = *reinterpret_cast<const bf16x8*>(Bb + p * PLANE + (64 * wn + 32 * bn + r32) * LDP + 8 * hl);
-#pragma unroll
-  for (int bm = 0; bm < 2; bm++)
-#pragma unroll
-    for (int bn = 0; bn < 2; bn++) acc[bm][bn] = mfma_parts6(fa[bm], fb[bn], acc[bm][bn]);
-}
+// Both reductions run on the bf16 matrix cores at fp32 accuracy (three exact bf16 parts per fp32 operand, six part
+// products: bzpf_x3.h). A 256-thread workgroup computes a 128 x 128 tile over K stages of 16 (one MFMA K-step), two
+// workgroups per CU. The outer sum takes both operands split beforehand (one pass over the MSA) and copies them
+// straight into LDS; the weighted average takes its weights split beforehand (pwa_wsplit_k) as register fragments
+// and splits the v columns in its loop.
 
 // ---------------------------------------------------------------- outer product mean
 // The outer sum takes its operands already split: a pass over the MSA writes the masked values
@@ -252,50 +195,63 @@ __global__ __launch_bounds__(256) void pwa_softmax_k(const float* __restrict__ l
   for (int j = l; j < ldw; j += 64) wr[j] = j < N ? expf(x[j] + (1.0f - mr[j]) * -inf - mx) * inv : 0.0f;
 }
 
+// The weights' parts for the average: chunk (h, ib, jg, p) at byte (((h NIB + ib) NJG + jg) 3 + p) 1024
+// (NIB = ceil(N / 32), NJG = ldw / 16 rounded up to even) holds part p of w[h][i][j] for rows i = 32 ib .. + 31 and
+// tokens j = 16 jg .. + 15 (zeros past N and past ldw), as 32 rows of 16 bf16, so a wave's 16-byte loads of one
+// chunk are one contiguous KB. A workgroup takes one (h, ib, jg) chunk triple: thread (row t / 8, token pair t % 8).
+__global__ __launch_bounds__(256) void pwa_wsplit_k(const float* __restrict__ w, int64_t ldw, __bf16* __restrict__ wp,
+                                                    int N, int nib, int njg) {
+  const int jg = (int)blockIdx.x, ib = (int)blockIdx.y, h = (int)blockIdx.z, t = threadIdx.x;
+  const int row = t >> 3, jp = t & 7, i = 32 * ib + row;
+  float2 x = {0.0f, 0.0f};
+  if (i < N && 16 * jg < ldw) x = *reinterpret_cast<const float2*>(w + ((int64_t)h * N + i) * ldw + 16 * jg + 2 * jp);
+  const Pair3 q = split3_pair(x.x, x.y);
+  char* base = reinterpret_cast<char*>(wp) + (((int64_t)h * nib + ib) * njg + jg) * 3 * 1024 + row * 32 + 4 * jp;
+#pragma unroll
+  for (int p = 0; p < 3; p++) *reinterpret_cast<uint32_t*>(base + p * 1024) = q.p[p];
+}
+
 // The average, on the three-part bf16 scheme above. Workgroup tile: rows i0 .. i0 + 127 of head h (A = w[h], k = j)
-// x four MSA rows s0 .. s0 + 3 times the head's 32 channels (B columns (s, d)); a stage is 16 tokens j. The w rows
-// arrive K-contiguous; the v rows arrive d-contiguous, so a thread takes two consecutive tokens of 4 channels and
-// stores each channel's pair of parts as one dword.
-__global__ __launch_bounds__(256, 2) void pwa_avg_k(const float* __restrict__ w, int64_t ldw,
+// x four MSA rows s0 .. s0 + 3 times the head's 32 channels (B columns (s, d)); a stage is 16 tokens j. Wave w takes
+// rows 32 w .. + 31 against all 128 columns (1 x 4 blocks, block bn = MSA row s0 + bn). The A parts come split from
+// pwa_wsplit_k (a weight serves every MSA-row tile, so it is split once, not once per tile) and a wave's A fragments
+// are loaded from them straight into registers, two stages ahead (each wave reads rows no other wave reads). The v
+// rows arrive d-contiguous, so a thread takes two consecutive tokens of 4 channels (two stages ahead in registers),
+// splits them and stores each channel's pair of parts as one dword of the K-contiguous B planes (LDS
+// double-buffered, one barrier per stage, two workgroups per CU).
+__global__ __launch_bounds__(256, 2) void pwa_avg_k(const __bf16* __restrict__ wp, int nib, int njg,
                                                     const float* __restrict__ v, int64_t ldv,
                                                     const float* __restrict__ g, int64_t ldg, float* __restrict__ out,
                                                     int64_t ldo, int S, int N) {
-  __shared__ LDS_ALIGN __bf16 As[2][3 * PLANE];
   __shared__ LDS_ALIGN __bf16 Bs[2][3 * PLANE];
   const int t = threadIdx.x, wave = t >> 6, l = t & 63, r32 = l & 31, hl = l >> 5;
-  const int wm = wave >> 1, wn = wave & 1;
   const int i0 = 128 * (int)blockIdx.x, s0 = 4 * (int)blockIdx.y, h = (int)blockIdx.z;
-  const float* wh = w + (int64_t)h * N * ldw;
-  // staging roles: A vector vv of thread t is row (t + 256 vv) / 4, tokens 4 ((t + 256 vv) % 4) .. + 3; the B item
-  // of thread t is MSA row s0 + t / 64, tokens 2 (t % 8) and 2 (t % 8) + 1, channels 4 ((t / 8) % 8) .. + 3
-  const int bp = t & 7, bq = (t >> 3) & 7, bs = t >> 6;
-  // two register sets carry the next two stages' values (their loads have two stages of compute to land)
-  f4 ra0[2], rb0[2], ra1[2], rb1[2];
-  // Loads without conditions: rows past N and MSA rows past S read the last valid ones (their outputs are not
-  // stored), and tokens past N read token N - 1's v, which meets w[i][j] = 0 there (w rows are zero past N).
-  const int sb = min(s0 + bs, S - 1);
-  auto gload = [&](f4 (&ra)[2], f4 (&rb)[2], int stage) {
-    const int j0 = stage * KS;
+  const int nst = njg;  // even (the split weights are zero in a padding stage)
+  // A fragment p of stage st: chunk (h, ib = 4 blockIdx.x + wave (clamped to the last; rows past N are zero), st, p),
+  // lane bytes 32 r32 + 16 hl
+  const int ib = min(4 * (int)blockIdx.x + wave, nib - 1);
+  const char* wa = reinterpret_cast<const char*>(wp) + ((int64_t)h * nib + ib) * njg * 3072 + r32 * 32 + 16 * hl;
+  typedef bf16x8 AFrag[3];
+  AFrag fa0, fa1;  // two named sets (an array indexed by the stage parity would live in scratch)
+  auto aload = [&](AFrag& fa, int st) {
+    st = min(st, nst - 1);  // loads past the last stage repeat it (never used)
 #pragma unroll
-    for (int vv = 0; vv < 2; vv++) {
-      const int e = t + 256 * vv, row = min(i0 + (e >> 2), N - 1), jq = e & 3;
-      ra[vv] = *reinterpret_cast<const f4*>(wh + (int64_t)row * ldw + j0 + 4 * jq);
-    }
+    for (int p = 0; p < 3; p++) fa[p] = *reinterpret_cast<const bf16x8*>(wa + ((int64_t)st * 3 + p) * 1024);
+  };
+  // B item of thread t: MSA row s0 + t / 64, tokens 2 (t % 8) and 2 (t % 8) + 1, channels 4 ((t / 8) % 8) .. + 3.
+  // Loads without conditions: MSA rows past S read the last valid one (their outputs are not stored), and tokens
+  // past N (and past the last stage) read token N - 1's v, which meets zero weights there.
+  const int bp = t & 7, bq = (t >> 3) & 7, bs = t >> 6;
+  const int sb = min(s0 + bs, S - 1);
+  f4 rb0[2], rb1[2];
+  auto gload = [&](f4 (&rb)[2], int stage) {
 #pragma unroll
     for (int b = 0; b < 2; b++) {
-      const int key = min(j0 + 2 * bp + b, N - 1);
+      const int key = min(stage * KS + 2 * bp + b, N - 1);
       rb[b] = *reinterpret_cast<const f4*>(v + ((int64_t)sb * N + key) * ldv + 32 * h + 4 * bq);
     }
   };
-  auto lstore = [&](const f4 (&ra)[2], const f4 (&rb)[2], int buf) {
-#pragma unroll
-    for (int vv = 0; vv < 2; vv++) {
-      const int e = t + 256 * vv, row = e >> 2, jq = e & 3;
-      const Pair3 x01 = split3_pair(ra[vv][0], ra[vv][1]), x23 = split3_pair(ra[vv][2], ra[vv][3]);
-      __bf16* dst = As[buf] + row * LDP + 4 * jq;
-#pragma unroll
-      for (int p = 0; p < 3; p++) *reinterpret_cast<uint2*>(dst + p * PLANE) = uint2{x01.p[p], x23.p[p]};
-    }
+  auto lstore = [&](const f4 (&rb)[2], int buf) {
 #pragma unroll
     for (int q = 0; q < 4; q++) {
       const Pair3 x = split3_pair(rb[0][q], rb[1][q]);
@@ -304,58 +260,71 @@ __global__ __launch_bounds__(256, 2) void pwa_avg_k(const float* __restrict__ w,
       for (int p = 0; p < 3; p++) *reinterpret_cast<uint32_t*>(dst + p * PLANE) = x.p[p];
     }
   };
-  f16x acc[2][2];
+  f16x acc[4];
 #pragma unroll
-  for (int a = 0; a < 2; a++)
+  for (int b = 0; b < 4; b++)
 #pragma unroll
-    for (int b = 0; b < 2; b++)
+    for (int e = 0; e < 16; e++) acc[b][e] = 0.0f;
+  // one stage: B fragments of columns 32 bn + r32 from the B planes, the six part products per block
+  auto compute = [&](const AFrag& fa, const __bf16* Bb) {
+    bf16x8 fb[4][3];
 #pragma unroll
-      for (int e = 0; e < 16; e++) acc[a][b][e] = 0.0f;
-  const int nst = (int)(ldw / KS);
-  gload(ra0, rb0, 0);
-  lstore(ra0, rb0, 0);
+    for (int bn = 0; bn < 4; bn++)
+#pragma unroll
+      for (int p = 0; p < 3; p++)
+        fb[bn][p] = *reinterpret_cast<const bf16x8*>(Bb + p * PLANE + (32 * bn + r32) * LDP + 8 * hl);
+#pragma unroll
+    for (int bn = 0; bn < 4; bn++) acc[bn] = mfma_parts6(fa, fb[bn], acc[bn]);
+  };
+  // the prologue issues its loads in the steps' order (B of stage 1, A of 1, B of 2, then A of 2 in step 0), so the
+  // first steps wait for the same loads as the later ones
+  aload(fa0, 0);
+  gload(rb0, 0);
+  lstore(rb0, 0);
   __syncthreads();
-  if (nst > 1) gload(ra0, rb0, 1);
-  if (nst > 2) gload(ra1, rb1, 2);
-  // stage st computes from buffer st & 1; the stores of stage st + 1 go to the other buffer, whose last reader (stage
-  // st - 1) every wave finished before the previous barrier
-  for (int st = 0; st < nst; st += 2) {
-    parts_stage(As[0], Bs[0], wm, wn, r32, hl, acc);
-    if (st + 1 < nst) lstore(ra0, rb0, 1);
+  __builtin_amdgcn_sched_barrier(0);
+  gload(rb0, 1);
+  aload(fa1, 1);
+  gload(rb1, 2);
+  __builtin_amdgcn_sched_barrier(0);
+  // step st: computes stage st (A set st & 1, B buffer st & 1) and then loads A of stage st + 2 into the set; stores
+  // B of stage st + 1 (in rn) into the other buffer, whose last reader (stage st - 1) every wave finished before the
+  // previous barrier (past the last stage: a buffer nobody reads); after the barrier rn takes B of stage st + 3
+  // (the scheduling barriers keep each step's work on its side of the barrier: a split hoisted from the next step
+  // would wait for that step's B loads, the youngest)
+  auto step = [&](int st, AFrag& fa, f4 (&rn)[2]) {
+    compute(fa, Bs[st & 1]);
+    aload(fa, st + 2);
+    lstore(rn, (st + 1) & 1);
     __syncthreads();
-    if (st + 3 < nst) gload(ra0, rb0, st + 3);
-    if (st + 1 < nst) {
-      parts_stage(As[1], Bs[1], wm, wn, r32, hl, acc);
-      if (st + 2 < nst) lstore(ra1, rb1, 0);
-      __syncthreads();
-      if (st + 4 < nst) gload(ra1, rb1, st + 4);
-    }
+    __builtin_amdgcn_sched_barrier(0);
+    gload(rn, st + 3);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  for (int st = 0; st < nst; st += 2) {
+    step(st, fa0, rb0);
+    step(st + 1, fa1, rb1);
   }
-  // block (bm, bn) register r: row i0 + 64 wm + 32 bm + 8 (r / 4) + 4 hl + r % 4, column 64 wn + 32 bn + r32 =
-  // (MSA row, channel d). All 32 gate values of a column are loaded (rows clamped to N - 1) before any is used, so
-  // their latencies overlap instead of following one another.
+  // block bn register r: row i0 + 32 wave + 8 (r / 4) + 4 hl + r % 4, MSA row s0 + bn, channel r32. The 16 gate
+  // values of a block are loaded (rows clamped to N - 1) before its first store, so their latencies overlap.
+  const int d = r32;
 #pragma unroll
-  for (int bn = 0; bn < 2; bn++) {
-    const int col = 64 * wn + 32 * bn + r32;
-    const int s = s0 + (col >> 5), d = col & 31;
+  for (int bn = 0; bn < 4; bn++) {
+    const int s = s0 + bn;
     if (s >= S) continue;  // wave-uniform
     const float* gs = g + (int64_t)s * N * ldg + 32 * h + d;
     float* os = out + (int64_t)s * N * ldo + 32 * h + d;
-    float gv[2][16];
+    float gv[16];
 #pragma unroll
-    for (int bm = 0; bm < 2; bm++)
+    for (int r = 0; r < 16; r++) {
+      const int i = i0 + 32 * wave + 8 * (r >> 2) + 4 * hl + (r & 3);
+      gv[r] = gs[(int64_t)(i < N ? i : N - 1) * ldg];
+    }
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int i = i0 + 64 * wm + 32 * bm + 8 * (r >> 2) + 4 * hl + (r & 3);
-        gv[bm][r] = gs[(int64_t)(i < N ? i : N - 1) * ldg];
-      }
-#pragma unroll
-    for (int bm = 0; bm < 2; bm++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int i = i0 + 64 * wm + 32 * bm + 8 * (r >> 2) + 4 * hl + (r & 3);
-        if (i < N) os[(int64_t)i * ldo] = acc[bm][bn][r] * sigmoidf_(gv[bm][r]);
-      }
+    for (int r = 0; r < 16; r++) {
+      const int i = i0 + 32 * wave + 8 * (r >> 2) + 4 * hl + (r & 3);
+      if (i < N) os[(int64_t)i * ldo] = acc[bn][r] * sigmoidf_(gv[r]);
+    }
   }
 }
 
@@ -396,14 +365,29 @@ hipError_t launch_pwa_softmax(const float* logits, const float* pm, float inf, f
   return hipGetLastError();
 }
 
-hipError_t launch_pwa_avg(const float* w, int64_t ldw, const float* v, int64_t ldv, const float* g, int64_t ldg,
+int64_t pwa_wsplit_bytes(int N, int64_t ldw, int H) {
+  return (int64_t)H * ((N + 31) / 32) * ((ldw / KS + 1) & ~1) * 3 * 1024;
+}
+
+hipError_t launch_pwa_wsplit(const float* w, int64_t ldw, void* wp, int N, int H, hipStream_t st) {
+  const auto al = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; };
+  if (N < 1 || H < 1 || H > 65535 || ldw < N || ldw % KS || ldw / KS > INT32_MAX || !al(w, 8) || !al(wp, 16))
+    return hipErrorInvalidValue;
+  const int nib = (N + 31) / 32, njg = (int)((ldw / KS + 1) & ~1);
+  pwa_wsplit_k<<<dim3((unsigned)njg, (unsigned)nib, (unsigned)H), 256, 0, st>>>(w, ldw, static_cast<__bf16*>(wp), N,
+                                                                                 nib, njg);
+  return hipGetLastError();
+}
+
+hipError_t launch_pwa_avg(const void* wp, int64_t ldw, const float* v, int64_t ldv, const float* g, int64_t ldg,
                           float* out, int64_t ldo, int S, int N, int H, hipStream_t st) {
   const auto al = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; };
-  if (S < 1 || N < 1 || H < 1 || ldw < N || ldw % KS || ldv % 4 || ldv < 32 * H || ldg < 32 * H ||
-      ldo < 32 * H || !al(w, 16) || !al(v, 16) || S > 4 * 65535 || H > 65535)
+  if (S < 1 || N < 1 || H < 1 || ldw < N || ldw % KS || ldw / KS > INT32_MAX || ldv % 4 || ldv < 32 * H ||
+      ldg < 32 * H || ldo < 32 * H || !al(wp, 16) || !al(v, 16) || S > 4 * 65535 || H > 65535)
     return hipErrorInvalidValue;
   const dim3 grid((unsigned)((N + 127) / 128), (unsigned)((S + 3) / 4), (unsigned)H);
-  pwa_avg_k<<<grid, 256, 0, st>>>(w, ldw, v, ldv, g, ldg, out, ldo, S, N);
+  pwa_avg_k<<<grid, 256, 0, st>>>(static_cast<const __bf16*>(wp), (N + 31) / 32, (int)((ldw / KS + 1) & ~1), v, ldv,
+                                  g, ldg, out, ldo, S, N);
   return hipGetLastError();
 }
 

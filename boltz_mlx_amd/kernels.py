@@ -712,9 +712,24 @@ def pwa_avg(w: torch.Tensor, v: torch.Tensor, g: torch.Tensor, S: int, N: int) -
             raise ValueError("pwa_avg: v and g must be fp32 [S * N, >= 32 H] views with unit column stride")
     if Nw != N or not w.is_contiguous():
         raise ValueError("pwa_avg: w must be the contiguous [H, N, ldw] output of pwa_softmax")
+    wp = pwa_wsplit(w)
     out = torch.empty((S * N, HC), dtype=torch.float32, device=v.device)
-    call("bzpf_pwa_avg", _p(w), ldw, _p(v), v.stride(0), _p(g), g.stride(0), _p(out), HC, S, N, H, _stream())
+    call("bzpf_pwa_avg", _p(wp), ldw, _p(v), v.stride(0), _p(g), g.stride(0), _p(out), HC, S, N, H, _stream())
     return out
+
+
+def pwa_wsplit(w: torch.Tensor) -> torch.Tensor:
+    """The weights w [H, N, ldw] of pwa_softmax as three exact bf16 parts in the chunks pwa_avg loads
+    ([H, ceil(N / 32), G, 3, 32, 16] bf16: head, 32-row block, 16-token stage (G = ldw / 16 rounded up to even, zeros
+    past N), part, row, token)."""
+    _dev(w)
+    H, N, ldw = w.shape
+    if w.dtype != torch.float32 or not w.is_contiguous() or ldw % 16 or ldw < N:
+        raise ValueError("pwa_wsplit: w must be the contiguous fp32 [H, N, ldw] output of pwa_softmax")
+    wp = torch.empty((H, (N + 31) // 32, (ldw // 16 + 1) // 2 * 2, 3, 32, 16), dtype=torch.bfloat16, device=w.device)
+    assert wp.numel() * 2 == _lib.load().bzpf_pwa_wsplit_bytes(N, ldw, H)
+    call("bzpf_pwa_wsplit", _p(w), ldw, _p(wp), N, H, _stream())
+    return wp
 
 
 def pair_bias(z: torch.Tensor, ln, w: torch.Tensor) -> torch.Tensor:

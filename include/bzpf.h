@@ -267,11 +267,20 @@ int bzpf_opm_outer(const void* planes, const float* num, void* out, int out_dt, 
 int bzpf_pwa_softmax(const float* logits, const float* pair_mask, float inf, float* w, int N, int64_t ldw, int H,
                      void* stream);
 
+/* The weights of bzpf_pwa_softmax (w fp32 [H, N, ldw]) as three exact bf16 parts w = w1 + w2 + w3 for
+ * bzpf_pwa_avg: wp (16-byte aligned, bzpf_pwa_wsplit_bytes(N, ldw, H) bytes) holds 1 KB chunk (h, ib, jg, p) at byte
+ * (((h * ceil(N / 32) + ib) * G + jg) * 3 + p) * 1024 (G = ldw / 16 rounded up to even): part p + 1 of w[h][i][j]
+ * for i = 32 ib .. + 31, j = 16 jg .. + 15 (zeros past N and past ldw), as 32 rows of 16 bf16. The weights' operand staging of kernels_msa.pwa_avg
+ * (boltz_mlx/kernels_msa.py:620-653). bzpf_pwa_wsplit_bytes returns -1 for bad sizes. */
+int64_t bzpf_pwa_wsplit_bytes(int N, int64_t ldw, int H);
+int bzpf_pwa_wsplit(const float* w, int64_t ldw, void* wp, int N, int H, void* stream);
+
 /* Pair-weighted average with its gate: out[s][i][h*32 + d] = sigmoid(g[s][i][h*32 + d]) *
- * sum_j w[h][i][j] v[s][j][h*32 + d] for w from bzpf_pwa_softmax and v, g, out fp32 rows (s, i) of pitch
- * ldv / ldg / ldo (fp32 MFMA accumulation). Replaces kernels_msa.pwa_avg (boltz_mlx/kernels_msa.py:620-653,
+ * sum_j w[h][i][j] v[s][j][h*32 + d] for the split weights wp of bzpf_pwa_wsplit (ldw as given there) and v, g, out
+ * fp32 rows (s, i) of pitch ldv / ldg / ldo. Each product is the six bf16 part products w_a v_b with a + b <= 4,
+ * accumulated in fp32 (fp32 accuracy). Replaces kernels_msa.pwa_avg (boltz_mlx/kernels_msa.py:620-653,
  * boltz_mlx/layers/pair_averaging.py:50-57). */
-int bzpf_pwa_avg(const float* w, int64_t ldw, const float* v, int64_t ldv, const float* g, int64_t ldg, float* out,
+int bzpf_pwa_avg(const void* wp, int64_t ldw, const float* v, int64_t ldv, const float* g, int64_t ldg, float* out,
                  int64_t ldo, int n_seq, int N, int H, void* stream);
 
 /* Pair bias out[h][r] = LN(z[r]; ln_w, ln_b, eps) . W[h] for r < rows (z fp32 [rows, D = 128], W [H, D], H <= 16).

@@ -117,6 +117,31 @@ def test_gemm_f16_tiles(R, Kd, M):
         assert O.metrics(f.double().cpu().numpy(), s.double().cpu().numpy())["max_rel"] <= 2e-3
 
 
+@pytest.mark.parametrize("R,Kd,M", [(1, 16, 1), (129, 48, 64), (4100, 64, 512), (3000, 256, 64), (257, 32, 200)])
+def test_linear_fp32_accuracy(R, Kd, M):
+    """fp32 linear (the fp32-MFMA kernel for K % 32 == 0, the generic one otherwise; row and column tiles cut short)
+    against float64 on the same fp32 values at fp32 accuracy, plain, with bias and accumulated; 0/1 operands (the
+    pair counts' mask^T mask) give exact integers."""
+    from boltz_mlx_amd import kernels as K
+
+    rng = np.random.default_rng(R * Kd + M)
+    x = rng.standard_normal((R, Kd)).astype(np.float32)
+    w = (rng.standard_normal((M, Kd)) / np.sqrt(Kd)).astype(np.float32)
+    b = rng.standard_normal(M).astype(np.float32)
+    y0 = rng.standard_normal((R, M)).astype(np.float32)
+    ref = x.astype(np.float64) @ w.astype(np.float64).T
+    y = K.linear(dev(x), dev(w)).cpu().numpy()
+    yb = K.linear(dev(x), dev(w), bias=dev(b)).cpu().numpy()
+    yacc = dev(y0)
+    K.linear(dev(x), dev(w), out=yacc, accumulate=True)
+    assert O.metrics(y, ref)["max_rel"] <= 1e-6
+    assert O.metrics(yb, ref + b)["max_rel"] <= 1e-6
+    assert O.metrics(yacc.cpu().numpy(), ref + y0)["max_rel"] <= 1e-6
+    xm = (rng.random((R, Kd)) > 0.3).astype(np.float32)
+    wm = (rng.random((M, Kd)) > 0.3).astype(np.float32)
+    assert np.array_equal(K.linear(dev(xm), dev(wm)).cpu().numpy(), xm @ wm.T)
+
+
 def test_gemm_f16_large_grid_tiles():
     """A grid of 2048+ 128 x 128 tiles takes the 128 x 128 kernel (smaller grids the 64 x 64 one): its rows equal
     the 64 x 64 kernel's on the same rows bit for bit (same k order per element), and the last row tile, cut short,

@@ -393,6 +393,19 @@ int bzpf_opm_outer(const void* planes, const float* num, void* out, int out_dt, 
   return done(bzpf::launch_opm_outer(planes, num, out, out_dt, n_seq, N, i_base, n_i, S(stream)), "bzpf_opm_outer");
 }
 
+int bzpf_ln_linear_f32(const float* x, const float* ln_w, const float* ln_b, float eps, const float* w, float* y,
+                       int64_t rows, int K, int M, void* stream) {
+  REQUIRE(x && ln_w && ln_b && w && y, "bzpf_ln_linear_f32: NULL pointer");
+  REQUIRE(K == 64 && M >= 256 && M % 256 == 0, "bzpf_ln_linear_f32: need K = 64 and M a multiple of 256 (K=%d M=%d)",
+          K, M);
+  REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(w) % 16 == 0 &&
+              reinterpret_cast<uintptr_t>(ln_w) % 16 == 0 && reinterpret_cast<uintptr_t>(ln_b) % 16 == 0,
+          "bzpf_ln_linear_f32: x, w, ln_w and ln_b must be 16-byte aligned");
+  REQUIRE(rows >= 0, "bzpf_ln_linear_f32: rows < 0");
+  if (rows == 0) return BZPF_OK;
+  return done(bzpf::launch_ln_linear_x3(x, ln_w, ln_b, eps, w, y, rows, K, M, S(stream)), "bzpf_ln_linear_f32");
+}
+
 int bzpf_pwa_softmax(const float* logits, const float* pair_mask, float inf, float* w, int N, int64_t ldw, int H,
                      void* stream) {
   REQUIRE(logits && pair_mask && w, "bzpf_pwa_softmax: NULL pointer");

@@ -1,0 +1,150 @@
+// The MSA track's input projection, LayerNorm and Linear in one kernel at fp32 accuracy:
+//   y[r][m] = LN(x[r]; ln_w, ln_b, eps) . W[m]   for fp32 x [R, 64], W [M, 64] (M a multiple of 256), y [R, M]
+// (PairWeightedAveraging's norm_m + proj_m | proj_g, boltz_mlx/layers/pair_averaging.py:36-41, fp32 in both
+// precision modes). The LayerNorm is the arithmetic of bzpf_layernorm (16 lanes per row, the same sums), so its
+// output is the same fp32 values; the product runs on the bf16 matrix cores with both operands split into three
+// exact bf16 parts (bzpf_x3.h). The projection has K = 64 and writes M fp32 values per row, so it is bound by its
+// stores: the kernel is persistent, one 8-wave workgroup per CU, with a 256-column block of W split into LDS once,
+// and each 128-row tile's x rows loaded while the previous tile computes and stores.
+#include "bzpf_common.h"
+#include "bzpf_kernels.h"
+#include "bzpf_rowgemm.h"
+#include "bzpf_x3.h"
+
+namespace bzpf {
+
+namespace {
+
+constexpr int LNP_K = 64, LNP_BR = 128, LNP_BC = 256;  // channels, rows per tile, columns per workgroup
+constexpr int LNP_ROWB = 2 * LNP_K;                    // bytes of one plane row (64 bf16)
+
+// Byte offset of 16-byte chunk c (k = 8 c .. 8 c + 7) of plane row r: the chunks of a row are permuted by r % 8, so
+// the fragment reads (8 lanes on 8 consecutive rows at one logical chunk) hit distinct banks.
+__device__ __forceinline__ int lnp_off(int r, int c) { return r * LNP_ROWB + 16 * (c ^ (r & 7)); }
+
+// Workgroup b takes column block cb = b % ncb and the row tiles b / ncb, b / ncb + gridDim.x / ncb, ... Wave
+// (wr, wc) = (wave / 4, wave % 4) computes rows 64 wr .. + 63 x columns 64 wc .. + 63 of the tile (2 x 2 blocks).
+__global__ __launch_bounds__(512, 1) void ln_linear_x3_k(const float* __restrict__ x, const float* __restrict__ lnw,
+                                                         const float* __restrict__ lnb, float eps,
+                                                         const float* __restrict__ w, float* __restrict__ y,
+                                                         int64_t R, int M, int ncb, int nrt) {
+  __shared__ __attribute__((aligned(16))) char Ws[3 * LNP_BC * LNP_ROWB];  // 96 KB: the W block's three planes
+  __shared__ __attribute__((aligned(16))) char Xs[3 * LNP_BR * LNP_ROWB];  // 48 KB: the tile's LN(x) planes
+  const int t = threadIdx.x, wave = t >> 6, l = t & 63, r32 = l & 31, hl = l >> 5;
+  const int wr = wave >> 2, wc = wave & 3;
+  const int cb = (int)blockIdx.x % ncb, m0 = cb * LNP_BC;
+  // the W block, split once: f4 item e = t + 512 v is row e / 16 (clamped to M - 1), k = 4 (e % 16) .. + 3
+#pragma unroll
+  for (int v = 0; v < 8; v++) {
+    const int e = t + 512 * v, row = e >> 4, kq = e & 15;
+    const f4 a = *reinterpret_cast<const f4*>(w + (int64_t)min(m0 + row, M - 1) * LNP_K + 4 * kq);
+    const Pair3 q01 = split3_pair(a[0], a[1]), q23 = split3_pair(a[2], a[3]);
+#pragma unroll
+    for (int p = 0; p < 3; p++)
+      *reinterpret_cast<uint2*>(Ws + p * LNP_BC * LNP_ROWB + lnp_off(row, kq >> 1) + 8 * (kq & 1)) =
+          uint2{q01.p[p], q23.p[p]};
+  }
+  // x rows: pass v takes tile row t / 16 + 32 v, lane c = t % 16 channels 4 c .. + 3 (rows past R read row R - 1;
+  // their outputs are not stored)
+  const int xc = t & 15, xrow = t >> 4;
+  const f4 gw = *reinterpret_cast<const f4*>(lnw + 4 * xc), gb = *reinterpret_cast<const f4*>(lnb + 4 * xc);
+  f4 xv[4];
+  auto xload = [&](int rt) {
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const int64_t r = min((int64_t)rt * LNP_BR + xrow + 32 * v, R - 1);
+      xv[v] = *reinterpret_cast<const f4*>(x + r * LNP_K + 4 * xc);
+    }
+  };
+  // LN (bzpf_layernorm's order of operations), then the split into the X planes
+  auto xstage = [&]() {
+#pragma unroll
+    for (int v = 0; v < 4; v++) {
+      const f4 a = xv[v];
+      float s = 0.f;
+      s += a[0] + a[1] + a[2] + a[3];
+      const float mean = group_sum<16>(s) * (1.0f / LNP_K);
+      float ss = 0.f;
+      const f4 d = a - mean;
+      ss += d[0] * d[0] + d[1] * d[1] + d[2] * d[2] + d[3] * d[3];
+      const float rstd = 1.0f / sqrtf(group_sum<16>(ss) * (1.0f / LNP_K) + eps);
+      f4 o = (a - mean) * rstd;
+      o *= gw;
+      o += gb;
+      const Pair3 q01 = split3_pair(o[0], o[1]), q23 = split3_pair(o[2], o[3]);
+      const int row = xrow + 32 * v;
+#pragma unroll
+      for (int p = 0; p < 3; p++)
+        *reinterpret_cast<uint2*>(Xs + p * LNP_BR * LNP_ROWB + lnp_off(row, xc >> 1) + 8 * (xc & 1)) =
+            uint2{q01.p[p], q23.p[p]};
+    }
+  };
+  const int rstep = (int)gridDim.x / ncb;
+  int rt = (int)blockIdx.x / ncb;
+  if (rt < nrt) xload(rt);
+  for (; rt < nrt; rt += rstep) {  // workgroup-uniform
+    xstage();
+    __syncthreads();  // the X planes (and, the first time, the W planes) are complete
+    if (rt + rstep < nrt) xload(rt + rstep);
+    f16x acc[2][2];
+#pragma unroll
+    for (int a = 0; a < 2; a++)
+#pragma unroll
+      for (int b = 0; b < 2; b++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) acc[a][b][e] = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < LNP_K / 16; kk++) {
+      bf16x8 fa[2][3], fb[2][3];
+#pragma unroll
+      for (int bm = 0; bm < 2; bm++)
+#pragma unroll
+        for (int p = 0; p < 3; p++)
+          fa[bm][p] = *reinterpret_cast<const bf16x8*>(Xs + p * LNP_BR * LNP_ROWB +
+                                                       lnp_off(64 * wr + 32 * bm + r32, 2 * kk + hl));
+#pragma unroll
+      for (int bn = 0; bn < 2; bn++)
+#pragma unroll
+        for (int p = 0; p < 3; p++)
+          fb[bn][p] = *reinterpret_cast<const bf16x8*>(Ws + p * LNP_BC * LNP_ROWB +
+                                                       lnp_off(64 * wc + 32 * bn + r32, 2 * kk + hl));
+#pragma unroll
+      for (int bm = 0; bm < 2; bm++)
+#pragma unroll
+        for (int bn = 0; bn < 2; bn++) acc[bm][bn] = mfma_parts6(fa[bm], fb[bn], acc[bm][bn]);
+    }
+    // block (bm, bn) register e: tile row 64 wr + 32 bm + 8 (e / 4) + 4 hl + e % 4, column m0 + 64 wc + 32 bn + r32
+#pragma unroll
+    for (int bn = 0; bn < 2; bn++) {
+      const int col = m0 + 64 * wc + 32 * bn + r32;
+#pragma unroll
+      for (int bm = 0; bm < 2; bm++)
+#pragma unroll
+        for (int e = 0; e < 16; e++) {
+          const int64_t row = (int64_t)rt * LNP_BR + 64 * wr + 32 * bm + 8 * (e >> 2) + 4 * hl + (e & 3);
+          if (row < R && col < M) y[row * M + col] = acc[bm][bn][e];
+        }
+    }
+    __syncthreads();  // every wave has read the X planes before the next tile's are written
+  }
+}
+
+}  // namespace
+
+hipError_t launch_ln_linear_x3(const float* x, const float* lnw, const float* lnb, float eps, const float* w, float* y,
+                               int64_t R, int K, int M, hipStream_t st) {
+  const auto al = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; };
+  if (R < 1 || K != LNP_K || M < LNP_BC || M % LNP_BC || !lnw || !lnb || !al(x, 16) || !al(w, 16) || !al(lnw, 16) ||
+      !al(lnb, 16) || (R + LNP_BR - 1) / LNP_BR > INT32_MAX)
+    return hipErrorInvalidValue;
+  static int cache[kMaxDevices];
+  const int resident = resident_grid(ln_linear_x3_k, 512, cache);
+  if (resident <= 0) return hipErrorInvalidDevice;
+  const int ncb = M / LNP_BC, nrt = (int)((R + LNP_BR - 1) / LNP_BR);
+  // whole groups of ncb workgroups (one per column block), no more row-tile slots than row tiles
+  const int per_cb = max(1, min(nrt, resident / ncb));
+  ln_linear_x3_k<<<ncb * per_cb, 512, 0, st>>>(x, lnw, lnb, eps, w, y, R, M, ncb, nrt);
+  return hipGetLastError();
+}
+
+}  // namespace bzpf

@@ -687,6 +687,22 @@ def opm_outer(ab: torch.Tensor, mask: torch.Tensor, i_base: int = 0, n_i: int | 
     return out
 
 
+def ln_linear_f32(x: torch.Tensor, ln, w: torch.Tensor) -> torch.Tensor:
+    """LN(x; ln.weight, ln.bias, ln.eps) w^T for fp32 x [rows, 64] and fp32 w [M, 64] (M a multiple of 256) in one
+    kernel (the LayerNorm of bzpf_layernorm, the product at fp32 accuracy) -> [rows, M] fp32
+    (pair_averaging.py:36-41)."""
+    _dev(x, w)
+    rows, Kd = x.shape
+    M = w.shape[0]
+    if x.dtype != torch.float32 or w.dtype != torch.float32 or Kd != 64 or w.shape[1] != 64 or M % 256 \
+            or not x.is_contiguous() or not w.is_contiguous():
+        raise ValueError("ln_linear_f32: need contiguous fp32 x [rows, 64] and w [M, 64] with M % 256 == 0")
+    lw, lb = f32c(ln.weight), f32c(ln.bias)
+    y = torch.empty((rows, M), dtype=torch.float32, device=x.device)
+    call("bzpf_ln_linear_f32", _p(x), _p(lw), _p(lb), float(ln.eps), _p(w), _p(y), rows, 64, M, _stream())
+    return y
+
+
 def pwa_softmax(logits: torch.Tensor, pair_mask: torch.Tensor, inf: float) -> torch.Tensor:
     """softmax_j(logits[h, i, j] + (1 - pair_mask[i, j]) * -inf) for fp32 logits [H, N, N] as [H, N, ldw] with
     ldw = N rounded up to 16 and zeros past N (pair_averaging.py:43-49)."""

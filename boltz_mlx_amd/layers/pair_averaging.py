@@ -1,10 +1,11 @@
 """PairWeightedAveraging on the bzpf kernels: same constructor, parameter names and call signature as
 boltz_mlx/layers/pair_averaging.py:10-59 (inference).
 
-  v | g = LN(m) [W_m; W_g]^T                              bzpf_layernorm + bzpf_linear (fp32)
+  v | g = LN(m) [W_m; W_g]^T                              bzpf_ln_linear_f32 (one kernel; fp32 accuracy)
   logits = LN(z) W_z^T                                      bzpf_pair_bias (fp32 statistics and logits)
   w = softmax_j(logits + (1 - pair_mask) * -inf)            bzpf_pwa_softmax
-  o = sigmoid(g) * sum_j w[h, i, j] v[s, j, h]              bzpf_pwa_avg (fp32 MFMA)
+  o = sigmoid(g) * sum_j w[h, i, j] v[s, j, h]              bzpf_pwa_wsplit + bzpf_pwa_avg (fp32 accuracy on the
+                                                            bf16 matrix cores: three exact parts per operand)
   out (+)= o W_o^T                                          bzpf_linear (fp32)
 In f16 mode W_z is the fp16 weight copy (upcast; the logits stay fp32) and proj_m / proj_g / proj_o stay fp32, as in
 the reference's fused path (pair_averaging.py:61-77).
@@ -51,9 +52,11 @@ class PairWeightedAveraging(torch.nn.Module):
         HC = self.c_h * self.num_heads
         w_mg, w_o = K.kernel_weight(self, "w_mg"), K.kernel_weight(self, "w_o")
         w_z = K.kernel_weight(self, "w_z").float()
-        mn = K.layer_norm(m.reshape(S * N, self.c_m).to(torch.float32), self.norm_m.weight, self.norm_m.bias,
-                          self.norm_m.eps)
-        vg = K.linear(mn, w_mg)
+        m2 = m.reshape(S * N, self.c_m).to(torch.float32)
+        if self.c_m == 64 and (2 * HC) % 256 == 0:
+            vg = K.ln_linear_f32(m2.contiguous(), self.norm_m, w_mg)
+        else:
+            vg = K.linear(K.layer_norm(m2, self.norm_m.weight, self.norm_m.bias, self.norm_m.eps), w_mg)
         logits = K.pair_bias(z.to(torch.float32).contiguous(), self.norm_z, w_z)
         w = K.pwa_softmax(logits, pair_mask.to(torch.float32).contiguous(), self.inf)
         og = K.pwa_avg(w, vg[:, :HC], vg[:, HC:], S, N)

@@ -260,6 +260,14 @@ int bzpf_opm_split(const float* ab, int64_t ld_ab, const float* mask, void* plan
 int bzpf_opm_outer(const void* planes, const float* num, void* out, int out_dt, int n_seq, int N, int i_base, int n_i,
                    void* stream);
 
+/* The MSA track's LayerNorm + fp32 Linear in one kernel: y[r][m] = LN(x[r]; ln_w, ln_b, eps) . W[m] for x fp32
+ * [rows, K = 64], W fp32 [M, 64] (M a multiple of 256), y fp32 [rows, M]. The LayerNorm is bzpf_layernorm's arithmetic;
+ * each product is the six bf16 part products of the three-part split (fp32 accuracy). Replaces norm_m + proj_m |
+ * proj_g of PairWeightedAveraging (boltz_mlx/layers/pair_averaging.py:36-41): bzpf_layernorm + bzpf_linear without
+ * the [rows, 64] intermediate. */
+int bzpf_ln_linear_f32(const float* x, const float* ln_w, const float* ln_b, float eps, const float* w, float* y,
+                       int64_t rows, int K, int M, void* stream);
+
 /* Pair-weighted-averaging weights: w[h][i][j] = softmax_j(logits[h][i][j] + (1 - pair_mask[i][j]) * -inf) for
  * logits fp32 [H, N, N], pair_mask fp32 [N, N]; w fp32 [H, N, ldw] with zeros for N <= j < ldw (ldw a multiple of
  * 16 and >= N). Replaces the softmax of kernels_msa.pwa_weights (boltz_mlx/kernels_msa.py:461-500,

@@ -47,6 +47,12 @@ def test_library_host_only_calls():
     assert rc == -1 and b"xn" in lib.bzpf_last_error()
     rc = lib.bzpf_triattn_proj(None, None, 0, 1.0, 1.0, None, None, None, 0, 10, 64, 128, 4, 32, None)
     assert rc == -1
+    # the weight-split size: 3 KB per (head, 32-row block, 16-token stage), stages rounded up to even
+    assert lib.bzpf_pwa_wsplit_bytes(400, 400, 8) == 8 * 13 * 26 * 3072
+    assert lib.bzpf_pwa_wsplit_bytes(37, 48, 8) == 8 * 2 * 4 * 3072
+    assert lib.bzpf_pwa_wsplit_bytes(37, 40, 8) == -1 and lib.bzpf_pwa_wsplit_bytes(50, 48, 8) == -1
+    rc = lib.bzpf_opm_split(None, 64, None, None, 10, 10, None)
+    assert rc == -1 and b"NULL" in lib.bzpf_last_error()
 
 
 def test_header_signatures_match_ctypes():

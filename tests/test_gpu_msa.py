@@ -130,6 +130,51 @@ def test_pwa_weights(N, wdt):
     assert m["rel_fro"] < 1e-5 and m["max_rel"] < 1e-5, m
 
 
+@pytest.mark.parametrize("N", [37, 64, 130])
+def test_pwa_wsplit_parts_and_layout(N):
+    """The weight chunks hold w = w1 + w2 + w3 (w1 = bf16(w), w2 = bf16(w - w1), w3 the exact rest) with chunk
+    (h, ib, jg, p) = part p of rows 32 ib .. + 31 and tokens 16 jg .. + 15, zeros past N and in the padding stage."""
+    from boltz_mlx_amd import kernels as K
+
+    rng = np.random.default_rng(N)
+    H, ldw = 8, (N + 15) // 16 * 16
+    w = np.zeros((H, N, ldw), np.float32)
+    x = rng.random((H, N, N)).astype(np.float32)
+    w[:, :, :N] = x / x.sum(-1, keepdims=True)
+    got = K.pwa_wsplit(dev(w)).cpu()
+    nib, G = (N + 31) // 32, (ldw // 16 + 1) // 2 * 2
+    assert got.shape == (H, nib, G, 3, 32, 16)
+    full = torch.zeros((H, nib * 32, G * 16))
+    full[:, :N, :ldw] = torch.from_numpy(w)
+    p1 = full.to(torch.bfloat16)
+    p2 = (full - p1.float()).to(torch.bfloat16)
+    p3 = (full - p1.float() - p2.float()).to(torch.bfloat16)
+    assert torch.equal(p1.float() + p2.float() + p3.float(), full)
+    # [H, nib * 32, G * 16] per part -> [H, ib, jg, part, row, token]
+    want = torch.stack([p1, p2, p3]).view(3, H, nib, 32, G, 16).permute(1, 2, 4, 0, 3, 5)
+    assert torch.equal(got.view(torch.int16), want.contiguous().view(torch.int16))
+
+
+@pytest.mark.parametrize("rows,M", [(1, 256), (300, 512), (4100, 512), (129, 768)])
+def test_ln_linear_f32(rows, M):
+    """The fused LayerNorm + projection against bzpf_layernorm's fp32 output times W in float64: the LayerNorm is the
+    same arithmetic, the product fp32-accurate (row tiles cut short, one to three column blocks)."""
+    from boltz_mlx_amd import kernels as K
+
+    rng = np.random.default_rng(rows + M)
+    x = (rng.standard_normal((rows, 64)) * 2 + 0.3).astype(np.float32)
+    w = (rng.standard_normal((M, 64)) / 8).astype(np.float32)
+
+    class LN:
+        weight = dev(1 + 0.1 * rng.standard_normal(64))
+        bias = dev(0.1 * rng.standard_normal(64))
+        eps = 1e-5
+
+    got = K.ln_linear_f32(dev(x), LN, dev(w)).cpu().numpy()
+    xn = K.layer_norm(dev(x), LN.weight, LN.bias, LN.eps).cpu().numpy().astype(np.float64)
+    assert O.metrics(got, xn @ w.astype(np.float64).T)["max_rel"] <= 1e-6
+
+
 @pytest.mark.parametrize("S,N", [(249, 37), (1, 130), (7, 64), (6, 200)])
 def test_pwa_avg(S, N):
     from boltz_mlx_amd import kernels as K

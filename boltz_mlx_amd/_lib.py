@@ -45,6 +45,7 @@ SIGNATURES = {
     "bzpf_channels_to_rows": [vp, i32, vp, i32, i64, i64, i32, vp],
     "bzpf_triattn_pack": [vp, i32, f32, f32, vp, vp, vp, i32, i64, i64, i32, i32, vp],
     "bzpf_opm_split": [vp, i64, vp, vp, i32, i32, vp],
+    "bzpf_opm_ln_split": [vp, vp, vp, f32, vp, vp, vp, i32, i32, vp],
     "bzpf_opm_outer": [vp, vp, vp, i32, i32, i32, i32, i32, vp],
     "bzpf_pwa_softmax": [vp, vp, f32, vp, i32, i64, i32, vp],
     "bzpf_ln_linear_f32": [vp, vp, vp, f32, vp, vp, i64, i32, i32, vp],

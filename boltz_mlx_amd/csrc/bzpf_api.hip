@@ -382,6 +382,19 @@ int bzpf_opm_split(const float* ab, int64_t ld_ab, const float* mask, void* plan
   return done(bzpf::launch_opm_split(ab, ld_ab, mask, planes, n_seq, N, S(stream)), "bzpf_opm_split");
 }
 
+int bzpf_opm_ln_split(const float* m, const float* ln_w, const float* ln_b, float eps, const float* w_ab,
+                      const float* mask, void* planes, int n_seq, int N, void* stream) {
+  REQUIRE(m && ln_w && ln_b && w_ab && mask && planes, "bzpf_opm_ln_split: NULL pointer");
+  REQUIRE(reinterpret_cast<uintptr_t>(m) % 16 == 0 && reinterpret_cast<uintptr_t>(w_ab) % 16 == 0 &&
+              reinterpret_cast<uintptr_t>(ln_w) % 16 == 0 && reinterpret_cast<uintptr_t>(ln_b) % 16 == 0 &&
+              reinterpret_cast<uintptr_t>(planes) % 16 == 0,
+          "bzpf_opm_ln_split: m, w_ab, ln_w, ln_b and planes must be 16-byte aligned");
+  REQUIRE(n_seq >= 1 && n_seq <= 16 * 65535 && N >= 1 && (int64_t)N * 6144 <= INT32_MAX,
+          "bzpf_opm_ln_split: bad sizes (n_seq=%d N=%d)", n_seq, N);
+  return done(bzpf::launch_opm_ln_split(m, ln_w, ln_b, eps, w_ab, mask, planes, n_seq, N, S(stream)),
+              "bzpf_opm_ln_split");
+}
+
 int bzpf_opm_outer(const void* planes, const float* num, void* out, int out_dt, int n_seq, int N, int i_base,
                    int n_i, void* stream) {
   REQUIRE(planes && num && out, "bzpf_opm_outer: NULL pointer");

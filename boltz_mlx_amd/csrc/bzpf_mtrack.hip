@@ -129,7 +129,142 @@ __global__ __launch_bounds__(512, 1) void ln_linear_x3_k(const float* __restrict
   }
 }
 
+// The outer-product-mean operands from the MSA in one kernel: x = mask[s][n] (LN(m[s][n]) . W_ab[ch]) for the 64
+// channels ch (a = 0..31, b = 32..63), fp32-accurate as above, written as the three bf16 parts in the chunk layout
+// of bzpf_opm_split (chunk (g, n, p, h) at byte ((g N + n) 6 + 2 p + h) 1024: 32 channel rows of 16 MSA rows, zeros
+// past S). Replaces bzpf_layernorm + bzpf_linear (a | b) + bzpf_opm_split. A tile is stage g (MSA rows 16 g .. + 15)
+// of tokens 8 nb .. + 7: tile row 16 tl + k is (s = 16 g + k, n = 8 nb + tl). Wave w computes tile rows 32 w .. + 31
+// (tokens 2 w, 2 w + 1) against the 64 channels (blocks h = a, b), so its accumulators hold whole chunk rows.
+__global__ __launch_bounds__(256, 2) void opm_ln_split_k(const float* __restrict__ m, const float* __restrict__ lnw,
+                                                         const float* __restrict__ lnb, float eps,
+                                                         const float* __restrict__ w, const float* __restrict__ mask,
+                                                         __bf16* __restrict__ planes, int S, int N, int nnb,
+                                                         int ntiles) {
+  __shared__ __attribute__((aligned(16))) char Ws[3 * 64 * LNP_ROWB];      // 24 KB: W_ab's three planes
+  __shared__ __attribute__((aligned(16))) char Xs[3 * LNP_BR * LNP_ROWB];  // 48 KB: the tile's LN(m) planes
+  __shared__ float Ms[LNP_BR];                                             // the tile rows' mask values
+  const int t = threadIdx.x, wave = t >> 6, l = t & 63, r32 = l & 31, hl = l >> 5;
+  // W_ab split once: f4 item e = t + 256 v is row e / 16, k = 4 (e % 16) .. + 3
+#pragma unroll
+  for (int v = 0; v < 4; v++) {
+    const int e = t + 256 * v, row = e >> 4, kq = e & 15;
+    const f4 a = *reinterpret_cast<const f4*>(w + row * LNP_K + 4 * kq);
+    const Pair3 q01 = split3_pair(a[0], a[1]), q23 = split3_pair(a[2], a[3]);
+#pragma unroll
+    for (int p = 0; p < 3; p++)
+      *reinterpret_cast<uint2*>(Ws + p * 64 * LNP_ROWB + lnp_off(row, kq >> 1) + 8 * (kq & 1)) =
+          uint2{q01.p[p], q23.p[p]};
+  }
+  // m rows: pass v takes tile row t / 16 + 16 v, lane c = t % 16 channels 4 c .. + 3 (rows past S or N read a valid
+  // row; past S their mask is taken as 0, past N their outputs are not stored)
+  const int xc = t & 15, xr = t >> 4;
+  const f4 gw = *reinterpret_cast<const f4*>(lnw + 4 * xc), gb = *reinterpret_cast<const f4*>(lnb + 4 * xc);
+  f4 xv[8];
+  float mv[8];
+  auto xload = [&](int tile) {
+    const int g = tile / nnb, nb = tile % nnb;
+#pragma unroll
+    for (int v = 0; v < 8; v++) {
+      const int row = xr + 16 * v, s = 16 * g + (row & 15), n = min(8 * nb + (row >> 4), N - 1);
+      const int64_t src = (int64_t)min(s, S - 1) * N + n;
+      xv[v] = *reinterpret_cast<const f4*>(m + src * LNP_K + 4 * xc);
+      const float mk = mask[src];
+      mv[v] = s < S ? mk : 0.0f;
+    }
+  };
+  auto xstage = [&]() {
+#pragma unroll
+    for (int v = 0; v < 8; v++) {
+      const f4 a = xv[v];
+      float s = 0.f;
+      s += a[0] + a[1] + a[2] + a[3];
+      const float mean = group_sum<16>(s) * (1.0f / LNP_K);
+      float ss = 0.f;
+      const f4 d = a - mean;
+      ss += d[0] * d[0] + d[1] * d[1] + d[2] * d[2] + d[3] * d[3];
+      const float rstd = 1.0f / sqrtf(group_sum<16>(ss) * (1.0f / LNP_K) + eps);
+      f4 o = (a - mean) * rstd;
+      o *= gw;
+      o += gb;
+      const Pair3 q01 = split3_pair(o[0], o[1]), q23 = split3_pair(o[2], o[3]);
+      const int row = xr + 16 * v;
+#pragma unroll
+      for (int p = 0; p < 3; p++)
+        *reinterpret_cast<uint2*>(Xs + p * LNP_BR * LNP_ROWB + lnp_off(row, xc >> 1) + 8 * (xc & 1)) =
+            uint2{q01.p[p], q23.p[p]};
+      if (xc == 0) Ms[row] = mv[v];
+    }
+  };
+  int tile = (int)blockIdx.x;
+  if (tile < ntiles) xload(tile);
+  for (; tile < ntiles; tile += (int)gridDim.x) {  // workgroup-uniform
+    xstage();
+    __syncthreads();  // the X planes, the masks (and, the first time, the W planes) are complete
+    if (tile + (int)gridDim.x < ntiles) xload(tile + (int)gridDim.x);
+    f16x acc[2];
+#pragma unroll
+    for (int h = 0; h < 2; h++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) acc[h][e] = 0.0f;
+#pragma unroll
+    for (int kk = 0; kk < LNP_K / 16; kk++) {
+      bf16x8 fa[3], fb[2][3];
+#pragma unroll
+      for (int p = 0; p < 3; p++)
+        fa[p] = *reinterpret_cast<const bf16x8*>(Xs + p * LNP_BR * LNP_ROWB + lnp_off(32 * wave + r32, 2 * kk + hl));
+#pragma unroll
+      for (int h = 0; h < 2; h++)
+#pragma unroll
+        for (int p = 0; p < 3; p++)
+          fb[h][p] = *reinterpret_cast<const bf16x8*>(Ws + p * 64 * LNP_ROWB + lnp_off(32 * h + r32, 2 * kk + hl));
+#pragma unroll
+      for (int h = 0; h < 2; h++) acc[h] = mfma_parts6(fa, fb[h], acc[h]);
+    }
+    // register e of block h: tile row 32 wave + 8 (e / 4) + 4 hl + e % 4 = token 2 wave + e / 8, MSA row
+    // k = 8 ((e / 4) % 2) + 4 hl + e % 4 of the stage; channel 32 h + r32. Registers e, e + 1 (e even) are MSA rows
+    // k, k + 1: one dword per part.
+    const int g = tile / nnb, nb = tile % nnb;
+#pragma unroll
+    for (int tk = 0; tk < 2; tk++) {
+      const int n = 8 * nb + 2 * wave + tk;
+      if (n >= N) continue;  // wave-uniform
+      char* cbase = reinterpret_cast<char*>(planes) + ((int64_t)g * N + n) * 6144 + r32 * 32;
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const int e0 = 8 * tk + 4 * j, k = 8 * j + 4 * hl;
+        const int trow = 32 * wave + 16 * tk + k;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+          const Pair3 q01 = split3_pair(acc[h][e0] * Ms[trow], acc[h][e0 + 1] * Ms[trow + 1]);
+          const Pair3 q23 = split3_pair(acc[h][e0 + 2] * Ms[trow + 2], acc[h][e0 + 3] * Ms[trow + 3]);
+#pragma unroll
+          for (int p = 0; p < 3; p++)
+            *reinterpret_cast<uint2*>(cbase + (2 * p + h) * 1024 + 2 * k) = uint2{q01.p[p], q23.p[p]};
+        }
+      }
+    }
+    __syncthreads();  // every wave has read the X planes and masks before the next tile's are written
+  }
+}
+
 }  // namespace
+
+hipError_t launch_opm_ln_split(const float* m, const float* lnw, const float* lnb, float eps, const float* w_ab,
+                               const float* mask, void* planes, int S, int N, hipStream_t st) {
+  const auto al = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; };
+  if (S < 1 || N < 1 || !lnw || !lnb || !al(m, 16) || !al(w_ab, 16) || !al(lnw, 16) || !al(lnb, 16) ||
+      !al(planes, 16) || (int64_t)N * 6144 > INT32_MAX)
+    return hipErrorInvalidValue;
+  const int64_t G = (S + 15) / 16, nnb = (N + 7) / 8;
+  if (G * nnb > INT32_MAX) return hipErrorInvalidValue;
+  static int cache[kMaxDevices];
+  const int resident = resident_grid(opm_ln_split_k, 256, cache);
+  if (resident <= 0) return hipErrorInvalidDevice;
+  const int ntiles = (int)(G * nnb);
+  opm_ln_split_k<<<min(ntiles, resident), 256, 0, st>>>(m, lnw, lnb, eps, w_ab, mask, static_cast<__bf16*>(planes), S,
+                                                       N, (int)nnb, ntiles);
+  return hipGetLastError();
+}
 
 hipError_t launch_ln_linear_x3(const float* x, const float* lnw, const float* lnb, float eps, const float* w, float* y,
                                int64_t R, int K, int M, hipStream_t st) {

@@ -665,26 +665,46 @@ def opm_split(ab: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
     return planes
 
 
-def opm_outer(ab: torch.Tensor, mask: torch.Tensor, i_base: int = 0, n_i: int | None = None,
-              out_dtype=torch.float16, num: torch.Tensor | None = None,
-              planes: torch.Tensor | None = None) -> torch.Tensor:
-    """OuterProductMean's outer sum for one MSA: ab fp32 [S, N, 64] (LN(m) [W_a; W_b]^T, unmasked), mask fp32
-    [S, N] -> [n_i * N, 1024] with row (i - i_base) * N + j and column c * 32 + d holding
-    sum_s mask_si mask_sj a[s, i, c] b[s, j, d] / max(sum_s mask_si mask_sj, 1) (outer_product_mean.py:37-45).
-    planes: opm_split(ab, mask), when the caller already holds it (one split serves every i chunk)."""
-    _dev(ab, mask)
-    S, N, C2 = ab.shape
+def opm_ln_split(m: torch.Tensor, ln, w_ab: torch.Tensor, mask: torch.Tensor) -> torch.Tensor:
+    """The opm_split planes straight from the MSA: mask[s, n] * (LN(m[s, n]) w_ab^T) for m fp32 [S, N, 64], w_ab fp32
+    [64, 64] ([proj_a; proj_b]), mask fp32 [S, N], in one kernel (outer_product_mean.py:37-45)."""
+    _dev(m, w_ab, mask)
+    S, N, C = m.shape
+    if m.dtype != torch.float32 or C != 64 or not m.is_contiguous() or w_ab.shape != (64, 64) \
+            or w_ab.dtype != torch.float32 or not w_ab.is_contiguous() or mask.shape != (S, N) \
+            or mask.dtype != torch.float32 or not mask.is_contiguous():
+        raise ValueError("opm_ln_split: need contiguous fp32 m [S, N, 64], w_ab [64, 64] and mask [S, N]")
+    lw, lb = f32c(ln.weight), f32c(ln.bias)
+    planes = torch.empty(((S + 15) // 16, N, 3, 2, 32, 16), dtype=torch.bfloat16, device=m.device)
+    call("bzpf_opm_ln_split", _p(m), _p(lw), _p(lb), float(ln.eps), _p(w_ab), _p(mask), _p(planes), S, N, _stream())
+    return planes
+
+
+def opm_outer_planes(planes: torch.Tensor, num: torch.Tensor, S: int, N: int, i_base: int = 0,
+                     n_i: int | None = None, out_dtype=torch.float16) -> torch.Tensor:
+    """The outer sum over opm_split / opm_ln_split planes for S MSA rows and N tokens: [n_i * N, 1024], row
+    (i - i_base) * N + j, column c * 32 + d, divided by max(num[i, j], 1) (outer_product_mean.py:37-45)."""
+    _dev(planes, num)
     n_i = N - i_base if n_i is None else n_i
-    planes = opm_split(ab, mask) if planes is None else planes
     if planes.shape != ((S + 15) // 16, N, 3, 2, 32, 16) or planes.dtype != torch.bfloat16 \
             or not planes.is_contiguous():
-        raise ValueError("opm_outer: planes must be the contiguous output of opm_split for this ab")
-    num = opm_counts(mask) if num is None else num
+        raise ValueError("opm_outer: planes must be the contiguous output of opm_split for S, N")
     if num.shape != (N, N) or num.dtype != torch.float32 or not num.is_contiguous():
         raise ValueError("opm_outer: num must be the contiguous fp32 [N, N] pair counts")
-    out = torch.empty((n_i * N, 1024), dtype=out_dtype, device=ab.device)
+    out = torch.empty((n_i * N, 1024), dtype=out_dtype, device=planes.device)
     call("bzpf_opm_outer", _p(planes), _p(num), _p(out), _dt(out), S, N, int(i_base), int(n_i), _stream())
     return out
+
+
+def opm_outer(ab: torch.Tensor, mask: torch.Tensor, i_base: int = 0, n_i: int | None = None,
+              out_dtype=torch.float16, num: torch.Tensor | None = None) -> torch.Tensor:
+    """OuterProductMean's outer sum for one MSA: ab fp32 [S, N, 64] (LN(m) [W_a; W_b]^T, unmasked), mask fp32
+    [S, N] -> [n_i * N, 1024] with row (i - i_base) * N + j and column c * 32 + d holding
+    sum_s mask_si mask_sj a[s, i, c] b[s, j, d] / max(sum_s mask_si mask_sj, 1) (outer_product_mean.py:37-45):
+    opm_split, then opm_outer_planes."""
+    S, N, _ = ab.shape
+    num = opm_counts(mask) if num is None else num
+    return opm_outer_planes(opm_split(ab, mask), num, S, N, i_base, n_i, out_dtype)
 
 
 def ln_linear_f32(x: torch.Tensor, ln, w: torch.Tensor) -> torch.Tensor:

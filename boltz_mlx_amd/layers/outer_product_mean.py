@@ -1,9 +1,8 @@
 """OuterProductMean on the bzpf kernels: same constructor, parameter names and call signature as
 boltz_mlx/layers/outer_product_mean.py:12-50 (inference).
 
-  ab = LN(m) [W_a; W_b]^T                                  bzpf_layernorm + bzpf_linear (fp32)
+  x = mask * (LN(m) [W_a; W_b]^T) as three bf16 parts      bzpf_opm_ln_split (one kernel, fp32 accuracy)
   num = mask^T mask                                        bzpf_linear (fp32, the pair counts)
-  x = mask * ab as three bf16 parts                        bzpf_opm_split (once per MSA)
   z16 = (sum_s mask_si mask_sj a_si (x) b_sj) / max(num, 1)  bzpf_opm_outer (fp32-accurate: six bf16 part products
                                                            per product, fp32 sums; fp16 out in f16 mode)
   out (+)= z16 W_o^T + bias                                bzpf_linear (fp16 GEMM in f16 mode, fp32 accumulate)
@@ -52,14 +51,17 @@ class OuterProductMean(torch.nn.Module):
         S, N, c_in = m.shape
         co = self.proj_o.out_features
         w_ab, w_o = K.kernel_weight(self, "w_ab"), K.kernel_weight(self, "w_o")
-        mn = K.layer_norm(m.reshape(S * N, c_in).to(torch.float32), self.norm.weight, self.norm.bias, self.norm.eps)
-        ab = K.linear(mn, w_ab).view(S, N, 2 * self.c_hidden)
         mk = mask.to(torch.float32).reshape(S, N).contiguous()
+        m3 = m.to(torch.float32).reshape(S, N, c_in)
+        if c_in == 64 and self.c_hidden == 32:
+            planes = K.opm_ln_split(m3.contiguous(), self.norm, w_ab, mk)
+        else:
+            mn = K.layer_norm(m3.reshape(S * N, c_in), self.norm.weight, self.norm.bias, self.norm.eps)
+            planes = K.opm_split(K.linear(mn, w_ab).view(S, N, 2 * self.c_hidden), mk)
         z2 = z.view(N * N, co)
         num = K.opm_counts(mk)
-        planes = K.opm_split(ab, mk)
         step = max(1, min(N, OPM_PAIRS_PER_CHUNK // N))
         for i0 in range(0, N, step):
             n = min(step, N - i0)
-            zz = K.opm_outer(ab, mk, i0, n, out_dtype=w_o.dtype, num=num, planes=planes)
+            zz = K.opm_outer_planes(planes, num, S, N, i0, n, out_dtype=w_o.dtype)
             K.linear(zz, w_o, bias=self.proj_o.bias, out=z2[i0 * N:(i0 + n) * N], accumulate=accumulate)

@@ -251,6 +251,14 @@ int bzpf_linear_swiglu(const void* x, const void* w, void* u, int64_t rows, int 
  * boltz_mlx/layers/outer_product_mean.py:37-45). */
 int bzpf_opm_split(const float* ab, int64_t ld_ab, const float* mask, void* planes, int n_seq, int N, void* stream);
 
+/* The same planes from the MSA itself: x = mask[s][n] * (LN(m[s][n]; ln_w, ln_b, eps) . W_ab[ch]) for m fp32
+ * [n_seq, N, 64], W_ab fp32 [64, 64] = [proj_a.weight; proj_b.weight], mask fp32 [n_seq, N], in one kernel (the
+ * LayerNorm of bzpf_layernorm; each product the six bf16 part products of the three-part split, fp32 accuracy).
+ * Replaces norm + proj_a / proj_b + the masking of OuterProductMean (boltz_mlx/layers/outer_product_mean.py:37-45,
+ * boltz_mlx/kernels_msa.py:292-343): bzpf_layernorm + bzpf_linear + bzpf_opm_split without the intermediates. */
+int bzpf_opm_ln_split(const float* m, const float* ln_w, const float* ln_b, float eps, const float* w_ab,
+                      const float* mask, void* planes, int n_seq, int N, void* stream);
+
 /* Outer-product-mean outer sum over the planes of bzpf_opm_split: for i_base <= i < i_base + n_i and j < N,
  *   out[(i - i_base) * N + j][c * 32 + d] = sum_s mask[s][i] mask[s][j] a[s][i][c] b[s][j][d] / max(num[i][j], 1),
  * num fp32 [N, N] = mask^T mask (the pair counts; one bzpf_linear of the transposed mask with itself, as the

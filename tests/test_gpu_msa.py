@@ -88,6 +88,38 @@ def test_opm_split_parts_and_layout(S, N):
     assert torch.equal(got.view(torch.int16), want.contiguous().view(torch.int16))
 
 
+@pytest.mark.parametrize("S,N", [(37, 5), (64, 130), (17, 9)])
+def test_opm_ln_split(S, N):
+    """The planes from the MSA itself: their three parts add up to mask * (LN(m) W_ab^T) (LN as bzpf_layernorm, the
+    product fp32-accurate), in the opm_split layout, zeros past S; the outer sum over them matches the oracle."""
+    from boltz_mlx_amd import kernels as K
+
+    rng = np.random.default_rng(S * N)
+    m = (rng.standard_normal((S, N, 64)) * 1.5 + 0.2).astype(np.float32)
+    mask = (rng.random((S, N)) > 0.2).astype(np.float32)
+    w_ab = (rng.standard_normal((64, 64)) / 8).astype(np.float32)
+
+    class LN:
+        weight = dev(1 + 0.1 * rng.standard_normal(64))
+        bias = dev(0.1 * rng.standard_normal(64))
+        eps = 1e-5
+
+    planes = K.opm_ln_split(dev(m), LN, dev(w_ab), dev(mask))
+    G = (S + 15) // 16
+    x = planes.float().sum(2).double().cpu().numpy()  # [G, N, 2, 32, 16]: the parts' sum is exact
+    got = x.transpose(0, 4, 1, 2, 3).reshape(G * 16, N, 64)
+    mn = K.layer_norm(dev(m.reshape(S * N, 64)), LN.weight, LN.bias, LN.eps).cpu().numpy().astype(np.float64)
+    ab = (mn @ w_ab.astype(np.float64).T).reshape(S, N, 64)
+    ref = np.zeros((G * 16, N, 64))
+    ref[:S] = ab * mask[:, :, None]
+    assert np.all(got[S:] == 0)
+    assert O.metrics(got[:S], ref[:S])["max_rel"] <= 1e-6
+    num = K.opm_counts(dev(mask))
+    out = K.opm_outer_planes(planes, num, S, N, out_dtype=torch.float32).double().cpu().numpy()
+    oref = OM.opm_outer(ab, mask.astype(np.float64)).reshape(N * N, 1024)
+    assert O.metrics(out, oref)["max_rel"] < 1e-5
+
+
 def test_opm_outer_zero_count_pair():
     """Two tokens that never share an unmasked MSA row: their pair's count is 0, clamped to 1, and z is 0."""
     from boltz_mlx_amd import kernels as K

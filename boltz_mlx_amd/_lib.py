@@ -48,6 +48,7 @@ SIGNATURES = {
     "bzpf_opm_ln_split": [vp, vp, vp, f32, vp, vp, vp, i32, i32, vp],
     "bzpf_opm_outer": [vp, vp, vp, i32, i32, i32, i32, i32, vp],
     "bzpf_pwa_softmax": [vp, vp, f32, vp, i32, i64, i32, vp],
+    "bzpf_transition64_f16": [vp, vp, vp, f32, vp, vp, i64, i32, vp],
     "bzpf_ln_linear_f32": [vp, vp, vp, f32, vp, vp, i64, i32, i32, vp],
     "bzpf_pwa_wsplit_bytes": [i32, i64, i32],
     "bzpf_pwa_wsplit": [vp, i64, vp, i32, i32, vp],

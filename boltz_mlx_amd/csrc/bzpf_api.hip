@@ -406,6 +406,20 @@ int bzpf_opm_outer(const void* planes, const float* num, void* out, int out_dt, 
   return done(bzpf::launch_opm_outer(planes, num, out, out_dt, n_seq, N, i_base, n_i, S(stream)), "bzpf_opm_outer");
 }
 
+int bzpf_transition64_f16(float* x, const float* ln_w, const float* ln_b, float eps, const void* w12, const void* w3,
+                          int64_t rows, int hidden, void* stream) {
+  REQUIRE(x && ln_w && ln_b && w12 && w3, "bzpf_transition64_f16: NULL pointer");
+  REQUIRE(hidden >= 64 && hidden % 64 == 0 && hidden <= 384,
+          "bzpf_transition64_f16: need hidden a multiple of 64, at most 384 (hidden=%d)", hidden);
+  REQUIRE(reinterpret_cast<uintptr_t>(x) % 16 == 0 && reinterpret_cast<uintptr_t>(ln_w) % 16 == 0 &&
+              reinterpret_cast<uintptr_t>(ln_b) % 16 == 0,
+          "bzpf_transition64_f16: x, ln_w and ln_b must be 16-byte aligned");
+  REQUIRE(rows >= 0, "bzpf_transition64_f16: rows < 0");
+  if (rows == 0) return BZPF_OK;
+  return done(bzpf::launch_transition64_f16(x, ln_w, ln_b, eps, w12, w3, rows, hidden, S(stream)),
+              "bzpf_transition64_f16");
+}
+
 int bzpf_ln_linear_f32(const float* x, const float* ln_w, const float* ln_b, float eps, const float* w, float* y,
                        int64_t rows, int K, int M, void* stream) {
   REQUIRE(x && ln_w && ln_b && w && y, "bzpf_ln_linear_f32: NULL pointer");

@@ -85,6 +85,8 @@ hipError_t launch_opm_outer(const void* planes, const float* num, void* out, int
                             int n_i, hipStream_t st);
 hipError_t launch_opm_ln_split(const float* m, const float* lnw, const float* lnb, float eps, const float* w_ab,
                                const float* mask, void* planes, int S, int N, hipStream_t st);
+hipError_t launch_transition64_f16(float* x, const float* lnw, const float* lnb, float eps, const void* w12,
+                                   const void* w3, int64_t R, int H, hipStream_t st);
 hipError_t launch_ln_linear_x3(const float* x, const float* lnw, const float* lnb, float eps, const float* w, float* y,
                                int64_t R, int K, int M, hipStream_t st);
 hipError_t launch_pwa_softmax(const float* logits, const float* pm, float inf, float* w, int N, int64_t ldw, int H,

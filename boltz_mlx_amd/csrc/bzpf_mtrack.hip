@@ -247,7 +247,156 @@ __global__ __launch_bounds__(256, 2) void opm_ln_split_k(const float* __restrict
   }
 }
 
+// The 64-channel Transition in fp16 as one persistent kernel, in place: x += fc3(silu(xn fc1^T) * (xn fc2^T)) with
+// xn = fp16(LN(x; ln_w, ln_b, eps)) for fp32 x [R, 64], w12 fp16 [2H, 64] = [fc1; fc2], w3 fp16 [64, H]
+// (boltz_mlx/layers/transition.py:27-92 at 64 channels: the MSA track's transition and the template stack's; the
+// fp16 overflow margin is folded into the weights by the caller). A wave takes 32 rows; everything runs transposed,
+// so that a lane keeps one row throughout: h^T = W1 xn^T (the hidden units in a block's registers, the row in its
+// lane), a = silu(h1) h2 rounded to fp16 is then already the B fragment of out^T = W3 a^T, and out^T's registers are
+// the row's channels, added to the x values the lane loaded for the LayerNorm. The K order of each product is
+// permuted within groups of 16 (lane half hl takes k = 4 hl .. + 3 and 8 + 4 hl .. + 3), which is where the
+// accumulator layout puts a lane's values; the weights are staged in LDS with the same permutation, so each
+// fragment is one 16-byte read. All weights stay in LDS (384 H bytes, H a multiple of 64); 8 waves, one workgroup
+// per CU.
+constexpr int TR64_MAXH = 384;
+
+// position of k within its 16-group in the permuted order: j = 8 hl + 4 q + i holds k = 4 hl + i + 8 q
+__device__ __forceinline__ int tr64_perm(int j) { return 4 * ((j >> 3) & 1) + (j & 3) + 8 * ((j >> 2) & 1); }
+
+__global__ __launch_bounds__(512, 1) void transition64_f16_k(float* __restrict__ x, const float* __restrict__ lnw,
+                                                             const float* __restrict__ lnb, float eps,
+                                                             const half_t* __restrict__ w12,
+                                                             const half_t* __restrict__ w3, int64_t R, int H,
+                                                             int ntiles) {
+  extern __shared__ __attribute__((aligned(16))) char tr64_lds[];
+  half_t* W12s = reinterpret_cast<half_t*>(tr64_lds);  // [2H][64] permuted, 16-byte chunks swizzled by row % 8
+  half_t* W3s = W12s + 2 * H * 64;                      // [64][H] permuted, chunks swizzled by row % 8
+  const int t = threadIdx.x, wave = t >> 6, l = t & 63, r32 = l & 31, hl = l >> 5;
+  // stage the weights: element (row, k) goes to k's permuted position, 16-byte chunk c of a row to c ^ (row % 8)
+  for (int e = t; e < 2 * H * 64; e += 512) {
+    const int row = e >> 6, j = e & 63, g = j & ~15;
+    const int k = g + tr64_perm(j & 15);
+    W12s[row * 64 + 8 * (((j >> 3) ^ (row & 7)) & 7) + (j & 7)] = w12[row * 64 + k];
+  }
+  for (int e = t; e < 64 * H; e += 512) {
+    const int row = e / H, j = e % H, g = j & ~15;
+    const int k = g + tr64_perm(j & 15);
+    const int c = j >> 3, cs = (c & ~7) | ((c ^ row) & 7);
+    W3s[row * H + 8 * cs + (j & 7)] = w3[row * H + k];
+  }
+  // lane (r32, hl) of wave w: row 32 w + r32 of the tile, channels 8 q + 4 hl .. + 3 for q = 0..7
+  const f4* gw = reinterpret_cast<const f4*>(lnw);
+  const f4* gb = reinterpret_cast<const f4*>(lnb);
+  f4 xv[8], xn_next[8];
+  auto xload = [&](f4 (&dst)[8], int tile) {
+    const int64_t r = min((int64_t)tile * 256 + 32 * wave + r32, R - 1);
+#pragma unroll
+    for (int q = 0; q < 8; q++) dst[q] = *reinterpret_cast<const f4*>(x + r * 64 + 8 * q + 4 * hl);
+  };
+  int tile = (int)blockIdx.x;
+  if (tile < ntiles) xload(xv, tile);
+  __syncthreads();  // the weights are staged
+  for (; tile < ntiles; tile += (int)gridDim.x) {  // workgroup-uniform
+    if (tile + (int)gridDim.x < ntiles) xload(xn_next, tile + (int)gridDim.x);
+    // LayerNorm over the row's 64 channels (the lane pair hl = 0, 1), then the fp16 B fragments of xn^T
+    float s = 0.f;
+#pragma unroll
+    for (int q = 0; q < 8; q++) s += xv[q][0] + xv[q][1] + xv[q][2] + xv[q][3];
+    s += __shfl_xor(s, 32, 64);
+    const float mean = s * (1.0f / 64);
+    float ss = 0.f;
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      const f4 d = xv[q] - mean;
+      ss += d[0] * d[0] + d[1] * d[1] + d[2] * d[2] + d[3] * d[3];
+    }
+    ss += __shfl_xor(ss, 32, 64);
+    const float rstd = 1.0f / sqrtf(ss * (1.0f / 64) + eps);
+    half8 xb[4];
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      f4 o = (xv[q] - mean) * rstd;
+      o *= gw[2 * q + hl];
+      o += gb[2 * q + hl];
+#pragma unroll
+      for (int i = 0; i < 4; i++) xb[q >> 1][4 * (q & 1) + i] = (half_t)o[i];
+    }
+    f16x out[2];
+#pragma unroll
+    for (int b = 0; b < 2; b++)
+#pragma unroll
+      for (int e = 0; e < 16; e++) out[b][e] = 0.0f;
+    for (int c = 0; c < H / 32; c++) {
+      f16x h1, h2;
+#pragma unroll
+      for (int e = 0; e < 16; e++) h1[e] = h2[e] = 0.0f;
+      const int u = 32 * c + r32;  // the A rows (hidden units) of this lane
+#pragma unroll
+      for (int kk = 0; kk < 4; kk++) {
+        const int ch = ((2 * kk + hl) ^ (u & 7)) & 7;
+        const half8 a1 = *reinterpret_cast<const half8*>(W12s + u * 64 + 8 * ch);
+        const half8 a2 = *reinterpret_cast<const half8*>(W12s + (H + u) * 64 + 8 * ch);
+        h1 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a1, xb[kk], h1, 0, 0, 0);
+        h2 = __builtin_amdgcn_mfma_f32_32x32x16_f16(a2, xb[kk], h2, 0, 0, 0);
+      }
+      // register e: hidden unit 32 c + 8 (e / 4) + 4 hl + e % 4 of this lane's row; k-step kk2 of fc3 takes
+      // e = 8 kk2 .. + 7 (units 32 c + 16 kk2 + the permuted group)
+      half8 ab[2];
+#pragma unroll
+      for (int e = 0; e < 16; e++) ab[e >> 3][e & 7] = (half_t)(siluf_(h1[e]) * h2[e]);
+#pragma unroll
+      for (int kk2 = 0; kk2 < 2; kk2++) {
+        const int cc = (32 * c + 16 * kk2 + 8 * hl) >> 3;
+#pragma unroll
+        for (int b = 0; b < 2; b++) {
+          const int d = 32 * b + r32;
+          const int cs = (cc & ~7) | ((cc ^ d) & 7);
+          const half8 a3 = *reinterpret_cast<const half8*>(W3s + d * H + 8 * cs);
+          out[b] = __builtin_amdgcn_mfma_f32_32x32x16_f16(a3, ab[kk2], out[b], 0, 0, 0);
+        }
+      }
+    }
+    // out[b] register e: channel 32 b + 8 (e / 4) + 4 hl + e % 4 = 8 q + 4 hl + i with q = 4 b + e / 4
+    const int64_t r = (int64_t)tile * 256 + 32 * wave + r32;
+    if (r < R) {
+#pragma unroll
+      for (int q = 0; q < 8; q++) {
+        const f4 o = f4{out[q >> 2][4 * (q & 3)], out[q >> 2][4 * (q & 3) + 1], out[q >> 2][4 * (q & 3) + 2],
+                        out[q >> 2][4 * (q & 3) + 3]};
+        *reinterpret_cast<f4*>(x + r * 64 + 8 * q + 4 * hl) = xv[q] + o;
+      }
+    }
+#pragma unroll
+    for (int q = 0; q < 8; q++) xv[q] = xn_next[q];
+  }
+}
+
 }  // namespace
+
+hipError_t launch_transition64_f16(float* x, const float* lnw, const float* lnb, float eps, const void* w12,
+                                   const void* w3, int64_t R, int H, hipStream_t st) {
+  const auto al = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; };
+  if (R < 1 || H < 64 || H % 64 || H > TR64_MAXH || !lnw || !lnb || !al(x, 16) || !al(lnw, 16) || !al(lnb, 16) ||
+      (R + 255) / 256 > INT32_MAX)
+    return hipErrorInvalidValue;
+  const size_t lds = (size_t)384 * H;
+  static bool attr_set[kMaxDevices];
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  if (!attr_set[dev]) {
+    const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(transition64_f16_k),
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, 384 * TR64_MAXH);
+    if (e != hipSuccess) return e;
+    attr_set[dev] = true;
+  }
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || cus < 1)
+    return hipErrorInvalidDevice;
+  const int ntiles = (int)((R + 255) / 256);
+  transition64_f16_k<<<min(ntiles, cus), 512, lds, st>>>(x, lnw, lnb, eps, static_cast<const half_t*>(w12),
+                                                         static_cast<const half_t*>(w3), R, H, ntiles);
+  return hipGetLastError();
+}
 
 hipError_t launch_opm_ln_split(const float* m, const float* lnw, const float* lnb, float eps, const float* w_ab,
                                const float* mask, void* planes, int S, int N, hipStream_t st) {

@@ -707,6 +707,20 @@ def opm_outer(ab: torch.Tensor, mask: torch.Tensor, i_base: int = 0, n_i: int | 
     return opm_outer_planes(opm_split(ab, mask), num, S, N, i_base, n_i, out_dtype)
 
 
+def transition64_f16(x: torch.Tensor, ln, w12: torch.Tensor, w3: torch.Tensor) -> None:
+    """x (fp32 [rows, 64], in place) += fc3(silu(xn fc1^T) * (xn fc2^T)), xn = fp16(LN(x)), for fp16 w12 [2H, 64]
+    ([fc1; fc2]) and w3 [64, H] in one kernel (transition.py:27-92 at 64 channels)."""
+    _dev(x, w12, w3)
+    rows, Dx = x.shape
+    H = w3.shape[1]
+    if x.dtype != torch.float32 or Dx != 64 or not x.is_contiguous() or w12.shape != (2 * H, 64) \
+            or w3.shape != (64, H) or w12.dtype != torch.float16 or w3.dtype != torch.float16 \
+            or not w12.is_contiguous() or not w3.is_contiguous():
+        raise ValueError("transition64_f16: need contiguous fp32 x [rows, 64], fp16 w12 [2H, 64] and w3 [64, H]")
+    call("bzpf_transition64_f16", _p(x), _p(f32c(ln.weight)), _p(f32c(ln.bias)), float(ln.eps), _p(w12), _p(w3),
+         rows, H, _stream())
+
+
 def ln_linear_f32(x: torch.Tensor, ln, w: torch.Tensor) -> torch.Tensor:
     """LN(x; ln.weight, ln.bias, ln.eps) w^T for fp32 x [rows, 64] and fp32 w [M, 64] (M a multiple of 256) in one
     kernel (the LayerNorm of bzpf_layernorm, the product at fp32 accuracy) -> [rows, M] fp32

@@ -38,7 +38,7 @@ class MSALayer(torch.nn.Module):
         for b in range(z.shape[0]):
             self.pair_weighted_averaging.accumulate(m[b], m[b], z[b], pm[b])
             m2 = m[b].view(S * N, D)
-            self.msa_transition.unfused(self.msa_transition.norm.to_storage(m2), out=m2, accumulate=True)
+            self.msa_transition.inplace(m2)
             self.outer_product_mean.accumulate(z[b], m[b], msa_mask[b])
         self.pairformer_layer.inplace(z, pm)
         return z, m

@@ -95,6 +95,17 @@ class Transition(torch.nn.Module):
         w12, w3 = self.prepare()
         return K.attn_out_transition(o, w_o, trans, z, self.norm, w12, w3, next_ln, pair_bias)
 
+    def inplace(self, x: torch.Tensor) -> None:
+        """x (fp32 [rows, dim], contiguous) += self(x). At 64 channels in f16 mode over many rows (the MSA track) one
+        kernel computes the LayerNorm, both projections and the residual (bzpf_transition64_f16); otherwise
+        norm + unfused."""
+        if K.f16() and self.fc1.in_features == 64 and self.fc3.out_features == 64 and self.hidden % 64 == 0 \
+                and self.hidden <= 384 and x.shape[0] >= FUSED_MIN_ROWS:
+            w12, w3 = self.prepare()
+            K.transition64_f16(x, self.norm, w12, w3)
+            return
+        self.unfused(self.norm.to_storage(x), out=x, accumulate=True)
+
     def unfused(self, xn: torch.Tensor, out: Optional[torch.Tensor] = None, accumulate: bool = False):
         """fc3(SwiGLU(xn fc12^T)) as row GEMMs (in fp16 the up-projection carries the SwiGLU product in its
         epilogue); accumulate adds into the fp32 `out`."""

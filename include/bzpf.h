@@ -268,6 +268,14 @@ int bzpf_opm_ln_split(const float* m, const float* ln_w, const float* ln_b, floa
 int bzpf_opm_outer(const void* planes, const float* num, void* out, int out_dt, int n_seq, int N, int i_base, int n_i,
                    void* stream);
 
+/* The 64-channel Transition in fp16, in place, in one kernel: x += fc3(silu(xn fc1^T) * (xn fc2^T)) with
+ * xn = fp16(LN(x; ln_w, ln_b, eps)), for x fp32 [rows, 64], w12 fp16 [2 hidden, 64] = [fc1; fc2], w3 fp16
+ * [64, hidden] (hidden a multiple of 64, at most 384); fp32 accumulation, the SwiGLU product rounded to fp16 as the
+ * fc3 operand. Replaces Transition at 64 channels (boltz_mlx/layers/transition.py:27-92; the MSA track's
+ * transition): bzpf_layernorm + bzpf_linear_swiglu + bzpf_linear without the [rows, hidden] intermediate. */
+int bzpf_transition64_f16(float* x, const float* ln_w, const float* ln_b, float eps, const void* w12, const void* w3,
+                          int64_t rows, int hidden, void* stream);
+
 /* The MSA track's LayerNorm + fp32 Linear in one kernel: y[r][m] = LN(x[r]; ln_w, ln_b, eps) . W[m] for x fp32
  * [rows, K = 64], W fp32 [M, 64] (M a multiple of 256), y fp32 [rows, M]. The LayerNorm is bzpf_layernorm's arithmetic;
  * each product is the six bf16 part products of the three-part split (fp32 accuracy). Replaces norm_m + proj_m |

@@ -293,3 +293,68 @@ def test_msa_layer(precision):
         assert mz["rel_fro"] < 1e-5 and mm["rel_fro"] < 1e-5, (mz, mm)
     else:
         assert mz["rel_fro"] < 5e-3 and mm["rel_fro"] < 5e-3, (mz, mm)
+
+
+@pytest.mark.parametrize("rows,H", [(300, 256), (5000, 256), (257, 128), (20000, 384)])
+def test_transition64_f16(rows, H):
+    """The fused 64-channel transition against the float64 formula on the same fp16 weights, with xn and the SwiGLU
+    product rounded to fp16 as the kernel's operands (the reference's f16 transition), and against the unfused
+    kernels (LayerNorm, GEMM with the SwiGLU epilogue, GEMM): the update within fp16 operand rounding."""
+    from boltz_mlx_amd import kernels as K
+
+    rng = np.random.default_rng(rows + H)
+    x = (rng.standard_normal((rows, 64)) * 1.3 + 0.1).astype(np.float32)
+    w12 = torch.tensor(rng.standard_normal((2 * H, 64)) / 8, dtype=torch.float16)
+    w3 = torch.tensor(rng.standard_normal((64, H)) / 16, dtype=torch.float16)
+
+    class LN:
+        weight = dev(1 + 0.1 * rng.standard_normal(64))
+        bias = dev(0.1 * rng.standard_normal(64))
+        eps = 1e-5
+
+    xg = dev(x)
+    K.transition64_f16(xg, LN, w12.cuda(), w3.cuda())
+    got = xg.cpu().numpy().astype(np.float64) - x
+    xn = torch.tensor(O.layer_norm(x.astype(np.float64), LN.weight.double().cpu().numpy(),
+                                   LN.bias.double().cpu().numpy())).half().double().numpy()
+    h = xn @ w12.double().numpy().T
+    a = torch.tensor(h[:, :H] / (1 + np.exp(-h[:, :H])) * h[:, H:]).half().double().numpy()
+    ref = a @ w3.double().numpy().T
+    m = O.metrics(got, ref)
+    assert m["max_rel"] < 1e-2 and m["rel_fro"] < 2e-3, m
+    xu = dev(x)
+    xnu = K.layer_norm(xu, LN.weight, LN.bias, LN.eps, out_dtype=torch.float16)
+    a16 = K.swiglu(K.linear(xnu, w12.cuda()))
+    K.linear(a16, w3.cuda(), out=xu, out_dtype=torch.float32, accumulate=True)
+    mu = O.metrics(got, xu.cpu().numpy().astype(np.float64) - x)
+    assert mu["max_rel"] < 1e-2 and mu["rel_fro"] < 2e-3, mu
+
+
+def test_msa_layer_fused_transition(monkeypatch):
+    """The MSA layer in f16 mode with the m transition on the fused 64-channel kernel (taken from 16,384 rows; forced
+    here at 23 x 40) against the oracle, at the f16 layer gate."""
+    from boltz_mlx_amd import kernels as K
+    from boltz_mlx_amd.layers import transition as T
+    from boltz_mlx_amd.layers.msa import MSALayer
+    from boltz_mlx_amd.weights import load_module
+
+    monkeypatch.setattr(T, "FUSED_MIN_ROWS", 1)
+    old = K.PRECISION
+    K.set_precision("f16")
+    try:
+        N, S = 40, 23
+        p = rand_params(shapes_msa_layer(), seed=31, std=0.05)
+        z, _, pm = pair_inputs(N, 128, seed=32, n_pad=3)
+        rng = np.random.default_rng(33)
+        m = rng.standard_normal((1, S, N, 64))
+        msa_mask = (rng.random((1, S, N)) > 0.1).astype(np.float64)
+        mod = load_module(MSALayer(64, 128), p).cuda()
+        zg, mg = mod(dev(z), dev(m), dev(pm), dev(msa_mask))
+    finally:
+        K.set_precision(old)
+    zr, mr = OM.msa_layer(z, m, pm, msa_mask, p)
+    v = N - 3
+    zg, mg = zg.cpu().numpy(), mg.cpu().numpy()
+    mz = O.metrics(zg[:, :v, :v] - z[:, :v, :v], zr[:, :v, :v] - z[:, :v, :v])
+    mm = O.metrics(mg[:, :, :v] - m[:, :, :v], mr[:, :, :v] - m[:, :, :v])
+    assert mz["rel_fro"] < 5e-3 and mm["rel_fro"] < 5e-3, (mz, mm)

@@ -78,7 +78,11 @@ class Transition(torch.nn.Module):
             if pair_bias is not None:
                 raise NotImplementedError("the pair-bias epilogue needs the 128-channel transition kernel")
             z2 = z.view(-1, z.shape[-1])
-            self.unfused(xn, out=z2, accumulate=accumulate)
+            if accumulate and self._fused64_ok(z2):  # xn = norm(z): the kernel recomputes it from z
+                w12, w3 = self.prepare()
+                K.transition64_f16(z2, self.norm, w12, w3)
+            else:
+                self.unfused(xn, out=z2, accumulate=accumulate)
             return None if next_ln is None else next_ln.to_storage(z2).reshape(z2.shape)
         w12, w3 = self.prepare()
         return K.transition(xn, w12, w3, z, accumulate, next_ln, pair_bias)
@@ -95,12 +99,18 @@ class Transition(torch.nn.Module):
         w12, w3 = self.prepare()
         return K.attn_out_transition(o, w_o, trans, z, self.norm, w12, w3, next_ln, pair_bias)
 
+    def _fused64_ok(self, x: torch.Tensor) -> bool:
+        """Whether x (fp32 [rows, dim]) takes bzpf_transition64_f16: f16 mode, 64 channels, hidden a multiple of 64
+        up to 384, and the large row counts (the MSA track, the template stack's pairs)."""
+        return (K.f16() and self.fc1.in_features == 64 and self.fc3.out_features == 64 and self.hidden % 64 == 0
+                and self.hidden <= 384 and x.dtype == torch.float32 and x.is_contiguous()
+                and x.shape[0] >= FUSED_MIN_ROWS)
+
     def inplace(self, x: torch.Tensor) -> None:
         """x (fp32 [rows, dim], contiguous) += self(x). At 64 channels in f16 mode over many rows (the MSA track) one
         kernel computes the LayerNorm, both projections and the residual (bzpf_transition64_f16); otherwise
         norm + unfused."""
-        if K.f16() and self.fc1.in_features == 64 and self.fc3.out_features == 64 and self.hidden % 64 == 0 \
-                and self.hidden <= 384 and x.shape[0] >= FUSED_MIN_ROWS:
+        if self._fused64_ok(x):
             w12, w3 = self.prepare()
             K.transition64_f16(x, self.norm, w12, w3)
             return

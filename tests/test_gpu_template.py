@@ -108,6 +108,30 @@ def test_noseq_layer_c64(precision, N, n_pad):
         assert mt["max_rel"] <= 3e-2 and mt["rel_fro"] <= 1e-2, mt
 
 
+@pytest.mark.parametrize("N,n_pad", [(24, 2), (70, 5)])
+def test_noseq_layer_c64_fused_transition(monkeypatch, N, n_pad):
+    """f16 with the pair transition on the fused 64-channel kernel (taken from 16,384 pairs; forced here)."""
+    from boltz_mlx_amd import kernels as K
+    from boltz_mlx_amd.layers import transition as T
+    from boltz_mlx_amd.layers.pairformer import PairformerNoSeqLayer
+    from boltz_mlx_amd.weights import load_module
+
+    monkeypatch.setattr(T, "FUSED_MIN_ROWS", 1)
+    p = rand_params(shapes_noseq_layer(64), seed=N, std=0.1)
+    z, _, pm = pair_inputs(N, 64, seed=N + 1, n_pad=n_pad)
+    old = K.PRECISION
+    K.set_precision("f16")
+    try:
+        mod = load_module(PairformerNoSeqLayer(64), p).cuda()
+        got = mod(dev(z), dev(pm)).cpu().numpy()
+    finally:
+        K.set_precision(old)
+    f = lambda x: np.asarray(x, np.float32)  # noqa: E731 (float32 oracle: see test_noseq_layer_c64)
+    ref = OM.pairformer_noseq_layer(f(z), f(pm), {k: f(v) for k, v in p.items()})
+    mt = O.metrics(got - z, ref - z)
+    assert mt["finite"] and mt["max_rel"] <= 3e-2 and mt["rel_fro"] <= 1e-2, mt
+
+
 @pytest.mark.parametrize("precision", ["fp32", "f16"], indirect=True)
 def test_noseq_module_c64_two_blocks(precision):
     """The template stack's shape: two NoSeq blocks at c_z = 64 (trunkv2.py:64-71)."""

@@ -15,51 +15,57 @@ namespace bzpf {
 
 namespace {
 
-constexpr int LNP_K = 64, LNP_BR = 128, LNP_BC = 256;  // channels, rows per tile, columns per workgroup
+constexpr int LNP_K = 64, LNP_BR = 128, LNP_BC = 256;  // channels; the largest row and column tiles
 constexpr int LNP_ROWB = 2 * LNP_K;                    // bytes of one plane row (64 bf16)
 
 // Byte offset of 16-byte chunk c (k = 8 c .. 8 c + 7) of plane row r: the chunks of a row are permuted by r % 8, so
 // the fragment reads (8 lanes on 8 consecutive rows at one logical chunk) hit distinct banks.
 __device__ __forceinline__ int lnp_off(int r, int c) { return r * LNP_ROWB + 16 * (c ^ (r & 7)); }
 
-// Workgroup b takes column block cb = b % ncb and the row tiles b / ncb, b / ncb + gridDim.x / ncb, ... Wave
-// (wr, wc) = (wave / 4, wave % 4) computes rows 64 wr .. + 63 x columns 64 wc .. + 63 of the tile (2 x 2 blocks).
-__global__ __launch_bounds__(512, 1) void ln_linear_x3_k(const float* __restrict__ x, const float* __restrict__ lnw,
-                                                         const float* __restrict__ lnb, float eps,
-                                                         const float* __restrict__ w, float* __restrict__ y,
-                                                         int64_t R, int M, int ncb, int nrt) {
-  __shared__ __attribute__((aligned(16))) char Ws[3 * LNP_BC * LNP_ROWB];  // 96 KB: the W block's three planes
-  __shared__ __attribute__((aligned(16))) char Xs[3 * LNP_BR * LNP_ROWB];  // 48 KB: the tile's LN(x) planes
+// Workgroup b takes column block cb = b % ncb and the row tiles b / ncb, b / ncb + gridDim.x / ncb, ... of BR rows
+// against BC columns; wave (wr, wc) = (wave / WC, wave % WC) computes rows BR / WR wr .. x columns BC / WC wc .. of
+// the tile (MB x NB blocks of 32 x 32).
+template <int BR, int BC, int WR, int WC>
+__global__ __launch_bounds__(64 * WR * WC, 8 / (WR * WC)) void ln_linear_x3_k(const float* __restrict__ x,
+                                                                 const float* __restrict__ lnw,
+                                                                 const float* __restrict__ lnb, float eps,
+                                                                 const float* __restrict__ w, float* __restrict__ y,
+                                                                 int64_t R, int M, int ncb, int nrt) {
+  constexpr int NT = 64 * WR * WC, MB = BR / WR / 32, NB = BC / WC / 32;
+  constexpr int XP = BR * 16 / NT, WP = BC * 16 / NT;  // x rows per thread, W f4 items per thread
+  static_assert(MB >= 1 && NB >= 1 && XP >= 1 && WP >= 1, "tile shape");
+  __shared__ __attribute__((aligned(16))) char Ws[3 * BC * LNP_ROWB];  // the W block's three planes
+  __shared__ __attribute__((aligned(16))) char Xs[3 * BR * LNP_ROWB];  // the tile's LN(x) planes
   const int t = threadIdx.x, wave = t >> 6, l = t & 63, r32 = l & 31, hl = l >> 5;
-  const int wr = wave >> 2, wc = wave & 3;
-  const int cb = (int)blockIdx.x % ncb, m0 = cb * LNP_BC;
-  // the W block, split once: f4 item e = t + 512 v is row e / 16 (clamped to M - 1), k = 4 (e % 16) .. + 3
+  const int wr = wave / WC, wc = wave % WC;
+  const int cb = (int)blockIdx.x % ncb, m0 = cb * BC;
+  // the W block, split once: f4 item e = t + NT v is row e / 16 (clamped to M - 1), k = 4 (e % 16) .. + 3
 #pragma unroll
-  for (int v = 0; v < 8; v++) {
-    const int e = t + 512 * v, row = e >> 4, kq = e & 15;
+  for (int v = 0; v < WP; v++) {
+    const int e = t + NT * v, row = e >> 4, kq = e & 15;
     const f4 a = *reinterpret_cast<const f4*>(w + (int64_t)min(m0 + row, M - 1) * LNP_K + 4 * kq);
     const Pair3 q01 = split3_pair(a[0], a[1]), q23 = split3_pair(a[2], a[3]);
 #pragma unroll
     for (int p = 0; p < 3; p++)
-      *reinterpret_cast<uint2*>(Ws + p * LNP_BC * LNP_ROWB + lnp_off(row, kq >> 1) + 8 * (kq & 1)) =
+      *reinterpret_cast<uint2*>(Ws + p * BC * LNP_ROWB + lnp_off(row, kq >> 1) + 8 * (kq & 1)) =
           uint2{q01.p[p], q23.p[p]};
   }
-  // x rows: pass v takes tile row t / 16 + 32 v, lane c = t % 16 channels 4 c .. + 3 (rows past R read row R - 1;
-  // their outputs are not stored)
+  // x rows: pass v takes tile row t / 16 + NT / 16 v, lane c = t % 16 channels 4 c .. + 3 (rows past R read row
+  // R - 1; their outputs are not stored)
   const int xc = t & 15, xrow = t >> 4;
   const f4 gw = *reinterpret_cast<const f4*>(lnw + 4 * xc), gb = *reinterpret_cast<const f4*>(lnb + 4 * xc);
-  f4 xv[4];
+  f4 xv[XP];
   auto xload = [&](int rt) {
 #pragma unroll
-    for (int v = 0; v < 4; v++) {
-      const int64_t r = min((int64_t)rt * LNP_BR + xrow + 32 * v, R - 1);
+    for (int v = 0; v < XP; v++) {
+      const int64_t r = min((int64_t)rt * BR + xrow + NT / 16 * v, R - 1);
       xv[v] = *reinterpret_cast<const f4*>(x + r * LNP_K + 4 * xc);
     }
   };
   // LN (bzpf_layernorm's order of operations), then the split into the X planes
   auto xstage = [&]() {
 #pragma unroll
-    for (int v = 0; v < 4; v++) {
+    for (int v = 0; v < XP; v++) {
       const f4 a = xv[v];
       float s = 0.f;
       s += a[0] + a[1] + a[2] + a[3];
@@ -72,10 +78,10 @@ __global__ __launch_bounds__(512, 1) void ln_linear_x3_k(const float* __restrict
       o *= gw;
       o += gb;
       const Pair3 q01 = split3_pair(o[0], o[1]), q23 = split3_pair(o[2], o[3]);
-      const int row = xrow + 32 * v;
+      const int row = xrow + NT / 16 * v;
 #pragma unroll
       for (int p = 0; p < 3; p++)
-        *reinterpret_cast<uint2*>(Xs + p * LNP_BR * LNP_ROWB + lnp_off(row, xc >> 1) + 8 * (xc & 1)) =
+        *reinterpret_cast<uint2*>(Xs + p * BR * LNP_ROWB + lnp_off(row, xc >> 1) + 8 * (xc & 1)) =
             uint2{q01.p[p], q23.p[p]};
     }
   };
@@ -86,42 +92,43 @@ __global__ __launch_bounds__(512, 1) void ln_linear_x3_k(const float* __restrict
     xstage();
     __syncthreads();  // the X planes (and, the first time, the W planes) are complete
     if (rt + rstep < nrt) xload(rt + rstep);
-    f16x acc[2][2];
+    f16x acc[MB][NB];
 #pragma unroll
-    for (int a = 0; a < 2; a++)
+    for (int a = 0; a < MB; a++)
 #pragma unroll
-      for (int b = 0; b < 2; b++)
+      for (int b = 0; b < NB; b++)
 #pragma unroll
         for (int e = 0; e < 16; e++) acc[a][b][e] = 0.0f;
 #pragma unroll
     for (int kk = 0; kk < LNP_K / 16; kk++) {
-      bf16x8 fa[2][3], fb[2][3];
+      bf16x8 fa[MB][3], fb[NB][3];
 #pragma unroll
-      for (int bm = 0; bm < 2; bm++)
-#pragma unroll
-        for (int p = 0; p < 3; p++)
-          fa[bm][p] = *reinterpret_cast<const bf16x8*>(Xs + p * LNP_BR * LNP_ROWB +
-                                                       lnp_off(64 * wr + 32 * bm + r32, 2 * kk + hl));
-#pragma unroll
-      for (int bn = 0; bn < 2; bn++)
+      for (int bm = 0; bm < MB; bm++)
 #pragma unroll
         for (int p = 0; p < 3; p++)
-          fb[bn][p] = *reinterpret_cast<const bf16x8*>(Ws + p * LNP_BC * LNP_ROWB +
-                                                       lnp_off(64 * wc + 32 * bn + r32, 2 * kk + hl));
+          fa[bm][p] = *reinterpret_cast<const bf16x8*>(Xs + p * BR * LNP_ROWB +
+                                                       lnp_off(BR / WR * wr + 32 * bm + r32, 2 * kk + hl));
 #pragma unroll
-      for (int bm = 0; bm < 2; bm++)
+      for (int bn = 0; bn < NB; bn++)
 #pragma unroll
-        for (int bn = 0; bn < 2; bn++) acc[bm][bn] = mfma_parts6(fa[bm], fb[bn], acc[bm][bn]);
+        for (int p = 0; p < 3; p++)
+          fb[bn][p] = *reinterpret_cast<const bf16x8*>(Ws + p * BC * LNP_ROWB +
+                                                       lnp_off(BC / WC * wc + 32 * bn + r32, 2 * kk + hl));
+#pragma unroll
+      for (int bm = 0; bm < MB; bm++)
+#pragma unroll
+        for (int bn = 0; bn < NB; bn++) acc[bm][bn] = mfma_parts6(fa[bm], fb[bn], acc[bm][bn]);
     }
-    // block (bm, bn) register e: tile row 64 wr + 32 bm + 8 (e / 4) + 4 hl + e % 4, column m0 + 64 wc + 32 bn + r32
+    // block (bm, bn) register e: tile row BR / WR wr + 32 bm + 8 (e / 4) + 4 hl + e % 4, column
+    // m0 + BC / WC wc + 32 bn + r32
 #pragma unroll
-    for (int bn = 0; bn < 2; bn++) {
-      const int col = m0 + 64 * wc + 32 * bn + r32;
+    for (int bn = 0; bn < NB; bn++) {
+      const int col = m0 + BC / WC * wc + 32 * bn + r32;
 #pragma unroll
-      for (int bm = 0; bm < 2; bm++)
+      for (int bm = 0; bm < MB; bm++)
 #pragma unroll
         for (int e = 0; e < 16; e++) {
-          const int64_t row = (int64_t)rt * LNP_BR + 64 * wr + 32 * bm + 8 * (e >> 2) + 4 * hl + (e & 3);
+          const int64_t row = (int64_t)rt * BR + BR / WR * wr + 32 * bm + 8 * (e >> 2) + 4 * hl + (e & 3);
           if (row < R && col < M) y[row * M + col] = acc[bm][bn][e];
         }
     }
@@ -415,20 +422,26 @@ hipError_t launch_opm_ln_split(const float* m, const float* lnw, const float* ln
   return hipGetLastError();
 }
 
+template <int BR, int BC, int WR, int WC>
+static hipError_t ln_linear_x3_t(const float* x, const float* lnw, const float* lnb, float eps, const float* w, float* y,
+                                 int64_t R, int M, hipStream_t st) {
+  static int cache[kMaxDevices];
+  const int resident = resident_grid(ln_linear_x3_k<BR, BC, WR, WC>, 64 * WR * WC, cache);
+  if (resident <= 0) return hipErrorInvalidDevice;
+  const int ncb = M / BC, nrt = (int)((R + BR - 1) / BR);
+  // whole groups of ncb workgroups (one per column block), no more row-tile slots than row tiles
+  const int per_cb = max(1, min(nrt, resident / ncb));
+  ln_linear_x3_k<BR, BC, WR, WC><<<ncb * per_cb, 64 * WR * WC, 0, st>>>(x, lnw, lnb, eps, w, y, R, M, ncb, nrt);
+  return hipGetLastError();
+}
+
 hipError_t launch_ln_linear_x3(const float* x, const float* lnw, const float* lnb, float eps, const float* w, float* y,
                                int64_t R, int K, int M, hipStream_t st) {
   const auto al = [](const void* p, uintptr_t a) { return (reinterpret_cast<uintptr_t>(p) & (a - 1)) == 0; };
   if (R < 1 || K != LNP_K || M < LNP_BC || M % LNP_BC || !lnw || !lnb || !al(x, 16) || !al(w, 16) || !al(lnw, 16) ||
       !al(lnb, 16) || (R + LNP_BR - 1) / LNP_BR > INT32_MAX)
     return hipErrorInvalidValue;
-  static int cache[kMaxDevices];
-  const int resident = resident_grid(ln_linear_x3_k, 512, cache);
-  if (resident <= 0) return hipErrorInvalidDevice;
-  const int ncb = M / LNP_BC, nrt = (int)((R + LNP_BR - 1) / LNP_BR);
-  // whole groups of ncb workgroups (one per column block), no more row-tile slots than row tiles
-  const int per_cb = max(1, min(nrt, resident / ncb));
-  ln_linear_x3_k<<<ncb * per_cb, 512, 0, st>>>(x, lnw, lnb, eps, w, y, R, M, ncb, nrt);
-  return hipGetLastError();
+  return ln_linear_x3_t<128, 256, 2, 4>(x, lnw, lnb, eps, w, y, R, M, st);
 }
 
 }  // namespace bzpf

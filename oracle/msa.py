@@ -1,4 +1,5 @@
-"""numpy restatement of the reference's MSA-block pair kernels (test infrastructure: the checker, never the product).
+"""numpy restatement of the reference's MSA-block pair kernels (test infrastructure: the reference results the tests
+compare against, never the product).
 
 Like oracle/pairformer.py, every function computes in the dtype of its inputs (float64 pins the parity tests) and
 takes parameter dicts keyed by the reference's PyTorch qualified names relative to the module.

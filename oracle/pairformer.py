@@ -1,4 +1,5 @@
-"""numpy restatement of the reference's Pairformer pair path (test infrastructure: the checker, never the product).
+"""numpy restatement of the reference's Pairformer pair path (test infrastructure: the reference results the tests
+compare against, never the product).
 
 Every function computes in the dtype of its inputs: float64 pins the parity tests, float32 is the
 reference-equivalent CPU path timed beside the GPU (the reference's own CPU path is MLX fp32; MLX is not

@@ -482,7 +482,7 @@ def main() -> int:
                          "FETCH_SIZE / WRITE_SIZE counters of rocprofv3 --pmc); skips the measured ceilings")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
+        print("bench.py measures one GPU: the library has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         return 2
 
     import torch

@@ -37,6 +37,7 @@ SIGNATURES = {
     "bzpf_attn_out_transition": [vp, vp, i32, vp, vp, f32, vp, vp, vp, vp, vp, f32, vp, vp, vp, vp, f32, vp, i32, i32,
                                  i64, i32, i32, vp],
     "bzpf_linear": [vp, vp, vp, vp, i32, i32, i64, i32, i32, i32, vp],
+    "bzpf_linear_residual": [vp, vp, vp, vp, i64, vp, i32, i64, i32, i32, vp],
     "bzpf_swiglu": [vp, vp, i32, i64, i32, vp],
     "bzpf_seq_attention": [vp, vp, vp, vp, i64, vp, vp, f32, vp, i64, i32, i32, i64, i32, i32, vp],
     "bzpf_linear_swiglu3": [vp, vp, vp, i64, i32, i32, vp],

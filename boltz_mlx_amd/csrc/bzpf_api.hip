@@ -257,6 +257,28 @@ int bzpf_linear(const void* x, const void* w, const float* bias, void* y, int dt
   return done(bzpf::launch_linear(x, w, bias, y, dt, y_dt, rows, K, M, accumulate ? 1 : 0, S(stream)), "bzpf_linear");
 }
 
+int bzpf_linear_residual(const void* x, const void* w, const float* bias, const float* res, int64_t ld_res, float* y,
+                         int dt, int64_t rows, int K, int M, void* stream) {
+  REQUIRE_PTR(x);
+  REQUIRE_PTR(w);
+  REQUIRE(res != nullptr && y != nullptr, "bzpf_linear_residual: NULL pointer");
+  REQUIRE(dt_ok(dt), "bzpf_linear_residual: bad dtype");
+  REQUIRE(K >= 8 && K % 8 == 0 && M >= 1, "bzpf_linear_residual: need K %% 8 == 0, M >= 1 (K=%d M=%d)", K, M);
+  REQUIRE(ld_res >= M && ld_res % 4 == 0 && reinterpret_cast<uintptr_t>(res) % 16 == 0,
+          "bzpf_linear_residual: res must be 16-byte aligned with a pitch >= M, a multiple of 4 (ld_res=%lld)",
+          (long long)ld_res);
+  REQUIRE(rows >= 0, "bzpf_linear_residual: rows < 0");
+  if (rows == 0) return BZPF_OK;
+  if (bzpf::gemm_nt_ok(dt, x, w, bias, y, rows, K, M, res, ld_res))
+    return done(bzpf::launch_gemm_nt(x, w, bias, y, dt, BZPF_F32, rows, K, M, 3, res, ld_res, rows, S(stream)),
+                "bzpf_linear_residual");
+  // other shapes: the residual copied into y, then the accumulating layer (the same sums)
+  const hipError_t e = hipMemcpy2DAsync(y, (size_t)M * 4, res, (size_t)ld_res * 4, (size_t)M * 4, (size_t)rows,
+                                        hipMemcpyDeviceToDevice, S(stream));
+  if (e != hipSuccess) return done(e, "bzpf_linear_residual");
+  return done(bzpf::launch_linear(x, w, bias, y, dt, BZPF_F32, rows, K, M, 1, S(stream)), "bzpf_linear_residual");
+}
+
 int bzpf_swiglu(const void* h, void* a, int dt, int64_t rows, int hidden, void* stream) {
   REQUIRE(h != nullptr && a != nullptr, "bzpf_swiglu: NULL pointer");
   REQUIRE(dt_ok(dt), "bzpf_swiglu: bad dtype");

@@ -2,6 +2,8 @@
 //   y[r][m] = x[r] . W[m] + bias[m]                     (epi 0: stored as fp16 or fp32)
 //   y[r][m] += x[r] . W[m] + bias[m]                    (epi 1: fp32 y)
 //   y[r][m] += sigmoid(gate[r % gate_rows][m]) * (..)   (epi 2: fp32 y, the diffusion transformer's gated residuals)
+//   y[r][m] = res[r][m] + x[r] . W[m] + bias[m]         (epi 3: fp32 y, res passed as `gate` with pitch ld_gate: an
+//                                                        update written out of place, same sums as a copy + epi 1)
 // with x [R][K] and W [M][K] both K-contiguous (nn.Linear), K a multiple of 128 bytes (64 fp16 / 32 fp32 elements).
 // Reference behaviour: the nn.Linear / lin16 calls these replace (boltz_mlx/kernels.py:1360-1370;
 // boltz_mlx/modules/transformersv2.py:199-264).
@@ -154,7 +156,10 @@ __global__ __launch_bounds__(256, 2) void gemm_nt_k(const TX* __restrict__ x, co
         }
         TY* yp = y + r * M + m;
         if constexpr (sizeof(TY) == 4) {
-          if (epi >= 1) v4 += *reinterpret_cast<const f4*>(yp);
+          if (epi == 3)
+            v4 += *reinterpret_cast<const f4*>(gate + r * ld_gate + m);
+          else if (epi >= 1)
+            v4 += *reinterpret_cast<const f4*>(yp);
           *reinterpret_cast<f4*>(yp) = v4;
         } else {
           *reinterpret_cast<half4*>(yp) = half4{(half_t)v4[0], (half_t)v4[1], (half_t)v4[2], (half_t)v4[3]};
@@ -260,7 +265,8 @@ __global__ __launch_bounds__(256, BM * BR > 128 * 64 ? 1 : 2) void gemm_lds_k(co
         for (int q = 0; q < 4; q++) {
           const int m = m0 + BM / 2 * wm + 32 * mb + 8 * q + 4 * hh;
           const bool in = rin && m < M;
-          ypre[rb][mb][q] = in && epi >= 1 ? *reinterpret_cast<const f4*>(y + r * M + m) : f4{0.f, 0.f, 0.f, 0.f};
+          const float* src = epi == 3 ? gate + r * ld_gate + m : y + r * M + m;  // the residual's source
+          ypre[rb][mb][q] = in && epi >= 1 ? *reinterpret_cast<const f4*>(src) : f4{0.f, 0.f, 0.f, 0.f};
           gpre[rb][mb][q] = in && grow != nullptr ? *reinterpret_cast<const f4*>(grow + m) : f4{0.f, 0.f, 0.f, 0.f};
         }
     }
@@ -337,13 +343,16 @@ __global__ __launch_bounds__(256, BM * BR > 128 * 64 ? 1 : 2) void gemm_lds_k(co
         f4 v4 = f4{acc[mb][rb][4 * q], acc[mb][rb][4 * q + 1], acc[mb][rb][4 * q + 2], acc[mb][rb][4 * q + 3]};
         if (bias != nullptr) v4 += *reinterpret_cast<const f4*>(bias + m);
         TY* yp = y + r * M + m;
-        if constexpr (sizeof(TY) == 4) {  // epi 1 and 2 (fp32 y only)
+        if constexpr (sizeof(TY) == 4) {  // epi 1, 2 and 3 (fp32 y only)
           if (epi == 2) {
             const f4 gv = PRE ? gpre[rb][mb][q] : *reinterpret_cast<const f4*>(gate + (r % gate_rows) * ld_gate + m);
             v4 = f4{v4[0] * sigmoidf_(gv[0]), v4[1] * sigmoidf_(gv[1]), v4[2] * sigmoidf_(gv[2]),
                     v4[3] * sigmoidf_(gv[3])};
           }
-          if (epi >= 1) v4 += PRE ? ypre[rb][mb][q] : *reinterpret_cast<const f4*>(yp);
+          if (epi >= 1)
+            v4 += PRE        ? ypre[rb][mb][q]
+                  : epi == 3 ? *reinterpret_cast<const f4*>(gate + r * ld_gate + m)
+                             : *reinterpret_cast<const f4*>(yp);
           *reinterpret_cast<f4*>(yp) = v4;
         } else {
           *reinterpret_cast<half4*>(yp) = half4{(half_t)v4[0], (half_t)v4[1], (half_t)v4[2], (half_t)v4[3]};
@@ -556,7 +565,7 @@ hipError_t launch_gemm_nt(const void* x, const void* w, const float* bias, void*
                           int K, int M, int epi, const float* gate, int64_t ld_gate, int64_t gate_rows,
                           hipStream_t st) {
   if ((x_dt != DT_F16 && x_dt != DT_F32) || !gemm_nt_ok(x_dt, x, w, bias, y, R, K, M, gate, ld_gate) || epi < 0 ||
-      epi > 2 || (epi >= 1 && y_dt != DT_F32) || (epi == 2 && (gate == nullptr || gate_rows < 1)))
+      epi > 3 || (epi >= 1 && y_dt != DT_F32) || (epi >= 2 && (gate == nullptr || gate_rows < 1)))
     return hipErrorInvalidValue;
   if (x_dt == DT_F32)  // fp32 operands: 64 x 64 tiles (the m track's 409,600-row projections)
     return gemm_t<64, 64, float>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st);

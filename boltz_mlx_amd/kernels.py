@@ -508,6 +508,22 @@ def linear(x, w, bias=None, out=None, out_dtype=None, accumulate: bool = False) 
     return out
 
 
+def linear_residual(x, w, res: torch.Tensor, out: torch.Tensor, bias=None) -> torch.Tensor:
+    """out (fp32) = res + x w^T + bias over the rows of x, for an fp32 res [rows, M] with unit column stride (a
+    residual update written out of place: the same sums as copying res into out and accumulating)."""
+    _dev(x, w, out)
+    K = x.shape[-1]
+    M = w.shape[0]
+    rows = x.numel() // K
+    if w.shape[1] != K or w.dtype != x.dtype or out.dtype != torch.float32 or out.numel() != rows * M \
+            or not res.is_cuda or res.dtype != torch.float32 or res.dim() != 2 or res.shape != (rows, M) \
+            or res.stride(1) != 1:
+        raise ValueError("linear_residual: shape/dtype mismatch")
+    b = None if bias is None else f32c(bias)
+    call("bzpf_linear_residual", _p(x), _p(w), _p(b), _p(res), res.stride(0), _p(out), _dt(x), rows, K, M, _stream())
+    return out
+
+
 def linear_gated(x, w, gate: torch.Tensor, out: torch.Tensor, bias=None) -> torch.Tensor:
     """out (fp32) += sigmoid(gate) * (x w^T + bias) over the rows of x; gate is an fp32 [rows_g, M] view whose
     rows may have a pitch (a slice of the precomputed conditioning), row r using gate row r % rows_g

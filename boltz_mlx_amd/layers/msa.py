@@ -31,14 +31,17 @@ class MSALayer(torch.nn.Module):
                 **unused) -> tuple[torch.Tensor, torch.Tensor]:
         """z [B, N, N, token_z], m [B, S, N, msa_s], token_mask: the pair mask [B, N, N], msa_mask [B, S, N] ->
         (z, m) fp32. The reference's chunk_* / use_kernels keywords are accepted and ignored."""
-        z = z.to(torch.float32).clone().contiguous()
-        m = m.to(torch.float32).clone().contiguous()
+        # the first update of each stream is written out of place (input + update), so the inputs are not copied
+        z_in = z.to(torch.float32).contiguous()
+        m_in = m.to(torch.float32).contiguous()
+        z = torch.empty_like(z_in)
+        m = torch.empty_like(m_in)
         pm = token_mask.to(torch.float32).contiguous()
         S, N, D = m.shape[1:]
         for b in range(z.shape[0]):
-            self.pair_weighted_averaging.accumulate(m[b], m[b], z[b], pm[b])
+            self.pair_weighted_averaging.accumulate(m[b], m_in[b], z_in[b], pm[b], resid=m_in[b])
             m2 = m[b].view(S * N, D)
             self.msa_transition.inplace(m2)
-            self.outer_product_mean.accumulate(z[b], m[b], msa_mask[b])
+            self.outer_product_mean.accumulate(z[b], m[b], msa_mask[b], resid=z_in[b])
         self.pairformer_layer.inplace(z, pm)
         return z, m

@@ -46,8 +46,10 @@ class OuterProductMean(torch.nn.Module):
             self.accumulate(out[b], m[b], mask[b], accumulate=False)
         return out
 
-    def accumulate(self, z: torch.Tensor, m: torch.Tensor, mask: torch.Tensor, accumulate: bool = True) -> None:
-        """z [N, N, c_out] fp32 contiguous (+)= the layer's output for one MSA m [S, N, c_in], mask [S, N]."""
+    def accumulate(self, z: torch.Tensor, m: torch.Tensor, mask: torch.Tensor, accumulate: bool = True,
+                   resid: torch.Tensor | None = None) -> None:
+        """z [N, N, c_out] fp32 contiguous (+)= the layer's output for one MSA m [S, N, c_in], mask [S, N]; with
+        resid (fp32 [N, N, c_out], not overlapping z) z = resid + the output instead."""
         S, N, c_in = m.shape
         co = self.proj_o.out_features
         w_ab, w_o = K.kernel_weight(self, "w_ab"), K.kernel_weight(self, "w_o")
@@ -64,4 +66,8 @@ class OuterProductMean(torch.nn.Module):
         for i0 in range(0, N, step):
             n = min(step, N - i0)
             zz = K.opm_outer_planes(planes, num, S, N, i0, n, out_dtype=w_o.dtype)
-            K.linear(zz, w_o, bias=self.proj_o.bias, out=z2[i0 * N:(i0 + n) * N], accumulate=accumulate)
+            if resid is not None:
+                r2 = resid.reshape(N * N, co)[i0 * N:(i0 + n) * N]
+                K.linear_residual(zz, w_o, r2, z2[i0 * N:(i0 + n) * N], bias=self.proj_o.bias)
+            else:
+                K.linear(zz, w_o, bias=self.proj_o.bias, out=z2[i0 * N:(i0 + n) * N], accumulate=accumulate)

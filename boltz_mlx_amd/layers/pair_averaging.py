@@ -46,8 +46,9 @@ class PairWeightedAveraging(torch.nn.Module):
         return out
 
     def accumulate(self, out: torch.Tensor, m: torch.Tensor, z: torch.Tensor, pair_mask: torch.Tensor,
-                   accumulate: bool = True) -> None:
-        """out [S, N, c_m] fp32 contiguous (+)= the layer's output for one MSA m [S, N, c_m] and z [N, N, c_z]."""
+                   accumulate: bool = True, resid: torch.Tensor | None = None) -> None:
+        """out [S, N, c_m] fp32 contiguous (+)= the layer's output for one MSA m [S, N, c_m] and z [N, N, c_z];
+        with resid (fp32 [S, N, c_m], not overlapping out) out = resid + the output instead."""
         S, N, _ = m.shape
         HC = self.c_h * self.num_heads
         w_mg, w_o = K.kernel_weight(self, "w_mg"), K.kernel_weight(self, "w_o")
@@ -60,4 +61,7 @@ class PairWeightedAveraging(torch.nn.Module):
         logits = K.pair_bias(z.to(torch.float32).contiguous(), self.norm_z, w_z)
         w = K.pwa_softmax(logits, pair_mask.to(torch.float32).contiguous(), self.inf)
         og = K.pwa_avg(w, vg[:, :HC], vg[:, HC:], S, N)
-        K.linear(og, w_o, out=out.view(S * N, self.c_m), accumulate=accumulate)
+        if resid is not None:
+            K.linear_residual(og, w_o, resid.reshape(S * N, self.c_m), out.view(S * N, self.c_m))
+        else:
+            K.linear(og, w_o, out=out.view(S * N, self.c_m), accumulate=accumulate)

@@ -162,6 +162,13 @@ int bzpf_attn_out_transition(const void* o, const void* w_o, int trans, const fl
 int bzpf_linear(const void* x, const void* w, const float* bias, void* y, int dt, int y_dt, int64_t rows, int K,
                 int M, int accumulate, void* stream);
 
+/* The same layer written out of place onto a residual: y[r] = res[r] + x[r] . W^T + bias for fp32 y [rows, M] and
+ * fp32 res rows of pitch ld_res (16-byte aligned, ld_res % 4 == 0; res may not overlap y), the same sums as copying
+ * res into y and calling bzpf_linear with accumulate. The residual updates of the MSA block
+ * (boltz_mlx/layers/msa.py: m + pair_weighted_averaging(m), z + outer_product_mean(m)) without copying the inputs. */
+int bzpf_linear_residual(const void* x, const void* w, const float* bias, const float* res, int64_t ld_res, float* y,
+                         int dt, int64_t rows, int K, int M, void* stream);
+
 /* a[r][c] = silu(h[r][c]) * h[r][hidden + c]. Replaces the SwiGLU of Transition
  * (boltz_mlx/layers/transition.py:148-154; kernels.swiglu16, boltz_mlx/kernels.py:1378-1386). */
 int bzpf_swiglu(const void* h, void* a, int dt, int64_t rows, int hidden, void* stream);

@@ -142,6 +142,27 @@ def test_linear_fp32_accuracy(R, Kd, M):
     assert np.array_equal(K.linear(dev(xm), dev(wm)).cpu().numpy(), xm @ wm.T)
 
 
+@pytest.mark.parametrize("dt,R,Kd,M", [(torch.float32, 300, 64, 64), (torch.float32, 129, 48, 20),
+                                       (torch.float16, 2100, 1024, 128), (torch.float16, 130, 192, 260)])
+def test_linear_residual_equals_copy_and_accumulate(dt, R, Kd, M):
+    """out = res + x w^T + bias written out of place equals copying res and accumulating, bit for bit, on the
+    fp32-MFMA, generic, LDS-direct and register-staged fp16 kernels; res may be a strided row view."""
+    from boltz_mlx_amd import kernels as K
+
+    rng = np.random.default_rng(R + Kd + M)
+    x = dev(rng.standard_normal((R, Kd)), dt)
+    w = dev(rng.standard_normal((M, Kd)) / np.sqrt(Kd), dt)
+    b = dev(rng.standard_normal(M))
+    big = dev(rng.standard_normal((R, M + 12)))
+    res = big[:, 4:4 + M]
+    got = torch.empty((R, M), device="cuda")
+    K.linear_residual(x, w, res, got, bias=b)
+    want = res.contiguous().clone()
+    K.linear(x, w, bias=b, out=want, accumulate=True)
+    torch.cuda.synchronize()
+    assert torch.equal(got, want)
+
+
 def test_gemm_f16_large_grid_tiles():
     """A grid of 2048+ 128 x 128 tiles takes the 128 x 128 kernel (smaller grids the 64 x 64 one): its rows equal
     the 64 x 64 kernel's on the same rows bit for bit (same k order per element), and the last row tile, cut short,

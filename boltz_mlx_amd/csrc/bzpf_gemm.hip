@@ -574,6 +574,11 @@ hipError_t launch_gemm_nt(const void* x, const void* w, const float* bias, void*
   // gated outputs 12.6 -> 11.7 and 17.2 -> 16.1 us (64 x 64). Same sums in the same order. The s track's GEMMs
   // (N rows) keep the register-staged form: they run beside the attention core, and there the LDS-direct form's
   // workgroups found compute units far later (0.85 ms against 0.04 ms per launch at N = 1000).
+  // 128 columns over many rows (the outer product mean's proj_o, 160,000 x 1024 -> 128 at N = 400): one 128-wide
+  // column tile, so each x row is read once (124.8 against 148.0 us on 64 x 64 tiles; 128 x 64 and 64 x 128 with
+  // three stages 130.5 and 129.0)
+  if (M == 128 && R >= 65536)
+    return gemm_lds_t<128, 128, 2>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st);
   if (gemm_tile_choice(R, M) != 0 && R >= 1536)
     return M >= 2048 ? gemm_lds_t<192, 128, 3>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st)
                      : gemm_lds_t<64, 64, 3>(x, w, bias, y, y_dt, R, K, M, epi, gate, ld_gate, gate_rows, st);

@@ -407,11 +407,12 @@ def test_step_graph_replays_equal_eager(precision):
         _ = (torch.randn(1000, device="cuda") * 2).sum().item()  # unrelated eager work between replays
 
 
-@pytest.mark.parametrize("R,Kd,M", [(1537, 64, 132), (1600, 192, 2052), (2000, 768, 3072), (2100, 768, 772)])
+@pytest.mark.parametrize("R,Kd,M", [(1537, 64, 132), (1600, 192, 2052), (2000, 768, 3072), (2100, 768, 772),
+                                    (65600, 128, 128)])
 def test_gemm_lds_direct_paths(R, Kd, M):
-    """The LDS-direct GEMM (1536+ rows: 64 x 64 tiles, 192 x 128 for 2048+ output columns; tiles dealt to the XCDs
-    in contiguous ranges, ragged tile counts) in all four epilogues against float64, and bit for bit against the
-    register-staged kernel on the first 100 rows (same k order per element)."""
+    """The LDS-direct GEMM (1536+ rows: 64 x 64 tiles, 192 x 128 for 2048+ output columns, 128 x 128 for 128 columns
+    over 65,536+ rows; tiles dealt to the XCDs in contiguous ranges, ragged tile counts) in all four epilogues against
+    float64, and bit for bit against the register-staged kernel on the first 100 rows (same k order per element)."""
     from boltz_mlx_amd import kernels as K
 
     rng = np.random.default_rng(R + Kd + M)

@@ -358,3 +358,30 @@ def test_msa_layer_fused_transition(monkeypatch):
     mz = O.metrics(zg[:, :v, :v] - z[:, :v, :v], zr[:, :v, :v] - z[:, :v, :v])
     mm = O.metrics(mg[:, :, :v] - m[:, :, :v], mr[:, :, :v] - m[:, :, :v])
     assert mz["rel_fro"] < 5e-3 and mm["rel_fro"] < 5e-3, (mz, mm)
+
+
+@pytest.mark.parametrize("precision", ["fp32", "f16"], indirect=True)
+def test_msa_layer_batch2(precision):
+    """Two batch elements through the MSA layer (its first updates written out of place onto each element's inputs,
+    the inputs left unchanged) against the oracle."""
+    from boltz_mlx_amd.layers.msa import MSALayer
+    from boltz_mlx_amd.weights import load_module
+
+    N, S = 24, 19
+    p = rand_params(shapes_msa_layer(), seed=41, std=0.05)
+    z, _, pm = pair_inputs(N, 128, seed=42, n_pad=2, B=2)
+    rng = np.random.default_rng(43)
+    m = rng.standard_normal((2, S, N, 64))
+    msa_mask = (rng.random((2, S, N)) > 0.1).astype(np.float64)
+    mod = load_module(MSALayer(64, 128), p).cuda()
+    zd, md = dev(z), dev(m)
+    zg, mg = mod(zd, md, dev(pm), dev(msa_mask))
+    assert torch.equal(zd, dev(z)) and torch.equal(md, dev(m))  # inputs untouched
+    zr, mr = OM.msa_layer(z, m, pm, msa_mask, p)
+    v = N - 2
+    zg, mg = zg.cpu().numpy(), mg.cpu().numpy()
+    mz = O.metrics(zg[:, :v, :v] - z[:, :v, :v], zr[:, :v, :v] - z[:, :v, :v])
+    mm = O.metrics(mg[:, :, :v] - m[:, :, :v], mr[:, :, :v] - m[:, :, :v])
+    assert mz["finite"] and mm["finite"]
+    tol = 1e-5 if precision == "fp32" else 5e-3
+    assert mz["rel_fro"] < tol and mm["rel_fro"] < tol, (mz, mm)

@@ -581,7 +581,7 @@ def main() -> int:
                       if not k.endswith(K.SIDE) and kernel_work(k, args.n_small)[0] > 0}
     value = args.steps / dt
     out = {
-        "metric": "Pairformer blocks/sec at N=1000 fp16",
+        "metric": f"Pairformer blocks/sec at N={args.n} fp16",
         "value": round(value, 4),
         "unit": "blocks/s",
         "n_gpus": 1,

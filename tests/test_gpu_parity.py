@@ -321,7 +321,7 @@ def test_attention_pair_bias_f16_keeps_fp32_projections(N):
 
 
 @pytest.mark.parametrize("precision", ["fp32", "f16"], indirect=True)
-@pytest.mark.parametrize("N,n_pad", [(24, 3), (50, 0)])
+@pytest.mark.parametrize("N,n_pad", [(1, 0), (2, 1), (24, 3), (50, 0), (65, 6)])
 def test_pairformer_layer(precision, N, n_pad):
     from boltz_mlx_amd.layers.pairformer import PairformerLayer
 

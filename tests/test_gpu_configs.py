@@ -373,6 +373,30 @@ def test_pairformer_layer_B2(precision):
     check("pairformer_layer B=2 s", s_g.cpu().numpy(), s_r, precision, F16_LAYER)
 
 
+@pytest.mark.parametrize("precision", ["fp32", "f16"], indirect=True)
+def test_pairformer_module_B2(precision):
+    """Two blocks over a batch of two with different padding: the module's schedule for B > 1 (each element's s track
+    on the side stream, no norm_in carry between layers)."""
+    from boltz_mlx_amd.layers.pairformer import PairformerModule
+
+    N, cs, cz, H, nb = 29, 384, 128, 16, 2
+    p = {}
+    for i in range(nb):
+        p.update({f"layers.{i}.{k}": v for k, v in rand_params(shapes_layer(cs, cz, H), seed=1700 + i, std=0.05).items()})
+    rng = np.random.default_rng(1702)
+    z = rng.standard_normal((2, N, N, cz))
+    s = rng.standard_normal((2, N, cs))
+    tok = np.ones((2, N))
+    tok[0, -2:] = 0
+    tok[1, -7:] = 0
+    pm = tok[:, :, None] * tok[:, None, :]
+    f32 = np.float32
+    s_r, z_r = O.pairformer_module(s.astype(f32), z.astype(f32), tok.astype(f32), pm.astype(f32), cast(p, f32), nb, H)
+    s_g, z_g = load(PairformerModule(cs, cz, nb, H), p)(dev(s), dev(z), dev(tok), dev(pm))
+    check("pairformer_module B=2 z", z_g.cpu().numpy(), z_r, precision, F16_LAYER)
+    check("pairformer_module B=2 s", s_g.cpu().numpy(), s_r, precision, F16_LAYER)
+
+
 # ------------------------------------------------------------------------------------------------ xn contract
 
 @pytest.mark.parametrize("starting", [True, False])

@@ -248,6 +248,44 @@ def test_c4_trunk_f16_vs_fp32_and_padding(N):
         K.set_precision(old)
 
 
+@pytest.mark.timeout(600)
+def test_trunk_blocks_N1537_f16_vs_fp32():
+    """Beyond the benchmark's sizes: two blocks at N = 1537 (rows padded to 1600, a partial 256-wide contraction tile
+    and query block, 13 query blocks per attention row) with 3% padded tokens; f16 against the fp32 kernels, both on
+    the GPU (the float64 oracle at this size would take minutes), and padding invariance bit for bit."""
+    from boltz_mlx_amd import kernels as K
+
+    N, blocks = 1537, 2
+    n_real = N - 46
+    old = K.PRECISION
+    try:
+        m, s, z, tok, pm = _trunk(N, blocks, seed=7)
+        tok.fill_(1.0)
+        tok[:, n_real:] = 0
+        pm.copy_(tok[:, :, None] * tok[:, None, :])
+        K.set_precision("f16")
+        with torch.no_grad():
+            s16, z16 = m(s, z, tok, pm)
+            z2 = z.clone()
+            z2[:, n_real:] = 3 * torch.randn_like(z2[:, n_real:])
+            s16b, z16b = m(s, z2, tok, pm)
+        torch.cuda.synchronize()
+        assert torch.isfinite(z16).all() and torch.isfinite(s16).all() and m.fp16_fallbacks == 0
+        assert torch.equal(z16b[:, :n_real, :n_real], z16[:, :n_real, :n_real])
+        assert torch.equal(s16b[:, :n_real], s16[:, :n_real])
+        del z2, s16b, z16b
+        K.set_precision("fp32")
+        with torch.no_grad():
+            s32, z32 = m(s, z, tok, pm)
+        torch.cuda.synchronize()
+        rz = _rel_fro(z16[:, :n_real, :n_real] - z[:, :n_real, :n_real], z32[:, :n_real, :n_real] - z[:, :n_real, :n_real])
+        rs = _rel_fro(s16[:, :n_real] - s[:, :n_real], s32[:, :n_real] - s[:, :n_real])
+        print(f"N={N} two blocks f16 vs fp32: rel_fro(z update)={rz:.3e} rel_fro(s update)={rs:.3e}", flush=True)
+        assert rz <= TRUNK_REL_FRO and rs <= TRUNK_REL_FRO
+    finally:
+        K.set_precision(old)
+
+
 # ------------------------------------------------------------------------------------------------ C5
 
 def _diff_params(D, depth, std, seed):

@@ -138,7 +138,7 @@ def test_c2_tri_att_N400(precision, starting):
 # ------------------------------------------------------------------------------------------------ C3
 
 @pytest.mark.timeout(600)
-@pytest.mark.parametrize("precision", ["f16"], indirect=True)
+@pytest.mark.parametrize("precision", ["fp32", "f16"], indirect=True)
 @pytest.mark.parametrize("outgoing", [True, False])
 def test_c3_tri_mul_N800(precision, outgoing):
     from boltz_mlx_amd.layers.triangular_mult import TriangleMultiplicationIncoming, TriangleMultiplicationOutgoing

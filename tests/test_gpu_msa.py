@@ -295,6 +295,36 @@ def test_msa_layer(precision):
         assert mz["rel_fro"] < 5e-3 and mm["rel_fro"] < 5e-3, (mz, mm)
 
 
+@pytest.mark.timeout(600)
+@pytest.mark.parametrize("precision", ["fp32", "f16"], indirect=True)
+def test_msa_layer_N260(precision):
+    """The MSA layer at N = 260 (67,600 pairs: the outer product mean's output projection on the 128-column
+    LDS-direct tiles for 65,536+ rows, the fused 64-channel kernels on full tiles) with 48 MSA rows, 6 padded tokens
+    and a random MSA mask, against the oracle."""
+    from boltz_mlx_amd.layers.msa import MSALayer
+    from boltz_mlx_amd.weights import load_module
+
+    N, S, npad = 260, 48, 6
+    p = rand_params(shapes_msa_layer(), seed=41, std=0.05)
+    z, _, pm = pair_inputs(N, 128, seed=42, n_pad=npad)
+    rng = np.random.default_rng(43)
+    m = rng.standard_normal((1, S, N, 64))
+    msa_mask = (rng.random((1, S, N)) > 0.1).astype(np.float64)
+    mod = load_module(MSALayer(64, 128), p).cuda()
+    zg, mg = mod(dev(z), dev(m), dev(pm), dev(msa_mask))
+    zr, mr = OM.msa_layer(z, m, pm, msa_mask, p)
+    v = N - npad
+    zg, mg = zg.cpu().numpy(), mg.cpu().numpy()
+    assert np.isfinite(zg).all() and np.isfinite(mg).all()
+    mz = O.metrics(zg[:, :v, :v] - z[:, :v, :v], zr[:, :v, :v] - z[:, :v, :v])
+    mm = O.metrics(mg[:, :, :v] - m[:, :, :v], mr[:, :, :v] - m[:, :, :v])
+    print(f"msa layer N={N} S={S} [{precision}]: z {mz} m {mm}", flush=True)
+    if precision == "fp32":
+        assert mz["rel_fro"] < 1e-5 and mm["rel_fro"] < 1e-5, (mz, mm)
+    else:
+        assert mz["rel_fro"] < 5e-3 and mm["rel_fro"] < 5e-3, (mz, mm)
+
+
 @pytest.mark.parametrize("rows,H", [(300, 256), (5000, 256), (257, 128), (20000, 384)])
 def test_transition64_f16(rows, H):
     """The fused 64-channel transition against the float64 formula on the same fp16 weights, with xn and the SwiGLU

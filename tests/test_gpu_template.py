@@ -86,7 +86,7 @@ def test_channels_to_rows():
 
 
 @pytest.mark.parametrize("precision", ["fp32", "f16"], indirect=True)
-@pytest.mark.parametrize("N,n_pad", [(24, 2), (70, 5)])
+@pytest.mark.parametrize("N,n_pad", [(24, 2), (70, 5), (260, 6)])
 def test_noseq_layer_c64(precision, N, n_pad):
     from boltz_mlx_amd.layers.pairformer import PairformerNoSeqLayer
     from boltz_mlx_amd.weights import load_module
